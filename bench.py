@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Gaussian-splatting rasterizer.
+
+Metric: fwd+bwd iterations/s and forward FPS at 1M Gaussians,
+SH degree 3, 1920x1080 (config 3: antialias, 8 orbit views), plus the HBM
+roofline fraction.  A step is one view: GaussianModel.render -> L1 loss
+against a seeded U(0,1) target -> backward to every raw parameter.  Inputs,
+targets and parameters are resident in HBM before timing starts.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+
+Prints one JSON line.  ``roofline`` is for the dominant kernel, from its
+algorithmic bytes per launch and its mean duration measured with HIP events
+on its launch stream during the timed steps; ``cpu_baseline`` times the CPU
+oracle (C, OpenMP) on one fwd+bwd iteration of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=24)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-stages", action="store_true",
+                    help="print per-stage times to stderr")
+    return ap.parse_args()
+
+
+def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
+    """Compulsory HBM bytes per stage (each tensor read or written once)."""
+    Cw = C if sh_path else 0
+    dz = 4 if depth else 0
+    raster_fwd = D * (28 + 4 * C + dz) + P * (4 * C + 8 + dz)
+    raster_bwd = D * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C)
+    pre_fwd = N * (44 + 12 * Ka) + N * (36 + 4 * Cw)
+    binning = 28 * N + 44 * D
+    pre_bwd = N * (44 + 12 * Ka + 24 + 4 * Cw) + N * (44 + 12 * Ka)
+    fwd = pre_fwd + binning + raster_fwd
+    bwd = raster_bwd + pre_bwd
+    loss = 12 * C * P
+    return dict(raster_fwd=raster_fwd, raster_bwd=raster_bwd, preprocess_fwd=pre_fwd,
+                binning=binning, preprocess_bwd=pre_bwd, fwd=fwd, bwd=bwd, loss=loss,
+                iter=fwd + bwd + loss)
+
+
+def _traffic(kernel: str, workload: str):
+    """HBM bytes per launch measured by rocprofv3 PMC runs, if recorded."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"traffic_{kernel}_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(scene, view: int, cfg_name: str):
+    """One fwd+bwd iteration of the oracle on the host cores."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import oracle as O
+
+    threads = O.default_threads()
+    cam = scene.cameras[view]
+    f = cam.gsx_fields()
+    oc = O.make_camera(f["R"], f["t"], f["center"], f["fx"], f["fy"], f["cx"], f["cy"],
+                       f["lim_x"], f["lim_y"], f["znear"], f["width"], f["height"])
+    if scene.features is not None:
+        scales, opac, flags, sh = scene.scales, scene.opacities, 0, None
+    else:
+        scales, opac = scene.log_scales, scene.logit_opacities
+        flags = O.LOG_SCALES | O.LOGIT_OPACITY
+        sh = np.concatenate([scene.sh_dc, scene.sh_rest], 1)
+    if scene.antialias:
+        flags |= O.ANTIALIAS
+    target = scene.target(cam)
+    t0 = time.perf_counter()
+    pre = O.preprocess_fwd(oc, scene.means, scene.quats, scales, opac, sh=sh,
+                           degree=scene.sh_degree, flags=flags, threads=threads)
+    feats = pre["colors"] if sh is not None else scene.features
+    ids, ranges, _, _ = O.bin_gaussians(pre["means2d"], pre["radii"], pre["depths"], cam.width,
+                                        cam.height, threads=threads)
+    r = O.raster_fwd(pre["means2d"], pre["conics"], pre["opac_eff"], feats, ids, ranges,
+                     cam.width, cam.height, depths=pre["depths"] if scene.depth else None,
+                     threads=threads)
+    t1 = time.perf_counter()
+    if scene.backward:
+        g_img = (np.sign(r["image"] - target) / np.float32(target.size)).astype(np.float32)
+        gr = O.raster_bwd(pre["means2d"], pre["conics"], pre["opac_eff"], feats, ids, ranges,
+                          cam.width, cam.height, r["final_T"], r["n_contrib"], g_img,
+                          threads=threads)
+        O.preprocess_bwd(oc, scene.means, scene.quats, scales, opac,
+                         pre["colors"] if sh is not None else None,
+                         0 if sh is None else sh.shape[1], scene.sh_degree, flags,
+                         gr["means2d"], gr["conics"], gr["opacities"],
+                         gr["features"] if sh is not None else None, threads=threads)
+    t2 = time.perf_counter()
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    total = t2 - t0
+    return {"value": round(1.0 / total, 4), "unit": "it/s" if scene.backward else "frames/s",
+            "cores": threads, "kind": "port",
+            "sample": f"1 {'fwd+bwd iteration' if scene.backward else 'forward'} of view {view} "
+                      f"of {cfg_name} (full frame), C oracle + OpenMP",
+            "fwd_s": round(t1 - t0, 3), "iter_s": round(total, 3), "cpu_model": cpu}
+
+
+def main():
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: only --gpus 1 is supported (got --gpus {args.gpus}, WORLD_SIZE "
+              f"{world}). This build measures the rasterizer on one MI355X; DESIGN.md describes "
+              "how the path would shard across GPUs.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from mlx3d_amd import _lib, scenes
+    from mlx3d_amd.profiling import StageTimer
+    from mlx3d_amd.splatting import GaussianModel, render_gaussian_features
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    scene = scenes.make_scene(args.config)
+    cams = scene.cameras
+    nviews = len(cams)
+    feat_mode = scene.features is not None
+    cu = lambda a: torch.as_tensor(a).to(dev)  # noqa: E731
+    if feat_mode:
+        leaf = {k: cu(v).requires_grad_(scene.backward) for k, v in dict(
+            means=scene.means, quats=scene.quats, scales=scene.scales,
+            opacities=scene.opacities, features=scene.features).items()}
+    else:
+        model = GaussianModel({"means": cu(scene.means), "quats": cu(scene.quats),
+                               "scales": cu(scene.log_scales),
+                               "opacities": cu(scene.logit_opacities),
+                               "sh_dc": cu(scene.sh_dc), "sh_rest": cu(scene.sh_rest)},
+                              sh_degree=3)
+        model.active_sh_degree = scene.sh_degree
+        model.requires_grad_(scene.backward)
+        leaf = model.params
+    targets = [cu(scene.target(c)) for c in cams]
+    torch.cuda.synchronize()
+
+    def render(i):
+        cam = cams[i % nviews]
+        if feat_mode:
+            out = render_gaussian_features(cam, leaf["means"], leaf["quats"], leaf["scales"],
+                                           leaf["opacities"], leaf["features"],
+                                           antialias=scene.antialias, return_depth=scene.depth)
+            return out["features"]
+        out = model.render(cam, antialias=scene.antialias, return_depth=scene.depth)
+        return out["image"]
+
+    def step(i):
+        for p in leaf.values():
+            p.grad = None
+        if not scene.backward:
+            with torch.no_grad():
+                render(i)
+            return
+        img = render(i)
+        loss = (img - targets[i % nviews]).abs().mean()
+        loss.backward()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    timer = StageTimer()
+    with timer:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+
+    # forward-only frames per second over the same views
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        f0 = time.perf_counter()
+        for i in range(args.steps):
+            render(i)
+        torch.cuda.synchronize()
+        f1 = time.perf_counter()
+    ms_fwd = (f1 - f0) * 1e3 / args.steps
+
+    N = scene.n
+    P = cams[0].width * cams[0].height
+    C = scene.channels
+    Ka = 0 if feat_mode else (scene.sh_degree + 1) ** 2
+    D = float(np.mean(timer.counters["duplicates"]))
+    B = algorithmic_bytes(N, D, P, C, Ka, not feat_mode, scene.depth)
+    stages = {}
+    for name in ("preprocess_fwd", "binning", "raster_fwd", "raster_bwd", "preprocess_bwd"):
+        ms = timer.mean_ms(name)
+        if not math.isnan(ms):
+            gbs = B[name] / (ms * 1e-3) / 1e9
+            stages[name] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
+                            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    kernels = [k for k in ("raster_fwd", "raster_bwd", "preprocess_fwd", "preprocess_bwd")
+               if k in stages]
+    dom = max(kernels, key=lambda k: stages[k]["ms"])
+    achieved = stages[dom]["GB/s"]
+    workload = scene.name
+    fwd_gbs = B["fwd"] / (ms_fwd * 1e-3) / 1e9
+    it_s = 1e3 / ms_step
+    out = {
+        "metric": "fwd+bwd iters/s, 1M Gaussians SH3 @1920x1080 (GaussianModel.render + L1 + "
+                  "backward)" if scene.backward else "forward frames/s",
+        "value": round(it_s, 3),
+        "unit": "it/s" if scene.backward else "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy PCG64 scene, random-init parameters)",
+        "config": {"workload": workload, "gaussians": N, "width": cams[0].width,
+                   "height": cams[0].height, "views": nviews, "sh_degree": scene.sh_degree,
+                   "channels": C, "antialias": scene.antialias, "depth": scene.depth,
+                   "duplicates_mean": int(D)},
+        "fwd_fps": round(1e3 / ms_fwd, 2),
+        "fwd_ms": round(ms_fwd, 4),
+        "fwd_hbm_roofline_frac": round(fwd_gbs / HBM_PEAK_GBS, 4),
+        "iter_hbm_roofline_frac": round(B["iter"] / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _traffic(dom, workload),
+                     "algorithmic_bytes": int(B[dom]), "mean_ms": stages[dom]["ms"]},
+        "stages": stages,
+    }
+    if not args.no_cpu_baseline:
+        print("bench: timing CPU oracle baseline ...", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(scene, 0, workload)
+    else:
+        out["cpu_baseline"] = None
+    if args.profile_stages:
+        print(json.dumps(stages, indent=1), file=sys.stderr)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,221 @@
+/*
+ * gsx.h -- C ABI of the MI355X (gfx950) Gaussian-splatting rasterizer.
+ *
+ * This is the drop-in boundary for mlx3D's tile-based 3DGS path.  The
+ * reference (amirhossein-razlighi/mlx3D v0.2.0, paths under src/mlx3d/) is
+ * pure Python on MLX; its device boundary is the set of mx.fast.metal_kernel
+ * launches and MLX-op pipelines listed beside each entry point below.  The
+ * Python package mlx3d_amd binds these symbols with ctypes (see
+ * mlx3d_amd/_lib.py) behind the reference's own function names.
+ *
+ * Conventions
+ *  - Every pointer is device memory (hipMalloc/torch CUDA tensors) unless
+ *    documented otherwise, contiguous, float32 or int32/uint32 as named.
+ *  - The caller owns all buffers; no entry point allocates device memory.
+ *    Scratch space comes in through an explicit workspace argument.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
+ *    Only gsx_bin_sort synchronises the stream (one 8-byte readback of the
+ *    duplicate count, as the reference does at tiles.py:68).
+ *  - Return value: GSX_OK (0) on success, > 0 = required capacity (retry
+ *    with a larger buffer), < 0 = error code (gsx_strerror).
+ *  - No C++ exception crosses the ABI.  Entry points are reentrant; calls
+ *    on different streams may run concurrently.
+ */
+#ifndef GSX_H
+#define GSX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GSX_ABI_VERSION 1
+#define GSX_TILE_SIZE 16 /* tiles.py:14 */
+
+enum gsx_status {
+    GSX_OK = 0,
+    GSX_ERR_INVALID = -1,     /* bad size / null pointer / unsupported shape */
+    GSX_ERR_HIP = -2,         /* a HIP runtime call failed                   */
+    GSX_ERR_WORKSPACE = -3,   /* workspace smaller than gsx_*_workspace_bytes */
+    GSX_ERR_TOO_LARGE = -4    /* a count exceeds the int32 index range       */
+};
+
+/* Flags of gsx_preprocess_fwd/bwd. */
+enum gsx_flags {
+    GSX_LOG_SCALES = 1,     /* scales are log-sigma: exp applied (model.py:116-118)  */
+    GSX_LOGIT_OPACITY = 2,  /* opacities are logits: sigmoid (model.py:120-122)      */
+    GSX_ANTIALIAS = 4       /* Mip-Splatting compensation (projection.py:125-129)    */
+};
+
+/* Pinhole camera, OpenCV convention, X_cam = R X_world + t
+ * (cameras/cameras.py:139-173).  All values are the float32 numbers the
+ * reference's float32 arithmetic sees: fx..cy rounded from the Python
+ * floats, lim_x/lim_y = float32(1.3 * 0.5 * width / fx) computed in double
+ * (projection.py:70-73), center = -(R^T t) (cameras.py:270-273). */
+typedef struct gsx_camera {
+    float R[9];
+    float t[3];
+    float center[3];
+    float fx, fy, cx, cy;
+    float lim_x, lim_y;
+    float znear;
+    int32_t width, height;
+} gsx_camera;
+
+const char* gsx_strerror(int status);
+int gsx_abi_version(void);
+/* Name of the GPU the library runs on and whether its code object matches. */
+int gsx_device_check(char* name_out, int name_len);
+
+/* ---------------------------------------------------------- projection --
+ * Replaces project_gaussians (splatting/projection.py:24-146): EWA
+ * projection to means2d (N,2), conics (N,3), depths (N), radii (N, float
+ * holding integers), compensation (N). */
+int gsx_project_fwd(const gsx_camera* cam, int64_t n, const float* means,
+                    const float* quats, const float* scales, float blur,
+                    int32_t antialias, float* means2d, float* conics,
+                    float* depths, float* radii, float* compensation,
+                    void* stream);
+
+/* VJP of project_gaussians (what MLX autodiff computes through
+ * projection.py:56-138).  Any cotangent may be NULL (= zero). */
+int gsx_project_bwd(const gsx_camera* cam, int64_t n, const float* means,
+                    const float* quats, const float* scales, float blur,
+                    int32_t antialias, const float* g_means2d,
+                    const float* g_conics, const float* g_depths,
+                    const float* g_compensation, float* g_means,
+                    float* g_quats, float* g_scales, void* stream);
+
+/* ------------------------------------------------------------------ SH --
+ * Replaces eval_sh (splatting/sh.py:41-78): sh (N,K,C), dirs (N,3) ->
+ * out (N,C) = sum_k basis_k(dir) sh[:,k] + 0.5, degree 0..3. */
+int gsx_eval_sh_fwd(int64_t n, int32_t K, int32_t C, int32_t degree,
+                    const float* sh, const float* dirs, float* out,
+                    void* stream);
+/* VJP of eval_sh: g_sh (N,K,C) fully written; g_dirs (N,3) may be NULL. */
+int gsx_eval_sh_bwd(int64_t n, int32_t K, int32_t C, int32_t degree,
+                    const float* sh, const float* dirs, const float* g_out,
+                    float* g_sh, float* g_dirs, void* stream);
+
+/* --------------------------------------------------- fused preprocess --
+ * One pass per Gaussian replacing GaussianModel.render's activations
+ * (model.py:116-126), project_gaussians, render_gaussians' opacity
+ * compensation, view directions and SH colour (render.py:73-80), and the
+ * per-Gaussian half of bin_gaussians (tiles.py:54-65).
+ *
+ * SH coefficients are read as coefficient 0 from sh0 (float3 per Gaussian,
+ * stride sh0_stride floats) and coefficients 1..K-1 from sh_rest (stride
+ * sh_rest_stride floats), so both a packed (N,K,3) tensor and the model's
+ * separate sh_dc (N,1,3) / sh_rest (N,K-1,3) tensors are read in place.
+ * sh0 == NULL selects colours mode: `colors` (N,3) are used as given.
+ *
+ * Outputs: means2d (N,2), depths (N), radii (N), compensation (N),
+ * conic_opacity (N,4) = (conic a, b, c, opacity*compensation),
+ * colors_out (N,3) (SH mode only), and for binning tile_counts (N),
+ * depth_keys (N) and tile_rects (N,2) (packed xmin|ymin<<16, w|h<<16). */
+int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means,
+                       const float* quats, const float* scales,
+                       const float* opacities, const float* sh0,
+                       int64_t sh0_stride, const float* sh_rest,
+                       int64_t sh_rest_stride, int32_t K, int32_t degree,
+                       uint32_t flags, float blur, float* means2d,
+                       float* depths, float* radii, float* compensation,
+                       float* conic_opacity, float* colors_out,
+                       uint32_t* tile_counts, uint32_t* depth_keys,
+                       uint32_t* tile_rects, void* stream);
+
+/* VJP of gsx_preprocess_fwd (MLX autodiff of the same expressions,
+ * render.py:75-80 with dirs under stop_gradient, colour clamp mask from
+ * colors_out).  g_means2d/g_conics/g_opac_eff come from gsx_raster_bwd;
+ * g_means2d_extra, g_depths, g_compensation are extra cotangents of the
+ * returned means2d/depths/compensation and may be NULL.  g_sh0/g_sh_rest
+ * use the strides of the forward; coefficients >= (degree+1)^2 are written
+ * as zero. */
+int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means,
+                       const float* quats, const float* scales,
+                       const float* opacities, const float* colors_out,
+                       int32_t K, int32_t degree, uint32_t flags, float blur,
+                       const float* g_means2d, const float* g_conics,
+                       const float* g_opac_eff, const float* g_colors,
+                       const float* g_means2d_extra, const float* g_depths,
+                       const float* g_compensation, float* g_means,
+                       float* g_quats, float* g_scales, float* g_opacities,
+                       float* g_sh0, int64_t sh0_stride, float* g_sh_rest,
+                       int64_t sh_rest_stride, void* stream);
+
+/* ------------------------------------------------------------- binning --
+ * Replaces bin_gaussians (splatting/tiles.py:19-182, refine_tiles off).
+ *
+ * gsx_bin_prepare: tiles.py:54-65 for externally supplied means2d (N,2),
+ * radii (N), depths (N) -> tile_counts, depth_keys, tile_rects. */
+int gsx_bin_prepare(int64_t n, const float* means2d, const float* radii,
+                    const float* depths, int32_t width, int32_t height,
+                    uint32_t* tile_counts, uint32_t* depth_keys,
+                    uint32_t* tile_rects, void* stream);
+
+/* Bytes of workspace gsx_bin_sort needs for n Gaussians, `capacity`
+ * duplicates and num_tiles tiles. */
+int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles);
+
+/* tiles.py:67-182: depth-sort, duplicate per tile, sort by tile, ranges.
+ * Order within a tile is (depth ascending, Gaussian index ascending) --
+ * the order of key = tile*N + rank(depth) with a stable argsort.  Writes
+ * sorted_ids (D) int32 and tile_ranges (num_tiles,2) int32 [start,end),
+ * (0,0) for empty tiles.  Synchronises `stream` once to read D into
+ * *num_dups.  Returns 1 (nothing written but *num_dups) if D > capacity. */
+int gsx_bin_sort(int64_t n, const uint32_t* tile_counts,
+                 const uint32_t* depth_keys, const uint32_t* tile_rects,
+                 int32_t width, int32_t height, void* workspace,
+                 int64_t workspace_bytes, int64_t capacity,
+                 int32_t* sorted_ids, int32_t* tile_ranges,
+                 int64_t* num_dups, void* stream);
+
+/* ---------------------------------------------------------- rasterizer --
+ * Packs conics (N,3) and opacities (N) into conic_opacity (N,4), the
+ * layout the rasterizer gathers (rasterize.py:432-438 inputs). */
+int gsx_pack_conic_opacity(int64_t n, const float* conics,
+                           const float* opacities, float* conic_opacity,
+                           void* stream);
+
+/* Replaces gs_rasterize_forward (rasterize.py:28-98) for C channels in one
+ * pass (rasterize_features, rasterize.py:449-545, chunks of 3), with the
+ * expected depth of gs_rasterize_depth (rasterize.py:223-290) fused as an
+ * extra output when depths != NULL.  features (N,C); sorted_ids
+ * (num_ids); tile ranges are clamped to [0, num_ids] and ids outside [0, n)
+ * are treated as transparent, so malformed inputs cannot read out of
+ * bounds; background (C) or NULL (zeros); out (H,W,C); final_T (H,W);
+ * n_contrib (H,W) int32; depth_out (H,W) when depths != NULL. */
+int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
+                   const float* conic_opacity, const float* features,
+                   const float* depths, const int32_t* sorted_ids,
+                   int64_t num_ids, const int32_t* tile_ranges,
+                   const float* background,
+                   int32_t width, int32_t height, float* out, float* final_T,
+                   int32_t* n_contrib, float* depth_out, void* stream);
+
+/* Replaces gs_rasterize_backward (rasterize.py:100-221) and the vjp wiring
+ * of _rasterize_core (rasterize.py:364-403).  grad_out (H,W,C);
+ * grad_final_T (H,W) or NULL.  Outputs (zeroed here, then accumulated):
+ * g_means2d (N,2), g_conics (N,3), g_features (N,C), g_opacities (N).
+ * No gradient is produced for the background (rasterize.py:401). */
+int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
+                   const float* conic_opacity, const float* features,
+                   const int32_t* sorted_ids, int64_t num_ids,
+                   const int32_t* tile_ranges,
+                   const float* background, int32_t width, int32_t height,
+                   const float* final_T, const int32_t* n_contrib,
+                   const float* grad_out, const float* grad_final_T,
+                   float* g_means2d, float* g_conics, float* g_features,
+                   float* g_opacities, void* stream);
+
+/* ---------------------------------------------------------- diagnostics --
+ * Evaluates the device exp used by the rasterizer (the stand-in for
+ * metal::exp at rasterize.py:80,171,274) on n inputs; tests check it
+ * bit-for-bit against the CPU oracle. */
+int gsx_debug_expf(int64_t n, const float* x, float* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GSX_H */

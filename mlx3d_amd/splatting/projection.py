@@ -1,0 +1,87 @@
+"""EWA projection of 3D Gaussians (``src/mlx3d/splatting/projection.py:24-146``).
+
+``project_gaussians`` runs ``gsx_project_fwd``; its VJP (what MLX autodiff
+computes through the reference's expressions) is ``gsx_project_bwd``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..cameras import Camera
+
+__all__ = ["project_gaussians", "project_gaussians_ut"]
+
+
+class _Project(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means, quats, scales, cam, blur, antialias):
+        dev = _lib.require_device(means, quats, scales)
+        n = means.shape[0]
+        f = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)  # noqa: E731
+        means2d, conics, depths, radii, comp = f(n, 2), f(n, 3), f(n), f(n), f(n)
+        L = _lib.load()
+        _lib.check(L.gsx_project_fwd(cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
+                                     blur, int(antialias), _lib.ptr(means2d), _lib.ptr(conics),
+                                     _lib.ptr(depths), _lib.ptr(radii), _lib.ptr(comp),
+                                     _lib.stream_handle(dev)), "gsx_project_fwd")
+        ctx.save_for_backward(means, quats, scales)
+        ctx.cam, ctx.blur, ctx.antialias = cam, blur, antialias
+        ctx.mark_non_differentiable(radii)
+        return means2d, conics, depths, radii, comp
+
+    @staticmethod
+    def backward(ctx, g_means2d, g_conics, g_depths, _g_radii, g_comp):
+        means, quats, scales = ctx.saved_tensors
+        n = means.shape[0]
+        dev = means.device
+        gm = torch.empty((n, 3), dtype=torch.float32, device=dev)
+        gq = torch.empty((n, 4), dtype=torch.float32, device=dev)
+        gs = torch.empty((n, 3), dtype=torch.float32, device=dev)
+        c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+        g_means2d, g_conics, g_depths, g_comp = map(c, (g_means2d, g_conics, g_depths, g_comp))
+        L = _lib.load()
+        _lib.check(L.gsx_project_bwd(ctx.cam, n, _lib.ptr(means), _lib.ptr(quats),
+                                     _lib.ptr(scales), ctx.blur, int(ctx.antialias),
+                                     _lib.ptr(g_means2d), _lib.ptr(g_conics), _lib.ptr(g_depths),
+                                     _lib.ptr(g_comp), _lib.ptr(gm), _lib.ptr(gq), _lib.ptr(gs),
+                                     _lib.stream_handle(dev)), "gsx_project_bwd")
+        return gm, gq, gs, None, None, None
+
+
+def project_gaussians(camera: Camera, means: torch.Tensor, quats: torch.Tensor,
+                      scales: torch.Tensor, blur: float = 0.3,
+                      antialias: bool = False) -> dict[str, torch.Tensor]:
+    """Project 3D Gaussians into screen space (projection.py:24-146).
+
+    Args:
+        camera: the viewing camera.
+        means: (N, 3) centres; quats: (N, 4) wxyz rotations (need not be
+            normalised); scales: (N, 3) per-axis standard deviations.
+        blur: screen-space dilation added to the covariance diagonal.
+        antialias: also return Mip-Splatting opacity compensation.
+
+    Returns:
+        ``means2d`` (N, 2), ``conics`` (N, 3), ``depths`` (N,), ``radii``
+        (N,) (float, 0 for culled Gaussians) and ``compensation`` (N,).
+    """
+    if means.ndim != 2 or means.shape[1] != 3:
+        raise ValueError("means must have shape (N, 3).")
+    if quats.shape != (means.shape[0], 4) or scales.shape != means.shape:
+        raise ValueError("quats must be (N, 4) and scales (N, 3).")
+    means2d, conics, depths, radii, comp = _Project.apply(
+        _lib.f32c(means), _lib.f32c(quats), _lib.f32c(scales), camera.to_gsx(), float(blur),
+        bool(antialias))
+    return {"means2d": means2d, "conics": conics, "depths": depths, "radii": radii,
+            "compensation": comp}
+
+
+def project_gaussians_ut(camera, means, quats, scales, blur: float = 0.3, antialias: bool = False):
+    """3DGUT-style Unscented-Transform projection (projection.py:149-205).
+
+    Not part of this build yet: it serves distorted and fisheye cameras,
+    which the rasterizer's pinhole camera does not model.
+    """
+    raise NotImplementedError("projection='ut' (project_gaussians_ut) is not implemented; "
+                              "use the EWA projection")

@@ -1,0 +1,122 @@
+/*
+ * gsx_oracle.h -- CPU restatement of mlx3D's tile-based Gaussian-splatting
+ * rasterizer, used ONLY as test infrastructure (the checker in tests/, the
+ * cpu_baseline leg of bench.py and __graft_entry__.smoke()).  Nothing in the
+ * product package links, loads or calls this code.
+ *
+ * Every function restates one piece of the reference (paths relative to the
+ * reference repository root):
+ *   orc_expf            -- own exp (Cody-Waite reduction + degree-7 Taylor);
+ *                          stands in for metal::exp at rasterize.py:80,171,274
+ *   orc_project         -- src/mlx3d/splatting/projection.py:24-146
+ *   orc_eval_sh         -- src/mlx3d/splatting/sh.py:41-78
+ *   orc_preprocess_fwd  -- render.py:73-80 + projection + model.py:116-126
+ *   orc_bin             -- src/mlx3d/splatting/tiles.py:19-182 (no refine)
+ *   orc_raster_fwd      -- rasterize.py:28-98 (+ depth rasterize.py:223-290)
+ *   orc_raster_bwd      -- rasterize.py:100-221, vjp wiring :364-403
+ *   orc_project_bwd /
+ *   orc_preprocess_bwd  -- hand-derived VJP of projection.py:56-138,
+ *                          sh.py:52-78, render.py:75-80, model.py:116-122
+ *                          (what MLX autodiff computes for the reference)
+ *
+ * Arithmetic is IEEE float32 in the reference's operation order, compiled
+ * with -ffp-contract=off so no multiply-add is fused behind our back.
+ *
+ * The camera struct has the same layout as gsx_camera in include/gsx.h.
+ */
+#ifndef GSX_ORACLE_H
+#define GSX_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct orc_camera {
+    float R[9];
+    float t[3];
+    float center[3];
+    float fx, fy, cx, cy;
+    float lim_x, lim_y;
+    float znear;
+    int32_t width, height;
+} orc_camera;
+
+enum {
+    ORC_LOG_SCALES = 1,     /* scales given as log-sigma: apply exp      */
+    ORC_LOGIT_OPACITY = 2,  /* opacities given as logits: apply sigmoid  */
+    ORC_ANTIALIAS = 4       /* Mip-Splatting compensation (blur > 0)     */
+};
+
+float orc_expf(float x);
+void orc_expf_array(int64_t n, const float* x, float* y);
+
+void orc_project(const orc_camera* cam, int64_t n, const float* means,
+                 const float* quats, const float* scales, float blur,
+                 int antialias, float* means2d, float* conics, float* depths,
+                 float* radii, float* comp, int nthreads);
+
+void orc_project_bwd(const orc_camera* cam, int64_t n, const float* means,
+                     const float* quats, const float* scales, float blur,
+                     int antialias, const float* g_means2d,
+                     const float* g_conics, const float* g_depths,
+                     const float* g_comp, float* g_means, float* g_quats,
+                     float* g_scales, int nthreads);
+
+void orc_eval_sh(int64_t n, int K, int C, int degree, const float* sh,
+                 const float* dirs, float* out, int nthreads);
+
+void orc_eval_sh_bwd(int64_t n, int K, int C, int degree, const float* sh,
+                     const float* dirs, const float* g_out, float* g_sh,
+                     float* g_dirs, int nthreads);
+
+/* sh == NULL selects colors mode: colors are used as given (no clamp). */
+void orc_preprocess_fwd(const orc_camera* cam, int64_t n, const float* means,
+                        const float* quats, const float* scales,
+                        const float* opacities, const float* sh, int K,
+                        int degree, uint32_t flags, float blur,
+                        float* means2d, float* conics, float* depths,
+                        float* radii, float* comp, float* opac_eff,
+                        float* colors_out, int nthreads);
+
+void orc_preprocess_bwd(const orc_camera* cam, int64_t n, const float* means,
+                        const float* quats, const float* scales,
+                        const float* opacities, const float* colors_out,
+                        int K, int degree, uint32_t flags, float blur,
+                        const float* g_means2d, const float* g_conics,
+                        const float* g_opac_eff, const float* g_colors,
+                        const float* g_depths, const float* g_comp,
+                        float* g_means, float* g_quats, float* g_scales,
+                        float* g_opacities, float* g_sh, int nthreads);
+
+/* Returns D (number of duplicates).  Writes sorted_ids only if D <= cap.
+ * tile_ranges (tiles_x*tiles_y, 2) is always written. */
+int64_t orc_bin(int64_t n, const float* means2d, const float* radii,
+                const float* depths, int width, int height,
+                int32_t* sorted_ids, int64_t cap, int32_t* tile_ranges,
+                int nthreads);
+
+/* tiles == NULL renders every tile; else only the listed tile ids (outputs
+ * of other tiles are left untouched). */
+void orc_raster_fwd(int64_t n, int C, const float* means2d,
+                    const float* conics, const float* opacities,
+                    const float* feats, const float* depths,
+                    const int32_t* sorted_ids, const int32_t* tile_ranges,
+                    const float* bg, int width, int height, float* out,
+                    float* final_T, int32_t* n_contrib, float* depth_out,
+                    const int32_t* tiles, int64_t n_tiles, int nthreads);
+
+void orc_raster_bwd(int64_t n, int C, const float* means2d,
+                    const float* conics, const float* opacities,
+                    const float* feats, const int32_t* sorted_ids,
+                    const int32_t* tile_ranges, const float* bg, int width,
+                    int height, const float* final_T,
+                    const int32_t* n_contrib, const float* grad_out,
+                    const float* grad_final_T, float* g_means2d,
+                    float* g_conics, float* g_feats, float* g_opac,
+                    int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,287 @@
+"""GPU parity against the CPU oracle on the same seeded float32 inputs.
+
+Bit-exact: exp, projection outputs, SH colour, fused preprocess, sorted ids,
+tile ranges, n_contrib, image/final_T/depth (identical operation order on
+both sides).  Gradients: max|d|/max|ref| < 1e-3 (the tolerance the
+reference's own gradient test uses, test_splatting.py:390-414); the GPU
+sums with float atomics in a different order than the oracle.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import (assert_bits, cu, host, oracle_backward, oracle_forward, rel_err, say)
+from mlx3d_amd import _lib
+from mlx3d_amd.splatting import (GaussianModel, bin_gaussians, eval_sh, project_gaussians,
+                                 rasterize, rasterize_depth, rasterize_features,
+                                 render_gaussian_depth, render_gaussian_features,
+                                 render_gaussians)
+from oracle import oracle as O
+from refimpl import oracle_camera, random_scene
+
+pytestmark = pytest.mark.gpu
+
+
+def test_device_is_gfx950():
+    buf = ctypes.create_string_buffer(64)
+    rc = _lib.load().gsx_device_check(buf, 64)
+    say(f"device arch {buf.value.decode()}")
+    assert rc == 1
+
+
+def test_exp_bitwise():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        np.linspace(-90.0, 90.0, 1_000_001, dtype=np.float32),
+        rng.uniform(-10.0, 0.0, 1_000_000).astype(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -86.0, 88.0, 1e-30, -1e-30], np.float32),
+    ])
+    xt = cu(x)
+    y = torch.empty_like(xt)
+    _lib.check(_lib.load().gsx_debug_expf(x.size, _lib.ptr(xt), _lib.ptr(y),
+                                          _lib.stream_handle(xt.device)), "exp")
+    assert_bits(host(y), O.expf(x), "exp")
+
+
+@pytest.mark.parametrize("antialias", [False, True])
+def test_projection_bitexact(antialias):
+    cam, means, quats, scales, opac, colors = random_scene(0, n=5000)
+    means[:50, 2] = -6.0  # behind the camera
+    means[50:100, 0] = 8.0  # off-screen: frustum clip active
+    out = project_gaussians(cam, cu(means), cu(quats), cu(scales), antialias=antialias)
+    ref = O.project(oracle_camera(cam), means, quats, scales, antialias=antialias)
+    for k in ("means2d", "conics", "depths", "radii", "compensation"):
+        assert_bits(host(out[k]), ref[k], k)
+
+
+@pytest.mark.parametrize("antialias", [False, True])
+def test_projection_vjp(antialias):
+    cam, means, quats, scales, opac, colors = random_scene(1, n=3000)
+    rng = np.random.default_rng(1)
+    tm, tq, ts = (cu(a).requires_grad_(True) for a in (means, quats, scales))
+    out = project_gaussians(cam, tm, tq, ts, antialias=antialias)
+    g = {k: rng.standard_normal(out[k].shape).astype(np.float32)
+         for k in ("means2d", "conics", "depths", "compensation")}
+    loss = sum((out[k] * cu(v)).sum() for k, v in g.items())
+    loss.backward()
+    rm, rq, rs = O.project_bwd(oracle_camera(cam), means, quats, scales, g["means2d"],
+                               g["conics"], g["depths"], g["compensation"], antialias=antialias)
+    for name, a, b in [("means", tm.grad, rm), ("quats", tq.grad, rq), ("scales", ts.grad, rs)]:
+        e = rel_err(host(a), b)
+        say(f"project vjp {name}: rel {e:.2e}")
+        assert e < 1e-5
+
+
+@pytest.mark.parametrize("degree", [0, 1, 2, 3])
+def test_eval_sh(degree):
+    rng = np.random.default_rng(degree)
+    n = 4000
+    sh = (rng.standard_normal((n, 16, 3)) * 0.3).astype(np.float32)
+    d = rng.standard_normal((n, 3))
+    dirs = (d / np.linalg.norm(d, axis=1, keepdims=True)).astype(np.float32)
+    tsh, td = cu(sh).requires_grad_(True), cu(dirs).requires_grad_(True)
+    out = eval_sh(degree, tsh, td)
+    assert_bits(host(out), O.eval_sh(degree, sh, dirs), "eval_sh")
+    g = rng.standard_normal((n, 3)).astype(np.float32)
+    (out * cu(g)).sum().backward()
+    gsh, gd = O.eval_sh_bwd(degree, sh, dirs, g)
+    assert rel_err(host(tsh.grad), gsh) < 1e-6
+    assert rel_err(host(td.grad), gd) < 1e-5
+
+
+def _bin_case(means2d, radii, depths, W, H, what):
+    ids, ranges, tx, ty = bin_gaussians(cu(means2d), cu(radii), cu(depths), W, H)
+    rids, rranges, rtx, rty = O.bin_gaussians(means2d, radii, depths, W, H, threads=8)
+    say(f"binning {what}: D={rids.shape[0]}")
+    assert (tx, ty) == (rtx, rty)
+    np.testing.assert_array_equal(host(ranges), rranges)
+    np.testing.assert_array_equal(host(ids), rids)
+
+
+def test_binning_bitexact_scenes():
+    for seed in range(3):
+        cam, means, quats, scales, opac, colors = random_scene(seed, n=20000, width=640,
+                                                               height=360)
+        p = O.project(oracle_camera(cam), means, quats, scales)
+        _bin_case(p["means2d"], p["radii"], p["depths"], cam.width, cam.height, f"seed {seed}")
+
+
+def test_binning_edge_cases():
+    W, H = 200, 120
+    _bin_case(np.zeros((0, 2), np.float32), np.zeros(0, np.float32), np.zeros(0, np.float32),
+              W, H, "empty")
+    rng = np.random.default_rng(7)
+    m = rng.uniform(0, 200, (500, 2)).astype(np.float32)
+    _bin_case(m, np.zeros(500, np.float32), np.ones(500, np.float32), W, H, "all culled")
+    # exact depth ties everywhere
+    _bin_case(m, rng.integers(1, 30, 500).astype(np.float32),
+              rng.choice(np.array([1.0, 2.0, 3.0], np.float32), 500), W, H, "ties")
+    # one splat covering every tile plus a few small ones
+    m2 = np.concatenate([[[100.0, 60.0]], m[:20]]).astype(np.float32)
+    r2 = np.concatenate([[1e5], np.full(20, 5.0)]).astype(np.float32)
+    _bin_case(m2, r2, rng.uniform(1, 2, 21).astype(np.float32), W, H, "huge splat")
+    # a single tile image
+    _bin_case(m[:50] * 0.05, np.full(50, 3.0, np.float32), rng.uniform(1, 2, 50).astype(np.float32),
+              8, 8, "one tile")
+
+
+def test_rasterize_building_block_bitexact():
+    cam, means, quats, scales, opac, colors = random_scene(2, n=3000, width=200, height=150)
+    p = O.project(oracle_camera(cam), means, quats, scales)
+    ids, ranges, tx, ty = O.bin_gaussians(p["means2d"], p["radii"], p["depths"], 200, 150)
+    bg = np.array([0.1, 0.2, 0.3], np.float32)
+    out = rasterize(cu(p["means2d"]), cu(p["conics"]), cu(colors), cu(opac), cu(ids), cu(ranges),
+                    200, 150, tx, ty, background=cu(bg))
+    ref = O.raster_fwd(p["means2d"], p["conics"], opac, colors, ids, ranges, 200, 150, bg=bg)
+    np.testing.assert_array_equal(host(out["n_contrib"]), ref["n_contrib"])
+    assert_bits(host(out["image"]), ref["image"], "image")
+    assert_bits(host(out["final_T"]), ref["final_T"], "final_T")
+    d = rasterize_depth(cu(p["means2d"]), cu(p["conics"]), cu(opac), cu(p["depths"]), cu(ids),
+                        cu(ranges), 200, 150, tx, ty)
+    refd = O.raster_fwd(p["means2d"], p["conics"], opac, p["depths"][:, None], ids, ranges,
+                        200, 150, depths=p["depths"])
+    assert_bits(host(d["depth"]), refd["depth"], "depth")
+
+
+def test_rasterize_backward():
+    cam, means, quats, scales, opac, colors = random_scene(3, n=3000, width=200, height=150)
+    p = O.project(oracle_camera(cam), means, quats, scales)
+    ids, ranges, tx, ty = O.bin_gaussians(p["means2d"], p["radii"], p["depths"], 200, 150)
+    bg = np.array([0.3, 0.1, 0.2], np.float32)
+    rng = np.random.default_rng(3)
+    g_img = rng.standard_normal((150, 200, 3)).astype(np.float32)
+    g_a = rng.standard_normal((150, 200)).astype(np.float32)
+    t = [cu(a).requires_grad_(True) for a in (p["means2d"], p["conics"], colors, opac)]
+    out = rasterize(*t, cu(ids), cu(ranges), 200, 150, tx, ty, background=cu(bg))
+    ((out["image"] * cu(g_img)).sum() + (out["alpha"] * cu(g_a)).sum()).backward()
+    ref = O.raster_fwd(p["means2d"], p["conics"], opac, colors, ids, ranges, 200, 150, bg=bg)
+    rg = O.raster_bwd(p["means2d"], p["conics"], opac, colors, ids, ranges, 200, 150,
+                      ref["final_T"], ref["n_contrib"], g_img, grad_final_T=-g_a, bg=bg)
+    for name, a, key in [("means2d", t[0], "means2d"), ("conics", t[1], "conics"),
+                         ("colors", t[2], "features"), ("opacities", t[3], "opacities")]:
+        e = rel_err(host(a.grad), rg[key])
+        say(f"raster bwd {name}: rel {e:.2e}")
+        assert e < 1e-4
+
+
+@pytest.mark.parametrize("antialias", [False, True])
+def test_render_gaussians_colors(antialias):
+    cam, means, quats, scales, opac, colors = random_scene(4, n=4000, width=160, height=96)
+    bg = np.array([0.1, 0.2, 0.3], np.float32)
+    flags = O.ANTIALIAS if antialias else 0
+    opac = np.minimum(opac, 0.95).astype(np.float32)
+    t = [cu(a).requires_grad_(True) for a in (means, quats, scales, opac, colors)]
+    out = render_gaussians(cam, t[0], t[1], t[2], t[3], colors=t[4], background=cu(bg),
+                           antialias=antialias, return_depth=True)
+    pre, feats, ids, ranges, r = oracle_forward(cam, means, quats, scales, opac, colors=colors,
+                                                flags=flags, bg=bg, depth=True)
+    np.testing.assert_array_equal(host(out["sorted_ids"]), ids)
+    np.testing.assert_array_equal(host(out["n_contrib"]), r["n_contrib"])
+    for k, ref in [("image", r["image"]), ("final_T", r["final_T"]), ("depth", r["depth"]),
+                   ("means2d", pre["means2d"]), ("depths", pre["depths"]), ("radii", pre["radii"]),
+                   ("compensation", pre["compensation"])]:
+        assert_bits(host(out[k]), ref, k)
+    rng = np.random.default_rng(4)
+    g_img = rng.standard_normal(r["image"].shape).astype(np.float32)
+    g_a = rng.standard_normal(r["final_T"].shape).astype(np.float32)
+    ((out["image"] * cu(g_img)).sum() + (out["alpha"] * cu(g_a)).sum()).backward()
+    g = oracle_backward(cam, means, quats, scales, opac, pre, feats, ids, ranges, r, g_img, g_a,
+                        flags=flags, bg=bg)
+    for name, a, key in [("means", t[0], "means"), ("quats", t[1], "quats"),
+                         ("scales", t[2], "scales"), ("opacities", t[3], "opacities"),
+                         ("colors", t[4], "features")]:
+        e = rel_err(host(a.grad), g[key])
+        say(f"render colors aa={antialias} grad {name}: rel {e:.2e}")
+        assert e < 1e-3
+
+
+@pytest.mark.parametrize("degree", [0, 3])
+def test_model_render_sh_raw_params(degree):
+    cam, means, quats, scales, opac, _ = random_scene(5, n=5000, width=192, height=128)
+    rng = np.random.default_rng(50 + degree)
+    n = means.shape[0]
+    sh = (rng.standard_normal((n, 16, 3)) * 0.2).astype(np.float32)
+    ls = np.log(scales).astype(np.float32)
+    lo = np.clip(rng.standard_normal(n), -4, 3).astype(np.float32)
+    model = GaussianModel({"means": cu(means), "quats": cu(quats), "scales": cu(ls),
+                           "opacities": cu(lo), "sh_dc": cu(sh[:, :1]),
+                           "sh_rest": cu(sh[:, 1:])}, sh_degree=3)
+    model.active_sh_degree = degree
+    model.requires_grad_(True)
+    out = model.render(cam)
+    flags = O.LOG_SCALES | O.LOGIT_OPACITY
+    pre, feats, ids, ranges, r = oracle_forward(cam, means, quats, ls, lo, sh=sh, degree=degree,
+                                                flags=flags)
+    np.testing.assert_array_equal(host(out["n_contrib"]), r["n_contrib"])
+    assert_bits(host(out["image"]), r["image"], "image")
+    assert_bits(host(out["means2d"]), pre["means2d"], "means2d")
+    g_img = rng.standard_normal(r["image"].shape).astype(np.float32)
+    g_a = rng.standard_normal(r["final_T"].shape).astype(np.float32)
+    ((out["image"] * cu(g_img)).sum() + (out["alpha"] * cu(g_a)).sum()).backward()
+    g = oracle_backward(cam, means, quats, ls, lo, pre, feats, ids, ranges, r, g_img, g_a, sh=sh,
+                        degree=degree, flags=flags)
+    p = model.params
+    shg = np.concatenate([host(p["sh_dc"].grad), host(p["sh_rest"].grad)], 1)
+    for name, a, b in [("means", host(p["means"].grad), g["means"]),
+                       ("quats", host(p["quats"].grad), g["quats"]),
+                       ("scales", host(p["scales"].grad), g["scales"]),
+                       ("opacities", host(p["opacities"].grad), g["opacities"]),
+                       ("sh", shg, g["sh"])]:
+        e = rel_err(a, b)
+        say(f"model sh{degree} grad {name}: rel {e:.2e}")
+        assert e < 1e-3
+
+
+@pytest.mark.parametrize("channels", [1, 5, 32, 37])
+def test_features(channels):
+    cam, means, quats, scales, opac, _ = random_scene(6, n=3000, width=128, height=96)
+    opac = np.minimum(opac, 0.95).astype(np.float32)
+    rng = np.random.default_rng(channels)
+    feats = rng.standard_normal((3000, channels)).astype(np.float32)
+    bg = np.linspace(-0.2, 0.2, channels).astype(np.float32)
+    t = [cu(a).requires_grad_(True) for a in (means, quats, scales, opac, feats)]
+    out = render_gaussian_features(cam, *t, background=cu(bg), return_depth=True)
+    pre, f, ids, ranges, r = oracle_forward(cam, means, quats, scales, opac, colors=feats, bg=bg,
+                                            depth=True)
+    assert out["features"].shape == (96, 128, channels)
+    np.testing.assert_array_equal(host(out["n_contrib"]), r["n_contrib"])
+    assert_bits(host(out["features"]), r["image"], "features")
+    assert_bits(host(out["depth"]), r["depth"], "depth")
+    g_img = rng.standard_normal(r["image"].shape).astype(np.float32)
+    g_a = rng.standard_normal(r["final_T"].shape).astype(np.float32)
+    ((out["features"] * cu(g_img)).sum() + (out["alpha"] * cu(g_a)).sum()).backward()
+    g = oracle_backward(cam, means, quats, scales, opac, pre, f, ids, ranges, r, g_img, g_a, bg=bg)
+    for name, a, key in [("means", t[0], "means"), ("opacities", t[3], "opacities"),
+                         ("features", t[4], "features")]:
+        e = rel_err(host(a.grad), g[key])
+        say(f"features C={channels} grad {name}: rel {e:.2e}")
+        assert e < 1e-3
+
+
+def test_normalized_features_match_depth():
+    # test_splatting.py:312-337
+    cam, means, quats, scales, opac, _ = random_scene(7, n=3000, width=128, height=96)
+    m, q, s, o = (cu(a) for a in (means, quats, scales, opac))
+    depth = render_gaussian_depth(cam, m, q, s, o)
+    feat = render_gaussian_features(cam, m, q, s, o, depth["depths"][:, None],
+                                    background=cu(np.array([10.0], np.float32)), normalize=True)
+    valid = host(depth["alpha"]) > 1e-3
+    np.testing.assert_allclose(host(feat["alpha"]), host(depth["alpha"]), atol=1e-6)
+    np.testing.assert_allclose(host(feat["features"][..., 0])[valid], host(depth["depth"])[valid],
+                               rtol=1e-5)
+    assert np.abs(host(feat["features"][..., 0])[~valid]).max(initial=0) < 1e-6
+
+
+def test_empty_and_culled_render():
+    cam, means, quats, scales, opac, colors = random_scene(8, n=10, width=64, height=48)
+    means[:, 2] = -10.0  # all behind the camera
+    out = render_gaussians(cam, cu(means), cu(quats), cu(scales), cu(opac), colors=cu(colors))
+    assert host(out["sorted_ids"]).shape == (0,)
+    assert (host(out["final_T"]) == 1.0).all() and (host(out["image"]) == 0).all()
+    z = np.zeros((0, 3), np.float32)
+    out = render_gaussians(cam, cu(z), cu(np.zeros((0, 4), np.float32)), cu(z),
+                           cu(np.zeros(0, np.float32)), colors=cu(z))
+    assert (host(out["alpha"]) == 0).all()

@@ -1,0 +1,82 @@
+"""Host-side behaviour of the drop-in API that needs no GPU: argument
+validation raises the reference's ValueErrors before any kernel, and CPU
+tensors are refused rather than silently computed elsewhere."""
+
+import numpy as np
+import pytest
+import torch
+
+from mlx3d_amd.cameras import Camera
+from mlx3d_amd.renderer import Renderer
+from mlx3d_amd.splatting import (GaussianModel, bin_gaussians, num_sh_bases, project_gaussians,
+                                 rasterize_features, render_gaussian_features, render_gaussians,
+                                 rgb_to_sh, sh_to_rgb)
+
+
+def _scene(n=10):
+    g = torch.Generator().manual_seed(0)
+    return (torch.randn(n, 3, generator=g) * 0.3, torch.randn(n, 4, generator=g),
+            torch.full((n, 3), 0.05), torch.full((n,), 0.5), torch.rand(n, 3, generator=g))
+
+
+def test_sh_helpers():
+    rgb = torch.rand(10, 3)
+    assert torch.allclose(sh_to_rgb(rgb_to_sh(rgb)), rgb, atol=1e-6)
+    assert num_sh_bases(3) == 16
+
+
+def test_exactly_one_of_colors_or_sh():
+    cam = Camera.look_at(eye=(0, 0, -3.0), width=32, height=32)
+    m, q, s, o, c = _scene()
+    with pytest.raises(ValueError, match="exactly one"):
+        render_gaussians(cam, m, q, s, o)
+    with pytest.raises(ValueError, match="exactly one"):
+        render_gaussians(cam, m, q, s, o, colors=c, sh=torch.zeros(10, 16, 3))
+
+
+def test_projection_name_validated():
+    cam = Camera.look_at(eye=(0, 0, -3.0), width=32, height=32)
+    m, q, s, o, c = _scene()
+    with pytest.raises(ValueError, match="projection"):
+        render_gaussians(cam, m, q, s, o, colors=c, projection="bad")
+
+
+def test_feature_shape_validation():
+    cam = Camera.look_at(eye=(0, 0, -3.0), width=32, height=32)
+    m, q, s, o, c = _scene()
+    with pytest.raises(ValueError, match="features must have shape"):
+        render_gaussian_features(cam, m, q, s, o, c[:, 0])
+    with pytest.raises(ValueError, match="same first dimension"):
+        render_gaussian_features(cam, m, q, s, o, c[:-1])
+    with pytest.raises(ValueError, match="at least one channel"):
+        rasterize_features(torch.zeros(10, 2), torch.zeros(10, 3), torch.zeros(10, 0),
+                           torch.zeros(10), torch.zeros(0, dtype=torch.int32),
+                           torch.zeros(4, 2, dtype=torch.int32), 32, 32, 2, 2)
+
+
+def test_cpu_tensors_are_refused():
+    cam = Camera.look_at(eye=(0, 0, -3.0), width=32, height=32)
+    m, q, s, o, c = _scene()
+    with pytest.raises(ValueError, match="GPU only"):
+        render_gaussians(cam, m, q, s, o, colors=c)
+    with pytest.raises(ValueError, match="GPU only"):
+        project_gaussians(cam, m, q, s)
+    with pytest.raises(ValueError, match="GPU only"):
+        bin_gaussians(torch.zeros(4, 2), torch.ones(4), torch.ones(4), 32, 32)
+
+
+def test_model_from_points_scales_and_layout():
+    pts = torch.tensor([[0.0, 0, 0], [1.0, 0, 0], [0, 2.0, 0], [0, 0, 3.0], [1.0, 1.0, 0]])
+    model = GaussianModel.from_points(pts, sh_degree=2)
+    assert model.num_gaussians == 5
+    assert model.sh.shape == (5, 9, 3)
+    assert model.active_sh_degree == 0
+    # point 0: nearest squared distances 1, 2, 4 -> mean 7/3
+    np.testing.assert_allclose(float(model.scales_act[0, 0]), np.sqrt(7 / 3), rtol=1e-5)
+    np.testing.assert_allclose(float(model.opacities_act[0]), 0.1, rtol=1e-5)
+    capped = GaussianModel.from_points(pts * 100, sh_degree=0, scale_init_max_scale=0.25)
+    assert float(capped.scales_act.max()) <= 0.250001
+
+
+def test_render_function_is_a_renderer():
+    assert isinstance(render_gaussians, Renderer)
