@@ -69,32 +69,79 @@ __device__ __forceinline__ float alpha_floor_power(float o) {
 
 // Which of the tile's four 8x8 quadrants (bit q = quadrant (q&1, q>>1)) the
 // pixels with alpha >= 1/255 of this Gaussian can lie in.  alpha >= 1/255
-// needs q(d) = a dx^2 + 2 b dx dy + c dy^2 <= 2 ln(255 o); the bounding box
-// of that ellipse has half-widths sqrt(2 tau c / det), sqrt(2 tau a / det).
-// With b^2 < 0.999 a c the float32 evaluation of the power is within 7.2e-4
-// relative of the exact value, so tau is inflated by 1% (+1e-3) and the box
-// by 0.05 px.  Ill-conditioned, non-positive or non-finite conics get no
-// culling (all four bits).
+// needs q(d) = a dx^2 + 2 b dx dy + c dy^2 <= 2 ln(255 o); a quadrant is
+// kept when the minimum of q over its rectangle of pixel centres (exact, in
+// float64: zero if the mean is inside, else the least of the four clipped
+// edge minimisers) is within that bound.  With b^2 < 0.999 a c the float32
+// evaluation of the power is within 7.2e-4 relative of the exact value, so
+// tau is inflated by 1% (+1e-3).  Ill-conditioned, non-positive or
+// non-finite conics get no culling (all four bits).
 __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, int px0, int py0) {
     const float o = c.w;
     if (!(o >= 0.0039215f)) return (o == o) ? 0u : 0xFu;  // alpha < 1/255 everywhere
     const double A = c.x, B = c.y, C = c.z;
     const double det = A * C - B * B;
     if (!(A > 0.0 && C > 0.0 && det > 1e-3 * A * C)) return 0xFu;
-    const double tau = log(255.0 * (double)o) * 1.01 + 1e-3;
-    const double ex = sqrt(2.0 * tau * C / det) + 0.05;
-    const double ey = sqrt(2.0 * tau * A / det) + 0.05;
+    const double t2 = 2.0 * (log(255.0 * (double)o) * 1.01 + 1e-3);
     const double xd = x, yd = y;
-    if (!(ex < 1e30 && ey < 1e30 && xd == xd && yd == yd)) return 0xFu;
+    if (!(t2 < 1e30 && A < 1e30 && C < 1e30 && fabs(xd) < 1e30 && fabs(yd) < 1e30)) return 0xFu;
+    const double ia = 1.0 / A, ic = 1.0 / C;
     uint32_t m = 0;
-#pragma unroll
+#pragma unroll 1
     for (int q = 0; q < 4; ++q) {
-        const double qx0 = px0 + (q & 1) * 8 + 0.5, qy0 = py0 + (q >> 1) * 8 + 0.5;
-        const bool hit = (xd + ex >= qx0) && (xd - ex <= qx0 + 7.0) && (yd + ey >= qy0) &&
-                         (yd - ey <= qy0 + 7.0);
-        m |= hit ? (1u << q) : 0u;
+        const double x0 = px0 + (q & 1) * 8 + 0.5 - xd, x1 = x0 + 7.0;
+        const double y0 = py0 + (q >> 1) * 8 + 0.5 - yd, y1 = y0 + 7.0;
+        double qmin;
+        if (x0 <= 0.0 && x1 >= 0.0 && y0 <= 0.0 && y1 >= 0.0) {
+            qmin = 0.0;
+        } else {
+            qmin = 1e300;
+#pragma unroll 1
+            for (int e = 0; e < 2; ++e) {
+                const double xe = e ? x1 : x0, ye = e ? y1 : y0;
+                const double ys = fmin(fmax(-B * xe * ic, y0), y1);
+                const double xs = fmin(fmax(-B * ye * ia, x0), x1);
+                qmin = fmin(qmin, A * xe * xe + 2.0 * B * xe * ys + C * ys * ys);
+                qmin = fmin(qmin, A * xs * xs + 2.0 * B * xs * ye + C * ye * ye);
+            }
+        }
+        m |= (qmin <= t2) ? (1u << q) : 0u;
     }
     return m;
+}
+
+// A staged Gaussian is "plain" when every quantity the per-pixel loop reads
+// is finite and small enough that the float32 power is finite and, for a
+// pixel that passes the alpha bound, within [-86, 0]: then exp needs no
+// range handling and a zero weight leaves the accumulators unchanged.
+template <int CH>
+__device__ __forceinline__ bool plain_gaussian(float x, float y, float4 c, float thr,
+                                               const float4* f) {
+    bool ok = fabsf(x) < 1e6f && fabsf(y) < 1e6f && fabsf(c.x) < 1e20f && fabsf(c.y) < 1e20f &&
+              fabsf(c.z) < 1e20f && c.w >= 0.0f && c.w < 1e30f && thr >= -86.0f;
+    constexpr int F4 = (CH + 3) / 4;
+#pragma unroll
+    for (int k = 0; k < F4; ++k)
+        ok = ok && fabsf(f[k].x) < 1e30f && fabsf(f[k].y) < 1e30f && fabsf(f[k].z) < 1e30f &&
+             fabsf(f[k].w) < 1e30f;
+    return ok;
+}
+
+// exp for arguments known to lie in [-86, 88]: the dexp sequence without its
+// range checks (identical results there).
+__device__ __forceinline__ float dexp_inrange(float x) {
+    const float k = rintf(x * 1.44269504088896341f);
+    float r = fmaf(k, -0.693145751953125f, x);
+    r = fmaf(k, -1.42860682030941723e-06f, r);
+    float p = 1.98412698412698413e-04f;
+    p = fmaf(p, r, 1.38888888888888889e-03f);
+    p = fmaf(p, r, 8.33333333333333333e-03f);
+    p = fmaf(p, r, 4.16666666666666667e-02f);
+    p = fmaf(p, r, 1.66666666666666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)k);
 }
 
 template <int CTRL, int ROW_MASK, int BANK_MASK>
@@ -195,6 +242,78 @@ __device__ __forceinline__ float comp4(const float4& v, int e) {
     return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
 }
 
+// One (pixel, Gaussian) step of the front-to-back loop (rasterize.py:74-87),
+// straight-line: lanes that do not composite keep their state through
+// selects.  PLAIN: the Gaussian passed plain_gaussian(), so exp needs no
+// range handling and a non-compositing lane can add a zero weight.
+template <int CH, bool DEPTH, bool PLAIN>
+__device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
+                                         const float4* __restrict__ fsrc, int jlast, float pxf,
+                                         float pyf, float& T, float* acc, float& dacc, int& last,
+                                         bool& done) {
+    constexpr int F4 = (CH + 3) / 4;
+    float4 fv[F4];
+#pragma unroll
+    for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
+    const float dx = r0.x - pxf, dy = r0.y - pyf;
+    const float power = -0.5f * (r1.x * dx * dx + r1.z * dy * dy) - r1.y * dx * dy;
+    const bool live = !done && !(power > 0.0f) && !(power < r0.z);
+    const float e = PLAIN ? dexp_inrange(power) : dexp_sel(power);
+    const float alpha = fminf(0.99f, r0.w * e);
+    const bool pass = live && !(alpha < 1.0f / 255.0f);
+    const float next_T = T * (1.0f - alpha);
+    const bool stop = pass && next_T < 1e-4f;
+    const bool add = pass && !stop;
+    const float w = alpha * T;
+    if (PLAIN) {
+        const float wa = add ? w : 0.0f;
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) acc[ch] = acc[ch] + comp4(fv[ch >> 2], ch & 3) * wa;
+        if (DEPTH) dacc = dacc + r1.w * wa;
+    } else {
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+            const float a2 = acc[ch] + comp4(fv[ch >> 2], ch & 3) * w;
+            acc[ch] = add ? a2 : acc[ch];
+        }
+        if (DEPTH) {
+            const float d2 = dacc + r1.w * w;
+            dacc = add ? d2 : dacc;
+        }
+    }
+    T = add ? next_T : T;
+    last = add ? jlast : last;
+    done = done || stop;
+}
+
+// Front-to-back walk of one quadrant wave over its staged Gaussians, two
+// records in flight (the next one is read from LDS while the current one is
+// evaluated; a finished walk re-reads its last index, which is harmless).
+template <int CH, bool DEPTH, bool PLAIN>
+__device__ __forceinline__ void fwd_walk(BitWalkUp& walk, const float4* s_r0, const float4* s_r1,
+                                         const float4 (*s_f)[(CH + 3) / 4], float pxf, float pyf,
+                                         int base, float& T, float* acc, float& dacc, int& last,
+                                         bool& done) {
+    int ja = walk.next();
+    if (ja < 0) return;
+    float4 a0 = s_r0[ja], a1 = s_r1[ja];
+    while (true) {
+        const int jb = walk.next();
+        const int lb = jb >= 0 ? jb : ja;
+        const float4 b0 = s_r0[lb], b1 = s_r1[lb];
+        fwd_pair<CH, DEPTH, PLAIN>(a0, a1, s_f[ja], base + ja + 1, pxf, pyf, T, acc, dacc, last,
+                                   done);
+        if (jb < 0 || __ballot(!done) == 0ull) return;
+        ja = walk.next();
+        const int la = ja >= 0 ? ja : jb;
+        a0 = s_r0[la];
+        a1 = s_r1[la];
+        fwd_pair<CH, DEPTH, PLAIN>(b0, b1, s_f[jb], base + jb + 1, pxf, pyf, T, acc, dacc, last,
+                                   done);
+        if (ja < 0 || __ballot(!done) == 0ull) return;
+    }
+}
+
 template <int CH, bool DEPTH>
 __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     const float2* __restrict__ xy, const float4* __restrict__ co, const float* __restrict__ feat,
@@ -231,15 +350,19 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
         if (__syncthreads_count(done) == kThreads) break;
         const int k = base + tid;
         uint32_t qm = 0;
+        bool plain = true;
         if (k < num) {
             const int g = ids[start + k];
             if ((uint32_t)g < (uint64_t)n) {
                 const float2 m = xy[g];
                 const float4 c = co[g];
-                s_r0[tid] = make_float4(m.x, m.y, alpha_floor_power(c.w), c.w);
-                s_r1[tid] = make_float4(c.x, c.y, c.z, DEPTH ? depths[g] : 0.0f);
+                const float thr = alpha_floor_power(c.w);
+                s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
+                const float dz = DEPTH ? depths[g] : 0.0f;
+                s_r1[tid] = make_float4(c.x, c.y, c.z, dz);
                 stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                 qm = quadrant_mask(m.x, m.y, c, px0, py0);
+                plain = plain_gaussian<CH>(m.x, m.y, c, thr, s_f[tid]) && fabsf(dz) < 1e30f;
             }
         }
 #pragma unroll
@@ -247,52 +370,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
             const uint64_t b = __ballot((qm >> q) & 1u);
             if (lane == 0) s_mask[q][wave] = b;
         }
-        __syncthreads();
+        const bool batch_plain = __syncthreads_and(plain);
         if (__ballot(!done) == 0ull) continue;
         BitWalkUp walk;
         walk.init(s_mask[wave], kWaves);
-        int j = walk.next();
-        if (j < 0) continue;
-        float4 r0 = s_r0[j], r1 = s_r1[j];
-        while (true) {
-            const int jn = walk.next();
-            float4 r0n = r0, r1n = r1;
-            if (jn >= 0) {
-                r0n = s_r0[jn];
-                r1n = s_r1[jn];
-            }
-            const float dx = r0.x - pxf, dy = r0.y - pyf;
-            const float power = -0.5f * (r1.x * dx * dx + r1.z * dy * dy) - r1.y * dx * dy;
-            const bool live = !done && !(power > 0.0f) && !(power < r0.z);
-            if (__ballot(live) != 0ull) {
-                float4 fv[F4];
-#pragma unroll
-                for (int q = 0; q < F4; ++q) fv[q] = s_f[j][q];
-                const float alpha = fminf(0.99f, r0.w * dexp_sel(power));
-                const bool pass = live && !(alpha < 1.0f / 255.0f);
-                const float next_T = T * (1.0f - alpha);
-                const bool stop = pass && next_T < 1e-4f;
-                const bool add = pass && !stop;
-                const float w = alpha * T;
-#pragma unroll
-                for (int ch = 0; ch < CH; ++ch) {
-                    const float a2 = acc[ch] + comp4(fv[ch >> 2], ch & 3) * w;
-                    acc[ch] = add ? a2 : acc[ch];
-                }
-                if (DEPTH) {
-                    const float d2 = dacc + r1.w * w;
-                    dacc = add ? d2 : dacc;
-                }
-                T = add ? next_T : T;
-                last = add ? base + j + 1 : last;
-                done = done || stop;
-                if (__ballot(!done) == 0ull) break;
-            }
-            if (jn < 0) break;
-            j = jn;
-            r0 = r0n;
-            r1 = r1n;
-        }
+        if (batch_plain)
+            fwd_walk<CH, DEPTH, true>(walk, s_r0, s_r1, s_f, pxf, pyf, base, T, acc, dacc, last,
+                                      done);
+        else
+            fwd_walk<CH, DEPTH, false>(walk, s_r0, s_r1, s_f, pxf, pyf, base, T, acc, dacc, last,
+                                       done);
     }
     if (inside) {
         const int64_t pid = (int64_t)py * W + px;
@@ -311,6 +398,115 @@ __global__ __launch_bounds__(kThreads) void k_raster_fwd(
     }
 }
 
+// Per-pixel state of the back-to-front replay.
+template <int CH>
+struct BwdPixel {
+    float T, T_final, last_alpha, bg_dot;
+    int last;
+    float gpix[CH], accum[CH], lastc[CH];
+};
+
+// One (pixel, Gaussian) step of the back-to-front replay
+// (rasterize.py:162-219).  When any lane of the wave contributes, lane 63
+// stores the wave sums of
+//   u = G dx dL/dG, w = G dy dL/dG, u dx, u dy, w dy, G dL/dalpha, alpha T g_c
+// in the wave's slot for Gaussian j; the flush turns them into the
+// reference's means2d, conic, opacity and colour gradients (linear in these
+// sums).  T is recovered with one reciprocal of (1 - alpha) per pair.
+template <int CH, bool PLAIN>
+__device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
+                                         const float4* __restrict__ fsrc, int j, int gj,
+                                         float4 (*part)[((CH + 6) + 3) / 4], float pxf, float pyf,
+                                         int lane, BwdPixel<CH>& px, uint64_t& wrote0,
+                                         uint64_t& wrote1) {
+    constexpr int F4 = (CH + 3) / 4;
+    constexpr int NV = CH + 6;
+    constexpr int NV4 = (NV + 3) / 4;
+    const float dx = r0.x - pxf, dy = r0.y - pyf;
+    const float power = -0.5f * (r1.x * dx * dx + r1.z * dy * dy) - r1.y * dx * dy;
+    bool ok = gj < px.last && !(power > 0.0f) && !(power < r0.z);
+    if (__ballot(ok) == 0ull) return;
+    const float G = PLAIN ? dexp_inrange(power) : dexp_sel(power);
+    const float alpha = fminf(0.99f, r0.w * G);
+    ok = ok && !(alpha < 1.0f / 255.0f);
+    if (__ballot(ok) == 0ull) return;
+    float4 fv[F4];
+#pragma unroll
+    for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
+    const float rcp = __builtin_amdgcn_rcpf(1.0f - alpha);
+    const float Tn = px.T * rcp;
+    px.T = ok ? Tn : px.T;
+    const float la1 = 1.0f - px.last_alpha;
+    float dl = 0.0f;
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+        const float f = comp4(fv[ch >> 2], ch & 3);
+        const float an = px.last_alpha * px.lastc[ch] + la1 * px.accum[ch];
+        px.accum[ch] = ok ? an : px.accum[ch];
+        px.lastc[ch] = ok ? f : px.lastc[ch];
+        dl = dl + (f - px.accum[ch]) * px.gpix[ch];
+    }
+    px.last_alpha = ok ? alpha : px.last_alpha;
+    float dL_dalpha = dl * px.T + (-px.T_final * rcp) * px.bg_dot;
+    float aT = alpha * px.T;
+    dL_dalpha = ok ? dL_dalpha : 0.0f;
+    aT = ok ? aT : 0.0f;
+    const float dL_dG = r0.w * dL_dalpha;
+    float v[4 * NV4];
+    const float u = G * dx * dL_dG, w = G * dy * dL_dG;
+    v[0] = u;
+    v[1] = w;
+    v[2] = u * dx;
+    v[3] = u * dy;
+    v[4] = w * dy;
+    v[5] = G * dL_dalpha;
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) v[6 + ch] = aT * px.gpix[ch];
+    if (!PLAIN) {
+#pragma unroll
+        for (int q = 0; q < NV; ++q) v[q] = ok ? v[q] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < NV; ++q) v[q] = wave_total_lane63(v[q]);
+#pragma unroll
+    for (int q = NV; q < 4 * NV4; ++q) v[q] = 0.0f;
+    if (lane == 63) {
+#pragma unroll
+        for (int q = 0; q < NV4; ++q)
+            part[j][q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+    if (j < kWave) wrote0 |= 1ull << j;
+    else wrote1 |= 1ull << (j - kWave);
+}
+
+// Back-to-front walk of one quadrant wave over its staged Gaussians, two
+// records in flight.
+template <int CH, bool PLAIN>
+__device__ __forceinline__ void bwd_walk(BitWalkDown& walk, const float4* s_r0,
+                                         const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+                                         float4 (*part)[((CH + 6) + 3) / 4], float pxf, float pyf,
+                                         int bbase, int lane, BwdPixel<CH>& px, uint64_t& wrote0,
+                                         uint64_t& wrote1) {
+    int ja = walk.next();
+    if (ja < 0) return;
+    float4 a0 = s_r0[ja], a1 = s_r1[ja];
+    while (true) {
+        const int jb = walk.next();
+        const int lb = jb >= 0 ? jb : ja;
+        const float4 b0 = s_r0[lb], b1 = s_r1[lb];
+        bwd_pair<CH, PLAIN>(a0, a1, s_f[ja], ja, bbase + ja, part, pxf, pyf, lane, px, wrote0,
+                            wrote1);
+        if (jb < 0) return;
+        ja = walk.next();
+        const int la = ja >= 0 ? ja : jb;
+        a0 = s_r0[la];
+        a1 = s_r1[la];
+        bwd_pair<CH, PLAIN>(b0, b1, s_f[jb], jb, bbase + jb, part, pxf, pyf, lane, px, wrote0,
+                            wrote1);
+        if (ja < 0) return;
+    }
+}
+
 template <int CH>
 __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const float2* __restrict__ xy, const float4* __restrict__ co, const float* __restrict__ feat,
@@ -321,7 +517,7 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     float* __restrict__ g_xy, float* __restrict__ g_conic, float* __restrict__ g_feat,
     float* __restrict__ g_opac) {
     constexpr int F4 = (CH + 3) / 4;
-    constexpr int NV = CH + 6;             // dx, dy, conic a, b, c, opacity, channels
+    constexpr int NV = CH + 6;             // u, w, u dx, u dy, w dy, opacity term, channels
     constexpr int NV4 = (NV + 3) / 4;
     constexpr int BB = (CH <= 4) ? 128 : 64;  // Gaussians per batch (bounded by slot LDS)
     constexpr int NLW = BB / kWave;
@@ -348,22 +544,24 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     int start, num;
     tile_span(ranges[tile], n_ids, start, num);
 
-    const float T_final = inside ? final_T[pid] : 1.0f;
-    float T = T_final;
-    const int last = inside ? n_contrib[pid] : 0;
-    float gpix[CH];
-    float bg_dot = 0.0f;
+    BwdPixel<CH> st;
+    st.T_final = inside ? final_T[pid] : 1.0f;
+    st.T = st.T_final;
+    st.last = inside ? n_contrib[pid] : 0;
+    st.bg_dot = 0.0f;
+    st.last_alpha = 0.0f;
 #pragma unroll
     for (int ch = 0; ch < CH; ++ch) {
-        gpix[ch] = (inside && ch < nc) ? grad_out[pid * C + c0 + ch] : 0.0f;
-        if (ch < nc) bg_dot = bg_dot + (bg ? bg[c0 + ch] : 0.0f) * gpix[ch];
+        st.gpix[ch] = (inside && ch < nc) ? grad_out[pid * C + c0 + ch] : 0.0f;
+        if (ch < nc) st.bg_dot = st.bg_dot + (bg ? bg[c0 + ch] : 0.0f) * st.gpix[ch];
+        st.accum[ch] = st.lastc[ch] = 0.0f;
     }
     // The alpha output's cotangent enters once, with the first channel block.
-    if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + grad_T[pid];
+    if (inside && c0 == 0 && grad_T) st.bg_dot = st.bg_dot + grad_T[pid];
 
     // Largest n_contrib of each quadrant: later list entries changed no pixel.
     {
-        int m = last;
+        int m = st.last;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, kWave));
         if (lane == 0) s_last[wave] = m;
@@ -375,14 +573,10 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     const int max_last = max(max(quad_last[0], quad_last[1]), max(quad_last[2], quad_last[3]));
     const int n_batches = (max_last + BB - 1) / BB;
 
-    float accum[CH], lastc[CH];
-#pragma unroll
-    for (int ch = 0; ch < CH; ++ch) accum[ch] = lastc[ch] = 0.0f;
-    float last_alpha = 0.0f;
-
     for (int b = n_batches - 1; b >= 0; --b) {
         __syncthreads();
         uint32_t qm = 0;
+        bool plain = true;
         if (tid < BB) {
             const int k = b * BB + tid;
             int gid = -1;
@@ -392,13 +586,15 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                     gid = g;
                     const float2 m = xy[g];
                     const float4 c = co[g];
-                    s_r0[tid] = make_float4(m.x, m.y, alpha_floor_power(c.w), c.w);
+                    const float thr = alpha_floor_power(c.w);
+                    s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
                     s_r1[tid] = make_float4(c.x, c.y, c.z, 0.0f);
                     stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                     qm = quadrant_mask(m.x, m.y, c, px0, py0);
 #pragma unroll
                     for (int q = 0; q < kWaves; ++q)
                         if (k >= quad_last[q]) qm &= ~(1u << q);
+                    plain = plain_gaussian<CH>(m.x, m.y, c, thr, s_f[tid]);
                 }
             }
             s_id[tid] = gid;
@@ -410,79 +606,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                 if (lane == 0) s_mask[q][wave] = bq;
             }
         }
-        __syncthreads();
+        const bool batch_plain = __syncthreads_and(plain);
         BitWalkDown walk;
         walk.init(s_mask[wave], NLW);
-        uint64_t wrote0 = 0ull, wrote1 = 0ull;  // NLW <= 2
-        int j = walk.next();
-        float4 r0 = make_float4(0, 0, 0, 0), r1 = r0;
-        if (j >= 0) {
-            r0 = s_r0[j];
-            r1 = s_r1[j];
-        }
-        while (j >= 0) {
-            const int jn = walk.next();
-            float4 r0n = r0, r1n = r1;
-            if (jn >= 0) {
-                r0n = s_r0[jn];
-                r1n = s_r1[jn];
-            }
-            const int gj = b * BB + j;
-            const float dx = r0.x - pxf, dy = r0.y - pyf;
-            const float power = -0.5f * (r1.x * dx * dx + r1.z * dy * dy) - r1.y * dx * dy;
-            bool ok = gj < last && !(power > 0.0f) && !(power < r0.z);
-            if (__ballot(ok) != 0ull) {
-                const float G = dexp_sel(power);
-                const float alpha = fminf(0.99f, r0.w * G);
-                ok = ok && !(alpha < 1.0f / 255.0f);
-                if (__ballot(ok) != 0ull) {
-                    float4 fv[F4];
-#pragma unroll
-                    for (int q = 0; q < F4; ++q) fv[q] = s_f[j][q];
-                    const float Tn = T / (1.0f - alpha);
-                    T = ok ? Tn : T;
-                    const float aT = alpha * T;
-                    float dl = 0.0f;
-#pragma unroll
-                    for (int ch = 0; ch < CH; ++ch) {
-                        const float f = comp4(fv[ch >> 2], ch & 3);
-                        const float an = last_alpha * lastc[ch] + (1.0f - last_alpha) * accum[ch];
-                        accum[ch] = ok ? an : accum[ch];
-                        lastc[ch] = ok ? f : lastc[ch];
-                        dl = dl + (f - accum[ch]) * gpix[ch];
-                    }
-                    last_alpha = ok ? alpha : last_alpha;
-                    float dL_dalpha = dl * T;
-                    dL_dalpha += (-T_final / (1.0f - alpha)) * bg_dot;
-                    const float dL_dG = r0.w * dL_dalpha;
-                    const float gdx = G * dx, gdy = G * dy;
-                    float v[4 * NV4];
-                    v[0] = -(gdx * r1.x + gdy * r1.y) * dL_dG;
-                    v[1] = -(gdy * r1.z + gdx * r1.y) * dL_dG;
-                    v[2] = -0.5f * gdx * dx * dL_dG;
-                    v[3] = -gdx * dy * dL_dG;
-                    v[4] = -0.5f * gdy * dy * dL_dG;
-                    v[5] = G * dL_dalpha;
-#pragma unroll
-                    for (int ch = 0; ch < CH; ++ch) v[6 + ch] = aT * gpix[ch];
-#pragma unroll
-                    for (int q = 0; q < NV; ++q) v[q] = wave_total_lane63(ok ? v[q] : 0.0f);
-#pragma unroll
-                    for (int q = NV; q < 4 * NV4; ++q) v[q] = 0.0f;
-                    if (lane == 63) {
-#pragma unroll
-                        for (int q = 0; q < NV4; ++q)
-                            s_part[wave][j][q] =
-                                make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-                    }
-                    if (j < kWave) wrote0 |= 1ull << j;
-                    else wrote1 |= 1ull << (j - kWave);
-                }
-            }
-            j = jn;
-            r0 = r0n;
-            r1 = r1n;
-        }
+        uint64_t wrote0 = 0ull, wrote1 = 0ull;
+        if (batch_plain)
+            bwd_walk<CH, true>(walk, s_r0, s_r1, s_f, s_part[wave], pxf, pyf, b * BB, lane, st,
+                               wrote0, wrote1);
+        else
+            bwd_walk<CH, false>(walk, s_r0, s_r1, s_f, s_part[wave], pxf, pyf, b * BB, lane, st,
+                                wrote0, wrote1);
         if (lane == 0) {
             s_wrote[wave][0] = wrote0;
             if (NLW > 1) s_wrote[wave][NLW - 1] = wrote1;
@@ -517,11 +650,16 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
                     e[4 * q + 2] = sum[q].z;
                     e[4 * q + 3] = sum[q].w;
                 }
-                if (e[0] != 0.0f) atomicAdd(&g_xy[2 * g], e[0]);
-                if (e[1] != 0.0f) atomicAdd(&g_xy[2 * g + 1], e[1]);
-                if (e[2] != 0.0f) atomicAdd(&g_conic[3 * g], e[2]);
-                if (e[3] != 0.0f) atomicAdd(&g_conic[3 * g + 1], e[3]);
-                if (e[4] != 0.0f) atomicAdd(&g_conic[3 * g + 2], e[4]);
+                // rasterize.py:197-218 in terms of the sums
+                const float4 c = s_r1[tid];
+                const float gx = -(c.x * e[0] + c.y * e[1]);
+                const float gy = -(c.y * e[0] + c.z * e[1]);
+                const float ga = -0.5f * e[2], gb = -e[3], gc = -0.5f * e[4];
+                if (gx != 0.0f) atomicAdd(&g_xy[2 * g], gx);
+                if (gy != 0.0f) atomicAdd(&g_xy[2 * g + 1], gy);
+                if (ga != 0.0f) atomicAdd(&g_conic[3 * g], ga);
+                if (gb != 0.0f) atomicAdd(&g_conic[3 * g + 1], gb);
+                if (gc != 0.0f) atomicAdd(&g_conic[3 * g + 2], gc);
                 if (e[5] != 0.0f) atomicAdd(&g_opac[g], e[5]);
 #pragma unroll
                 for (int ch = 0; ch < CH; ++ch)
