@@ -15,7 +15,9 @@
  *    Scratch space comes in through an explicit workspace argument.
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
  *    Only gsx_bin_sort synchronises the stream (one 8-byte readback of the
- *    duplicate count, as the reference does at tiles.py:68).
+ *    duplicate count, as the reference does at tiles.py:68);
+ *    gsx_bin_sort_async leaves that count on the device so the caller can
+ *    enqueue the rasterizer first and read it afterwards.
  *  - Return value: GSX_OK (0) on success, > 0 = required capacity (retry
  *    with a larger buffer), < 0 = error code (gsx_strerror).
  *  - No C++ exception crosses the ABI.  Entry points are reentrant; calls
@@ -38,7 +40,14 @@ enum gsx_status {
     GSX_ERR_INVALID = -1,     /* bad size / null pointer / unsupported shape */
     GSX_ERR_HIP = -2,         /* a HIP runtime call failed                   */
     GSX_ERR_WORKSPACE = -3,   /* workspace smaller than gsx_*_workspace_bytes */
-    GSX_ERR_TOO_LARGE = -4    /* a count exceeds the int32 index range       */
+    GSX_ERR_TOO_LARGE = -4,   /* a count exceeds the supported index range   */
+    GSX_ERR_DEVICE = -5       /* a device-side check failed (bounded wait)    */
+};
+
+/* Error bits of the device status word written by gsx_bin_sort_async. */
+enum gsx_bin_error {
+    GSX_BIN_ERR_LOOKBACK = 1, /* a chained-scan wait exceeded its bound       */
+    GSX_BIN_ERR_OVERFLOW = 2  /* the duplicate count exceeds 2^30 - 1         */
 };
 
 /* Flags of gsx_preprocess_fwd/bwd. */
@@ -108,7 +117,9 @@ int gsx_eval_sh_bwd(int64_t n, int32_t K, int32_t C, int32_t degree,
  * stride sh0_stride floats) and coefficients 1..K-1 from sh_rest (stride
  * sh_rest_stride floats), so both a packed (N,K,3) tensor and the model's
  * separate sh_dc (N,1,3) / sh_rest (N,K-1,3) tensors are read in place.
- * sh0 == NULL selects colours mode: `colors` (N,3) are used as given.
+ * sh0 == NULL selects colours mode: no colour is computed here (the
+ * caller's own (N,C) colours or features go to gsx_raster_fwd) and
+ * colors_out may be NULL.
  *
  * Outputs: means2d (N,2), depths (N), radii (N), compensation (N),
  * conic_opacity (N,4) = (conic a, b, c, opacity*compensation),
@@ -154,8 +165,8 @@ int gsx_bin_prepare(int64_t n, const float* means2d, const float* radii,
                     uint32_t* tile_counts, uint32_t* depth_keys,
                     uint32_t* tile_rects, void* stream);
 
-/* Bytes of workspace gsx_bin_sort needs for n Gaussians, `capacity`
- * duplicates and num_tiles tiles. */
+/* Bytes of workspace gsx_bin_sort(_async) needs for n Gaussians,
+ * `capacity` duplicates and num_tiles tiles. */
 int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles);
 
 /* tiles.py:67-182: depth-sort, duplicate per tile, sort by tile, ranges.
@@ -163,13 +174,33 @@ int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles);
  * the order of key = tile*N + rank(depth) with a stable argsort.  Writes
  * sorted_ids (D) int32 and tile_ranges (num_tiles,2) int32 [start,end),
  * (0,0) for empty tiles.  Synchronises `stream` once to read D into
- * *num_dups.  Returns 1 (nothing written but *num_dups) if D > capacity. */
+ * *num_dups.  Returns 1 if D > capacity (then only *num_dups is
+ * meaningful; retry with capacity >= D).  n and capacity < 2^30;
+ * sorted_ids must be 16-byte aligned. */
 int gsx_bin_sort(int64_t n, const uint32_t* tile_counts,
                  const uint32_t* depth_keys, const uint32_t* tile_rects,
                  int32_t width, int32_t height, void* workspace,
                  int64_t workspace_bytes, int64_t capacity,
                  int32_t* sorted_ids, int32_t* tile_ranges,
                  int64_t* num_dups, void* stream);
+
+/* The same pipeline without the readback: bin_status (2 device words) gets
+ * D and the gsx_bin_error bits.  If D > capacity, sorted_ids/tile_ranges
+ * hold an incomplete (but in-bounds: ids < n, ranges within [0, capacity])
+ * binning, so kernels enqueued behind it stay safe; the caller copies
+ * bin_status to the host when it needs D, checks it with
+ * gsx_bin_status_check and re-runs with a larger capacity if asked to. */
+int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts,
+                       const uint32_t* depth_keys, const uint32_t* tile_rects,
+                       int32_t width, int32_t height, void* workspace,
+                       int64_t workspace_bytes, int64_t capacity,
+                       int32_t* sorted_ids, int32_t* tile_ranges,
+                       uint32_t* bin_status, void* stream);
+
+/* Host-side: interprets a host copy of bin_status.  *num_dups = D; returns
+ * GSX_OK, 1 (D > capacity), GSX_ERR_TOO_LARGE or GSX_ERR_DEVICE. */
+int gsx_bin_status_check(const uint32_t* host_status, int64_t capacity,
+                         int64_t* num_dups);
 
 /* ---------------------------------------------------------- rasterizer --
  * Packs conics (N,3) and opacities (N) into conic_opacity (N,4), the

@@ -4,17 +4,27 @@
 // (tiles.py:166-172).  Here the same order is produced depth-first:
 //   1. stable LSD radix sort of the N per-Gaussian depth keys (4 x 8 bits),
 //      which orders Gaussians by (depth, index);
-//   2. exclusive scan of the tile counts gathered in that order (the only
-//      host readback: the duplicate total D);
-//   3. emission of the D (tile, gaussian) pairs in depth order, one lane per
-//      duplicate with a block-narrowed binary search (no long serial loops
-//      for Gaussians spanning thousands of tiles);
-//   4. stable LSD radix sort of the tile ids (ceil(log2 tiles)/8 passes),
-//      so inside a tile the depth order of step 1 is kept;
+//   2. exclusive scan of the tile counts in that order -> duplicate offsets
+//      and the duplicate count D (kept on the device);
+//   3. emission of the (tile, gaussian) pairs, balanced by duplicates: each
+//      workgroup owns 4096 consecutive duplicates, finds the Gaussians that
+//      own them with a cooperative search, stages those Gaussians in LDS and
+//      expands their tile rectangles (row-major, tiles.py:85-89).  It also
+//      histograms the tile-id digits for step 4;
+//   4. stable LSD radix sort of the tile ids (ceil(log2 tiles)/8 passes), so
+//      inside a tile the depth order of step 1 is kept;
 //   5. [start, end) ranges from the sorted tile ids; empty tiles stay (0,0)
 //      as the scatter-min/max of tiles.py:175-180 leaves them.
-// Only 2 passes run over the D-sized arrays at 1080p (13 tile bits) instead
-// of the 6 a 45-bit (tile, depth) key would need.
+// Radix passes are single-kernel "onesweep" passes (Adinets & Merrill,
+// 2022): digit histograms come from an earlier read, each pass ranks a chunk
+// with wave-level multi-split, publishes its digit counts and finds its
+// global offsets by decoupled look-back (Merrill & Garland, 2016), then
+// writes the chunk through LDS in digit order so the global stores are
+// runs of consecutive addresses.  The scan of step 2 uses the same
+// look-back.  Chunks are claimed through an atomic counter, so a chunk only
+// waits for chunks that are already running; each wait is bounded and
+// raises an error flag instead of spinning forever.  No host round trip
+// splits the pipeline: later steps size themselves from the device-side D.
 #include <algorithm>
 
 #include "gsx_device.h"
@@ -23,136 +33,91 @@ using namespace gsx;
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kItems = 16;
-constexpr int kChunk = kThreads * kItems;  // 4096 elements per workgroup
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
+constexpr int kMaxPasses = 4;
+// depth sort: 512 threads x 8 keys per chunk; tile sort: 1024 x 12
+constexpr int kDepthThreads = 512, kDepthItems = 8;
+constexpr int kTileThreads = 1024, kTileItems = 12;
+constexpr int kHistThreads = 256, kHistItems = 16;
+// count scan: 1024 threads x 4 Gaussians; emission: 1024 threads x 4 duplicates
+constexpr int kScanThreads = 1024, kScanItems = 4, kScanChunk = kScanThreads * kScanItems;
+constexpr int kEmitThreads = 1024, kEmitItems = 4, kEmitDups = kEmitThreads * kEmitItems;
+// Global digit histograms are kept in kHistCopies copies (workgroup b adds
+// into copy b % kHistCopies): same-address device atomics serialize, so one
+// shared copy would cost a serialized update per workgroup per bin.
+constexpr int kHistCopies = 16;
+constexpr int kHistStride = kMaxPasses * kRadix;  // words between copies
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// Look-back status word: 2 flag bits | 30-bit count.
+constexpr uint32_t kFlagAgg = 1u << 30;
+constexpr uint32_t kFlagInc = 2u << 30;
+constexpr uint32_t kCountMask = (1u << 30) - 1u;
+constexpr uint32_t kSpinLimit = 1u << 16;
 
-// LDS index padded by one word per 32 so that a lane reading its 16
-// consecutive elements hits 32 distinct banks across a half-wave.
-__device__ __forceinline__ int pad(int i) { return i + (i >> 5); }
-constexpr int kPadded = kChunk + kChunk / 32;
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Exclusive scan of the kChunk values in s (padded layout), plus `carry`.
-// Returns the chunk total.  Every thread of the block must call it.
-__device__ uint32_t block_scan_chunk(uint32_t* s, uint32_t* s_wave, uint32_t carry) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint32_t v[kItems];
-    uint32_t sum = 0;
-#pragma unroll
-    for (int k = 0; k < kItems; ++k) {
-        v[k] = s[pad(tid * kItems + k)];
-        sum += v[k];
-    }
-    const uint32_t incl = wave_incl_scan(sum);
-    if (lane == 63) s_wave[wave] = incl;
-    __syncthreads();
-    uint32_t wave_off = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) {
-        const uint32_t t = s_wave[w];
-        if (w < wave) wave_off += t;
-        total += t;
-    }
-    uint32_t run = carry + wave_off + incl - sum;
-#pragma unroll
-    for (int k = 0; k < kItems; ++k) {
-        s[pad(tid * kItems + k)] = run;
-        run += v[k];
-    }
-    __syncthreads();
-    return total;
+// Status words are read and written with relaxed device-scope atomics.
+// Each word carries everything a waiting chunk needs (flag + count), and the
+// scattered keys are only read by the next kernel, so no acquire/release
+// ordering is required -- on this GPU an agent-scope release or acquire
+// would write back or invalidate the XCD's whole L2 on every publish/poll.
+__device__ __forceinline__ uint32_t status_load(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void status_store(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* s_wave) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Exclusive prefix of one counter column for chunk `chunk`: sums earlier
+// chunks' published counts, walking back until an inclusive one.  Statuses
+// are read kLookWindow at a time so a long walk costs few round trips.
+// Chunk 0 always publishes inclusive, so the walk ends; an unpublished
+// predecessor is polled at most kSpinLimit times, then the error flag is
+// raised.
+constexpr int kLookWindow = 8;
+__device__ __forceinline__ uint32_t look_back(const uint32_t* status, int64_t chunk, int stride,
+                                              int col, uint32_t* err) {
+    uint32_t prefix = 0;
+    uint32_t spins = 0;
+    int64_t c = chunk - 1;
+    while (c >= 0) {
+        uint32_t s[kLookWindow];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) s_wave[wave] = v;
-    __syncthreads();
-    uint32_t t = 0;
+        for (int k = 0; k < kLookWindow; ++k)  // before chunk 0: an inclusive zero
+            s[k] = c - k >= 0 ? status_load(status + (c - k) * stride + col) : kFlagInc;
+        int used = 0;
+        bool done = false, stalled = false;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) t += s_wave[w];
-    return t;
-}
-
-// Phase 1 of the reduce-then-scan: per-chunk sums.  `gather` (optional)
-// reads in[gather[i]] instead of in[i].
-__global__ __launch_bounds__(kThreads) void k_scan_reduce(const uint32_t* __restrict__ in,
-                                                          const uint32_t* __restrict__ gather,
-                                                          int64_t n, uint32_t* __restrict__ partials) {
-    __shared__ uint32_t s_wave[kThreads / 64];
-    const int64_t base = (int64_t)blockIdx.x * kChunk;
-    uint32_t s = 0;
-#pragma unroll 4
-    for (int k = 0; k < kItems; ++k) {
-        const int64_t i = base + k * kThreads + threadIdx.x;
-        if (i < n) s += gather ? in[gather[i]] : in[i];
-    }
-    const uint32_t t = block_sum(s, s_wave);
-    if (threadIdx.x == 0) partials[blockIdx.x] = t;
-}
-
-// Phase 2: one workgroup scans the partials (exclusive, in place), chunk by
-// chunk; the grand total goes to total_out[0] and, if given, total_out2[0].
-__global__ __launch_bounds__(kThreads) void k_scan_partials(uint32_t* __restrict__ partials,
-                                                            int64_t nparts,
-                                                            uint32_t* __restrict__ total_out,
-                                                            uint32_t* __restrict__ total_out2) {
-    __shared__ uint32_t s[kPadded];
-    __shared__ uint32_t s_wave[kThreads / 64];
-    uint32_t carry = 0;
-    for (int64_t base = 0; base < nparts; base += kChunk) {
-#pragma unroll 4
-        for (int k = 0; k < kItems; ++k) {
-            const int idx = k * kThreads + threadIdx.x;
-            const int64_t i = base + idx;
-            s[pad(idx)] = (i < nparts) ? partials[i] : 0u;
+        for (int k = 0; k < kLookWindow; ++k) {
+            if (done || stalled) continue;
+            const uint32_t flag = s[k] & ~kCountMask;
+            if (flag == 0u) {
+                stalled = true;
+                continue;
+            }
+            prefix += s[k] & kCountMask;
+            ++used;
+            done = flag == kFlagInc;
         }
-        __syncthreads();
-        carry += block_scan_chunk(s, s_wave, carry) ;
-        // block_scan_chunk returned the chunk total; carry now includes it.
-#pragma unroll 4
-        for (int k = 0; k < kItems; ++k) {
-            const int idx = k * kThreads + threadIdx.x;
-            const int64_t i = base + idx;
-            if (i < nparts) partials[i] = s[pad(idx)];
+        if (done) break;
+        c -= used;
+        if (stalled) {
+            if (++spins > kSpinLimit) {
+                atomicOr(err, GSX_BIN_ERR_LOOKBACK);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
-        __syncthreads();
     }
-    if (threadIdx.x == 0) {
-        total_out[0] = carry;
-        if (total_out2) total_out2[0] = carry;
-    }
+    return prefix;
 }
 
-// Phase 3: each chunk scanned with its carry-in.  In-place (out == in) is
-// allowed: a chunk is fully read into LDS before it is written.
-__global__ __launch_bounds__(kThreads) void k_scan_down(const uint32_t* in,
-                                                        const uint32_t* __restrict__ gather,
-                                                        int64_t n,
-                                                        const uint32_t* __restrict__ partials,
-                                                        uint32_t* out) {
-    __shared__ uint32_t s[kPadded];
-    __shared__ uint32_t s_wave[kThreads / 64];
-    const int64_t base = (int64_t)blockIdx.x * kChunk;
-#pragma unroll 4
-    for (int k = 0; k < kItems; ++k) {
-        const int idx = k * kThreads + threadIdx.x;
-        const int64_t i = base + idx;
-        s[pad(idx)] = (i < n) ? (gather ? in[gather[i]] : in[i]) : 0u;
-    }
-    __syncthreads();
-    block_scan_chunk(s, s_wave, partials[blockIdx.x]);
-#pragma unroll 4
-    for (int k = 0; k < kItems; ++k) {
-        const int idx = k * kThreads + threadIdx.x;
-        const int64_t i = base + idx;
-        if (i < n) out[i] = s[pad(idx)];
-    }
+// min(n_host, *n_dev) when the live length is only known on the device.
+__device__ __forceinline__ int64_t live_count(int64_t n_host, const uint32_t* n_dev) {
+    if (!n_dev) return n_host;
+    const int64_t d = (int64_t)*n_dev;
+    return d < n_host ? d : n_host;
 }
 
 // Lanes of the wave (among `valid` ones) holding the same 8-bit digit.
@@ -167,56 +132,168 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
     return valid ? m : 0ull;
 }
 
-// Digit histogram of one 4096-key chunk -> hist[digit * nblocks + block].
-// Element order inside a chunk: wave w owns [w*1024, (w+1)*1024), round r
-// covers 64 consecutive keys -- the same order the scatter ranks in.
-__global__ __launch_bounds__(kThreads) void k_radix_hist(const uint32_t* __restrict__ keys,
-                                                         int64_t n, int shift,
-                                                         uint32_t* __restrict__ hist,
-                                                         int64_t nblocks) {
-    __shared__ uint32_t s_h[kThreads / 64][kRadix];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) s_h[w][tid] = 0u;
-    __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kChunk + wave * (kChunk / 4);
-    const uint64_t lt = (1ull << lane) - 1ull;
-    for (int r = 0; r < kItems; ++r) {
-        const int64_t i = base + r * 64 + lane;
-        const bool valid = i < n;
-        const uint32_t d = valid ? (keys[i] >> shift) & (kRadix - 1) : 0u;
-        const uint64_t m = match_digit(d, valid);
-        if (valid && (m & lt) == 0ull) s_h[wave][d] += (uint32_t)__popcll(m);
-    }
-    __syncthreads();
-    uint32_t t = 0;
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) t += s_h[w][tid];
-    hist[(int64_t)tid * nblocks + blockIdx.x] = t;
+// LDS histogram add of one digit per valid lane.  Lanes sharing the digit
+// of the first valid lane are folded into one add (the common case for
+// high digits, which are nearly constant across a wave); the rest add 1.
+__device__ __forceinline__ void hist_add(uint32_t* s_h, uint32_t d, bool valid) {
+    const uint64_t act = __ballot(valid);
+    if (act == 0ull) return;
+    const int leader = __ffsll((unsigned long long)act) - 1;
+    const uint32_t first = __builtin_amdgcn_readlane(d, leader);
+    const uint64_t same = __ballot(valid && d == first);
+    if (!valid) return;
+    if (d != first) atomicAdd(&s_h[d], 1u);
+    else if ((int)(threadIdx.x & 63) == leader) atomicAdd(&s_h[d], (uint32_t)__popcll(same));
 }
 
-// Stable scatter of one chunk by digit using the scanned histogram.
-// vals_in == nullptr means "values are the element indices".
-__global__ __launch_bounds__(kThreads) void k_radix_scatter(
-    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
-    int shift, const uint32_t* __restrict__ hist_scanned, int64_t nblocks,
-    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
-    __shared__ uint32_t s_cnt[kThreads / 64][kRadix];
-    __shared__ uint32_t s_base[kRadix];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) s_cnt[w][tid] = 0u;
-    s_base[tid] = hist_scanned[(int64_t)tid * nblocks + blockIdx.x];
+// Exclusive scan over the workgroup; *total gets the sum.  Every thread
+// must call it; s_w holds THREADS/64 words.
+template <int THREADS>
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* s_w, uint32_t* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t incl = wave_incl_scan(v);
+    if (lane == 63) s_w[wave] = incl;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kChunk + wave * (kChunk / 4);
-    const uint64_t lt = (1ull << lane) - 1ull;
-    uint32_t key[kItems], val[kItems], rank[kItems];
+    uint32_t off = 0, tot = 0;
 #pragma unroll
-    for (int r = 0; r < kItems; ++r) {
-        const int64_t i = base + r * 64 + lane;
+    for (int w = 0; w < THREADS / 64; ++w) {
+        const uint32_t t = s_w[w];
+        if (w < wave) off += t;
+        tot += t;
+    }
+    *total = tot;
+    return off + incl - v;
+}
+
+// The same for two values at once (one barrier); s_w holds 2*THREADS/64 words.
+template <int THREADS>
+__device__ __forceinline__ void block_excl_scan2(uint32_t a, uint32_t b, uint32_t* s_w,
+                                                 uint32_t* ea, uint32_t* eb) {
+    constexpr int kW = THREADS / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t ia = wave_incl_scan(a), ib = wave_incl_scan(b);
+    if (lane == 63) {
+        s_w[wave] = ia;
+        s_w[kW + wave] = ib;
+    }
+    __syncthreads();
+    uint32_t oa = 0, ob = 0;
+#pragma unroll
+    for (int w = 0; w < kW; ++w)
+        if (w < wave) {
+            oa += s_w[w];
+            ob += s_w[kW + w];
+        }
+    *ea = oa + ia - a;
+    *eb = ob + ib - b;
+}
+
+// Largest o in [0, n) with offs[o] <= x (offs non-decreasing, offs[0] <= x),
+// found by the whole workgroup: each round probes THREADS evenly spaced
+// positions and keeps the interval after the last probe <= x.
+template <int THREADS>
+__device__ __forceinline__ int64_t block_find_owner(const uint32_t* __restrict__ offs, int64_t n,
+                                                    uint32_t x) {
+    int64_t a = 0, b = n;
+    while (b - a > 1) {
+        const int64_t step = ceil_div(b - a, THREADS);
+        const int64_t p = a + (int64_t)threadIdx.x * step;
+        const bool le = p < b && offs[p] <= x;
+        const int cnt = __syncthreads_count(le);  // probes are monotone; p = a always counts
+        a += (int64_t)(cnt - 1) * step;
+        b = min(a + step, b);
+    }
+    return a;
+}
+
+struct ZeroRanges {
+    uint32_t* p[4];
+    int64_t n[4];
+};
+
+__global__ __launch_bounds__(256) void k_zero_ranges(ZeroRanges z) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < z.n[r]; i += stride)
+            z.p[r][i] = 0u;
+}
+
+// Digit histograms of the 4 bytes of every depth key from one read, added
+// into copy blockIdx % kHistCopies of hist[copy][pass][digit].
+__global__ __launch_bounds__(kHistThreads) void k_depth_hist(const uint32_t* __restrict__ keys,
+                                                             int64_t n,
+                                                             uint32_t* __restrict__ hist) {
+    __shared__ uint32_t s_h[kMaxPasses][kRadix];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    for (int k = tid; k < kMaxPasses * kRadix; k += kHistThreads) (&s_h[0][0])[k] = 0u;
+    __syncthreads();
+    const int64_t base =
+        (int64_t)blockIdx.x * (kHistThreads * kHistItems) + wave * (64 * kHistItems);
+    for (int r = 0; r < kHistItems; ++r) {
+        const int64_t i = base + r * 64 + (tid & 63);
         const bool valid = i < n;
-        key[r] = valid ? keys_in[i] : 0u;
-        val[r] = valid ? (vals_in ? vals_in[i] : (uint32_t)i) : 0u;
+        const uint32_t key = valid ? keys[i] : 0u;
+#pragma unroll
+        for (int p = 0; p < kMaxPasses; ++p)
+            hist_add(s_h[p], (key >> (p * kRadixBits)) & (kRadix - 1), valid);
+    }
+    __syncthreads();
+    uint32_t* h = hist + (blockIdx.x % kHistCopies) * kHistStride;
+    for (int k = tid; k < kMaxPasses * kRadix; k += kHistThreads) {
+        const uint32_t v = (&s_h[0][0])[k];
+        if (v) atomicAdd(&h[k], v);
+    }
+}
+
+// One stable LSD pass over the 8 bits at `shift`.  Chunk c (claimed in
+// launch order) holds keys [c * chunk, (c + 1) * chunk); wave w of it owns
+// a contiguous slice, ranked round by round, so the order is stable.  The
+// chunk is regrouped by digit in LDS, then written out: element j of the
+// regrouped chunk goes to global_base[digit] + j - chunk_base[digit].
+// `hist` points at this pass's histogram in copy 0.  vals_in == nullptr
+// means "values are the element indices".
+template <int THREADS, int ITEMS>
+__global__ __launch_bounds__(THREADS) void k_onesweep(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n_host,
+    const uint32_t* __restrict__ n_dev, int shift, const uint32_t* __restrict__ hist,
+    uint32_t* __restrict__ status, uint32_t* __restrict__ counter,
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ err) {
+    constexpr int kWaves = THREADS / 64;
+    constexpr int kChunk = THREADS * ITEMS;
+    static_assert(THREADS >= kRadix, "one thread per digit");
+    __shared__ uint32_t s_cnt[kWaves][kRadix];
+    __shared__ uint32_t s_dexcl[kRadix];
+    __shared__ uint32_t s_shift[kRadix];
+    __shared__ uint32_t s_w[2 * kWaves];
+    __shared__ uint32_t s_key[kChunk], s_val[kChunk];
+    __shared__ uint32_t s_chunk;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t n = live_count(n_host, n_dev);
+    // The first ceil(n / chunk) workgroups claim exactly the live chunks;
+    // the rest leave without claiming, so no live chunk waits on them.
+    if ((int64_t)blockIdx.x * kChunk >= n) return;
+    if (tid == 0) s_chunk = atomicAdd(counter, 1u);
+    for (int k = tid; k < kWaves * kRadix; k += THREADS) (&s_cnt[0][0])[k] = 0u;
+    uint32_t dsum = 0;
+    if (tid < kRadix) {
+#pragma unroll 4
+        for (int c = 0; c < kHistCopies; ++c) dsum += hist[c * kHistStride + tid];
+    }
+    __syncthreads();
+    const int64_t chunk = s_chunk;
+    const int64_t base = chunk * kChunk + wave * (64 * ITEMS);
+    const uint64_t lt = (1ull << lane) - 1ull;
+    uint32_t key[ITEMS], val[ITEMS], rank[ITEMS];
+#pragma unroll
+    for (int r = 0; r < ITEMS; ++r) {
+        const int64_t i = base + r * 64 + lane;
+        key[r] = i < n ? keys_in[i] : 0u;
+        val[r] = i < n ? (vals_in ? vals_in[i] : (uint32_t)i) : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < ITEMS; ++r) {
+        const bool valid = base + r * 64 + lane < n;
         const uint32_t d = (key[r] >> shift) & (kRadix - 1);
         const uint64_t m = match_digit(d, valid);
         const uint32_t before = s_cnt[wave][d];
@@ -224,104 +301,258 @@ __global__ __launch_bounds__(kThreads) void k_radix_scatter(
         if (valid && (m & lt) == 0ull) s_cnt[wave][d] = before + (uint32_t)__popcll(m);
     }
     __syncthreads();
-    {
-        uint32_t run = 0;
+    uint32_t local = 0;
+    uint32_t* st = status + chunk * kRadix + tid;
+    if (tid < kRadix) {
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) {
+        for (int w = 0; w < kWaves; ++w) {
             const uint32_t c = s_cnt[w][tid];
-            s_cnt[w][tid] = run;
-            run += c;
+            s_cnt[w][tid] = local;
+            local += c;
         }
+        status_store(st, (chunk == 0 ? kFlagInc : kFlagAgg) | local);
     }
+    // in-chunk digit offsets and global digit bases
+    uint32_t dexcl, dbase;
+    block_excl_scan2<THREADS>(local, dsum, s_w, &dexcl, &dbase);
+    if (tid < kRadix) s_dexcl[tid] = dexcl;
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kItems; ++r) {
-        const int64_t i = base + r * 64 + lane;
-        if (i < n) {
+    for (int r = 0; r < ITEMS; ++r) {
+        if (base + r * 64 + lane < n) {
             const uint32_t d = (key[r] >> shift) & (kRadix - 1);
-            const uint32_t pos = s_base[d] + s_cnt[wave][d] + rank[r];
-            if (pos < (uint64_t)n) {  // always true for a consistent histogram
-                keys_out[pos] = key[r];
-                vals_out[pos] = val[r];
-            }
+            const uint32_t j = s_dexcl[d] + s_cnt[wave][d] + rank[r];
+            s_key[j] = key[r];
+            s_val[j] = val[r];
+        }
+    }
+    if (tid < kRadix) {
+        uint32_t prefix = 0;
+        if (chunk > 0) {
+            prefix = look_back(status, chunk, kRadix, tid, err);
+            status_store(st, kFlagInc | ((prefix + local) & kCountMask));
+        }
+        s_shift[tid] = dbase + prefix - dexcl;  // modular: + j >= dexcl below
+    }
+    __syncthreads();
+    const int cnt = (int)min<int64_t>(kChunk, n - chunk * kChunk);
+    for (int j = tid; j < cnt; j += THREADS) {
+        const uint32_t k = s_key[j];
+        const uint32_t pos = s_shift[(k >> shift) & (kRadix - 1)] + (uint32_t)j;
+        if (pos < (uint64_t)n) {  // always true for a consistent histogram
+            keys_out[pos] = k;
+            vals_out[pos] = s_val[j];
         }
     }
 }
 
-// Largest i in [lo, hi] with offs[i] <= d (offs non-decreasing,
-// offs[hi + 1] > d guaranteed by the caller).
-__device__ __forceinline__ int64_t find_owner(const uint32_t* __restrict__ offs, int64_t lo,
-                                              int64_t hi, uint32_t d) {
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (offs[mid] <= d) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
-constexpr int kEmitItems = 4;
-constexpr int kEmitChunk = kThreads * kEmitItems;
-
-// One lane per duplicate: duplicate d belongs to the depth-ordered Gaussian
-// whose [offs[i], offs[i+1]) contains d; its tile is the (d - offs[i])-th
-// cell of the Gaussian's tile rectangle in row-major order (tiles.py:85-89).
-__global__ __launch_bounds__(kThreads) void k_emit(int64_t nd, int64_t n,
-                                                   const uint32_t* __restrict__ offs,
-                                                   const uint32_t* __restrict__ gids,
-                                                   const uint2* __restrict__ rects, int tiles_x,
-                                                   uint32_t* __restrict__ keys_out,
-                                                   uint32_t* __restrict__ vals_out) {
-    __shared__ int64_t s_range[2];
-    const int64_t d0 = (int64_t)blockIdx.x * kEmitChunk;
-    if (threadIdx.x < 2) {
-        const int64_t dq = threadIdx.x == 0 ? d0 : min(d0 + kEmitChunk - 1, nd - 1);
-        s_range[threadIdx.x] = find_owner(offs, 0, n - 1, (uint32_t)dq);
+// Exclusive scan of the tile counts in depth order: offs[i] = sum of the
+// counts of depth-ordered Gaussians 0..i-1, offs[n] = D, *d_total = D.
+__global__ __launch_bounds__(kScanThreads) void k_count_scan(
+    int64_t n, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ gids,
+    uint32_t* __restrict__ status, uint32_t* __restrict__ counter, uint32_t* __restrict__ offs,
+    uint32_t* __restrict__ d_total, uint32_t* __restrict__ err) {
+    __shared__ uint32_t s_w[kScanThreads / 64];
+    __shared__ uint32_t s_chunk, s_prefix;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_chunk = atomicAdd(counter, 1u);
+    __syncthreads();
+    const int64_t chunk = s_chunk;
+    const int64_t nchunks = ceil_div(n, kScanChunk);
+    if (chunk >= nchunks) return;  // not reached: the grid has exactly nchunks workgroups
+    const int64_t i0 = chunk * kScanChunk + (int64_t)tid * kScanItems;
+    uint32_t c[kScanItems];
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) c[j] = i0 + j < n ? counts[gids[i0 + j]] : 0u;
+    uint32_t total;
+    const uint32_t excl = block_excl_scan<kScanThreads>(c[0] + c[1] + c[2] + c[3], s_w, &total);
+    if (tid == 0) {
+        uint32_t prefix = 0;
+        uint32_t* st = status + chunk;
+        if (total > kCountMask) atomicOr(err, GSX_BIN_ERR_OVERFLOW);
+        if (chunk == 0) {
+            status_store(st, kFlagInc | (total & kCountMask));
+        } else {
+            status_store(st, kFlagAgg | (total & kCountMask));
+            prefix = look_back(status, chunk, 1, 0, err);
+            if ((uint64_t)prefix + total > kCountMask) atomicOr(err, GSX_BIN_ERR_OVERFLOW);
+            status_store(st, kFlagInc | ((prefix + total) & kCountMask));
+        }
+        s_prefix = prefix;
+        if (chunk == nchunks - 1) {
+            *d_total = prefix + total;
+            offs[n] = prefix + total;
+        }
     }
     __syncthreads();
-    const int64_t lo = s_range[0], hi = s_range[1];
+    uint32_t run = s_prefix + excl;
 #pragma unroll
-    for (int k = 0; k < kEmitItems; ++k) {
-        const int64_t d = d0 + k * kThreads + threadIdx.x;
-        if (d >= nd) break;
-        const int64_t i = find_owner(offs, lo, hi, (uint32_t)d);
-        const uint32_t g = gids[i];
-        const uint32_t local = (uint32_t)d - offs[i];
-        const uint2 r = rects[g];
-        const uint32_t w = r.y & 0xFFFFu;
-        const uint32_t tx = (r.x & 0xFFFFu) + local % w;
-        const uint32_t ty = (r.x >> 16) + local / w;
-        keys_out[d] = ty * (uint32_t)tiles_x + tx;
-        vals_out[d] = g;
+    for (int j = 0; j < kScanItems; ++j) {
+        if (i0 + j < n) offs[i0 + j] = run;
+        run += c[j];
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_fill_u32(uint32_t* __restrict__ p, int64_t n,
-                                                       uint32_t v) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i < n) p[i] = v;
+// Duplicate emission, kEmitDups duplicates per workgroup (of the
+// min(D, cap) that fit the output).  Duplicate d belongs to the
+// depth-ordered Gaussian o with offs[o] <= d < offs[o + 1]; its tile is the
+// (d - offs[o])-th cell of o's tile rectangle in row-major order.  The
+// owners of a workgroup's duplicates form a contiguous range, staged in LDS
+// when it fits (always, unless zero-count Gaussians sit between owners);
+// otherwise each duplicate searches offs directly.  The digit histograms
+// of the emitted tile ids (passes x 256) go into copy
+// blockIdx % kHistCopies of tile_hist.
+__global__ __launch_bounds__(kEmitThreads) void k_emit(
+    int64_t n, int64_t cap, const uint32_t* __restrict__ d_total,
+    const uint32_t* __restrict__ offs, const uint32_t* __restrict__ gids,
+    const uint2* __restrict__ rects, int tiles_x, int passes, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, uint32_t* __restrict__ tile_hist) {
+    __shared__ uint32_t s_off[kEmitDups];
+    __shared__ uint2 s_rect[kEmitDups];
+    __shared__ uint32_t s_gid[kEmitDups];
+    __shared__ uint32_t s_h[kMaxPasses][kRadix];
+    const int tid = threadIdx.x;
+    const int64_t nd = live_count(cap, d_total);
+    const int64_t d0 = (int64_t)blockIdx.x * kEmitDups;
+    if (d0 >= nd) return;
+    const int64_t d1 = min(d0 + kEmitDups, nd);
+    for (int k = tid; k < kMaxPasses * kRadix; k += kEmitThreads) (&s_h[0][0])[k] = 0u;
+    const int64_t lo = block_find_owner<kEmitThreads>(offs, n, (uint32_t)d0);
+    const int64_t hi = block_find_owner<kEmitThreads>(offs, n, (uint32_t)(d1 - 1));
+    const int64_t w = hi - lo + 1;
+    const bool staged = w <= kEmitDups;  // uniform
+    if (staged) {
+        for (int k = tid; k < w; k += kEmitThreads) {
+            const uint32_t g = gids[lo + k];
+            s_off[k] = offs[lo + k];
+            s_gid[k] = g;
+            s_rect[k] = rects[g];
+        }
+    }
+    __syncthreads();
+    const int64_t dd = d0 + (int64_t)tid * kEmitItems;
+    uint32_t t[kEmitItems], g[kEmitItems];
+    if (dd < d1) {
+        // owner of dd, then walk forward for the following duplicates
+        int64_t o;
+        if (staged) {
+            int a = 0, b = (int)w - 1;
+            while (a < b) {
+                const int mid = (a + b + 1) >> 1;
+                if (s_off[mid] <= (uint32_t)dd) a = mid;
+                else b = mid - 1;
+            }
+            o = a;
+        } else {
+            int64_t a = lo, b = hi;
+            while (a < b) {
+                const int64_t mid = (a + b + 1) >> 1;
+                if (offs[mid] <= (uint32_t)dd) a = mid;
+                else b = mid - 1;
+            }
+            o = a;
+        }
+#pragma unroll
+        for (int j = 0; j < kEmitItems; ++j) {
+            const uint32_t d = (uint32_t)(dd + j);
+            uint32_t off;
+            uint2 r;
+            if (staged) {
+                while (o + 1 < w && s_off[o + 1] <= d) ++o;
+                off = s_off[o];
+                r = s_rect[o];
+                g[j] = s_gid[o];
+            } else {
+                while (o + 1 <= hi && offs[o + 1] <= d) ++o;
+                off = offs[o];
+                g[j] = gids[o];
+                r = rects[g[j]];
+            }
+            const uint32_t local = d - off;
+            const uint32_t rw = r.y & 0xFFFFu;
+            const uint32_t tx = (r.x & 0xFFFFu) + local % rw;
+            const uint32_t ty = (r.x >> 16) + local / rw;
+            t[j] = ty * (uint32_t)tiles_x + tx;
+        }
+        if (dd + kEmitItems <= d1) {
+            *reinterpret_cast<uint4*>(keys_out + dd) = make_uint4(t[0], t[1], t[2], t[3]);
+            *reinterpret_cast<uint4*>(vals_out + dd) = make_uint4(g[0], g[1], g[2], g[3]);
+        } else {
+            for (int j = 0; j < kEmitItems; ++j)
+                if (dd + j < d1) {
+                    keys_out[dd + j] = t[j];
+                    vals_out[dd + j] = g[j];
+                }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kEmitItems; ++j) t[j] = 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < kEmitItems; ++j)
+        for (int p = 0; p < passes; ++p)
+            hist_add(s_h[p], (t[j] >> (p * kRadixBits)) & (kRadix - 1), dd + j < d1);
+    __syncthreads();
+    uint32_t* h = tile_hist + (blockIdx.x % kHistCopies) * kHistStride;
+    for (int k = tid; k < passes * kRadix; k += kEmitThreads) {
+        const uint32_t v = (&s_h[0][0])[k];
+        if (v) atomicAdd(&h[k], v);
+    }
 }
 
-__global__ __launch_bounds__(kThreads) void k_tile_ranges(int64_t nd,
-                                                          const uint32_t* __restrict__ tiles,
-                                                          int64_t num_tiles,
-                                                          int2* __restrict__ ranges) {
-    const int64_t d = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (d >= nd) return;
-    const uint32_t t = tiles[d];
-    if (t >= (uint64_t)num_tiles) return;
-    if (d == 0 || tiles[d - 1] != t) ranges[t].x = (int)d;
-    if (d == nd - 1 || tiles[d + 1] != t) ranges[t].y = (int)(d + 1);
+// Tile ranges from the sorted tile ids, 4 ids per thread: a tile starts
+// where the id differs from its predecessor and ends where it differs from
+// its successor.
+__global__ __launch_bounds__(256) void k_tile_ranges(int64_t cap,
+                                                     const uint32_t* __restrict__ nd_dev,
+                                                     const uint32_t* __restrict__ tiles,
+                                                     int64_t num_tiles,
+                                                     int2* __restrict__ ranges) {
+    const int64_t nd = live_count(cap, nd_dev);
+    const int64_t d0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (d0 >= nd) return;
+    uint32_t t[6];  // t[0] = predecessor, t[1..4] = own ids, t[5] = successor
+    if (d0 + 4 <= nd) {
+        const uint4 v = *reinterpret_cast<const uint4*>(tiles + d0);
+        t[1] = v.x; t[2] = v.y; t[3] = v.z; t[4] = v.w;
+    } else {
+        for (int j = 0; j < 4; ++j) t[1 + j] = d0 + j < nd ? tiles[d0 + j] : 0xFFFFFFFFu;
+    }
+    t[0] = d0 > 0 ? tiles[d0 - 1] : 0xFFFFFFFFu;
+    t[5] = d0 + 4 < nd ? tiles[d0 + 4] : 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t d = d0 + j;
+        const uint32_t cur = t[1 + j];
+        if (d >= nd || cur >= (uint64_t)num_tiles) continue;
+        if (d == 0 || t[j] != cur) ranges[cur].x = (int)d;
+        if (d == nd - 1 || t[2 + j] != cur) ranges[cur].y = (int)(d + 1);
+    }
 }
 
 // ------------------------------------------------------------ host side --
+inline int bits_for(int64_t count) {
+    int b = 0;
+    while ((int64_t(1) << b) < count) ++b;
+    return b;
+}
+
+// misc words: [0..3] depth-pass chunk counters, [4..7] tile-pass counters,
+// [8] emit counter, [12..13] status words of gsx_bin_sort, then the digit
+// histogram copies of the depth sort and of the tile sort.
+constexpr int kMiscCounters = 16;
+constexpr int kSyncStatusWord = 12;
+constexpr int kMiscWords = kMiscCounters + 2 * kHistCopies * kHistStride;
+
 struct Layout {
-    size_t dk0, dk1, dv0, dv1, offs, tk0, tk1, tv, hist, parts, misc, total;
+    size_t dk0, dk1, dv0, dv1, offs, tk0, tk1, tv, status, misc, total;
+    int64_t depth_chunks, tile_chunks, scan_chunks, emit_blocks, hist_blocks, status_words;
+    int tile_passes;
 };
 
 inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
-Layout make_layout(int64_t n, int64_t cap) {
+Layout make_layout(int64_t n, int64_t cap, int64_t num_tiles) {
     Layout L{};
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -329,9 +560,15 @@ Layout make_layout(int64_t n, int64_t cap) {
         o = align_up(o + bytes);
         return at;
     };
-    const size_t nn = (size_t)(n > 0 ? n : 1), cc = (size_t)(cap > 0 ? cap : 1);
-    const int64_t nb = ceil_div(std::max<int64_t>(std::max<int64_t>(n, cap), 1), kChunk);
-    const int64_t scan_len = std::max<int64_t>(nb * kRadix, n + 1);
+    const size_t nn = (size_t)std::max<int64_t>(n, 1), cc = (size_t)std::max<int64_t>(cap, 1);
+    L.depth_chunks = ceil_div((int64_t)nn, kDepthThreads * kDepthItems);
+    L.tile_chunks = ceil_div((int64_t)cc, kTileThreads * kTileItems);
+    L.scan_chunks = ceil_div((int64_t)nn, kScanChunk);
+    L.emit_blocks = ceil_div((int64_t)cc, kEmitDups);
+    L.hist_blocks = ceil_div((int64_t)nn, kHistThreads * kHistItems);
+    L.tile_passes = (bits_for(std::max<int64_t>(num_tiles, 1)) + kRadixBits - 1) / kRadixBits;
+    L.status_words =
+        (4 * L.depth_chunks + L.tile_passes * L.tile_chunks) * kRadix + L.scan_chunks;
     L.dk0 = take(4 * nn);
     L.dk1 = take(4 * nn);
     L.dv0 = take(4 * nn);
@@ -340,9 +577,8 @@ Layout make_layout(int64_t n, int64_t cap) {
     L.tk0 = take(4 * cc);
     L.tk1 = take(4 * cc);
     L.tv = take(4 * cc);
-    L.hist = take(4 * (size_t)(nb * kRadix));
-    L.parts = take(4 * (size_t)(ceil_div(scan_len, kChunk) + 1));
-    L.misc = take(4 * 16);
+    L.status = take(4 * (size_t)L.status_words);
+    L.misc = take(4 * (size_t)kMiscWords);
     L.total = o;
     return L;
 }
@@ -352,38 +588,28 @@ inline T* at(void* ws, size_t off) {
     return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
-int scan_exclusive(const uint32_t* in, const uint32_t* gather, int64_t len, uint32_t* out,
-                   uint32_t* partials, uint32_t* total, uint32_t* total2, hipStream_t st) {
-    const int64_t nparts = ceil_div(len, kChunk);
-    hipLaunchKernelGGL(k_scan_reduce, dim3((unsigned)nparts), dim3(kThreads), 0, st, in, gather,
-                       len, partials);
-    hipLaunchKernelGGL(k_scan_partials, dim3(1), dim3(kThreads), 0, st, partials, nparts, total,
-                       total2);
-    hipLaunchKernelGGL(k_scan_down, dim3((unsigned)nparts), dim3(kThreads), 0, st, in, gather, len,
-                       partials, out);
+inline unsigned grid_for(int64_t n, int64_t per) {
+    return (unsigned)std::max<int64_t>(1, ceil_div(n, per));
+}
+
+int zero(ZeroRanges z, hipStream_t st) {
+    int64_t most = 0;
+    for (int r = 0; r < 4; ++r) {
+        if (!z.p[r]) z.n[r] = 0;
+        most = std::max(most, z.n[r]);
+    }
+    if (most == 0) return GSX_OK;
+    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(most, 256), 4096);
+    hipLaunchKernelGGL(k_zero_ranges, dim3(grid), dim3(256), 0, st, z);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
 
-int radix_pass(const uint32_t* kin, const uint32_t* vin, int64_t count, int shift,
-               uint32_t* kout, uint32_t* vout, uint32_t* hist, uint32_t* parts, uint32_t* misc,
-               hipStream_t st) {
-    const int64_t nb = ceil_div(count, kChunk);
-    hipLaunchKernelGGL(k_radix_hist, dim3((unsigned)nb), dim3(kThreads), 0, st, kin, count, shift,
-                       hist, nb);
-    GSX_LAUNCH_CHECK();
-    const int rc = scan_exclusive(hist, nullptr, nb * kRadix, hist, parts, misc + 8, nullptr, st);
-    if (rc != GSX_OK) return rc;
-    hipLaunchKernelGGL(k_radix_scatter, dim3((unsigned)nb), dim3(kThreads), 0, st, kin, vin, count,
-                       shift, hist, nb, kout, vout);
-    GSX_LAUNCH_CHECK();
+int check_args(int64_t n, int32_t width, int32_t height, int64_t capacity) {
+    if (n < 0 || width <= 0 || height <= 0 || capacity < 0) return GSX_ERR_INVALID;
+    if (width > 0xFFFF * kTile || height > 0xFFFF * kTile) return GSX_ERR_INVALID;
+    if (n > (int64_t)kCountMask || capacity > (int64_t)kCountMask) return GSX_ERR_TOO_LARGE;
     return GSX_OK;
-}
-
-inline int bits_for(int64_t count) {
-    int b = 0;
-    while ((int64_t(1) << b) < count) ++b;
-    return b;
 }
 
 }  // namespace
@@ -391,85 +617,134 @@ inline int bits_for(int64_t count) {
 extern "C" {
 
 int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles) {
-    (void)num_tiles;
-    if (n < 0 || capacity < 0) return -1;
-    return (int64_t)make_layout(n, capacity).total;
+    if (n < 0 || capacity < 0 || num_tiles <= 0) return -1;
+    return (int64_t)make_layout(n, capacity, num_tiles).total;
+}
+
+int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
+                       const uint32_t* tile_rects, int32_t width, int32_t height, void* workspace,
+                       int64_t workspace_bytes, int64_t capacity, int32_t* sorted_ids,
+                       int32_t* tile_ranges, uint32_t* bin_status, void* stream) {
+    int rc = check_args(n, width, height, capacity);
+    if (rc != GSX_OK) return rc;
+    if (!tile_ranges || !bin_status) return GSX_ERR_INVALID;
+    if (n > 0 && (!tile_counts || !depth_keys || !tile_rects || !workspace)) return GSX_ERR_INVALID;
+    if (capacity > 0 && (!sorted_ids || ((uintptr_t)sorted_ids & 15u) != 0u))
+        return GSX_ERR_INVALID;  // emission stores 4 ids at a time
+    hipStream_t st = (hipStream_t)stream;
+    const int tiles_x = (width + kTile - 1) / kTile;
+    const int tiles_y = (height + kTile - 1) / kTile;
+    const int64_t T = (int64_t)tiles_x * tiles_y;
+    const Layout L = make_layout(n, capacity, T);
+    if (n > 0 && workspace_bytes < (int64_t)L.total) return GSX_ERR_WORKSPACE;
+    uint32_t* status = n > 0 ? at<uint32_t>(workspace, L.status) : nullptr;
+    uint32_t* misc = n > 0 ? at<uint32_t>(workspace, L.misc) : nullptr;
+    // ranges, D + error flags, look-back status words, counters and
+    // histograms all start at zero
+    rc = zero(ZeroRanges{{(uint32_t*)tile_ranges, bin_status, status, misc},
+                         {2 * T, 2, L.status_words, kMiscWords}},
+              st);
+    if (rc != GSX_OK || n == 0) return rc;
+
+    void* ws = workspace;
+    uint32_t* d_total = bin_status;
+    uint32_t* err = bin_status + 1;
+    uint32_t* depth_hist = misc + kMiscCounters;
+    uint32_t* tile_hist = depth_hist + kHistCopies * kHistStride;
+
+    // 1. stable sort of the Gaussians by depth key (index order breaks ties)
+    hipLaunchKernelGGL(k_depth_hist, dim3((unsigned)L.hist_blocks), dim3(kHistThreads), 0, st,
+                       depth_keys, n, depth_hist);
+    GSX_LAUNCH_CHECK();
+    const uint32_t* kin = depth_keys;
+    const uint32_t* vin = nullptr;
+    uint32_t* kbuf[2] = {at<uint32_t>(ws, L.dk0), at<uint32_t>(ws, L.dk1)};
+    uint32_t* vbuf[2] = {at<uint32_t>(ws, L.dv0), at<uint32_t>(ws, L.dv1)};
+    for (int p = 0; p < 4; ++p) {
+        hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems>), dim3((unsigned)L.depth_chunks),
+                           dim3(kDepthThreads), 0, st, kin, vin, n, (const uint32_t*)nullptr,
+                           p * kRadixBits, depth_hist + p * kRadix,
+                           status + (size_t)p * L.depth_chunks * kRadix, misc + p, kbuf[p & 1],
+                           vbuf[p & 1], err);
+        kin = kbuf[p & 1];
+        vin = vbuf[p & 1];
+    }
+    GSX_LAUNCH_CHECK();
+    const uint32_t* gids = vin;
+
+    // 2. scan of the counts in depth order; 3. emission (+ tile digit
+    //    histograms) into the buffers from which the tile passes end in
+    //    sorted_ids; 4. tile sort over the device-side D
+    const int passes = L.tile_passes;
+    uint32_t* tk[2] = {at<uint32_t>(ws, L.tk0), at<uint32_t>(ws, L.tk1)};
+    uint32_t* tv[2] = {(uint32_t*)sorted_ids, at<uint32_t>(ws, L.tv)};
+    int cur = passes & 1;
+    uint32_t* tstatus = status + (size_t)4 * L.depth_chunks * kRadix;
+    uint32_t* sstatus = tstatus + (size_t)passes * L.tile_chunks * kRadix;
+    uint32_t* offs = at<uint32_t>(ws, L.offs);
+    hipLaunchKernelGGL(k_count_scan, dim3((unsigned)L.scan_chunks), dim3(kScanThreads), 0, st, n,
+                       tile_counts, gids, sstatus, misc + 8, offs, d_total, err);
+    GSX_LAUNCH_CHECK();
+    if (capacity == 0) return GSX_OK;
+    hipLaunchKernelGGL(k_emit, dim3((unsigned)L.emit_blocks), dim3(kEmitThreads), 0, st, n,
+                       capacity, (const uint32_t*)d_total, (const uint32_t*)offs, gids,
+                       (const uint2*)tile_rects, tiles_x, passes, tk[cur], tv[cur], tile_hist);
+    GSX_LAUNCH_CHECK();
+    for (int p = 0; p < passes; ++p) {
+        hipLaunchKernelGGL((k_onesweep<kTileThreads, kTileItems>), dim3((unsigned)L.tile_chunks),
+                           dim3(kTileThreads), 0, st, tk[cur], tv[cur], capacity,
+                           (const uint32_t*)d_total, p * kRadixBits, tile_hist + p * kRadix,
+                           tstatus + (size_t)p * L.tile_chunks * kRadix, misc + 4 + p,
+                           tk[cur ^ 1], tv[cur ^ 1], err);
+        cur ^= 1;
+    }
+    GSX_LAUNCH_CHECK();
+    // 4. ranges
+    hipLaunchKernelGGL(k_tile_ranges, dim3(grid_for(capacity, 1024)), dim3(256), 0, st, capacity,
+                       (const uint32_t*)d_total, tk[cur], T, (int2*)tile_ranges);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_bin_status_check(const uint32_t* host_status, int64_t capacity, int64_t* num_dups) {
+    if (!host_status || !num_dups) return GSX_ERR_INVALID;
+    *num_dups = (int64_t)host_status[0];
+    if (host_status[1] & GSX_BIN_ERR_OVERFLOW) return GSX_ERR_TOO_LARGE;
+    if (host_status[1] != 0u) return GSX_ERR_DEVICE;
+    return *num_dups > capacity ? 1 : GSX_OK;
 }
 
 int gsx_bin_sort(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
                  const uint32_t* tile_rects, int32_t width, int32_t height, void* workspace,
                  int64_t workspace_bytes, int64_t capacity, int32_t* sorted_ids,
                  int32_t* tile_ranges, int64_t* num_dups, void* stream) {
-    if (n < 0 || width <= 0 || height <= 0 || capacity < 0 || !num_dups || !tile_ranges)
-        return GSX_ERR_INVALID;
-    if (n > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
+    if (!num_dups) return GSX_ERR_INVALID;
+    *num_dups = 0;
+    int rc = check_args(n, width, height, capacity);
+    if (rc != GSX_OK) return rc;
+    if (!tile_ranges) return GSX_ERR_INVALID;
     hipStream_t st = (hipStream_t)stream;
+    if (n == 0) {
+        const int64_t T = (int64_t)((width + kTile - 1) / kTile) * ((height + kTile - 1) / kTile);
+        return zero(ZeroRanges{{(uint32_t*)tile_ranges, nullptr, nullptr, nullptr}, {2 * T, 0, 0, 0}},
+                    st);
+    }
+    if (!workspace) return GSX_ERR_INVALID;
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
-    const int64_t T = (int64_t)tiles_x * tiles_y;
-    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)ceil_div(2 * T, kThreads)), dim3(kThreads), 0, st,
-                       (uint32_t*)tile_ranges, 2 * T, 0u);
-    GSX_LAUNCH_CHECK();
-    if (n == 0) {
-        *num_dups = 0;
-        return GSX_OK;
-    }
-    if (!tile_counts || !depth_keys || !tile_rects || !workspace) return GSX_ERR_INVALID;
-    const Layout L = make_layout(n, capacity);
+    const Layout L = make_layout(n, capacity, (int64_t)tiles_x * tiles_y);
     if (workspace_bytes < (int64_t)L.total) return GSX_ERR_WORKSPACE;
-    void* ws = workspace;
-    uint32_t* hist = at<uint32_t>(ws, L.hist);
-    uint32_t* parts = at<uint32_t>(ws, L.parts);
-    uint32_t* misc = at<uint32_t>(ws, L.misc);
-
-    // 1. stable sort of the Gaussians by depth key (index order breaks ties)
-    const uint32_t* kin = depth_keys;
-    const uint32_t* vin = nullptr;
-    uint32_t* kbuf[2] = {at<uint32_t>(ws, L.dk0), at<uint32_t>(ws, L.dk1)};
-    uint32_t* vbuf[2] = {at<uint32_t>(ws, L.dv0), at<uint32_t>(ws, L.dv1)};
-    for (int p = 0; p < 4; ++p) {
-        const int rc = radix_pass(kin, vin, n, p * kRadixBits, kbuf[p & 1], vbuf[p & 1], hist,
-                                  parts, misc, st);
-        if (rc != GSX_OK) return rc;
-        kin = kbuf[p & 1];
-        vin = vbuf[p & 1];
-    }
-    const uint32_t* gids = vin;
-
-    // 2. duplicate offsets in depth order; D = total
-    uint32_t* offs = at<uint32_t>(ws, L.offs);
-    int rc = scan_exclusive(tile_counts, gids, n, offs, parts, misc, offs + n, st);
+    // the status words sit in the workspace's counter block, past the counters
+    // the pipeline uses (it clears the whole block before the first kernel)
+    uint32_t* bs = at<uint32_t>(workspace, L.misc) + kSyncStatusWord;
+    rc = gsx_bin_sort_async(n, tile_counts, depth_keys, tile_rects, width, height, workspace,
+                            workspace_bytes, capacity, sorted_ids, tile_ranges, bs, stream);
     if (rc != GSX_OK) return rc;
-    uint32_t D32 = 0;
-    if (hipMemcpyAsync(&D32, misc, sizeof(uint32_t), hipMemcpyDeviceToHost, st) != hipSuccess)
+    uint32_t host[2] = {0u, 0u};
+    if (hipMemcpyAsync(host, bs, sizeof(host), hipMemcpyDeviceToHost, st) != hipSuccess)
         return GSX_ERR_HIP;
     if (hipStreamSynchronize(st) != hipSuccess) return GSX_ERR_HIP;
-    const int64_t D = (int64_t)D32;
-    *num_dups = D;
-    if (D > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
-    if (D > capacity) return 1;
-    if (D == 0) return GSX_OK;
-    if (!sorted_ids) return GSX_ERR_INVALID;
-
-    // 3. emit, 4. sort by tile so the final values land in sorted_ids
-    const int passes = (bits_for(T) + kRadixBits - 1) / kRadixBits;
-    uint32_t* tk[2] = {at<uint32_t>(ws, L.tk0), at<uint32_t>(ws, L.tk1)};
-    uint32_t* tv[2] = {(uint32_t*)sorted_ids, at<uint32_t>(ws, L.tv)};
-    int cur = (passes % 2 == 0) ? 0 : 1;
-    hipLaunchKernelGGL(k_emit, dim3((unsigned)ceil_div(D, kEmitChunk)), dim3(kThreads), 0, st, D, n,
-                       offs, gids, (const uint2*)tile_rects, tiles_x, tk[cur], tv[cur]);
-    GSX_LAUNCH_CHECK();
-    for (int p = 0; p < passes; ++p) {
-        rc = radix_pass(tk[cur], tv[cur], D, p * kRadixBits, tk[cur ^ 1], tv[cur ^ 1], hist, parts,
-                        misc, st);
-        if (rc != GSX_OK) return rc;
-        cur ^= 1;
-    }
-    // 5. ranges
-    hipLaunchKernelGGL(k_tile_ranges, dim3((unsigned)ceil_div(D, kThreads)), dim3(kThreads), 0, st,
-                       D, tk[cur], T, (int2*)tile_ranges);
-    GSX_LAUNCH_CHECK();
-    return GSX_OK;
+    return gsx_bin_status_check(host, capacity, num_dups);
 }
 
 }  // extern "C"

@@ -11,7 +11,9 @@ const char* gsx_strerror(int status) {
         case GSX_ERR_INVALID: return "invalid argument (size, null pointer, alignment or shape)";
         case GSX_ERR_HIP: return "HIP runtime error";
         case GSX_ERR_WORKSPACE: return "workspace smaller than gsx_bin_workspace_bytes()";
-        case GSX_ERR_TOO_LARGE: return "count exceeds the int32 index range";
+        case GSX_ERR_TOO_LARGE: return "count exceeds the supported index range";
+        case GSX_ERR_DEVICE:
+            return "device-side check failed (a bounded wait in the chained scan expired)";
         default: return status > 0 ? "capacity too small (retry with the returned size)"
                                    : "unknown gsx status";
     }

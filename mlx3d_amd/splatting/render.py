@@ -2,7 +2,7 @@
 
 The render functions run the fused pipeline
 
-    gsx_preprocess_fwd -> gsx_bin_sort -> gsx_raster_fwd
+    gsx_preprocess_fwd -> gsx_bin_sort_async -> gsx_raster_fwd -> (read D)
     gsx_raster_bwd -> gsx_preprocess_bwd            (backward)
 
 inside one ``torch.autograd.Function``: activations, projection, opacity
@@ -22,7 +22,7 @@ from ..cameras import Camera
 from ..profiling import count, stage
 from .rasterize import raster_backward, raster_forward
 from .sh import num_sh_bases
-from .tiles import _bin_sort
+from .tiles import BinJob
 
 __all__ = ["render_gaussians", "render_gaussian_depth", "render_gaussian_features"]
 
@@ -70,14 +70,26 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
             _lib.ptr(means2d), _lib.ptr(depths), _lib.ptr(radii), _lib.ptr(comp), _lib.ptr(co),
             _lib.ptr(colors_out), _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), st),
             "gsx_preprocess_fwd")
-    with stage("binning"):
-        ids, ranges = _bin_sort(counts, dkeys, rects, cfg.width, cfg.height)
-    count("duplicates", ids.shape[0])
     feats = colors_out if cfg.sh_mode else colors
-    with stage("raster_fwd"):
-        image, final_T, n_contrib, depth_map = raster_forward(
-            means2d, co, feats, ids, ranges, background, cfg.width, cfg.height,
-            depths=depths if cfg.return_depth else None)
+    with stage("binning"):
+        job = BinJob(counts, dkeys, rects, cfg.width, cfg.height)
+
+    def raster(ids):
+        with stage("raster_fwd"):
+            return raster_forward(means2d, co, feats, ids, job.ranges, background, cfg.width,
+                                  cfg.height, depths=depths if cfg.return_depth else None)
+
+    # The rasterizer runs on the full-capacity id buffer (its ranges never
+    # reach past D), so D is read back only after it has been enqueued.
+    image, final_T, n_contrib, depth_map = raster(job.ids)
+    if not job.finish():
+        with stage("binning"):
+            job.retry()
+        image, final_T, n_contrib, depth_map = raster(job.ids)
+        if not job.finish():
+            raise _lib.GsxError("gsx_bin_sort_async: capacity retry failed")
+    ids, ranges = job.result()
+    count("duplicates", ids.shape[0])
     return dict(means2d=means2d, depths=depths, radii=radii, compensation=comp, conic_opac=co,
                 feats=feats, sorted_ids=ids, tile_ranges=ranges, image=image, final_T=final_T,
                 n_contrib=n_contrib, depth=depth_map)

@@ -3,8 +3,9 @@
 ``bin_gaussians`` keeps the reference's signature and outputs: ``sorted_ids``
 (D,) int32 in (tile, depth, index) order and ``tile_ranges`` (tiles, 2)
 int32 with (0, 0) for empty tiles.  The work runs in ``gsx_bin_prepare`` and
-``gsx_bin_sort`` (device radix sorts); the only host sync is the 8-byte
-readback of D that the reference also does (tiles.py:68).
+``gsx_bin_sort_async`` (device radix sorts); the only host sync is the
+8-byte readback of D that the reference also does (tiles.py:68), and the
+renderer places it after the rasterizer has been enqueued.
 """
 
 from __future__ import annotations
@@ -12,6 +13,7 @@ from __future__ import annotations
 import ctypes
 import threading
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -22,16 +24,16 @@ __all__ = ["TILE_SIZE", "bin_gaussians"]
 
 
 class _Workspace:
-    """Grow-only scratch buffer for gsx_bin_sort, one per (device, stream)."""
+    """Grow-only scratch buffer for gsx_bin_sort_async, one per (device, stream)."""
 
     def __init__(self):
         self.buf = None
-        self.n = -1
-        self.cap = -1
         self.last_dups = 0
 
     def get(self, dev, n: int, cap: int, num_tiles: int) -> torch.Tensor:
         need = int(_lib.load().gsx_bin_workspace_bytes(n, cap, num_tiles))
+        if need < 0:
+            raise ValueError(f"bad binning sizes: n={n}, capacity={cap}")
         if self.buf is None or self.buf.numel() < need:
             self.buf = torch.empty(int(need * 1.1) + 4096, dtype=torch.uint8, device=dev)
         return self.buf
@@ -50,32 +52,78 @@ def _workspace_for(dev, stream) -> _Workspace:
     return ws
 
 
-def _bin_sort(counts, dkeys, rects, width: int, height: int):
-    """gsx_bin_sort with a capacity guess from the previous call; retried
-    once with the exact duplicate count when the guess is too small."""
-    dev = counts.device
-    n = counts.shape[0]
-    tiles_x = (width + TILE_SIZE - 1) // TILE_SIZE
-    tiles_y = (height + TILE_SIZE - 1) // TILE_SIZE
-    T = tiles_x * tiles_y
-    ranges = torch.empty((T, 2), dtype=torch.int32, device=dev)
-    st = _lib.stream_handle(dev)
-    ws = _workspace_for(dev, st)
-    cap = max(1024, int(ws.last_dups * 1.25), 4 * n)
-    L = _lib.load()
-    for _ in range(2):
-        buf = ws.get(dev, n, cap, T)
-        ids = torch.empty((cap,), dtype=torch.int32, device=dev)
+class BinJob:
+    """One binning on the device with the duplicate count D left there.
+
+    ``ids`` (capacity,) and ``ranges`` are usable by kernels enqueued behind
+    the job right away.  The two status words (D, error bits) are copied to
+    pinned host memory right behind the binning kernels, so ``finish()``
+    (the one host sync, as tiles.py:68 does) waits for the binning only,
+    not for work the caller enqueued after it.  It reports whether the
+    capacity sufficed; when it did not, ``retry()`` re-enqueues the binning
+    with room for D and the caller re-enqueues what it ran on the
+    incomplete result.
+    """
+
+    def __init__(self, counts, dkeys, rects, width: int, height: int):
+        self.dev = counts.device
+        self.args = (counts, dkeys, rects)
+        self.n = counts.shape[0]
+        self.width, self.height = int(width), int(height)
+        self.tiles_x = (self.width + TILE_SIZE - 1) // TILE_SIZE
+        self.tiles_y = (self.height + TILE_SIZE - 1) // TILE_SIZE
+        self.stream = _lib.stream_handle(self.dev)
+        self.ws = _workspace_for(self.dev, self.stream)
+        self.ranges = torch.empty((self.tiles_x * self.tiles_y, 2), dtype=torch.int32,
+                                  device=self.dev)
+        self.status = torch.empty((2,), dtype=torch.int32, device=self.dev)
+        self.num_dups = None
+        self._enqueue(max(1024, int(self.ws.last_dups * 1.25), 4 * self.n))
+
+    def _enqueue(self, cap: int):
+        counts, dkeys, rects = self.args
+        self.cap = int(cap)
+        buf = self.ws.get(self.dev, self.n, self.cap, self.tiles_x * self.tiles_y)
+        self.ids = torch.empty((self.cap,), dtype=torch.int32, device=self.dev)
+        _lib.check(_lib.load().gsx_bin_sort_async(
+            self.n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), self.width, self.height,
+            _lib.ptr(buf), buf.numel(), self.cap, _lib.ptr(self.ids), _lib.ptr(self.ranges),
+            _lib.ptr(self.status), self.stream), "gsx_bin_sort_async")
+        self.host = torch.empty((2,), dtype=torch.int32, pin_memory=True)
+        self.host.copy_(self.status, non_blocking=True)
+        self.ready = torch.cuda.Event()
+        self.ready.record()
+
+    def finish(self) -> bool:
+        """Read D back; True if the binning is complete, False if retry() is due."""
+        self.ready.synchronize()
+        host = np.ascontiguousarray(self.host.numpy().view(np.uint32))
         nd = ctypes.c_int64(0)
-        rc = _lib.check(L.gsx_bin_sort(n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), width,
-                                       height, _lib.ptr(buf), buf.numel(), cap, _lib.ptr(ids),
-                                       _lib.ptr(ranges), ctypes.byref(nd), st), "gsx_bin_sort")
-        D = int(nd.value)
-        ws.last_dups = D
-        if rc == _lib.GSX_OK:
-            return ids[:D], ranges
-        cap = D + D // 8 + 1024
-    raise _lib.GsxError("gsx_bin_sort: capacity retry failed")
+        rc = _lib.check(_lib.load().gsx_bin_status_check(
+            host.ctypes.data_as(ctypes.c_void_p), self.cap, ctypes.byref(nd)),
+            "gsx_bin_sort_async")
+        self.num_dups = int(nd.value)
+        self.ws.last_dups = self.num_dups
+        return rc == _lib.GSX_OK
+
+    def retry(self):
+        self._enqueue(self.num_dups + self.num_dups // 8 + 1024)
+        self.num_dups = None
+
+    def result(self):
+        """(sorted_ids (D,), tile_ranges) once finish() returned True."""
+        return self.ids[:self.num_dups], self.ranges
+
+
+def _bin_sort(counts, dkeys, rects, width: int, height: int):
+    """Binning with the capacity guessed from the previous call; one retry
+    with room for the exact duplicate count when the guess was short."""
+    job = BinJob(counts, dkeys, rects, width, height)
+    if not job.finish():
+        job.retry()
+        if not job.finish():
+            raise _lib.GsxError("gsx_bin_sort_async: capacity retry failed")
+    return job.result()
 
 
 def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, depths: torch.Tensor, width: int,

@@ -5,6 +5,8 @@ import ctypes
 import os
 import re
 
+import numpy as np
+
 from mlx3d_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -56,3 +58,29 @@ def test_invalid_arguments_rejected_before_launch():
                              None) == -1
     assert L.gsx_eval_sh_fwd(-1, 16, 3, 3, None, None, None, None) == -1
     assert L.gsx_eval_sh_fwd(10, 4, 3, 3, None, None, None, None) == -1  # K < (deg+1)^2
+
+
+def test_bin_status_check_is_host_only():
+    """gsx_bin_status_check interprets the two status words of
+    gsx_bin_sort_async: D, then error bits (1 = wait bound, 2 = overflow)."""
+    L = _lib.load()
+
+    def chk(words, cap):
+        h = np.array(words, dtype=np.uint32)
+        nd = ctypes.c_int64(-7)
+        rc = L.gsx_bin_status_check(h.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(nd))
+        return rc, nd.value
+
+    assert chk([123, 0], 123) == (0, 123)
+    assert chk([124, 0], 123) == (1, 124)
+    assert chk([5, 2], 100)[0] == -4
+    assert chk([5, 1], 100)[0] == -5
+    assert L.gsx_strerror(-5).decode().startswith("device-side check")
+    # binning entry points reject bad sizes before any launch
+    nd = ctypes.c_int64(0)
+    assert L.gsx_bin_sort(-1, None, None, None, 64, 64, None, 0, 0, None, None,
+                          ctypes.byref(nd), None) == -1
+    assert L.gsx_bin_sort(10, None, None, None, 64, 64, None, 0, 1 << 30, None, None,
+                          ctypes.byref(nd), None) == -4
+    assert L.gsx_bin_sort_async(10, None, None, None, 64, 64, None, 0, 100, None, None, None,
+                                None) == -1

@@ -128,6 +128,43 @@ def test_binning_edge_cases():
               8, 8, "one tile")
 
 
+def test_bin_sort_sync_abi_and_capacity():
+    """gsx_bin_sort (the synchronous entry point) at exact, short and zero
+    capacity: short capacity returns 1 with the true D; exact matches the
+    oracle bit for bit."""
+    cam, means, quats, scales, opac, colors = random_scene(4, n=30000, width=640, height=360)
+    p = O.project(oracle_camera(cam), means, quats, scales)
+    rids, rranges, tx, ty = O.bin_gaussians(p["means2d"], p["radii"], p["depths"], 640, 360,
+                                            threads=8)
+    D = rids.shape[0]
+    say(f"sync bin_sort: D={D}")
+    n = means.shape[0]
+    L = _lib.load()
+    dev = torch.device("cuda")
+    counts = torch.empty(n, dtype=torch.int32, device=dev)
+    dkeys = torch.empty(n, dtype=torch.int32, device=dev)
+    rects = torch.empty((n, 2), dtype=torch.int32, device=dev)
+    st = _lib.stream_handle(dev)
+    m2, rad, dep = cu(p["means2d"]), cu(p["radii"]), cu(p["depths"])  # alive past the launch
+    _lib.check(L.gsx_bin_prepare(n, _lib.ptr(m2), _lib.ptr(rad), _lib.ptr(dep), 640, 360,
+                                 _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), st),
+               "prepare")
+    ranges = torch.empty((tx * ty, 2), dtype=torch.int32, device=dev)
+    for cap, want in [(D - 1, 1), (0, 1), (D, 0), (D + 5000, 0)]:
+        ws = torch.empty(L.gsx_bin_workspace_bytes(n, cap, tx * ty), dtype=torch.uint8,
+                         device=dev)
+        ids = torch.full((max(cap, 1),), -1, dtype=torch.int32, device=dev)
+        nd = ctypes.c_int64(0)
+        rc = L.gsx_bin_sort(n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), 640, 360,
+                            _lib.ptr(ws), ws.numel(), cap, _lib.ptr(ids), _lib.ptr(ranges),
+                            ctypes.byref(nd), st)
+        say(f"  capacity {cap}: rc={rc} D={nd.value}")
+        assert rc == want and nd.value == D
+        if rc == 0:
+            np.testing.assert_array_equal(host(ids[:D]), rids)
+            np.testing.assert_array_equal(host(ranges), rranges)
+
+
 def test_rasterize_building_block_bitexact():
     cam, means, quats, scales, opac, colors = random_scene(2, n=3000, width=200, height=150)
     p = O.project(oracle_camera(cam), means, quats, scales)
