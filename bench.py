@@ -12,7 +12,16 @@ targets and parameters are resident in HBM before timing starts.
 Prints one JSON line.  ``roofline`` is for the dominant kernel, from its
 algorithmic bytes per launch and its mean duration measured with HIP events
 on its launch stream during the timed steps; ``cpu_baseline`` times the CPU
-oracle (C, OpenMP) on one fwd+bwd iteration of the same workload.
+oracle (C, OpenMP) on one fwd+bwd iteration per view of the same workload.
+
+Profiling helpers (used to produce profiles/):
+    --copy-probe MB    after timing, stream MB megabytes through a plain
+                       read-once/write-once kernel (gsx_debug_expf), the
+                       calibration for rocprofv3's FETCH_SIZE / WRITE_SIZE
+    --summarize-prof DIR --workload NAME
+                       turn rocprofv3 csv output under DIR (kernel stats,
+                       counter collections) into the text summary and the
+                       traffic record bench.py reads; no GPU needed
 """
 
 from __future__ import annotations
@@ -37,7 +46,17 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-stages", action="store_true",
                     help="print per-stage times to stderr")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB")
+    ap.add_argument("--summarize-prof", metavar="DIR", nargs="+")
+    ap.add_argument("--workload", default="c3_1m_sh3_aa_1080p_8views")
+    ap.add_argument("--command", default="", help="command line recorded in the summary")
     return ap.parse_args()
+
+
+# stage name -> device kernel symbol prefix (as rocprofv3 reports it)
+KERNEL_SYMBOL = {"raster_fwd": "k_raster_fwd", "raster_bwd": "k_raster_bwd",
+                 "preprocess_fwd": "k_preprocess_fwd", "preprocess_bwd": "k_preprocess_bwd"}
+COPY_PROBE_KERNEL = "k_debug_expf"
 
 
 def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
@@ -57,28 +76,110 @@ def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
                 iter=fwd + bwd + loss)
 
 
+def _profiles_dir():
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
 def _traffic(kernel: str, workload: str):
-    """HBM bytes per launch measured by rocprofv3 PMC runs, if recorded."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        f"traffic_{kernel}_{workload}.json")
+    """HBM bytes per launch (FETCH + WRITE, calibrated) from the rocprofv3
+    PMC runs recorded under profiles/, if present."""
+    path = os.path.join(_profiles_dir(), f"traffic_{kernel}_{workload}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-def cpu_baseline(scene, view: int, cfg_name: str):
-    """One fwd+bwd iteration of the oracle on the host cores."""
+def _read_csv(path):
+    import csv
+
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _short(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    return name.split("(")[0]
+
+
+def summarize_prof(dirs, workload: str, command: str):
+    """rocprofv3 csv output under dirs -> profiles/kernels_<workload>.md and,
+    with counter runs present, profiles/traffic_<kernel>_<workload>.json."""
+    import glob
+
+    out_dir = _profiles_dir()
+    os.makedirs(out_dir, exist_ok=True)
+
+    def find(pattern):
+        return sorted(p for d in dirs for p in glob.glob(os.path.join(d, "**", pattern),
+                                                         recursive=True))
+
+    stats = find("*kernel_stats.csv")
+    if stats:
+        rows = _read_csv(stats[0])
+        rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+        total = sum(float(r["TotalDurationNs"]) for r in rows)
+        lines = [f"# rocprofv3 kernel statistics: {workload}", "",
+                 "Command (run from the repository root on the MI355X box):", "",
+                 f"    {command}", "",
+                 "| kernel | calls | avg us | min us | max us | total ms | % |",
+                 "|---|---|---|---|---|---|---|"]
+        for r in rows[:30]:
+            lines.append(f"| `{_short(r['Name'])[:70]}` | {r['Calls']} | "
+                         f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                         f"{float(r['MaxNs']) / 1e3:.2f} | "
+                         f"{float(r['TotalDurationNs']) / 1e6:.3f} | "
+                         f"{100.0 * float(r['TotalDurationNs']) / total:.1f} |")
+        path = os.path.join(out_dir, f"kernels_{workload}.md")
+        with open(path, "w") as f:
+            f.write("\n".join(lines) + "\n")
+        print(f"wrote {path}")
+    counters = {}
+    for path in find("*counter_collection.csv"):
+        for r in _read_csv(path):
+            counters.setdefault(r["Counter_Name"], []).append(
+                (_short(r["Kernel_Name"]), float(r["Counter_Value"]), int(r["Grid_Size"])))
+    if "FETCH_SIZE" in counters and "WRITE_SIZE" in counters:
+        def per_kernel(cname, sym):
+            v = [x[1] for x in counters[cname] if x[0].startswith(sym)]
+            return sum(v) / len(v) if v else None
+
+        probe = [x for x in counters["FETCH_SIZE"] if x[0].startswith(COPY_PROBE_KERNEL)]
+        n_probe = max(x[2] for x in probe)  # grid = elements of the largest probe launch
+        known_kib = 4.0 * n_probe / 1024.0
+        f_probe = max(x[1] for x in probe)
+        w_probe = max(x[1] for x in counters["WRITE_SIZE"] if x[0].startswith(COPY_PROBE_KERNEL))
+        f_scale, w_scale = known_kib / f_probe, known_kib / w_probe
+        for stage, sym in KERNEL_SYMBOL.items():
+            fk, wk = per_kernel("FETCH_SIZE", sym), per_kernel("WRITE_SIZE", sym)
+            if fk is None or wk is None:
+                continue
+            rec = {"kernel": sym, "workload": workload,
+                   "fetch_kib_per_launch_raw": round(fk, 1),
+                   "write_kib_per_launch_raw": round(wk, 1),
+                   "calibration": {"probe_kernel": COPY_PROBE_KERNEL,
+                                   "probe_bytes_read": int(known_kib * 1024),
+                                   "probe_bytes_written": int(known_kib * 1024),
+                                   "fetch_scale": round(f_scale, 4),
+                                   "write_scale": round(w_scale, 4)},
+                   "hbm_bytes_per_launch": int((fk * f_scale + wk * w_scale) * 1024),
+                   "command": command}
+            path = os.path.join(out_dir, f"traffic_{stage}_{workload}.json")
+            with open(path, "w") as f:
+                json.dump(rec, f, indent=1)
+            print(f"wrote {path}")
+
+
+def cpu_baseline(scene, views, cfg_name: str):
+    """One fwd+bwd iteration of the oracle per view, on the host cores."""
     import numpy as np
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import oracle as O
 
     threads = O.default_threads()
-    cam = scene.cameras[view]
-    f = cam.gsx_fields()
-    oc = O.make_camera(f["R"], f["t"], f["center"], f["fx"], f["fy"], f["cx"], f["cy"],
-                       f["lim_x"], f["lim_y"], f["znear"], f["width"], f["height"])
     if scene.features is not None:
         scales, opac, flags, sh = scene.scales, scene.opacities, 0, None
     else:
@@ -87,28 +188,36 @@ def cpu_baseline(scene, view: int, cfg_name: str):
         sh = np.concatenate([scene.sh_dc, scene.sh_rest], 1)
     if scene.antialias:
         flags |= O.ANTIALIAS
-    target = scene.target(cam)
-    t0 = time.perf_counter()
-    pre = O.preprocess_fwd(oc, scene.means, scene.quats, scales, opac, sh=sh,
-                           degree=scene.sh_degree, flags=flags, threads=threads)
-    feats = pre["colors"] if sh is not None else scene.features
-    ids, ranges, _, _ = O.bin_gaussians(pre["means2d"], pre["radii"], pre["depths"], cam.width,
-                                        cam.height, threads=threads)
-    r = O.raster_fwd(pre["means2d"], pre["conics"], pre["opac_eff"], feats, ids, ranges,
-                     cam.width, cam.height, depths=pre["depths"] if scene.depth else None,
-                     threads=threads)
-    t1 = time.perf_counter()
-    if scene.backward:
-        g_img = (np.sign(r["image"] - target) / np.float32(target.size)).astype(np.float32)
-        gr = O.raster_bwd(pre["means2d"], pre["conics"], pre["opac_eff"], feats, ids, ranges,
-                          cam.width, cam.height, r["final_T"], r["n_contrib"], g_img,
-                          threads=threads)
-        O.preprocess_bwd(oc, scene.means, scene.quats, scales, opac,
-                         pre["colors"] if sh is not None else None,
-                         0 if sh is None else sh.shape[1], scene.sh_degree, flags,
-                         gr["means2d"], gr["conics"], gr["opacities"],
-                         gr["features"] if sh is not None else None, threads=threads)
-    t2 = time.perf_counter()
+    t_fwd = t_all = 0.0
+    for view in views:
+        cam = scene.cameras[view]
+        f = cam.gsx_fields()
+        oc = O.make_camera(f["R"], f["t"], f["center"], f["fx"], f["fy"], f["cx"], f["cy"],
+                           f["lim_x"], f["lim_y"], f["znear"], f["width"], f["height"])
+        target = scene.target(cam)
+        t0 = time.perf_counter()
+        pre = O.preprocess_fwd(oc, scene.means, scene.quats, scales, opac, sh=sh,
+                               degree=scene.sh_degree, flags=flags, threads=threads)
+        feats = pre["colors"] if sh is not None else scene.features
+        ids, ranges, _, _ = O.bin_gaussians(pre["means2d"], pre["radii"], pre["depths"],
+                                            cam.width, cam.height, threads=threads)
+        r = O.raster_fwd(pre["means2d"], pre["conics"], pre["opac_eff"], feats, ids, ranges,
+                         cam.width, cam.height, depths=pre["depths"] if scene.depth else None,
+                         threads=threads)
+        t1 = time.perf_counter()
+        if scene.backward:
+            g_img = (np.sign(r["image"] - target) / np.float32(target.size)).astype(np.float32)
+            gr = O.raster_bwd(pre["means2d"], pre["conics"], pre["opac_eff"], feats, ids,
+                              ranges, cam.width, cam.height, r["final_T"], r["n_contrib"],
+                              g_img, threads=threads)
+            O.preprocess_bwd(oc, scene.means, scene.quats, scales, opac,
+                             pre["colors"] if sh is not None else None,
+                             0 if sh is None else sh.shape[1], scene.sh_degree, flags,
+                             gr["means2d"], gr["conics"], gr["opacities"],
+                             gr["features"] if sh is not None else None, threads=threads)
+        t2 = time.perf_counter()
+        t_fwd += t1 - t0
+        t_all += t2 - t0
     cpu = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as fh:
@@ -118,16 +227,21 @@ def cpu_baseline(scene, view: int, cfg_name: str):
                     break
     except OSError:
         pass
-    total = t2 - t0
-    return {"value": round(1.0 / total, 4), "unit": "it/s" if scene.backward else "frames/s",
+    k = len(views)
+    what = "fwd+bwd iteration" if scene.backward else "forward"
+    return {"value": round(k / t_all, 4), "unit": "it/s" if scene.backward else "frames/s",
             "cores": threads, "kind": "port",
-            "sample": f"1 {'fwd+bwd iteration' if scene.backward else 'forward'} of view {view} "
-                      f"of {cfg_name} (full frame), C oracle + OpenMP",
-            "fwd_s": round(t1 - t0, 3), "iter_s": round(total, 3), "cpu_model": cpu}
+            "sample": f"{k} x 1 {what} (views {views[0]}..{views[-1]} of {cfg_name}, full "
+                      f"frames, loss L1 as on the GPU), C oracle + OpenMP on {threads} threads",
+            "fwd_s_per_view": round(t_fwd / k, 3), "iter_s_per_view": round(t_all / k, 3),
+            "cpu_model": cpu}
 
 
 def main():
     args = _parse()
+    if args.summarize_prof:
+        summarize_prof(args.summarize_prof, args.workload, args.command)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: only --gpus 1 is supported (got --gpus {args.gpus}, WORLD_SIZE "
@@ -216,6 +330,16 @@ def main():
         f1 = time.perf_counter()
     ms_fwd = (f1 - f0) * 1e3 / args.steps
 
+    if args.copy_probe > 0:  # counter calibration: reads and writes MB megabytes once
+        n = args.copy_probe * (1 << 20) // 4
+        src = torch.zeros(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            _lib.check(_lib.load().gsx_debug_expf(n, _lib.ptr(src), _lib.ptr(dst),
+                                                  _lib.stream_handle(dev)), "copy probe")
+        torch.cuda.synchronize()
+        del src, dst
+
     N = scene.n
     P = cams[0].width * cams[0].height
     C = scene.channels
@@ -258,7 +382,8 @@ def main():
         "fwd_ms": round(ms_fwd, 4),
         "fwd_hbm_roofline_frac": round(fwd_gbs / HBM_PEAK_GBS, 4),
         "iter_hbm_roofline_frac": round(B["iter"] / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS,
+        "roofline": {"bound": "hbm", "kernel": dom, "kernel_symbol": KERNEL_SYMBOL[dom],
+                     "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": _traffic(dom, workload),
                      "algorithmic_bytes": int(B[dom]), "mean_ms": stages[dom]["ms"]},
@@ -266,7 +391,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         print("bench: timing CPU oracle baseline ...", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(scene, 0, workload)
+        out["cpu_baseline"] = cpu_baseline(scene, list(range(nviews)), workload)
     else:
         out["cpu_baseline"] = None
     if args.profile_stages:
