@@ -150,18 +150,39 @@ __device__ __forceinline__ float dpp_f(float v) {
                                                        BANK_MASK, false));
 }
 
-// Sum over the 64 lanes of the wave; the total ends up in lane 63.
-// quad_perm xor1, xor2, half-row mirror, row mirror, then the gfx9
-// row_bcast15 / row_bcast31 steps fold the four rows.  All lanes must be
-// active.
-__device__ __forceinline__ float wave_total_lane63(float v) {
-    v += dpp_f<0xB1, 0xF, 0xF>(v);   // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E, 0xF, 0xF>(v);   // quad_perm [2,3,0,1]
-    v += dpp_f<0x141, 0xF, 0xF>(v);  // row_half_mirror
-    v += dpp_f<0x140, 0xF, 0xF>(v);  // row_mirror
-    v += dpp_f<0x142, 0xA, 0xF>(v);  // row_bcast15 -> rows 1, 3
-    v += dpp_f<0x143, 0xC, 0xF>(v);  // row_bcast31 -> rows 2, 3
-    return v;
+// Sums of NVP per-lane values (NVP a multiple of 4) over the 64 lanes of
+// the wave, spread over the four 16-lane rows: afterwards every lane of row
+// r holds in q[m] the total of value 4m + kRowValue[r].  Step 1 swaps the
+// upper half of value 2k with the lower half of value 2k + 1
+// (v_permlane32_swap) and adds, so each half carries one of the two values;
+// step 2 does the same between rows (v_permlane16_swap); step 3 sums each
+// row with four DPP steps.  NVP + NVP/2 + NVP exchanges/adds instead of 6 NVP
+// for a separate 64-lane reduction of every value.  All lanes must be active.
+__device__ constexpr int kRowValue[4] = {0, 2, 1, 3};
+
+template <int NVP>
+__device__ __forceinline__ void wave_reduce_rows(const float (&v)[NVP], float (&q)[NVP / 4]) {
+    static_assert(NVP % 4 == 0, "values come in groups of four");
+    float h[NVP / 2];
+#pragma unroll
+    for (int k = 0; k < NVP / 2; ++k) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2 * k]),
+                                                        __float_as_uint(v[2 * k + 1]), false,
+                                                        false);
+        h[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int m = 0; m < NVP / 4; ++m) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(h[2 * m]),
+                                                        __float_as_uint(h[2 * m + 1]), false,
+                                                        false);
+        float t = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        t += dpp_f<0xB1, 0xF, 0xF>(t);   // quad_perm [1,0,3,2]
+        t += dpp_f<0x4E, 0xF, 0xF>(t);   // quad_perm [2,3,0,1]
+        t += dpp_f<0x141, 0xF, 0xF>(t);  // row_half_mirror
+        t += dpp_f<0x140, 0xF, 0xF>(t);  // row_mirror
+        q[m] = t;
+    }
 }
 
 __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
@@ -407,12 +428,16 @@ struct BwdPixel {
 };
 
 // One (pixel, Gaussian) step of the back-to-front replay
-// (rasterize.py:162-219).  When any lane of the wave contributes, lane 63
-// stores the wave sums of
+// (rasterize.py:162-219).  When any lane of the wave contributes, the wave
+// sums of
 //   u = G dx dL/dG, w = G dy dL/dG, u dx, u dy, w dy, G dL/dalpha, alpha T g_c
-// in the wave's slot for Gaussian j; the flush turns them into the
+// go into the wave's slot for Gaussian j; the flush turns them into the
 // reference's means2d, conic, opacity and colour gradients (linear in these
-// sums).  T is recovered with one reciprocal of (1 - alpha) per pair.
+// sums).  alpha and the skip tests repeat the forward's float32 arithmetic
+// exactly (the replay must take the forward's decisions); the gradient
+// arithmetic itself uses fused multiply-adds.  T is recovered with one
+// reciprocal of (1 - alpha) per pair.  PLAIN: inputs are finite, so a lane
+// that does not contribute can run the same update with a zero weight.
 template <int CH, bool PLAIN>
 __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
                                          const float4* __restrict__ fsrc, int j, int gj,
@@ -421,12 +446,15 @@ __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
                                          uint64_t& wrote1) {
     constexpr int F4 = (CH + 3) / 4;
     constexpr int NV = CH + 6;
-    constexpr int NV4 = (NV + 3) / 4;
+    constexpr int NVP = 4 * ((NV + 3) / 4);
     const float dx = r0.x - pxf, dy = r0.y - pyf;
     const float power = -0.5f * (r1.x * dx * dx + r1.z * dy * dy) - r1.y * dx * dy;
     bool ok = gj < px.last && !(power > 0.0f) && !(power < r0.z);
     if (__ballot(ok) == 0ull) return;
-    const float G = PLAIN ? dexp_inrange(power) : dexp_sel(power);
+    // PLAIN: lanes that pass have power in [-86, 0]; clamping leaves them
+    // unchanged and keeps G finite (so zero weights stay zero) elsewhere.
+    const float G = PLAIN ? dexp_inrange(__builtin_amdgcn_fmed3f(power, -87.0f, 0.0f))
+                          : dexp_sel(power);
     const float alpha = fminf(0.99f, r0.w * G);
     ok = ok && !(alpha < 1.0f / 255.0f);
     if (__ballot(ok) == 0ull) return;
@@ -434,26 +462,37 @@ __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
 #pragma unroll
     for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
     const float rcp = __builtin_amdgcn_rcpf(1.0f - alpha);
-    const float Tn = px.T * rcp;
-    px.T = ok ? Tn : px.T;
-    const float la1 = 1.0f - px.last_alpha;
+    px.T = ok ? px.T * rcp : px.T;
     float dl = 0.0f;
+    if (PLAIN) {
+        const float la = ok ? px.last_alpha : 0.0f;  // la = 0: accum unchanged
+        const float la1 = 1.0f - la;
 #pragma unroll
-    for (int ch = 0; ch < CH; ++ch) {
-        const float f = comp4(fv[ch >> 2], ch & 3);
-        const float an = px.last_alpha * px.lastc[ch] + la1 * px.accum[ch];
-        px.accum[ch] = ok ? an : px.accum[ch];
-        px.lastc[ch] = ok ? f : px.lastc[ch];
-        dl = dl + (f - px.accum[ch]) * px.gpix[ch];
+        for (int ch = 0; ch < CH; ++ch) {
+            const float f = comp4(fv[ch >> 2], ch & 3);
+            const float an = fmaf(la, px.lastc[ch], la1 * px.accum[ch]);
+            px.accum[ch] = an;
+            px.lastc[ch] = ok ? f : px.lastc[ch];
+            dl = fmaf(f - an, px.gpix[ch], dl);
+        }
+    } else {
+        const float la1 = 1.0f - px.last_alpha;
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+            const float f = comp4(fv[ch >> 2], ch & 3);
+            const float an = fmaf(px.last_alpha, px.lastc[ch], la1 * px.accum[ch]);
+            px.accum[ch] = ok ? an : px.accum[ch];
+            px.lastc[ch] = ok ? f : px.lastc[ch];
+            dl = fmaf(f - px.accum[ch], px.gpix[ch], dl);
+        }
     }
     px.last_alpha = ok ? alpha : px.last_alpha;
-    float dL_dalpha = dl * px.T + (-px.T_final * rcp) * px.bg_dot;
-    float aT = alpha * px.T;
+    float dL_dalpha = fmaf(dl, px.T, (-px.T_final * rcp) * px.bg_dot);
     dL_dalpha = ok ? dL_dalpha : 0.0f;
-    aT = ok ? aT : 0.0f;
-    const float dL_dG = r0.w * dL_dalpha;
-    float v[4 * NV4];
-    const float u = G * dx * dL_dG, w = G * dy * dL_dG;
+    const float aT = ok ? alpha * px.T : 0.0f;
+    const float gd = G * (r0.w * dL_dalpha);  // G dL/dG
+    float v[NVP];
+    const float u = gd * dx, w = gd * dy;
     v[0] = u;
     v[1] = w;
     v[2] = u * dx;
@@ -462,18 +501,18 @@ __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
     v[5] = G * dL_dalpha;
 #pragma unroll
     for (int ch = 0; ch < CH; ++ch) v[6 + ch] = aT * px.gpix[ch];
+#pragma unroll
+    for (int q = NV; q < NVP; ++q) v[q] = 0.0f;
     if (!PLAIN) {
 #pragma unroll
         for (int q = 0; q < NV; ++q) v[q] = ok ? v[q] : 0.0f;
     }
+    float tot[NVP / 4];
+    wave_reduce_rows<NVP>(v, tot);
+    if ((lane & 15) == 15) {
+        float* dst = reinterpret_cast<float*>(part[j]) + kRowValue[lane >> 4];
 #pragma unroll
-    for (int q = 0; q < NV; ++q) v[q] = wave_total_lane63(v[q]);
-#pragma unroll
-    for (int q = NV; q < 4 * NV4; ++q) v[q] = 0.0f;
-    if (lane == 63) {
-#pragma unroll
-        for (int q = 0; q < NV4; ++q)
-            part[j][q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        for (int m = 0; m < NVP / 4; ++m) dst[4 * m] = tot[m];
     }
     if (j < kWave) wrote0 |= 1ull << j;
     else wrote1 |= 1ull << (j - kWave);
