@@ -15,6 +15,69 @@ constexpr int kThreads = 256;
 
 inline unsigned grid_for(int64_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
 
+// SH coefficient rows are moved between HBM and LDS by the whole workgroup
+// with consecutive lanes on consecutive floats, instead of each lane
+// touching its own 180-192 strided bytes (which costs one cache-line request
+// per lane per load).  LDS rows are padded to an odd length so that lane r
+// walking its own row hits distinct banks.
+enum ShMode { kShDirect = 0, kShSplit = 1, kShPacked = 2 };
+constexpr int kShMaxCols = 48;  // 16 coefficients x 3 channels
+constexpr int kShPad = kShMaxCols + 1;
+
+// Row r and column c of the flattened index j (cols >= 1, j < 2^20).
+__device__ __forceinline__ void row_col(int j, int cols, float inv, int& r, int& c) {
+    r = (int)(((float)j + 0.5f) * inv);
+    c = j - r * cols;
+    if (c < 0) {
+        --r;
+        c += cols;
+    } else if (c >= cols) {
+        ++r;
+        c -= cols;
+    }
+}
+
+// Rows [g0, g0 + rows) of `cols` floats (row r at base + (g0 + r) * stride)
+// into LDS rows of `pad` floats.  Loads go out kBatch at a time so their
+// latencies overlap.
+__device__ __forceinline__ void rows_to_lds(float* s, int pad, const float* __restrict__ base,
+                                            int64_t stride, int64_t g0, int rows, int cols) {
+    constexpr int kBatch = 16;
+    const int total = rows * cols;
+    const float inv = 1.0f / (float)cols;
+    for (int j0 = threadIdx.x; j0 < total; j0 += kBatch * kThreads) {
+        float v[kBatch];
+        int at[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int j = j0 + u * kThreads;
+            at[u] = -1;
+            v[u] = 0.0f;
+            if (j < total) {
+                int r, c;
+                row_col(j, cols, inv, r, c);
+                v[u] = base[(g0 + r) * stride + c];
+                at[u] = r * pad + c;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            if (at[u] >= 0) s[at[u]] = v[u];
+    }
+}
+
+// The reverse: LDS rows of `pad` floats out to rows of `cols` floats.
+__device__ __forceinline__ void lds_to_rows(const float* s, int pad, float* __restrict__ base,
+                                            int64_t stride, int64_t g0, int rows, int cols) {
+    const int total = rows * cols;
+    const float inv = 1.0f / (float)cols;
+    for (int j = threadIdx.x; j < total; j += kThreads) {
+        int r, c;
+        row_col(j, cols, inv, r, c);
+        base[(g0 + r) * stride + c] = s[r * pad + c];
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void k_project_fwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, float blur, bool aa, float2* __restrict__ means2d,
@@ -162,16 +225,28 @@ __global__ __launch_bounds__(kThreads) void k_eval_sh_bwd(int64_t n, int K, int 
 }
 
 // Fused forward preprocess: activations, projection, compensation, SH colour,
-// binning rectangle/count and depth key for one Gaussian per lane.
+// binning rectangle/count and depth key for one Gaussian per lane.  SH
+// coefficients come through LDS (sh_mode: split = rest rows staged, DC read
+// directly; packed = whole rows of 3 Ka floats staged; direct = no staging).
 __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities,
     const float* __restrict__ sh0, int64_t s0, const float* __restrict__ shr, int64_t sr, int K,
-    int degree, uint32_t flags, float blur, bool aa, int tiles_x, int tiles_y,
-    float2* __restrict__ means2d, float* __restrict__ depths, float* __restrict__ radii,
-    float* __restrict__ comp, float4* __restrict__ conic_opac, float* __restrict__ colors_out,
-    uint32_t* __restrict__ counts, uint32_t* __restrict__ dkeys, uint2* __restrict__ rects) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    int degree, int sh_mode, int sh_cols, uint32_t flags, float blur, bool aa, int tiles_x,
+    int tiles_y, float2* __restrict__ means2d, float* __restrict__ depths,
+    float* __restrict__ radii, float* __restrict__ comp, float4* __restrict__ conic_opac,
+    float* __restrict__ colors_out, uint32_t* __restrict__ counts, uint32_t* __restrict__ dkeys,
+    uint2* __restrict__ rects) {
+    __shared__ float s_sh[kThreads * kShPad];
+    const int64_t g0 = (int64_t)blockIdx.x * kThreads;
+    const int64_t i = g0 + threadIdx.x;
+    const int pad = sh_cols | 1;
+    if (sh_mode != kShDirect) {
+        const int rows = (int)min<int64_t>(kThreads, n - g0);
+        rows_to_lds(s_sh, pad, sh_mode == kShPacked ? sh0 : shr, sh_mode == kShPacked ? s0 : sr,
+                    g0, rows, sh_cols);
+        __syncthreads();
+    }
     if (i >= n) return;
     const float m0 = means[3 * i], m1 = means[3 * i + 1], m2 = means[3 * i + 2];
     const float4 q = quats[i];
@@ -194,12 +269,21 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
         const int Ka = (degree + 1) * (degree + 1);
         const float* a = sh0 + i * s0;
         const float* b = shr + i * sr;
+        const float* row = s_sh + threadIdx.x * pad;
 #pragma unroll
         for (int ch = 0; ch < 3; ++ch) {
             float c[16];
-            c[0] = a[ch];
+            c[0] = sh_mode == kShPacked ? row[ch] : a[ch];
 #pragma unroll
-            for (int k = 1; k < 16; ++k) c[k] = (k < Ka) ? b[3 * (k - 1) + ch] : 0.0f;
+            for (int k = 1; k < 16; ++k) {
+                float v = 0.0f;
+                if (k < Ka) {
+                    if (sh_mode == kShPacked) v = row[3 * k + ch];
+                    else if (sh_mode == kShSplit) v = row[3 * (k - 1) + ch];
+                    else v = b[3 * (k - 1) + ch];
+                }
+                c[k] = v;
+            }
             colors_out[3 * i + ch] = fmaxf(sh_eval(degree, bk, c, dx, dy, dz), 0.0f);
         }
     }
@@ -210,66 +294,89 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     rects[i] = rect;
 }
 
+// VJP of k_preprocess_fwd, one Gaussian per lane.  SH gradients (zero for
+// coefficients >= Ka) are written through LDS rows in the same sh_mode
+// layouts as the forward reads.
 __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities,
-    const float* __restrict__ colors_out, int K, int degree, uint32_t flags, float blur, bool aa,
-    const float2* __restrict__ g_means2d, const float* __restrict__ g_conics,
-    const float* __restrict__ g_opac_eff, const float* __restrict__ g_colors,
-    const float2* __restrict__ g_means2d_extra, const float* __restrict__ g_depths,
-    const float* __restrict__ g_comp, float* __restrict__ g_means, float4* __restrict__ g_quats,
-    float* __restrict__ g_scales, float* __restrict__ g_opacities, float* __restrict__ g_sh0,
-    int64_t s0, float* __restrict__ g_shr, int64_t sr) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const float m0 = means[3 * i], m1 = means[3 * i + 1], m2 = means[3 * i + 2];
-    const float4 q = quats[i];
-    const float sx = act_scale(scales[3 * i], flags);
-    const float sy = act_scale(scales[3 * i + 1], flags);
-    const float sz = act_scale(scales[3 * i + 2], flags);
-    const float o = act_opacity(opacities[i], flags);
-    Proj p;
-    project(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
-    const float goe = g_opac_eff[i];
-    const float g_o = goe * p.comp;
-    const float g_comp_total = (g_comp ? g_comp[i] : 0.0f) + goe * o;
-    float2 gm2 = g_means2d[i];
-    if (g_means2d_extra) {
-        const float2 e = g_means2d_extra[i];
-        gm2.x += e.x;
-        gm2.y += e.y;
-    }
-    float gm[3], gq[4], gs[3];
-    project_vjp(cam, p, aa, gm2.x, gm2.y, g_conics[3 * i], g_conics[3 * i + 1],
-                g_conics[3 * i + 2], g_depths ? g_depths[i] : 0.0f, g_comp_total, gm, gq, gs);
-    g_means[3 * i] = gm[0];
-    g_means[3 * i + 1] = gm[1];
-    g_means[3 * i + 2] = gm[2];
-    g_quats[i] = make_float4(gq[0], gq[1], gq[2], gq[3]);
-    const bool ls = flags & GSX_LOG_SCALES;
-    g_scales[3 * i] = ls ? gs[0] * sx : gs[0];
-    g_scales[3 * i + 1] = ls ? gs[1] * sy : gs[1];
-    g_scales[3 * i + 2] = ls ? gs[2] * sz : gs[2];
-    g_opacities[i] = (flags & GSX_LOGIT_OPACITY) ? g_o * o * (1.0f - o) : g_o;
-    if (g_sh0) {
-        float dx, dy, dz;
-        view_dir(cam, m0, m1, m2, dx, dy, dz);
-        float bk[16];
-        sh_basis(degree, dx, dy, dz, bk);
-        const int Ka = (degree + 1) * (degree + 1);
-        float gc[3];
-#pragma unroll
-        for (int ch = 0; ch < 3; ++ch)
-            gc[ch] = (colors_out[3 * i + ch] > 0.0f) ? g_colors[3 * i + ch] : 0.0f;
-        float* a = g_sh0 + i * s0;
-#pragma unroll
-        for (int ch = 0; ch < 3; ++ch) a[ch] = bk[0] * gc[ch];
-        float* b = g_shr + i * sr;
-        for (int k = 1; k < K; ++k) {
-            const float bv = (k < Ka) ? bk[k < 16 ? k : 0] : 0.0f;
-#pragma unroll
-            for (int ch = 0; ch < 3; ++ch) b[3 * (k - 1) + ch] = bv * gc[ch];
+    const float* __restrict__ colors_out, int K, int degree, int sh_mode, int sh_cols,
+    uint32_t flags, float blur, bool aa, const float2* __restrict__ g_means2d,
+    const float* __restrict__ g_conics, const float* __restrict__ g_opac_eff,
+    const float* __restrict__ g_colors, const float2* __restrict__ g_means2d_extra,
+    const float* __restrict__ g_depths, const float* __restrict__ g_comp,
+    float* __restrict__ g_means, float4* __restrict__ g_quats, float* __restrict__ g_scales,
+    float* __restrict__ g_opacities, float* __restrict__ g_sh0, int64_t s0,
+    float* __restrict__ g_shr, int64_t sr) {
+    __shared__ float s_sh[kThreads * kShPad];
+    const int64_t g0 = (int64_t)blockIdx.x * kThreads;
+    const int64_t i = g0 + threadIdx.x;
+    const int pad = sh_cols | 1;
+    if (i < n) {
+        const float m0 = means[3 * i], m1 = means[3 * i + 1], m2 = means[3 * i + 2];
+        const float4 q = quats[i];
+        const float sx = act_scale(scales[3 * i], flags);
+        const float sy = act_scale(scales[3 * i + 1], flags);
+        const float sz = act_scale(scales[3 * i + 2], flags);
+        const float o = act_opacity(opacities[i], flags);
+        Proj p;
+        project(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
+        const float goe = g_opac_eff[i];
+        const float g_o = goe * p.comp;
+        const float g_comp_total = (g_comp ? g_comp[i] : 0.0f) + goe * o;
+        float2 gm2 = g_means2d[i];
+        if (g_means2d_extra) {
+            const float2 e = g_means2d_extra[i];
+            gm2.x += e.x;
+            gm2.y += e.y;
         }
+        float gm[3], gq[4], gs[3];
+        project_vjp(cam, p, aa, gm2.x, gm2.y, g_conics[3 * i], g_conics[3 * i + 1],
+                    g_conics[3 * i + 2], g_depths ? g_depths[i] : 0.0f, g_comp_total, gm, gq, gs);
+        g_means[3 * i] = gm[0];
+        g_means[3 * i + 1] = gm[1];
+        g_means[3 * i + 2] = gm[2];
+        g_quats[i] = make_float4(gq[0], gq[1], gq[2], gq[3]);
+        const bool ls = flags & GSX_LOG_SCALES;
+        g_scales[3 * i] = ls ? gs[0] * sx : gs[0];
+        g_scales[3 * i + 1] = ls ? gs[1] * sy : gs[1];
+        g_scales[3 * i + 2] = ls ? gs[2] * sz : gs[2];
+        g_opacities[i] = (flags & GSX_LOGIT_OPACITY) ? g_o * o * (1.0f - o) : g_o;
+        if (g_sh0) {
+            float dx, dy, dz;
+            view_dir(cam, m0, m1, m2, dx, dy, dz);
+            float bk[16];
+            sh_basis(degree, dx, dy, dz, bk);
+            const int Ka = (degree + 1) * (degree + 1);
+            float gc[3];
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch)
+                gc[ch] = (colors_out[3 * i + ch] > 0.0f) ? g_colors[3 * i + ch] : 0.0f;
+            float* row = s_sh + threadIdx.x * pad;
+            if (sh_mode == kShPacked) {
+                for (int k = 0; k < K; ++k) {
+                    const float bv = (k < Ka) ? bk[k < 16 ? k : 0] : 0.0f;
+#pragma unroll
+                    for (int ch = 0; ch < 3; ++ch) row[3 * k + ch] = bv * gc[ch];
+                }
+            } else {
+                float* a = g_sh0 + i * s0;
+#pragma unroll
+                for (int ch = 0; ch < 3; ++ch) a[ch] = bk[0] * gc[ch];
+                float* b = sh_mode == kShSplit ? row : g_shr + i * sr;
+                for (int k = 1; k < K; ++k) {
+                    const float bv = (k < Ka) ? bk[k < 16 ? k : 0] : 0.0f;
+#pragma unroll
+                    for (int ch = 0; ch < 3; ++ch) b[3 * (k - 1) + ch] = bv * gc[ch];
+                }
+            }
+        }
+    }
+    if (sh_mode != kShDirect) {
+        __syncthreads();
+        const int rows = (int)min<int64_t>(kThreads, n - g0);
+        lds_to_rows(s_sh, pad, sh_mode == kShPacked ? g_sh0 : g_shr,
+                    sh_mode == kShPacked ? s0 : sr, g0, rows, sh_cols);
     }
 }
 
@@ -390,10 +497,23 @@ int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means, con
         return GSX_ERR_INVALID;
     const int tiles_x = (cam->width + kTile - 1) / kTile;
     const int tiles_y = (cam->height + kTile - 1) / kTile;
+    int sh_mode = kShDirect, sh_cols = 1;
+    if (sh0) {
+        const int Ka = (degree + 1) * (degree + 1);
+        if (sh_rest == sh0 + 3 && sh0_stride == sh_rest_stride && sh0_stride >= 3 * Ka &&
+            3 * Ka <= kShMaxCols && Ka > 1) {
+            sh_mode = kShPacked;  // one (N, K, 3) tensor: stage rows of 3 Ka floats
+            sh_cols = 3 * Ka;
+        } else if (Ka > 1 && 3 * (Ka - 1) <= kShMaxCols && sh_rest_stride >= 3 * (Ka - 1)) {
+            sh_mode = kShSplit;  // separate DC / rest tensors: stage the rest rows
+            sh_cols = 3 * (Ka - 1);
+        }
+    }
     hipLaunchKernelGGL(k_preprocess_fwd, dim3(grid_for(n)), dim3(kThreads), 0,
                        (hipStream_t)stream, *cam, n, means, (const float4*)quats, scales,
-                       opacities, sh0, sh0_stride, sh_rest, sh_rest_stride, K, degree, flags,
-                       blur, (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, tiles_x, tiles_y,
+                       opacities, sh0, sh0_stride, sh_rest, sh_rest_stride, K, degree, sh_mode,
+                       sh_cols, flags, blur, (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f,
+                       tiles_x, tiles_y,
                        (float2*)means2d, depths, radii, compensation, (float4*)conic_opacity,
                        colors_out, tile_counts, depth_keys, (uint2*)tile_rects);
     GSX_LAUNCH_CHECK();
@@ -423,9 +543,20 @@ int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means, con
     if (!aligned16(quats) || !aligned16(g_quats) || !aligned8(g_means2d) ||
         (g_means2d_extra && !aligned8(g_means2d_extra)))
         return GSX_ERR_INVALID;
+    int sh_mode = kShDirect, sh_cols = 1;
+    if (g_sh0) {
+        if (g_sh_rest == g_sh0 + 3 && sh0_stride == sh_rest_stride && sh0_stride >= 3 * K &&
+            3 * K <= kShMaxCols && K > 1) {
+            sh_mode = kShPacked;
+            sh_cols = 3 * K;
+        } else if (K > 1 && 3 * (K - 1) <= kShMaxCols && sh_rest_stride >= 3 * (K - 1)) {
+            sh_mode = kShSplit;
+            sh_cols = 3 * (K - 1);
+        }
+    }
     hipLaunchKernelGGL(k_preprocess_bwd, dim3(grid_for(n)), dim3(kThreads), 0,
                        (hipStream_t)stream, *cam, n, means, (const float4*)quats, scales,
-                       opacities, colors_out, K, degree, flags, blur,
+                       opacities, colors_out, K, degree, sh_mode, sh_cols, flags, blur,
                        (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, (const float2*)g_means2d,
                        g_conics, g_opac_eff, g_colors, (const float2*)g_means2d_extra, g_depths,
                        g_compensation, g_means, (float4*)g_quats, g_scales, g_opacities, g_sh0,
