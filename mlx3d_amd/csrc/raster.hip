@@ -152,13 +152,13 @@ __device__ __forceinline__ float dpp_f(float v) {
 
 // Sums of NVP per-lane values (NVP a multiple of 4) over the 64 lanes of
 // the wave, spread over the four 16-lane rows: afterwards every lane of row
-// r holds in q[m] the total of value 4m + kRowValue[r].  Step 1 swaps the
+// r holds in q[m] the total of value 4m + row_value(r).  Step 1 swaps the
 // upper half of value 2k with the lower half of value 2k + 1
 // (v_permlane32_swap) and adds, so each half carries one of the two values;
 // step 2 does the same between rows (v_permlane16_swap); step 3 sums each
 // row with four DPP steps.  NVP + NVP/2 + NVP exchanges/adds instead of 6 NVP
 // for a separate 64-lane reduction of every value.  All lanes must be active.
-__device__ constexpr int kRowValue[4] = {0, 2, 1, 3};
+__device__ __forceinline__ int row_value(int row) { return ((row & 1) << 1) | (row >> 1); }
 
 template <int NVP>
 __device__ __forceinline__ void wave_reduce_rows(const float (&v)[NVP], float (&q)[NVP / 4]) {
@@ -510,7 +510,7 @@ __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
     float tot[NVP / 4];
     wave_reduce_rows<NVP>(v, tot);
     if ((lane & 15) == 15) {
-        float* dst = reinterpret_cast<float*>(part[j]) + kRowValue[lane >> 4];
+        float* dst = reinterpret_cast<float*>(part[j]) + row_value(lane >> 4);
 #pragma unroll
         for (int m = 0; m < NVP / 4; ++m) dst[4 * m] = tot[m];
     }
