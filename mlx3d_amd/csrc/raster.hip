@@ -70,22 +70,26 @@ __device__ __forceinline__ float alpha_floor_power(float o) {
 // Which of the tile's four 8x8 quadrants (bit q = quadrant (q&1, q>>1)) the
 // pixels with alpha >= 1/255 of this Gaussian can lie in.  alpha >= 1/255
 // needs q(d) = a dx^2 + 2 b dx dy + c dy^2 <= 2 ln(255 o); a quadrant is
-// kept when the minimum of q over its rectangle of pixel centres (exact, in
-// float64: zero if the mean is inside, else the least of the four clipped
-// edge minimisers) is within that bound.  With b^2 < 0.999 a c the float32
+// kept when the minimum of q over its rectangle of pixel centres (float64:
+// zero if the mean is inside, else the least of the four clipped edge
+// minimisers) is within that bound.  With b^2 < 0.999 a c the float32
 // evaluation of the power is within 7.2e-4 relative of the exact value, so
-// tau is inflated by 1% (+1e-3).  Ill-conditioned, non-positive or
-// non-finite conics get no culling (all four bits).
+// tau is inflated by 1% (+1e-3); the float32 log of the bound and float32
+// reciprocals for the minimisers add errors of ~1e-7, well inside that.
+// Ill-conditioned, non-positive or non-finite conics get no culling (all
+// four bits).
 __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, int px0, int py0) {
     const float o = c.w;
     if (!(o >= 0.0039215f)) return (o == o) ? 0u : 0xFu;  // alpha < 1/255 everywhere
     const double A = c.x, B = c.y, C = c.z;
     const double det = A * C - B * B;
     if (!(A > 0.0 && C > 0.0 && det > 1e-3 * A * C)) return 0xFu;
-    const double t2 = 2.0 * (log(255.0 * (double)o) * 1.01 + 1e-3);
+    // log and the reciprocals in float32: their errors (~1e-7) are far inside
+    // the margin, and an inexact minimiser only over-estimates the minimum
+    const double t2 = 2.0 * ((double)__logf(255.0f * o) * 1.01 + 1e-3);
     const double xd = x, yd = y;
     if (!(t2 < 1e30 && A < 1e30 && C < 1e30 && fabs(xd) < 1e30 && fabs(yd) < 1e30)) return 0xFu;
-    const double ia = 1.0 / A, ic = 1.0 / C;
+    const double ia = (double)__builtin_amdgcn_rcpf(c.x), ic = (double)__builtin_amdgcn_rcpf(c.z);
     uint32_t m = 0;
 #pragma unroll 1
     for (int q = 0; q < 4; ++q) {
@@ -285,20 +289,22 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
     const float next_T = T * (1.0f - alpha);
     const bool stop = pass && next_T < 1e-4f;
     const bool add = pass && !stop;
+    // acc += rgb * (alpha * T) (rasterize.py:84) as one fused multiply-add,
+    // the contraction Metal's default fast-math applies to the reference
     const float w = alpha * T;
     if (PLAIN) {
         const float wa = add ? w : 0.0f;
 #pragma unroll
-        for (int ch = 0; ch < CH; ++ch) acc[ch] = acc[ch] + comp4(fv[ch >> 2], ch & 3) * wa;
-        if (DEPTH) dacc = dacc + r1.w * wa;
+        for (int ch = 0; ch < CH; ++ch) acc[ch] = fmaf(comp4(fv[ch >> 2], ch & 3), wa, acc[ch]);
+        if (DEPTH) dacc = fmaf(r1.w, wa, dacc);
     } else {
 #pragma unroll
         for (int ch = 0; ch < CH; ++ch) {
-            const float a2 = acc[ch] + comp4(fv[ch >> 2], ch & 3) * w;
+            const float a2 = fmaf(comp4(fv[ch >> 2], ch & 3), w, acc[ch]);
             acc[ch] = add ? a2 : acc[ch];
         }
         if (DEPTH) {
-            const float d2 = dacc + r1.w * w;
+            const float d2 = fmaf(r1.w, w, dacc);
             dacc = add ? d2 : dacc;
         }
     }

@@ -682,9 +682,12 @@ static void raster_tile_fwd(int64_t tile, int C, const float* means2d,
                     if (alpha < 1.0f / 255.0f) continue;
                     const float next_T = T * (1.0f - alpha);
                     if (next_T < 1e-4f) break;
+                    /* rasterize.py:84 `acc += rgb * (alpha * T)`, fused as Metal's
+                     * default fast-math contraction compiles it */
                     const float w = alpha * T;
-                    for (int k = 0; k < nc; ++k) acc[k] = acc[k] + feats[(int64_t)g * C + c0 + k] * w;
-                    if (depths) dacc = dacc + depths[g] * w; /* rasterize.py:276-279 */
+                    for (int k = 0; k < nc; ++k)
+                        acc[k] = fmaf(feats[(int64_t)g * C + c0 + k], w, acc[k]);
+                    if (depths) dacc = fmaf(depths[g], w, dacc); /* rasterize.py:276-279 */
                     T = next_T;
                     last = j + 1;
                 }
