@@ -24,6 +24,8 @@
 // per Gaussian adds the four waves' slots and issues one global atomic per
 // (Gaussian, tile, component) -- the reference issues one per (pixel,
 // Gaussian, component).
+#include <algorithm>
+
 #include "gsx_device.h"
 
 using namespace gsx;
@@ -715,9 +717,17 @@ __global__ __launch_bounds__(kThreads) void k_raster_bwd(
     }
 }
 
-__global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ p, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
+// Clears the four gradient outputs in one launch (a fill kernel rather than
+// hipMemsetAsync, so the call can sit inside a captured graph).
+__global__ __launch_bounds__(256) void k_zero_grads(float* __restrict__ a, int64_t na,
+                                                    float* __restrict__ b, int64_t nb,
+                                                    float* __restrict__ c, int64_t nc,
+                                                    float* __restrict__ d, int64_t nd) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < na; i += stride) a[i] = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nb; i += stride) b[i] = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nc; i += stride) c[i] = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nd; i += stride) d[i] = 0.0f;
 }
 
 int pick_ch(int nc) {
@@ -826,15 +836,13 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
         return GSX_ERR_INVALID;
     hipStream_t st = (hipStream_t)stream;
     if (n == 0) return GSX_OK;
-    auto zero = [&](float* p, int64_t cnt) {
-        hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, st, p,
-                           cnt);
-    };
-    zero(g_means2d, 2 * n);
-    zero(g_conics, 3 * n);
-    zero(g_features, (int64_t)C * n);
-    zero(g_opacities, n);
-    GSX_LAUNCH_CHECK();
+    {
+        const int64_t most = std::max<int64_t>((int64_t)C, 3) * n;
+        const unsigned blocks = (unsigned)std::min<int64_t>((most + 255) / 256, 8192);
+        hipLaunchKernelGGL(k_zero_grads, dim3(blocks), dim3(256), 0, st, g_means2d, 2 * n,
+                           g_conics, 3 * n, g_features, (int64_t)C * n, g_opacities, n);
+        GSX_LAUNCH_CHECK();
+    }
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
     const dim3 grid((unsigned)(tiles_x * tiles_y));

@@ -29,6 +29,7 @@ class _Project(torch.autograd.Function):
         ctx.save_for_backward(means, quats, scales)
         ctx.cam, ctx.blur, ctx.antialias = cam, blur, antialias
         ctx.mark_non_differentiable(radii)
+        ctx.set_materialize_grads(False)  # unused outputs: no zero-filled cotangents
         return means2d, conics, depths, radii, comp
 
     @staticmethod

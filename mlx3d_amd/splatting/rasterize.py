@@ -89,6 +89,7 @@ class _Rasterize(torch.autograd.Function):
                               n_contrib)
         ctx.size = (width, height)
         ctx.mark_non_differentiable(n_contrib)
+        ctx.set_materialize_grads(False)  # unused outputs: no zero-filled cotangents
         return out, final_T, n_contrib
 
     @staticmethod

@@ -106,6 +106,7 @@ class _RenderFn(torch.autograd.Function):
         depth = r["depth"] if r["depth"] is not None else r["final_T"].new_empty((0,))
         ctx.mark_non_differentiable(r["radii"], r["n_contrib"], depth, r["sorted_ids"],
                                     r["tile_ranges"])
+        ctx.set_materialize_grads(False)  # unused outputs: no zero-filled cotangents
         return (r["image"], r["final_T"], r["n_contrib"], r["means2d"], r["depths"], r["radii"],
                 r["compensation"], depth, r["sorted_ids"], r["tile_ranges"])
 
