@@ -554,8 +554,13 @@ __device__ __forceinline__ void bwd_walk(BitWalkDown& walk, const float4* s_r0,
     }
 }
 
+// Up to three channels the backward fits in 96 VGPRs, so it asks for five
+// waves per SIMD (more waves to hide LDS and ballot latencies); wider
+// variants keep the default allocation.
+constexpr int bwd_min_waves(int ch) { return ch <= 3 ? 5 : 1; }
+
 template <int CH>
-__global__ __launch_bounds__(kThreads) void k_raster_bwd(
+__global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     const float2* __restrict__ xy, const float4* __restrict__ co, const float* __restrict__ feat,
     int C, int c0, int nc, const int* __restrict__ ids, const int2* __restrict__ ranges,
     int64_t n, int64_t n_ids, const float* __restrict__ bg, int W, int H, int tiles_x,
