@@ -343,8 +343,12 @@ __device__ __forceinline__ void fwd_walk(BitWalkUp& walk, const float4* s_r0, co
     }
 }
 
+// Occupancy targets that the compiler meets without spilling: six waves per
+// SIMD (<= 80 VGPRs) up to four channels, five up to eight.
+constexpr int fwd_min_waves(int ch) { return ch <= 4 ? 6 : (ch <= 8 ? 5 : 1); }
+
 template <int CH, bool DEPTH>
-__global__ __launch_bounds__(kThreads) void k_raster_fwd(
+__global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     const float2* __restrict__ xy, const float4* __restrict__ co, const float* __restrict__ feat,
     int C, int c0, int nc, const float* __restrict__ depths, const int* __restrict__ ids,
     const int2* __restrict__ ranges, int64_t n, int64_t n_ids, const float* __restrict__ bg,
