@@ -173,32 +173,41 @@ int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles);
  * Order within a tile is (depth ascending, Gaussian index ascending) --
  * the order of key = tile*N + rank(depth) with a stable argsort.  Writes
  * sorted_ids (D) int32 and tile_ranges (num_tiles,2) int32 [start,end),
- * (0,0) for empty tiles.  Synchronises `stream` once to read D into
- * *num_dups.  Returns 1 if D > capacity (then only *num_dups is
- * meaningful; retry with capacity >= D).  n and capacity < 2^30;
- * sorted_ids must be 16-byte aligned. */
+ * (0,0) for empty tiles.  With conics != NULL (N rows of conic_stride >= 3
+ * floats, a b c first; means2d (N,2) required) a duplicate is kept only if
+ * the conic quadratic's minimum over the tile rectangle is <= 12
+ * (refine_tiles, tiles.py:91-164).  Synchronises `stream` once to read D
+ * into *num_dups.  Returns 1 if the duplicates exceed capacity (then
+ * *num_dups is the capacity needed; retry with at least that).  n and
+ * capacity < 2^30; sorted_ids must be 16-byte aligned. */
 int gsx_bin_sort(int64_t n, const uint32_t* tile_counts,
                  const uint32_t* depth_keys, const uint32_t* tile_rects,
+                 const float* means2d, const float* conics, int64_t conic_stride,
                  int32_t width, int32_t height, void* workspace,
                  int64_t workspace_bytes, int64_t capacity,
                  int32_t* sorted_ids, int32_t* tile_ranges,
                  int64_t* num_dups, void* stream);
 
-/* The same pipeline without the readback: bin_status (2 device words) gets
- * D and the gsx_bin_error bits.  If D > capacity, sorted_ids/tile_ranges
- * hold an incomplete (but in-bounds: ids < n, ranges within [0, capacity])
- * binning, so kernels enqueued behind it stay safe; the caller copies
- * bin_status to the host when it needs D, checks it with
- * gsx_bin_status_check and re-runs with a larger capacity if asked to. */
+/* The same pipeline without the readback: bin_status (4 device words) gets
+ * the number of duplicates emitted, the gsx_bin_error bits and the number
+ * refine_tiles dropped (they sort after all kept ones).  If the emitted
+ * duplicates exceed capacity, sorted_ids/tile_ranges hold an incomplete
+ * (but in-bounds: ids < n, ranges within [0, capacity]) binning, so kernels
+ * enqueued behind it stay safe; the caller copies bin_status to the host
+ * when it needs D, checks it with gsx_bin_status_check and re-runs with a
+ * larger capacity if asked to. */
 int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts,
                        const uint32_t* depth_keys, const uint32_t* tile_rects,
-                       int32_t width, int32_t height, void* workspace,
-                       int64_t workspace_bytes, int64_t capacity,
-                       int32_t* sorted_ids, int32_t* tile_ranges,
-                       uint32_t* bin_status, void* stream);
+                       const float* means2d, const float* conics,
+                       int64_t conic_stride, int32_t width, int32_t height,
+                       void* workspace, int64_t workspace_bytes,
+                       int64_t capacity, int32_t* sorted_ids,
+                       int32_t* tile_ranges, uint32_t* bin_status,
+                       void* stream);
 
-/* Host-side: interprets a host copy of bin_status.  *num_dups = D; returns
- * GSX_OK, 1 (D > capacity), GSX_ERR_TOO_LARGE or GSX_ERR_DEVICE. */
+/* Host-side: interprets a host copy of the 4 bin_status words.  Returns
+ * GSX_OK with *num_dups = D (duplicates kept), 1 with *num_dups = the
+ * capacity needed, GSX_ERR_TOO_LARGE or GSX_ERR_DEVICE. */
 int gsx_bin_status_check(const uint32_t* host_status, int64_t capacity,
                          int64_t* num_dups);
 

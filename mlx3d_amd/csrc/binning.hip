@@ -393,30 +393,67 @@ __global__ __launch_bounds__(kScanThreads) void k_count_scan(
     }
 }
 
+// refine_tiles (tiles.py:91-146): keep a (tile, Gaussian) duplicate only if
+// the minimum of q(d) = a dx^2 + 2 b dx dy + c dy^2 over the tile's
+// continuous rectangle (clipped to the image) is <= 12 -- the least of the
+// four corners and the four clipped edge minimisers, zero when the mean is
+// inside.  float32 in the reference's evaluation order.
+__device__ __forceinline__ float refine_q(float a, float b, float c, float dx, float dy) {
+    return (a * dx * dx + 2.0f * b * dx * dy) + c * dy * dy;
+}
+
+__device__ __forceinline__ bool refine_keep(uint32_t tx, uint32_t ty, int W, int H, float gx,
+                                            float gy, float a, float b, float c) {
+    const float x0 = (float)(tx * kTile), y0 = (float)(ty * kTile);
+    const float x1 = (float)min((int)(tx + 1) * kTile, W);
+    const float y1 = (float)min((int)(ty + 1) * kTile, H);
+    const float dxl = x0 - gx, dxr = x1 - gx, dyb = y0 - gy, dyt = y1 - gy;
+    if (dxl <= 0.0f && dxr >= 0.0f && dyb <= 0.0f && dyt >= 0.0f) return true;
+    const float dy_l = fminf(fmaxf(-(b / c) * dxl, dyb), dyt);
+    const float dy_r = fminf(fmaxf(-(b / c) * dxr, dyb), dyt);
+    const float dx_b = fminf(fmaxf(-(b / a) * dyb, dxl), dxr);
+    const float dx_t = fminf(fmaxf(-(b / a) * dyt, dxl), dxr);
+    float q = refine_q(a, b, c, dxl, dyb);
+    q = fminf(q, refine_q(a, b, c, dxl, dyt));
+    q = fminf(q, refine_q(a, b, c, dxr, dyb));
+    q = fminf(q, refine_q(a, b, c, dxr, dyt));
+    q = fminf(q, refine_q(a, b, c, dxl, dy_l));
+    q = fminf(q, refine_q(a, b, c, dxr, dy_r));
+    q = fminf(q, refine_q(a, b, c, dx_b, dyb));
+    q = fminf(q, refine_q(a, b, c, dx_t, dyt));
+    return q <= 12.0f;
+}
+
 // Duplicate emission, kEmitDups duplicates per workgroup (of the
 // min(D, cap) that fit the output).  Duplicate d belongs to the
 // depth-ordered Gaussian o with offs[o] <= d < offs[o + 1]; its tile is the
 // (d - offs[o])-th cell of o's tile rectangle in row-major order.  The
 // owners of a workgroup's duplicates form a contiguous range, staged in LDS
 // when it fits (always, unless zero-count Gaussians sit between owners);
-// otherwise each duplicate searches offs directly.  The digit histograms
-// of the emitted tile ids (passes x 256) go into copy
-// blockIdx % kHistCopies of tile_hist.
+// otherwise each duplicate searches offs directly.  With conics given,
+// duplicates refine_tiles rejects get the tile id `sentinel` (= the tile
+// count, so they sort after every tile and the range pass ignores them) and
+// are counted into *dropped.  The digit histograms of the emitted tile ids
+// (passes x 256) go into copy blockIdx % kHistCopies of tile_hist.
 __global__ __launch_bounds__(kEmitThreads) void k_emit(
     int64_t n, int64_t cap, const uint32_t* __restrict__ d_total,
     const uint32_t* __restrict__ offs, const uint32_t* __restrict__ gids,
-    const uint2* __restrict__ rects, int tiles_x, int passes, uint32_t* __restrict__ keys_out,
+    const uint2* __restrict__ rects, int tiles_x, int passes, const float2* __restrict__ xy,
+    const float* __restrict__ con, int64_t cstride, int W, int H, uint32_t sentinel,
+    uint32_t* __restrict__ dropped, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ tile_hist) {
     __shared__ uint32_t s_off[kEmitDups];
     __shared__ uint2 s_rect[kEmitDups];
     __shared__ uint32_t s_gid[kEmitDups];
     __shared__ uint32_t s_h[kMaxPasses][kRadix];
+    __shared__ uint32_t s_drop;
     const int tid = threadIdx.x;
     const int64_t nd = live_count(cap, d_total);
     const int64_t d0 = (int64_t)blockIdx.x * kEmitDups;
     if (d0 >= nd) return;
     const int64_t d1 = min(d0 + kEmitDups, nd);
     for (int k = tid; k < kMaxPasses * kRadix; k += kEmitThreads) (&s_h[0][0])[k] = 0u;
+    if (tid == 0) s_drop = 0u;
     const int64_t lo = block_find_owner<kEmitThreads>(offs, n, (uint32_t)d0);
     const int64_t hi = block_find_owner<kEmitThreads>(offs, n, (uint32_t)(d1 - 1));
     const int64_t w = hi - lo + 1;
@@ -432,6 +469,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(
     __syncthreads();
     const int64_t dd = d0 + (int64_t)tid * kEmitItems;
     uint32_t t[kEmitItems], g[kEmitItems];
+    uint32_t ndrop = 0;
     if (dd < d1) {
         // owner of dd, then walk forward for the following duplicates
         int64_t o;
@@ -473,6 +511,14 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(
             const uint32_t tx = (r.x & 0xFFFFu) + local % rw;
             const uint32_t ty = (r.x >> 16) + local / rw;
             t[j] = ty * (uint32_t)tiles_x + tx;
+            if (con && (int64_t)d < d1) {
+                const float2 m = xy[g[j]];
+                const float* cg = con + (int64_t)g[j] * cstride;
+                if (!refine_keep(tx, ty, W, H, m.x, m.y, cg[0], cg[1], cg[2])) {
+                    t[j] = sentinel;
+                    ++ndrop;
+                }
+            }
         }
         if (dd + kEmitItems <= d1) {
             *reinterpret_cast<uint4*>(keys_out + dd) = make_uint4(t[0], t[1], t[2], t[3]);
@@ -492,12 +538,17 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(
     for (int j = 0; j < kEmitItems; ++j)
         for (int p = 0; p < passes; ++p)
             hist_add(s_h[p], (t[j] >> (p * kRadixBits)) & (kRadix - 1), dd + j < d1);
+    if (con) {
+        const uint32_t wsum = wave_incl_scan(ndrop);
+        if ((tid & 63) == 63 && wsum) atomicAdd(&s_drop, wsum);
+    }
     __syncthreads();
     uint32_t* h = tile_hist + (blockIdx.x % kHistCopies) * kHistStride;
     for (int k = tid; k < passes * kRadix; k += kEmitThreads) {
         const uint32_t v = (&s_h[0][0])[k];
         if (v) atomicAdd(&h[k], v);
     }
+    if (tid == 0 && s_drop) atomicAdd(dropped, s_drop);
 }
 
 // Tile ranges from the sorted tile ids, 4 ids per thread: a tile starts
@@ -537,8 +588,12 @@ inline int bits_for(int64_t count) {
     return b;
 }
 
+inline int passes_for(int64_t max_key) {
+    return (bits_for(std::max<int64_t>(max_key, 1)) + kRadixBits - 1) / kRadixBits;
+}
+
 // misc words: [0..3] depth-pass chunk counters, [4..7] tile-pass counters,
-// [8] emit counter, [12..13] status words of gsx_bin_sort, then the digit
+// [8] emit counter, [12..15] status words of gsx_bin_sort, then the digit
 // histogram copies of the depth sort and of the tile sort.
 constexpr int kMiscCounters = 16;
 constexpr int kSyncStatusWord = 12;
@@ -566,7 +621,8 @@ Layout make_layout(int64_t n, int64_t cap, int64_t num_tiles) {
     L.scan_chunks = ceil_div((int64_t)nn, kScanChunk);
     L.emit_blocks = ceil_div((int64_t)cc, kEmitDups);
     L.hist_blocks = ceil_div((int64_t)nn, kHistThreads * kHistItems);
-    L.tile_passes = (bits_for(std::max<int64_t>(num_tiles, 1)) + kRadixBits - 1) / kRadixBits;
+    // room for the refine_tiles sentinel id (= num_tiles)
+    L.tile_passes = passes_for(num_tiles + 1);
     L.status_words =
         (4 * L.depth_chunks + L.tile_passes * L.tile_chunks) * kRadix + L.scan_chunks;
     L.dk0 = take(4 * nn);
@@ -622,13 +678,17 @@ int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles) 
 }
 
 int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
-                       const uint32_t* tile_rects, int32_t width, int32_t height, void* workspace,
+                       const uint32_t* tile_rects, const float* means2d, const float* conics,
+                       int64_t conic_stride, int32_t width, int32_t height, void* workspace,
                        int64_t workspace_bytes, int64_t capacity, int32_t* sorted_ids,
                        int32_t* tile_ranges, uint32_t* bin_status, void* stream) {
     int rc = check_args(n, width, height, capacity);
     if (rc != GSX_OK) return rc;
     if (!tile_ranges || !bin_status) return GSX_ERR_INVALID;
     if (n > 0 && (!tile_counts || !depth_keys || !tile_rects || !workspace)) return GSX_ERR_INVALID;
+    const bool refine = conics != nullptr;
+    if (refine && (!means2d || ((uintptr_t)means2d & 7u) != 0u || conic_stride < 3))
+        return GSX_ERR_INVALID;
     if (capacity > 0 && (!sorted_ids || ((uintptr_t)sorted_ids & 15u) != 0u))
         return GSX_ERR_INVALID;  // emission stores 4 ids at a time
     hipStream_t st = (hipStream_t)stream;
@@ -642,13 +702,14 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     // ranges, D + error flags, look-back status words, counters and
     // histograms all start at zero
     rc = zero(ZeroRanges{{(uint32_t*)tile_ranges, bin_status, status, misc},
-                         {2 * T, 2, L.status_words, kMiscWords}},
+                         {2 * T, 4, L.status_words, kMiscWords}},
               st);
     if (rc != GSX_OK || n == 0) return rc;
 
     void* ws = workspace;
     uint32_t* d_total = bin_status;
     uint32_t* err = bin_status + 1;
+    uint32_t* dropped = bin_status + 2;
     uint32_t* depth_hist = misc + kMiscCounters;
     uint32_t* tile_hist = depth_hist + kHistCopies * kHistStride;
 
@@ -675,12 +736,12 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     // 2. scan of the counts in depth order; 3. emission (+ tile digit
     //    histograms) into the buffers from which the tile passes end in
     //    sorted_ids; 4. tile sort over the device-side D
-    const int passes = L.tile_passes;
+    const int passes = refine ? L.tile_passes : passes_for(T);
     uint32_t* tk[2] = {at<uint32_t>(ws, L.tk0), at<uint32_t>(ws, L.tk1)};
     uint32_t* tv[2] = {(uint32_t*)sorted_ids, at<uint32_t>(ws, L.tv)};
     int cur = passes & 1;
     uint32_t* tstatus = status + (size_t)4 * L.depth_chunks * kRadix;
-    uint32_t* sstatus = tstatus + (size_t)passes * L.tile_chunks * kRadix;
+    uint32_t* sstatus = tstatus + (size_t)L.tile_passes * L.tile_chunks * kRadix;
     uint32_t* offs = at<uint32_t>(ws, L.offs);
     hipLaunchKernelGGL(k_count_scan, dim3((unsigned)L.scan_chunks), dim3(kScanThreads), 0, st, n,
                        tile_counts, gids, sstatus, misc + 8, offs, d_total, err);
@@ -688,7 +749,9 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     if (capacity == 0) return GSX_OK;
     hipLaunchKernelGGL(k_emit, dim3((unsigned)L.emit_blocks), dim3(kEmitThreads), 0, st, n,
                        capacity, (const uint32_t*)d_total, (const uint32_t*)offs, gids,
-                       (const uint2*)tile_rects, tiles_x, passes, tk[cur], tv[cur], tile_hist);
+                       (const uint2*)tile_rects, tiles_x, passes, (const float2*)means2d,
+                       conics, conic_stride, (int)width, (int)height, (uint32_t)T, dropped,
+                       tk[cur], tv[cur], tile_hist);
     GSX_LAUNCH_CHECK();
     for (int p = 0; p < passes; ++p) {
         hipLaunchKernelGGL((k_onesweep<kTileThreads, kTileItems>), dim3((unsigned)L.tile_chunks),
@@ -708,14 +771,18 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
 
 int gsx_bin_status_check(const uint32_t* host_status, int64_t capacity, int64_t* num_dups) {
     if (!host_status || !num_dups) return GSX_ERR_INVALID;
-    *num_dups = (int64_t)host_status[0];
+    const int64_t emitted = (int64_t)host_status[0];
+    *num_dups = emitted;
     if (host_status[1] & GSX_BIN_ERR_OVERFLOW) return GSX_ERR_TOO_LARGE;
     if (host_status[1] != 0u) return GSX_ERR_DEVICE;
-    return *num_dups > capacity ? 1 : GSX_OK;
+    if (emitted > capacity) return 1;
+    *num_dups = emitted - (int64_t)host_status[2];  // refine_tiles drops sort last
+    return GSX_OK;
 }
 
 int gsx_bin_sort(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
-                 const uint32_t* tile_rects, int32_t width, int32_t height, void* workspace,
+                 const uint32_t* tile_rects, const float* means2d, const float* conics,
+                 int64_t conic_stride, int32_t width, int32_t height, void* workspace,
                  int64_t workspace_bytes, int64_t capacity, int32_t* sorted_ids,
                  int32_t* tile_ranges, int64_t* num_dups, void* stream) {
     if (!num_dups) return GSX_ERR_INVALID;
@@ -737,10 +804,11 @@ int gsx_bin_sort(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_k
     // the status words sit in the workspace's counter block, past the counters
     // the pipeline uses (it clears the whole block before the first kernel)
     uint32_t* bs = at<uint32_t>(workspace, L.misc) + kSyncStatusWord;
-    rc = gsx_bin_sort_async(n, tile_counts, depth_keys, tile_rects, width, height, workspace,
-                            workspace_bytes, capacity, sorted_ids, tile_ranges, bs, stream);
+    rc = gsx_bin_sort_async(n, tile_counts, depth_keys, tile_rects, means2d, conics,
+                            conic_stride, width, height, workspace, workspace_bytes, capacity,
+                            sorted_ids, tile_ranges, bs, stream);
     if (rc != GSX_OK) return rc;
-    uint32_t host[2] = {0u, 0u};
+    uint32_t host[4] = {0u, 0u, 0u, 0u};
     if (hipMemcpyAsync(host, bs, sizeof(host), hipMemcpyDeviceToHost, st) != hipSuccess)
         return GSX_ERR_HIP;
     if (hipStreamSynchronize(st) != hipSuccess) return GSX_ERR_HIP;

@@ -134,7 +134,7 @@ class GaussianModel:
     def render(self, camera: Camera, background=None, antialias: bool = False,
                projection: str = "ewa", return_depth: bool = False) -> dict:
         """Render with the active SH degree (model.py:146-164)."""
-        _check_common(projection, False)
+        _check_common(projection)
         means, quats, scales, opac = self._raw()
         K = self.params["sh_dc"].shape[1] + self.params["sh_rest"].shape[1]
         return _run(camera, means, quats, scales, opac, sh_a=self.params["sh_dc"],
@@ -146,7 +146,7 @@ class GaussianModel:
     def render_depth(self, camera: Camera, antialias: bool = False,
                      projection: str = "ewa") -> dict:
         """Expected depth, forward only (model.py:166-180)."""
-        _check_common(projection, False)
+        _check_common(projection)
         means, quats, scales, opac = self._raw()
         with torch.no_grad():
             zeros = torch.zeros((means.shape[0], 1), dtype=torch.float32, device=means.device)

@@ -38,6 +38,7 @@ class _Cfg:
     K: int
     sh_mode: str | None  # "packed" (N,K,3) tensor, "split" (dc, rest) tensors, None = colours
     return_depth: bool
+    refine: bool = False  # refine_tiles: drop bbox tiles the conic never reaches
 
 
 def _sh_views(cfg: _Cfg, sh_a, sh_b):
@@ -72,7 +73,8 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
             "gsx_preprocess_fwd")
     feats = colors_out if cfg.sh_mode else colors
     with stage("binning"):
-        job = BinJob(counts, dkeys, rects, cfg.width, cfg.height)
+        job = BinJob(counts, dkeys, rects, cfg.width, cfg.height,
+                     refine=(means2d, co) if cfg.refine else None)
 
     def raster(ids):
         with stage("raster_fwd"):
@@ -144,13 +146,11 @@ class _RenderFn(torch.autograd.Function):
         return g_means, g_quats, g_scales, g_opac, g_sh_a, g_sh_b, g_colors, None, None
 
 
-def _check_common(projection: str, refine_tiles: bool):
+def _check_common(projection: str):
     if projection not in ("ewa", "ut"):
         raise ValueError("projection must be 'ewa' or 'ut'.")
     if projection == "ut":
         raise NotImplementedError("projection='ut' is not implemented; use 'ewa'")
-    if refine_tiles:
-        raise NotImplementedError("refine_tiles is not implemented yet")
 
 
 def _background(background, channels, dev):
@@ -166,7 +166,7 @@ def _background(background, channels, dev):
 
 def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=None,
          sh_mode=None, K=0, degree=0, colors=None, background=None, flags=0, antialias=False,
-         blur=0.3, return_depth=False):
+         blur=0.3, return_depth=False, refine_tiles=False):
     n = means.shape[0]
     if means.ndim != 2 or means.shape[1] != 3:
         raise ValueError("means must have shape (N, 3).")
@@ -178,7 +178,7 @@ def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=Non
         flags |= _lib.ANTIALIAS
     cfg = _Cfg(cam=camera.to_gsx(), width=int(camera.width), height=int(camera.height),
                flags=flags, blur=float(blur), degree=int(degree), K=int(K), sh_mode=sh_mode,
-               return_depth=bool(return_depth))
+               return_depth=bool(return_depth), refine=bool(refine_tiles))
     c = _lib.f32c
     (image, final_T, n_contrib, means2d, depths, radii, comp, depth, ids,
      ranges) = _RenderFn.apply(c(means), c(quats), c(scales), c(opacities),
@@ -208,7 +208,7 @@ def render_gaussians(camera: Camera, means, quats, scales, opacities, colors=Non
     """
     if (colors is None) == (sh is None):
         raise ValueError("Provide exactly one of `colors` or `sh`.")
-    _check_common(projection, refine_tiles)
+    _check_common(projection)
     if sh is not None:
         if sh.ndim != 3 or sh.shape[2] != 3 or sh.shape[1] < num_sh_bases(sh_degree):
             raise ValueError(f"sh must have shape (N, K>={num_sh_bases(sh_degree)}, 3).")
@@ -216,23 +216,23 @@ def render_gaussians(camera: Camera, means, quats, scales, opacities, colors=Non
             raise ValueError("sh_degree must be in [0, 3].")
         return _run(camera, means, quats, scales, opacities, sh_a=sh, sh_mode="packed",
                     K=sh.shape[1], degree=sh_degree, background=background, antialias=antialias,
-                    return_depth=return_depth)
+                    return_depth=return_depth, refine_tiles=refine_tiles)
     if colors.ndim != 2 or colors.shape != (means.shape[0], 3):
         raise ValueError("colors must have shape (N, 3).")
     return _run(camera, means, quats, scales, opacities, colors=colors, background=background,
-                antialias=antialias, return_depth=return_depth)
+                antialias=antialias, return_depth=return_depth, refine_tiles=refine_tiles)
 
 
 def render_gaussian_depth(camera: Camera, means, quats, scales, opacities,
                           refine_tiles: bool = False, antialias: bool = False,
                           projection: str = "ewa") -> dict:
     """Expected depth and alpha, forward only (render.py:115-161)."""
-    _check_common(projection, refine_tiles)
+    _check_common(projection)
     with torch.no_grad():
         dev = _lib.require_device(means)
         ones = torch.zeros((means.shape[0], 1), dtype=torch.float32, device=dev)
         out = _run(camera, means, quats, scales, opacities, colors=ones, antialias=antialias,
-                   return_depth=True)
+                   return_depth=True, refine_tiles=refine_tiles)
     return {"depth": out["depth"], "alpha": out["alpha"], "final_T": out["final_T"],
             "means2d": out["means2d"], "depths": out["depths"], "radii": out["radii"],
             "compensation": out["compensation"]}
@@ -254,10 +254,10 @@ def render_gaussian_features(camera: Camera, means, quats, scales, opacities, fe
     channels = int(features.shape[1])
     if channels <= 0:
         raise ValueError("features must contain at least one channel.")
-    _check_common(projection, refine_tiles)
+    _check_common(projection)
     bg = None if normalize else background
     out = _run(camera, means, quats, scales, opacities, colors=features, background=bg,
-               antialias=antialias, return_depth=return_depth)
+               antialias=antialias, return_depth=return_depth, refine_tiles=refine_tiles)
     feat = out.pop("image")
     if normalize:
         a = out["alpha"][..., None]

@@ -65,9 +65,11 @@ class BinJob:
     incomplete result.
     """
 
-    def __init__(self, counts, dkeys, rects, width: int, height: int):
+    def __init__(self, counts, dkeys, rects, width: int, height: int, refine=None):
+        """``refine`` = (means2d (N,2), conics (N,k>=3)) enables refine_tiles."""
         self.dev = counts.device
         self.args = (counts, dkeys, rects)
+        self.refine = refine
         self.n = counts.shape[0]
         self.width, self.height = int(width), int(height)
         self.tiles_x = (self.width + TILE_SIZE - 1) // TILE_SIZE
@@ -76,7 +78,7 @@ class BinJob:
         self.ws = _workspace_for(self.dev, self.stream)
         self.ranges = torch.empty((self.tiles_x * self.tiles_y, 2), dtype=torch.int32,
                                   device=self.dev)
-        self.status = torch.empty((2,), dtype=torch.int32, device=self.dev)
+        self.status = torch.empty((4,), dtype=torch.int32, device=self.dev)
         self.num_dups = None
         self._enqueue(max(1024, int(self.ws.last_dups * 1.25), 4 * self.n))
 
@@ -85,17 +87,20 @@ class BinJob:
         self.cap = int(cap)
         buf = self.ws.get(self.dev, self.n, self.cap, self.tiles_x * self.tiles_y)
         self.ids = torch.empty((self.cap,), dtype=torch.int32, device=self.dev)
+        m2, co = self.refine if self.refine is not None else (None, None)
         _lib.check(_lib.load().gsx_bin_sort_async(
-            self.n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), self.width, self.height,
+            self.n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), _lib.ptr(m2),
+            _lib.ptr(co), 0 if co is None else co.shape[1], self.width, self.height,
             _lib.ptr(buf), buf.numel(), self.cap, _lib.ptr(self.ids), _lib.ptr(self.ranges),
             _lib.ptr(self.status), self.stream), "gsx_bin_sort_async")
-        self.host = torch.empty((2,), dtype=torch.int32, pin_memory=True)
+        self.host = torch.empty((4,), dtype=torch.int32, pin_memory=True)
         self.host.copy_(self.status, non_blocking=True)
         self.ready = torch.cuda.Event()
         self.ready.record()
 
     def finish(self) -> bool:
-        """Read D back; True if the binning is complete, False if retry() is due."""
+        """Read D back; True if the binning is complete (num_dups = duplicates
+        kept), False if retry() is due (num_dups = capacity needed)."""
         self.ready.synchronize()
         host = np.ascontiguousarray(self.host.numpy().view(np.uint32))
         nd = ctypes.c_int64(0)
@@ -115,10 +120,10 @@ class BinJob:
         return self.ids[:self.num_dups], self.ranges
 
 
-def _bin_sort(counts, dkeys, rects, width: int, height: int):
+def _bin_sort(counts, dkeys, rects, width: int, height: int, refine=None):
     """Binning with the capacity guessed from the previous call; one retry
     with room for the exact duplicate count when the guess was short."""
-    job = BinJob(counts, dkeys, rects, width, height)
+    job = BinJob(counts, dkeys, rects, width, height, refine)
     if not job.finish():
         job.retry()
         if not job.finish():
@@ -130,12 +135,12 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, depths: torch.Tens
                   height: int, conics: torch.Tensor | None = None):
     """Assign Gaussians to 16x16 tiles and sort by (tile, depth) (tiles.py:19-182).
 
-    Returns ``(sorted_ids, tile_ranges, tiles_x, tiles_y)``.  Inputs carry no
-    gradient (tiles.py:44-47).
+    With ``conics`` (N, 3) the tiles of each Gaussian's square bbox whose
+    rectangle the conic's 3.46-sigma ellipse (q <= 12) does not reach are
+    dropped (refine_tiles, tiles.py:91-164).  Returns ``(sorted_ids,
+    tile_ranges, tiles_x, tiles_y)``.  Inputs carry no gradient
+    (tiles.py:44-47).
     """
-    if conics is not None:
-        raise NotImplementedError("refine_tiles (conic tile rejection, tiles.py:91-164) is "
-                                  "not implemented yet")
     n = means2d.shape[0]
     if means2d.shape != (n, 2) or radii.shape != (n,) or depths.shape != (n,):
         raise ValueError("means2d must be (N, 2), radii and depths (N,).")
@@ -150,7 +155,13 @@ def bin_gaussians(means2d: torch.Tensor, radii: torch.Tensor, depths: torch.Tens
     _lib.check(L.gsx_bin_prepare(n, _lib.ptr(m), _lib.ptr(r), _lib.ptr(d), width, height,
                                  _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects),
                                  _lib.stream_handle(dev)), "gsx_bin_prepare")
-    ids, ranges = _bin_sort(counts, dkeys, rects, width, height)
+    refine = None
+    if conics is not None:
+        if conics.shape != (n, 3):
+            raise ValueError("conics must be (N, 3).")
+        _lib.require_device(conics)
+        refine = (m, _lib.f32c(conics.detach()))
+    ids, ranges = _bin_sort(counts, dkeys, rects, width, height, refine)
     tiles_x = (width + TILE_SIZE - 1) // TILE_SIZE
     tiles_y = (height + TILE_SIZE - 1) // TILE_SIZE
     return ids, ranges, tiles_x, tiles_y

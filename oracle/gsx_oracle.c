@@ -571,10 +571,44 @@ static int64_t tile_rect(float x, float y, float r, int width, int height,
     return (int64_t)(*w) * (*h);
 }
 
+/* tiles.py:91-146: with conics given, a (tile, Gaussian) duplicate is kept
+ * only if the minimum of q(d) = a dx^2 + 2 b dx dy + c dy^2 over the tile's
+ * continuous rectangle (clipped to the image) is <= 12; the minimum is taken
+ * over the four corners and the four clipped edge minimisers, zero when the
+ * mean is inside.  float32 in the reference's evaluation order. */
+static float refine_q(float a, float b, float c, float dx, float dy) {
+    return (a * dx * dx + 2.0f * b * dx * dy) + c * dy * dy;
+}
+
+static float clipf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
+
+static int refine_keep(int tx, int ty, int width, int height, float gx, float gy,
+                       const float* co) {
+    const float x0 = (float)(tx * TILE), y0 = (float)(ty * TILE);
+    const float x1 = (float)((tx + 1) * TILE < width ? (tx + 1) * TILE : width);
+    const float y1 = (float)((ty + 1) * TILE < height ? (ty + 1) * TILE : height);
+    const float dx_min = x0 - gx, dx_max = x1 - gx, dy_min = y0 - gy, dy_max = y1 - gy;
+    if (dx_min <= 0.0f && dx_max >= 0.0f && dy_min <= 0.0f && dy_max >= 0.0f) return 1;
+    const float a = co[0], b = co[1], c = co[2];
+    const float dy_at_left = clipf(-(b / c) * dx_min, dy_min, dy_max);
+    const float dy_at_right = clipf(-(b / c) * dx_max, dy_min, dy_max);
+    const float dx_at_bottom = clipf(-(b / a) * dy_min, dx_min, dx_max);
+    const float dx_at_top = clipf(-(b / a) * dy_max, dx_min, dx_max);
+    float qmin = refine_q(a, b, c, dx_min, dy_min);
+    qmin = fminf(qmin, refine_q(a, b, c, dx_min, dy_max));
+    qmin = fminf(qmin, refine_q(a, b, c, dx_max, dy_min));
+    qmin = fminf(qmin, refine_q(a, b, c, dx_max, dy_max));
+    qmin = fminf(qmin, refine_q(a, b, c, dx_min, dy_at_left));
+    qmin = fminf(qmin, refine_q(a, b, c, dx_max, dy_at_right));
+    qmin = fminf(qmin, refine_q(a, b, c, dx_at_bottom, dy_min));
+    qmin = fminf(qmin, refine_q(a, b, c, dx_at_top, dy_max));
+    return qmin <= 12.0f;
+}
+
 int64_t orc_bin(int64_t n, const float* means2d, const float* radii,
-                const float* depths, int width, int height,
-                int32_t* sorted_ids, int64_t cap, int32_t* tile_ranges,
-                int nthreads) {
+                const float* depths, const float* conics, int64_t conic_stride,
+                int width, int height, int32_t* sorted_ids, int64_t cap,
+                int32_t* tile_ranges, int nthreads) {
     const int tiles_x = (width + TILE - 1) / TILE;
     const int tiles_y = (height + TILE - 1) / TILE;
     const int64_t T = (int64_t)tiles_x * tiles_y;
@@ -594,9 +628,15 @@ int64_t orc_bin(int64_t n, const float* means2d, const float* radii,
             int x0, y0, w, hh;
             const int64_t c = tile_rect(means2d[2 * i], means2d[2 * i + 1], radii[i], width,
                                         height, tiles_x, tiles_y, &x0, &y0, &w, &hh);
-            D += c;
+            if (!conics) D += c;
             for (int ty = y0; ty < y0 + hh; ++ty)
-                for (int tx = x0; tx < x0 + w; ++tx) h[(int64_t)ty * tiles_x + tx]++;
+                for (int tx = x0; tx < x0 + w; ++tx) {
+                    if (conics && !refine_keep(tx, ty, width, height, means2d[2 * i],
+                                               means2d[2 * i + 1], conics + i * conic_stride))
+                        continue;
+                    if (conics) ++D;
+                    h[(int64_t)ty * tiles_x + tx]++;
+                }
         }
     }
     if (D == 0 || D > cap) {
@@ -627,7 +667,12 @@ int64_t orc_bin(int64_t n, const float* means2d, const float* radii,
                       tiles_y, &x0, &y0, &w, &hh);
             const uint64_t key = ((uint64_t)depth_key(depths[i]) << 32) | (uint32_t)i;
             for (int ty = y0; ty < y0 + hh; ++ty)
-                for (int tx = x0; tx < x0 + w; ++tx) entries[cur[(int64_t)ty * tiles_x + tx]++] = key;
+                for (int tx = x0; tx < x0 + w; ++tx) {
+                    if (conics && !refine_keep(tx, ty, width, height, means2d[2 * i],
+                                               means2d[2 * i + 1], conics + i * conic_stride))
+                        continue;
+                    entries[cur[(int64_t)ty * tiles_x + tx]++] = key;
+                }
         }
     }
     /* Within a tile: depth ascending, ties by Gaussian index -- the order a

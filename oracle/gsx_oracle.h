@@ -11,7 +11,8 @@
  *   orc_project         -- src/mlx3d/splatting/projection.py:24-146
  *   orc_eval_sh         -- src/mlx3d/splatting/sh.py:41-78
  *   orc_preprocess_fwd  -- render.py:73-80 + projection + model.py:116-126
- *   orc_bin             -- src/mlx3d/splatting/tiles.py:19-182 (no refine)
+ *   orc_bin             -- src/mlx3d/splatting/tiles.py:19-182 (refine_tiles
+ *                          when conics are given)
  *   orc_raster_fwd      -- rasterize.py:28-98 (+ depth rasterize.py:223-290)
  *   orc_raster_bwd      -- rasterize.py:100-221, vjp wiring :364-403
  *   orc_project_bwd /
@@ -92,9 +93,9 @@ void orc_preprocess_bwd(const orc_camera* cam, int64_t n, const float* means,
 /* Returns D (number of duplicates).  Writes sorted_ids only if D <= cap.
  * tile_ranges (tiles_x*tiles_y, 2) is always written. */
 int64_t orc_bin(int64_t n, const float* means2d, const float* radii,
-                const float* depths, int width, int height,
-                int32_t* sorted_ids, int64_t cap, int32_t* tile_ranges,
-                int nthreads);
+                const float* depths, const float* conics, int64_t conic_stride,
+                int width, int height, int32_t* sorted_ids, int64_t cap,
+                int32_t* tile_ranges, int nthreads);
 
 /* tiles == NULL renders every tile; else only the listed tile ids (outputs
  * of other tiles are left untouched). */

@@ -79,7 +79,7 @@ def _declare(L):
                                      _P, _P, _P, _P, _P, _P, _P, _I]
     L.orc_preprocess_bwd.argtypes = [_P, _I64, _P, _P, _P, _P, _P, _I, _I, _U32, _F,
                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I]
-    L.orc_bin.argtypes = [_I64, _P, _P, _P, _I, _I, _P, _I64, _P, _I]
+    L.orc_bin.argtypes = [_I64, _P, _P, _P, _P, _I64, _I, _I, _P, _I64, _P, _I]
     L.orc_bin.restype = _I64
     L.orc_raster_fwd.argtypes = [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
                                  _P, _P, _P, _P, _P, _I64, _I]
@@ -217,17 +217,20 @@ def preprocess_bwd(cam, means, quats, scales, opacities, colors_out, K, degree, 
     return dict(means=gm, quats=gq, scales=gs, opacities=go, sh=gsh)
 
 
-def bin_gaussians(means2d, radii, depths, width, height, threads=1):
+def bin_gaussians(means2d, radii, depths, width, height, threads=1, conics=None):
+    """tiles.py:19-182; with ``conics`` (N,3) the refine_tiles pass (:91-164)."""
     means2d, radii, depths = _f32(means2d), _f32(radii), _f32(depths)
     n = means2d.shape[0]
+    co = None if conics is None else _f32(conics)
+    cs = 0 if co is None else co.shape[1]
     tx, ty = (width + 15) // 16, (height + 15) // 16
     ranges = np.empty((tx * ty, 2), np.int32)
-    D = lib().orc_bin(n, _ptr(means2d), _ptr(radii), _ptr(depths), width, height, None, 0,
-                      _ptr(ranges), threads)
+    D = lib().orc_bin(n, _ptr(means2d), _ptr(radii), _ptr(depths), _ptr(co), cs, width, height,
+                      None, 0, _ptr(ranges), threads)
     ids = np.empty((max(D, 0),), np.int32)
     if D > 0:
-        D2 = lib().orc_bin(n, _ptr(means2d), _ptr(radii), _ptr(depths), width, height,
-                           _ptr(ids), D, _ptr(ranges), threads)
+        D2 = lib().orc_bin(n, _ptr(means2d), _ptr(radii), _ptr(depths), _ptr(co), cs, width,
+                           height, _ptr(ids), D, _ptr(ranges), threads)
         assert D2 == D
     return ids, ranges, tx, ty
 

@@ -144,9 +144,36 @@ def tile_rects_np(means2d, radii, width, height):
     return xmin, xmax, ymin, ymax, on, tx_n, ty_n
 
 
-def bin_bruteforce(means2d, radii, depths, width, height):
-    """Enumerate every (tile, Gaussian) pair and sort by (tile, depth, index)
-    with Python's stable sort; ranges (0, 0) for empty tiles."""
+def refine_keep_np(tx, ty, width, height, gx, gy, conic):
+    """tiles.py:91-146 for one (tile, Gaussian), numpy float32 in the
+    reference's operation order: minimum of the conic quadratic over the
+    tile's continuous rectangle (corners + clipped edge minimisers) <= 12."""
+    f = np.float32
+    x0, y0 = f(tx * TILE), f(ty * TILE)
+    x1, y1 = f(min((tx + 1) * TILE, width)), f(min((ty + 1) * TILE, height))
+    gx, gy = f(gx), f(gy)
+    dxl, dxr, dyb, dyt = x0 - gx, x1 - gx, y0 - gy, y1 - gy
+    if dxl <= 0 and dxr >= 0 and dyb <= 0 and dyt >= 0:
+        return True
+    a, b, c = (f(v) for v in conic[:3])
+    two = f(2.0)
+
+    def q(dx, dy):
+        return (a * dx * dx + two * b * dx * dy) + c * dy * dy
+
+    def clip(v, lo, hi):
+        return min(max(v, lo), hi)
+
+    cands = [q(dxl, dyb), q(dxl, dyt), q(dxr, dyb), q(dxr, dyt),
+             q(dxl, clip(-(b / c) * dxl, dyb, dyt)), q(dxr, clip(-(b / c) * dxr, dyb, dyt)),
+             q(clip(-(b / a) * dyb, dxl, dxr), dyb), q(clip(-(b / a) * dyt, dxl, dxr), dyt)]
+    return bool(min(cands) <= f(12.0))
+
+
+def bin_bruteforce(means2d, radii, depths, width, height, conics=None):
+    """Enumerate every (tile, Gaussian) pair (dropping those refine_tiles
+    rejects when conics are given) and sort by (tile, depth, index) with
+    Python's stable sort; ranges (0, 0) for empty tiles."""
     xmin, xmax, ymin, ymax, on, tx_n, ty_n = tile_rects_np(means2d, radii, width, height)
     pairs = []
     for g in range(means2d.shape[0]):
@@ -154,6 +181,9 @@ def bin_bruteforce(means2d, radii, depths, width, height):
             continue
         for ty in range(ymin[g], ymax[g] + 1):
             for tx in range(xmin[g], xmax[g] + 1):
+                if conics is not None and not refine_keep_np(
+                        tx, ty, width, height, means2d[g, 0], means2d[g, 1], conics[g]):
+                    continue
                 pairs.append((ty * tx_n + tx, float(depths[g]), g))
     pairs.sort(key=lambda p: (p[0], p[1], p[2]))
     ids = np.array([p[2] for p in pairs], dtype=np.int32)

@@ -61,8 +61,9 @@ def test_invalid_arguments_rejected_before_launch():
 
 
 def test_bin_status_check_is_host_only():
-    """gsx_bin_status_check interprets the two status words of
-    gsx_bin_sort_async: D, then error bits (1 = wait bound, 2 = overflow)."""
+    """gsx_bin_status_check interprets the four status words of
+    gsx_bin_sort_async: duplicates emitted, error bits (1 = wait bound,
+    2 = overflow), duplicates dropped by refine_tiles."""
     L = _lib.load()
 
     def chk(words, cap):
@@ -71,16 +72,17 @@ def test_bin_status_check_is_host_only():
         rc = L.gsx_bin_status_check(h.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(nd))
         return rc, nd.value
 
-    assert chk([123, 0], 123) == (0, 123)
-    assert chk([124, 0], 123) == (1, 124)
-    assert chk([5, 2], 100)[0] == -4
-    assert chk([5, 1], 100)[0] == -5
+    assert chk([123, 0, 0, 0], 123) == (0, 123)
+    assert chk([123, 0, 20, 0], 123) == (0, 103)   # kept = emitted - dropped
+    assert chk([124, 0, 0, 0], 123) == (1, 124)    # capacity needed
+    assert chk([5, 2, 0, 0], 100)[0] == -4
+    assert chk([5, 1, 0, 0], 100)[0] == -5
     assert L.gsx_strerror(-5).decode().startswith("device-side check")
     # binning entry points reject bad sizes before any launch
     nd = ctypes.c_int64(0)
-    assert L.gsx_bin_sort(-1, None, None, None, 64, 64, None, 0, 0, None, None,
+    assert L.gsx_bin_sort(-1, None, None, None, None, None, 0, 64, 64, None, 0, 0, None, None,
                           ctypes.byref(nd), None) == -1
-    assert L.gsx_bin_sort(10, None, None, None, 64, 64, None, 0, 1 << 30, None, None,
-                          ctypes.byref(nd), None) == -4
-    assert L.gsx_bin_sort_async(10, None, None, None, 64, 64, None, 0, 100, None, None, None,
-                                None) == -1
+    assert L.gsx_bin_sort(10, None, None, None, None, None, 0, 64, 64, None, 0, 1 << 30, None,
+                          None, ctypes.byref(nd), None) == -4
+    assert L.gsx_bin_sort_async(10, None, None, None, None, None, 0, 64, 64, None, 0, 100, None,
+                                None, None, None) == -1

@@ -155,14 +155,61 @@ def test_bin_sort_sync_abi_and_capacity():
                          device=dev)
         ids = torch.full((max(cap, 1),), -1, dtype=torch.int32, device=dev)
         nd = ctypes.c_int64(0)
-        rc = L.gsx_bin_sort(n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), 640, 360,
-                            _lib.ptr(ws), ws.numel(), cap, _lib.ptr(ids), _lib.ptr(ranges),
-                            ctypes.byref(nd), st)
+        rc = L.gsx_bin_sort(n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), None, None, 0,
+                            640, 360, _lib.ptr(ws), ws.numel(), cap, _lib.ptr(ids),
+                            _lib.ptr(ranges), ctypes.byref(nd), st)
         say(f"  capacity {cap}: rc={rc} D={nd.value}")
         assert rc == want and nd.value == D
         if rc == 0:
             np.testing.assert_array_equal(host(ids[:D]), rids)
             np.testing.assert_array_equal(host(ranges), rranges)
+
+
+def _elongated(seed, n=3000, width=640, height=360):
+    rng = np.random.default_rng(seed)
+    means2d = rng.uniform(-20, [width + 20, height + 20], (n, 2)).astype(np.float32)
+    sig_major = rng.uniform(3.0, 40.0, n)
+    sig_minor = rng.uniform(0.4, 2.0, n)
+    th = rng.uniform(0, np.pi, n)
+    c, s = np.cos(th), np.sin(th)
+    cov = np.stack([c * c * sig_major**2 + s * s * sig_minor**2,
+                    c * s * (sig_major**2 - sig_minor**2),
+                    s * s * sig_major**2 + c * c * sig_minor**2], 1)
+    det = cov[:, 0] * cov[:, 2] - cov[:, 1] ** 2
+    conics = np.stack([cov[:, 2] / det, -cov[:, 1] / det, cov[:, 0] / det], 1).astype(np.float32)
+    radii = np.ceil(3.0 * sig_major).astype(np.float32)
+    depths = rng.choice(np.linspace(1, 5, 40), n).astype(np.float32)  # some depth ties
+    return means2d, radii, depths, conics
+
+
+def test_binning_refine_tiles_bitexact():
+    for seed in range(2):
+        m, r, d, co = _elongated(seed)
+        ids, ranges, tx, ty = bin_gaussians(cu(m), cu(r), cu(d), 640, 360, conics=cu(co))
+        rids, rranges, _, _ = O.bin_gaussians(m, r, d, 640, 360, threads=8, conics=co)
+        full, _, _, _ = O.bin_gaussians(m, r, d, 640, 360, threads=8)
+        say(f"refine seed {seed}: D={rids.shape[0]} of {full.shape[0]}")
+        np.testing.assert_array_equal(host(ranges), rranges)
+        np.testing.assert_array_equal(host(ids), rids)
+
+
+def test_render_refine_tiles_same_image_fewer_pairs():
+    cam, means, quats, scales, opac, colors = random_scene(6, n=4000, width=320, height=240)
+    scales[:, 0] *= 8.0  # elongated splats: square boxes cover many unreachable tiles
+    t = [cu(a) for a in (means, quats, scales, opac, colors)]
+    a = render_gaussians(cam, *t[:4], colors=t[4], antialias=True)
+    b = render_gaussians(cam, *t[:4], colors=t[4], antialias=True, refine_tiles=True)
+    assert_bits(host(a["image"]), host(b["image"]), "image")
+    assert_bits(host(a["final_T"]), host(b["final_T"]), "final_T")
+    assert b["sorted_ids"].shape[0] < a["sorted_ids"].shape[0]
+    p = O.project(oracle_camera(cam), means, quats, scales, antialias=True)
+    oe = (opac * p["compensation"]).astype(np.float32)
+    ids, ranges, _, _ = O.bin_gaussians(p["means2d"], p["radii"], p["depths"], 320, 240,
+                                        conics=p["conics"])
+    r = O.raster_fwd(p["means2d"], p["conics"], oe, colors, ids, ranges, 320, 240)
+    say(f"refine render: D {a['sorted_ids'].shape[0]} -> {b['sorted_ids'].shape[0]}")
+    np.testing.assert_array_equal(host(b["sorted_ids"]), ids)
+    np.testing.assert_array_equal(host(b["n_contrib"]), r["n_contrib"])
 
 
 def test_rasterize_building_block_bitexact():
