@@ -432,11 +432,22 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
 }
 
 // Per-pixel state of the back-to-front replay.
+//
+// The reference (rasterize.py:170-195) carries per channel the recursively
+// blended colour behind the current Gaussian, accum_c = S_c / T_after with
+// S_c = sum over later contributors k of c_k alpha_k T_k, and forms
+//   dL/dalpha_i = T_i sum_c g_c (c_i - accum_c) - T_final (bg . g) / (1 - alpha_i).
+// Since T_i / T_after = 1 / (1 - alpha_i), the channel sum of g_c accum_c
+// collapses into one scalar,
+//   Q = T_final (bg . g) + sum over later contributors k of alpha_k T_k (c_k . g),
+//   dL/dalpha_i = T_i (c_i . g) - Q / (1 - alpha_i),
+// so a pixel holds its cotangent g (CH floats) and Q instead of 3 CH floats.
 template <int CH>
 struct BwdPixel {
-    float T, T_final, last_alpha, bg_dot;
+    float T;  // transmittance in front of the current Gaussian
+    float Q;
     int last;
-    float gpix[CH], accum[CH], lastc[CH];
+    float gpix[CH];
 };
 
 // One (pixel, Gaussian) step of the back-to-front replay
@@ -475,33 +486,15 @@ __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
     for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
     const float rcp = __builtin_amdgcn_rcpf(1.0f - alpha);
     px.T = ok ? px.T * rcp : px.T;
-    float dl = 0.0f;
-    if (PLAIN) {
-        const float la = ok ? px.last_alpha : 0.0f;  // la = 0: accum unchanged
-        const float la1 = 1.0f - la;
+    float cg = 0.0f;  // c_i . g
 #pragma unroll
-        for (int ch = 0; ch < CH; ++ch) {
-            const float f = comp4(fv[ch >> 2], ch & 3);
-            const float an = fmaf(la, px.lastc[ch], la1 * px.accum[ch]);
-            px.accum[ch] = an;
-            px.lastc[ch] = ok ? f : px.lastc[ch];
-            dl = fmaf(f - an, px.gpix[ch], dl);
-        }
-    } else {
-        const float la1 = 1.0f - px.last_alpha;
-#pragma unroll
-        for (int ch = 0; ch < CH; ++ch) {
-            const float f = comp4(fv[ch >> 2], ch & 3);
-            const float an = fmaf(px.last_alpha, px.lastc[ch], la1 * px.accum[ch]);
-            px.accum[ch] = ok ? an : px.accum[ch];
-            px.lastc[ch] = ok ? f : px.lastc[ch];
-            dl = fmaf(f - px.accum[ch], px.gpix[ch], dl);
-        }
-    }
-    px.last_alpha = ok ? alpha : px.last_alpha;
-    float dL_dalpha = fmaf(dl, px.T, (-px.T_final * rcp) * px.bg_dot);
+    for (int ch = 0; ch < CH; ++ch) cg = fmaf(comp4(fv[ch >> 2], ch & 3), px.gpix[ch], cg);
+    float dL_dalpha = fmaf(cg, px.T, -(px.Q * rcp));
     dL_dalpha = ok ? dL_dalpha : 0.0f;
     const float aT = ok ? alpha * px.T : 0.0f;
+    // PLAIN: cg is finite, so aT = 0 leaves Q unchanged without a select.
+    const float qn = fmaf(aT, cg, px.Q);
+    px.Q = (PLAIN || ok) ? qn : px.Q;
     const float gd = G * (r0.w * dL_dalpha);  // G dL/dG
     float v[NVP];
     const float u = gd * dx, w = gd * dy;
@@ -558,10 +551,12 @@ __device__ __forceinline__ void bwd_walk(BitWalkDown& walk, const float4* s_r0,
     }
 }
 
-// Up to three channels the backward fits in 96 VGPRs, so it asks for five
-// waves per SIMD (more waves to hide LDS and ballot latencies); wider
-// variants keep the default allocation.
-constexpr int bwd_min_waves(int ch) { return ch <= 3 ? 5 : 1; }
+// Waves per SIMD the backward asks for (more waves hide LDS and ballot
+// latencies): five up to eight channels (96 VGPRs; the 31.6 KB of LDS of
+// the 128-Gaussian batches also caps the one- to four-channel variants at
+// five blocks per CU), four at 16 channels (112), three at 32 (145), all
+// without spills.
+constexpr int bwd_min_waves(int ch) { return ch <= 8 ? 5 : (ch <= 16 ? 4 : 3); }
 
 template <int CH>
 __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
@@ -601,19 +596,18 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     tile_span(ranges[tile], n_ids, start, num);
 
     BwdPixel<CH> st;
-    st.T_final = inside ? final_T[pid] : 1.0f;
-    st.T = st.T_final;
+    const float T_final = inside ? final_T[pid] : 1.0f;
+    st.T = T_final;
     st.last = inside ? n_contrib[pid] : 0;
-    st.bg_dot = 0.0f;
-    st.last_alpha = 0.0f;
+    float bg_dot = 0.0f;
 #pragma unroll
     for (int ch = 0; ch < CH; ++ch) {
         st.gpix[ch] = (inside && ch < nc) ? grad_out[pid * C + c0 + ch] : 0.0f;
-        if (ch < nc) st.bg_dot = st.bg_dot + (bg ? bg[c0 + ch] : 0.0f) * st.gpix[ch];
-        st.accum[ch] = st.lastc[ch] = 0.0f;
+        if (ch < nc) bg_dot = bg_dot + (bg ? bg[c0 + ch] : 0.0f) * st.gpix[ch];
     }
     // The alpha output's cotangent enters once, with the first channel block.
-    if (inside && c0 == 0 && grad_T) st.bg_dot = st.bg_dot + grad_T[pid];
+    if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + grad_T[pid];
+    st.Q = T_final * bg_dot;
 
     // Largest n_contrib of each quadrant: later list entries changed no pixel.
     {
