@@ -249,6 +249,65 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
                    float* g_means2d, float* g_conics, float* g_features,
                    float* g_opacities, void* stream);
 
+/* -------------------------------------------------------- training step --
+ * The calls GaussianTrainer.step (splatting/trainer.py:319-421) makes
+ * around the render. */
+
+/* Workspace for one image of the photometric loss: three (H,W,C) float
+ * maps of SSIM partial derivatives plus per-tile partial sums. */
+int64_t gsx_photometric_workspace_bytes(int32_t height, int32_t width,
+                                        int32_t channels);
+
+/* Replaces l1 = mean|pred - target| and ssim(pred, target, max_val,
+ * window_size, sigma) (trainer.py:303-305; losses/image_metrics.py:23-55,
+ * 66-85: Gaussian window, zero-padded depthwise correlation, c1 =
+ * (0.01 max_val)^2, c2 = (0.03 max_val)^2, mean over H*W*C).  pred and
+ * target (H,W,C); window_size odd, at most 15.  out (2 floats, device):
+ * [mean |pred - target|, mean SSIM].  The workspace keeps what
+ * gsx_photometric_bwd needs; it must not change in between. */
+int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels,
+                        const float* pred, const float* target,
+                        int32_t window_size, float sigma, float max_val,
+                        void* workspace, int64_t workspace_bytes, float* out,
+                        void* stream);
+
+/* Gradient of both outputs of gsx_photometric_fwd with respect to pred:
+ * grad_pred = grad_out[0] d(mean L1)/dpred + grad_out[1] d(mean SSIM)/dpred,
+ * with grad_out (2 floats) on the device (what MLX autodiff of
+ * image_metrics.py:29-55 computes).  sign(0) = 0 for the L1 term. */
+int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels,
+                        const float* pred, const float* target,
+                        int32_t window_size, float sigma,
+                        const void* workspace, int64_t workspace_bytes,
+                        const float* grad_out, float* grad_pred, void* stream);
+
+#define GSX_ADAM_MAX_GROUPS 8
+
+/* One parameter group of gsx_adam_step: n floats each (host struct). */
+typedef struct gsx_adam_group {
+    float* param;
+    const float* grad;
+    float* m;
+    float* v;
+    int64_t n;
+    float lr;
+} gsx_adam_group;
+
+/* Replaces the per-group mlx.optimizers.Adam(learning_rate=lr, eps=eps)
+ * updates of trainer.py:128, 339-342 (mlx >= 0.31, bias_correction off):
+ * m = b1 m + (1-b1) g; v = b2 v + (1-b2) g^2; p -= lr m / (sqrt(v) + eps),
+ * float32, in place, all groups in one launch.  m and v start at zero. */
+int gsx_adam_step(int32_t num_groups, const gsx_adam_group* groups,
+                  float beta1, float beta2, float eps, void* stream);
+
+/* Replaces the density-control statistics of trainer.py:357-365:
+ * grad_accum += |(g.x W/2, g.y H/2)| * (radii > 0); grad_count += (radii > 0).
+ * g_means2d (N,2) is dL/dmeans2d of the rasterizer (the reference's
+ * means2d probe gradient, trainer.py:264-275, 337). */
+int gsx_accum_screen_grads(int64_t n, const float* g_means2d,
+                           const float* radii, int32_t width, int32_t height,
+                           float* grad_accum, float* grad_count, void* stream);
+
 /* ---------------------------------------------------------- diagnostics --
  * Evaluates the device exp used by the rasterizer (the stand-in for
  * metal::exp at rasterize.py:80,171,274) on n inputs; tests check it

@@ -45,6 +45,22 @@ class GsxCamera(ctypes.Structure):
     ]
 
 
+ADAM_MAX_GROUPS = 8  # GSX_ADAM_MAX_GROUPS
+
+
+class GsxAdamGroup(ctypes.Structure):
+    """gsx_adam_group of include/gsx.h."""
+
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("m", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+        ("lr", ctypes.c_float),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -80,6 +96,13 @@ SIGNATURES = {
                                       _P, _P, _P, _P, _P]),
     "gsx_raster_bwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32, _P,
                                       _P, _P, _P, _P, _P, _P, _P, _P]),
+    "gsx_photometric_workspace_bytes": (_I64, [_I32, _I32, _I32]),
+    "gsx_photometric_fwd": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, _F, _F, _P, _I64, _P,
+                                           _P]),
+    "gsx_photometric_bwd": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, _F, _P, _I64, _P, _P,
+                                           _P]),
+    "gsx_adam_step": (ctypes.c_int, [_I32, ctypes.c_void_p, _F, _F, _F, _P]),
+    "gsx_accum_screen_grads": (ctypes.c_int, [_I64, _P, _P, _I32, _I32, _P, _P, _P]),
     "gsx_debug_expf": (ctypes.c_int, [_I64, _P, _P, _P]),
 }
 

@@ -129,6 +129,22 @@ class Camera:
             c[j] = -s
         return torch.from_numpy(c)
 
+    def world_to_camera(self, points: torch.Tensor) -> torch.Tensor:
+        """X_cam = X R^T + t for (..., 3) points (cameras.py:282-284)."""
+        R = self.R.to(points.device)
+        return points @ R.T + self.t.to(points.device)
+
+    def camera_to_world(self, points: torch.Tensor) -> torch.Tensor:
+        """(X_cam - t) R (cameras.py:286-288)."""
+        return (points - self.t.to(points.device)) @ self.R.to(points.device)
+
+    def unproject_points(self, xy: torch.Tensor, depth: torch.Tensor) -> torch.Tensor:
+        """Pixel coordinates (..., 2) with z-depths (...,) to world points
+        (cameras.py:327-336, pinhole)."""
+        x = (xy[..., 0] - self.cx) / self.fx
+        y = (xy[..., 1] - self.cy) / self.fy
+        return self.camera_to_world(torch.stack([x * depth, y * depth, depth], dim=-1))
+
     def gsx_fields(self) -> dict:
         """The float32 values the rasterizer's arithmetic sees.
 

@@ -1,0 +1,498 @@
+// train.hip -- the training step around the rasterizer on gfx950:
+//
+//   * photometric loss: mean |pred - target| and mean SSIM in one pass over
+//     the image (trainer.py:302-305; losses/image_metrics.py:23-55, 66-85),
+//     with the analytic gradient of both in a second pass;
+//   * Adam over several parameter groups in one launch (trainer.py:101-128,
+//     339-342; mlx.optimizers.Adam, mlx >= 0.31);
+//   * the screen-space gradient statistics of adaptive density control
+//     (trainer.py:357-366).
+//
+// All of it is HBM-bound elementwise or stencil work: no MFMA, coalesced
+// loads, LDS tiles for the 2D window.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "gsx.h"
+#include "gsx_device.h"
+
+namespace {
+
+using gsx::kWave;
+
+// ------------------------------------------------------------------- SSIM --
+//
+// mu_p = F(p), mu_t = F(t), E_pp = F(p p), E_tt = F(t t), E_pt = F(p t), with
+// F the zero-padded 'same' correlation with the separable Gaussian window
+// g g^T (image_metrics.py:23-45; mx.conv2d with padding = window // 2 pads
+// with zeros).  Per pixel and channel
+//   A = 2 mu_p mu_t + c1, B = mu_p^2 + mu_t^2 + c1,
+//   Cn = 2 (E_pt - mu_p mu_t) + c2, D = (E_pp - mu_p^2) + (E_tt - mu_t^2) + c2,
+//   S = (A / B) (Cn / D)                                 (image_metrics.py:47-54)
+// and the loss uses mean(S) over every pixel and channel.  The forward keeps
+// the partial derivatives of S with respect to (mu_p, E_pp, E_pt):
+//   dS/dE_pt = 2 l / D,   dS/dE_pp = -l cs / D,
+//   dS/dmu_p = 2 (mu_t - l mu_p) cs / B + 2 l (mu_p cs - mu_t) / D,
+// (l = A / B, cs = Cn / D), and the backward applies F^T, which equals F for
+// a symmetric window with zero padding:
+//   dS_mean/dp = (F(dS/dmu_p) + 2 p F(dS/dE_pp) + t F(dS/dE_pt)) / n.
+
+constexpr int kSsT = 16;                  // output tile edge (16 x 16 threads)
+constexpr int kSsMaxR = 7;                // window radius up to 7 (15 taps)
+
+struct SsimWindow {
+    float g[2 * kSsMaxR + 1];
+};
+
+template <int R>
+struct SsimTile {
+    static constexpr int kSpan = kSsT + 2 * R;
+};
+
+// Loads the (16 + 2R)^2 window of channel c of `src` around the tile into
+// `dst`, zero outside the image.
+template <int R>
+__device__ __forceinline__ void load_halo(float (*dst)[kSsT + 2 * R + 1], const float* __restrict__ src,
+                                          int H, int W, int C, int c, int x0, int y0) {
+    constexpr int S = SsimTile<R>::kSpan;
+    for (int i = threadIdx.x; i < S * S; i += kSsT * kSsT) {
+        const int ly = i / S, lx = i - ly * S;
+        const int gy = y0 - R + ly, gx = x0 - R + lx;
+        float v = 0.0f;
+        if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = src[((int64_t)gy * W + gx) * C + c];
+        dst[ly][lx] = v;
+    }
+}
+
+template <int R>
+__global__ __launch_bounds__(kSsT * kSsT) void k_ssim_fwd(
+    const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C,
+    SsimWindow win, float c1, float c2, float* __restrict__ maps, float* __restrict__ partials) {
+    constexpr int S = SsimTile<R>::kSpan;
+    constexpr int K = 2 * R + 1;
+    __shared__ float s_p[S][S + 1];
+    __shared__ float s_t[S][S + 1];
+    __shared__ float s_h[5][S][kSsT + 1];
+    __shared__ float s_red[2][kSsT * kSsT / kWave];
+
+    const int tid = threadIdx.x;
+    const int tx = tid & (kSsT - 1), ty = tid / kSsT;
+    const int x0 = blockIdx.x * kSsT, y0 = blockIdx.y * kSsT;
+    const int x = x0 + tx, y = y0 + ty;
+    const bool inside = x < W && y < H;
+    const int64_t plane = (int64_t)H * W * C;
+    const int64_t pix = ((int64_t)y * W + x) * C;
+    float l1 = 0.0f, ssum = 0.0f;
+
+    for (int c = 0; c < C; ++c) {
+        load_halo<R>(s_p, pred, H, W, C, c, x0, y0);
+        load_halo<R>(s_t, tgt, H, W, C, c, x0, y0);
+        __syncthreads();
+        for (int i = tid; i < S * kSsT; i += kSsT * kSsT) {
+            const int ly = i / kSsT, lx = i - ly * kSsT;
+            float a = 0.0f, b = 0.0f, pp = 0.0f, tt = 0.0f, pt = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const float w = win.g[k], p = s_p[ly][lx + k], t = s_t[ly][lx + k];
+                a = fmaf(w, p, a);
+                b = fmaf(w, t, b);
+                pp = fmaf(w, p * p, pp);
+                tt = fmaf(w, t * t, tt);
+                pt = fmaf(w, p * t, pt);
+            }
+            s_h[0][ly][lx] = a;
+            s_h[1][ly][lx] = b;
+            s_h[2][ly][lx] = pp;
+            s_h[3][ly][lx] = tt;
+            s_h[4][ly][lx] = pt;
+        }
+        __syncthreads();
+        float mp = 0.0f, mt = 0.0f, epp = 0.0f, ett = 0.0f, ept = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const float w = win.g[k];
+            mp = fmaf(w, s_h[0][ty + k][tx], mp);
+            mt = fmaf(w, s_h[1][ty + k][tx], mt);
+            epp = fmaf(w, s_h[2][ty + k][tx], epp);
+            ett = fmaf(w, s_h[3][ty + k][tx], ett);
+            ept = fmaf(w, s_h[4][ty + k][tx], ept);
+        }
+        if (inside) {
+            const float p = s_p[ty + R][tx + R], t = s_t[ty + R][tx + R];
+            const float mpp = mp * mp, mtt = mt * mt, mpt = mp * mt;
+            const float A = 2.0f * mpt + c1, B = mpp + mtt + c1;
+            const float Cn = 2.0f * (ept - mpt) + c2, D = (epp - mpp) + (ett - mtt) + c2;
+            const float cs = Cn / D, l = A / B;
+            ssum += l * cs;
+            l1 += fabsf(p - t);
+            maps[pix + c] = 2.0f * (mt - l * mp) * cs / B + 2.0f * l * (mp * cs - mt) / D;
+            maps[plane + pix + c] = -l * cs / D;
+            maps[2 * plane + pix + c] = 2.0f * l / D;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        l1 += __shfl_xor(l1, o, kWave);
+        ssum += __shfl_xor(ssum, o, kWave);
+    }
+    if ((tid & (kWave - 1)) == 0) {
+        s_red[0][tid / kWave] = l1;
+        s_red[1][tid / kWave] = ssum;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kSsT * kSsT / kWave; ++w) {
+            a += s_red[0][w];
+            b += s_red[1][w];
+        }
+        const int64_t blk = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+        partials[2 * blk] = a;
+        partials[2 * blk + 1] = b;
+    }
+}
+
+// Sums the per-tile partials in a fixed order (double accumulators) and
+// writes [mean |pred - target|, mean SSIM].
+__global__ __launch_bounds__(256) void k_loss_reduce(const float* __restrict__ partials,
+                                                     int64_t nblk, double inv_n,
+                                                     float* __restrict__ out) {
+    __shared__ double s[2][256];
+    double a = 0.0, b = 0.0;
+    for (int64_t i = threadIdx.x; i < nblk; i += 256) {
+        a += (double)partials[2 * i];
+        b += (double)partials[2 * i + 1];
+    }
+    s[0][threadIdx.x] = a;
+    s[1][threadIdx.x] = b;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) {
+            s[0][threadIdx.x] += s[0][threadIdx.x + w];
+            s[1][threadIdx.x] += s[1][threadIdx.x + w];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        out[0] = (float)(s[0][0] * inv_n);
+        out[1] = (float)(s[1][0] * inv_n);
+    }
+}
+
+// grad_pred = g_l1 sign(p - t) / n + g_ssim (F(dmu) + 2 p F(dpp) + t F(dpt)) / n
+template <int R>
+__global__ __launch_bounds__(kSsT * kSsT) void k_ssim_bwd(
+    const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C,
+    SsimWindow win, const float* __restrict__ maps, const float* __restrict__ grad_in,
+    float inv_n, float* __restrict__ grad) {
+    constexpr int S = SsimTile<R>::kSpan;
+    constexpr int K = 2 * R + 1;
+    __shared__ float s_m[3][S][S + 1];
+    __shared__ float s_h[3][S][kSsT + 1];
+
+    const int tid = threadIdx.x;
+    const int tx = tid & (kSsT - 1), ty = tid / kSsT;
+    const int x0 = blockIdx.x * kSsT, y0 = blockIdx.y * kSsT;
+    const int x = x0 + tx, y = y0 + ty;
+    const bool inside = x < W && y < H;
+    const int64_t plane = (int64_t)H * W * C;
+    const int64_t pix = ((int64_t)y * W + x) * C;
+    const float gl = grad_in[0] * inv_n, gs = grad_in[1] * inv_n;
+
+    for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int q = 0; q < 3; ++q) load_halo<R>(s_m[q], maps + q * plane, H, W, C, c, x0, y0);
+        __syncthreads();
+        for (int i = tid; i < S * kSsT; i += kSsT * kSsT) {
+            const int ly = i / kSsT, lx = i - ly * kSsT;
+            float a = 0.0f, b = 0.0f, d = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                const float w = win.g[k];
+                a = fmaf(w, s_m[0][ly][lx + k], a);
+                b = fmaf(w, s_m[1][ly][lx + k], b);
+                d = fmaf(w, s_m[2][ly][lx + k], d);
+            }
+            s_h[0][ly][lx] = a;
+            s_h[1][ly][lx] = b;
+            s_h[2][ly][lx] = d;
+        }
+        __syncthreads();
+        float fm = 0.0f, fpp = 0.0f, fpt = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const float w = win.g[k];
+            fm = fmaf(w, s_h[0][ty + k][tx], fm);
+            fpp = fmaf(w, s_h[1][ty + k][tx], fpp);
+            fpt = fmaf(w, s_h[2][ty + k][tx], fpt);
+        }
+        if (inside) {
+            const float p = pred[pix + c], t = tgt[pix + c];
+            const float sgn = (float)((p > t) - (p < t));
+            const float gss = fm + 2.0f * p * fpp + t * fpt;
+            grad[pix + c] = fmaf(gs, gss, gl * sgn);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------- Adam --
+//
+// mlx.optimizers.Adam.apply_single without bias correction (the default):
+//   m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g^2;  p = p - lr m / (sqrt(v) + eps)
+// in float32, each operation rounded once, in this order.
+
+constexpr int kAdamMaxGroups = GSX_ADAM_MAX_GROUPS;
+constexpr int kAdamPerBlock = 1024;  // 256 threads x 4 elements
+
+struct AdamArgs {
+    float* p[kAdamMaxGroups];
+    const float* g[kAdamMaxGroups];
+    float* m[kAdamMaxGroups];
+    float* v[kAdamMaxGroups];
+    int64_t n[kAdamMaxGroups];
+    float lr[kAdamMaxGroups];
+    int64_t blk[kAdamMaxGroups + 1];
+    int32_t vec[kAdamMaxGroups];
+    int32_t count;
+};
+
+__device__ __forceinline__ void adam_one(float& p, float g, float& m, float& v, float lr, float b1,
+                                         float omb1, float b2, float omb2, float eps) {
+    m = b1 * m + omb1 * g;
+    v = b2 * v + omb2 * (g * g);
+    p = p - (lr * m) / (sqrtf(v) + eps);
+}
+
+__global__ __launch_bounds__(256) void k_adam(AdamArgs a, float b1, float omb1, float b2,
+                                              float omb2, float eps) {
+    const int64_t b = blockIdx.x;
+    int gi = 0;
+    while (gi + 1 < a.count && b >= a.blk[gi + 1]) ++gi;
+    const int64_t n = a.n[gi];
+    const int64_t i0 = (b - a.blk[gi]) * kAdamPerBlock + (int64_t)threadIdx.x * 4;
+    if (i0 >= n) return;
+    float* __restrict__ P = a.p[gi];
+    const float* __restrict__ G = a.g[gi];
+    float* __restrict__ M = a.m[gi];
+    float* __restrict__ V = a.v[gi];
+    const float lr = a.lr[gi];
+    if (a.vec[gi] && i0 + 4 <= n) {
+        float4 p = *reinterpret_cast<const float4*>(P + i0);
+        const float4 g = *reinterpret_cast<const float4*>(G + i0);
+        float4 m = *reinterpret_cast<const float4*>(M + i0);
+        float4 v = *reinterpret_cast<const float4*>(V + i0);
+        adam_one(p.x, g.x, m.x, v.x, lr, b1, omb1, b2, omb2, eps);
+        adam_one(p.y, g.y, m.y, v.y, lr, b1, omb1, b2, omb2, eps);
+        adam_one(p.z, g.z, m.z, v.z, lr, b1, omb1, b2, omb2, eps);
+        adam_one(p.w, g.w, m.w, v.w, lr, b1, omb1, b2, omb2, eps);
+        *reinterpret_cast<float4*>(P + i0) = p;
+        *reinterpret_cast<float4*>(M + i0) = m;
+        *reinterpret_cast<float4*>(V + i0) = v;
+        return;
+    }
+    const int64_t i1 = std::min<int64_t>(i0 + 4, n);
+    for (int64_t i = i0; i < i1; ++i) {
+        float p = P[i], m = M[i], v = V[i];
+        adam_one(p, G[i], m, v, lr, b1, omb1, b2, omb2, eps);
+        P[i] = p;
+        M[i] = m;
+        V[i] = v;
+    }
+}
+
+// ------------------------------------------- density-control statistics --
+// trainer.py:358-365: gx = g_x (W / 2), gy = g_y (H / 2),
+// accum += sqrt(gx gx + gy gy) * visible, count += visible, visible = radii > 0.
+__global__ __launch_bounds__(256) void k_accum_screen_grads(int64_t n,
+                                                            const float2* __restrict__ g,
+                                                            const float* __restrict__ radii,
+                                                            float half_w, float half_h,
+                                                            float* __restrict__ accum,
+                                                            float* __restrict__ count) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float2 d = g[i];
+    const float gx = d.x * half_w, gy = d.y * half_h;
+    const float norm = sqrtf(gx * gx + gy * gy);
+    const float vis = radii[i] > 0.0f ? 1.0f : 0.0f;
+    accum[i] = accum[i] + norm * vis;
+    count[i] = count[i] + vis;
+}
+
+// ------------------------------------------------------------ host side --
+
+bool make_window(int32_t window_size, float sigma, SsimWindow& w) {
+    if (window_size < 1 || window_size > 2 * kSsMaxR + 1 || (window_size & 1) == 0) return false;
+    if (!(sigma > 0.0f) || !std::isfinite(sigma)) return false;
+    // image_metrics.py:23-26 in float32: x = k - (size - 1) / 2,
+    // g = exp(-(x x) / (2 sigma sigma)), g / sum(g).
+    float g[2 * kSsMaxR + 1];
+    float sum = 0.0f;
+    const float half = (float)((window_size - 1) / 2.0);
+    const float den = (float)(2.0 * (double)sigma * (double)sigma);
+    for (int k = 0; k < window_size; ++k) {
+        const float x = (float)k - half;
+        g[k] = std::exp(-(x * x) / den);
+        sum += g[k];
+    }
+    for (int k = 0; k < window_size; ++k) w.g[k] = g[k] / sum;
+    for (int k = window_size; k < 2 * kSsMaxR + 1; ++k) w.g[k] = 0.0f;
+    return true;
+}
+
+int64_t photometric_blocks(int32_t H, int32_t W) {
+    return (int64_t)((W + kSsT - 1) / kSsT) * ((H + kSsT - 1) / kSsT);
+}
+
+inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+}  // namespace
+
+extern "C" {
+
+int64_t gsx_photometric_workspace_bytes(int32_t height, int32_t width, int32_t channels) {
+    if (height <= 0 || width <= 0 || channels <= 0) return 0;
+    const int64_t maps = 3 * (int64_t)height * width * channels * (int64_t)sizeof(float);
+    return align256(maps) + align256(2 * photometric_blocks(height, width) * (int64_t)sizeof(float));
+}
+
+int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                        const float* target, int32_t window_size, float sigma, float max_val,
+                        void* workspace, int64_t workspace_bytes, float* out, void* stream) {
+    if (height <= 0 || width <= 0 || channels <= 0) return GSX_ERR_INVALID;
+    if (!pred || !target || !out || !workspace) return GSX_ERR_INVALID;
+    if ((int64_t)height * width * channels >= (int64_t(1) << 40)) return GSX_ERR_TOO_LARGE;
+    SsimWindow win;
+    if (!make_window(window_size, sigma, win)) return GSX_ERR_INVALID;
+    if (workspace_bytes < gsx_photometric_workspace_bytes(height, width, channels))
+        return GSX_ERR_WORKSPACE;
+    // image_metrics.py:51-52
+    const float c1 = (float)((0.01 * max_val) * (0.01 * max_val));
+    const float c2 = (float)((0.03 * max_val) * (0.03 * max_val));
+    float* maps = (float*)workspace;
+    float* partials = (float*)((char*)workspace +
+                               align256(3 * (int64_t)height * width * channels * 4));
+    const dim3 grid((unsigned)((width + kSsT - 1) / kSsT), (unsigned)((height + kSsT - 1) / kSsT));
+    hipStream_t st = (hipStream_t)stream;
+    switch (window_size / 2) {
+#define GSX_SSIM_FWD(RR)                                                                       \
+    case RR:                                                                                   \
+        hipLaunchKernelGGL(k_ssim_fwd<RR>, grid, dim3(kSsT * kSsT), 0, st, pred, target,      \
+                           height, width, channels, win, c1, c2, maps, partials);              \
+        break;
+        GSX_SSIM_FWD(0)
+        GSX_SSIM_FWD(1)
+        GSX_SSIM_FWD(2)
+        GSX_SSIM_FWD(3)
+        GSX_SSIM_FWD(4)
+        GSX_SSIM_FWD(5)
+        GSX_SSIM_FWD(6)
+        GSX_SSIM_FWD(7)
+#undef GSX_SSIM_FWD
+        default:
+            return GSX_ERR_INVALID;
+    }
+    GSX_LAUNCH_CHECK();
+    const double inv_n = 1.0 / ((double)height * width * channels);
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, partials,
+                       photometric_blocks(height, width), inv_n, out);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                        const float* target, int32_t window_size, float sigma,
+                        const void* workspace, int64_t workspace_bytes, const float* grad_out,
+                        float* grad_pred, void* stream) {
+    if (height <= 0 || width <= 0 || channels <= 0) return GSX_ERR_INVALID;
+    if (!pred || !target || !workspace || !grad_out || !grad_pred) return GSX_ERR_INVALID;
+    if ((int64_t)height * width * channels >= (int64_t(1) << 40)) return GSX_ERR_TOO_LARGE;
+    SsimWindow win;
+    if (!make_window(window_size, sigma, win)) return GSX_ERR_INVALID;
+    if (workspace_bytes < gsx_photometric_workspace_bytes(height, width, channels))
+        return GSX_ERR_WORKSPACE;
+    const float inv_n = (float)(1.0 / ((double)height * width * channels));
+    const dim3 grid((unsigned)((width + kSsT - 1) / kSsT), (unsigned)((height + kSsT - 1) / kSsT));
+    hipStream_t st = (hipStream_t)stream;
+    const float* maps = (const float*)workspace;
+    switch (window_size / 2) {
+#define GSX_SSIM_BWD(RR)                                                                       \
+    case RR:                                                                                   \
+        hipLaunchKernelGGL(k_ssim_bwd<RR>, grid, dim3(kSsT * kSsT), 0, st, pred, target,      \
+                           height, width, channels, win, maps, grad_out, inv_n, grad_pred);    \
+        break;
+        GSX_SSIM_BWD(0)
+        GSX_SSIM_BWD(1)
+        GSX_SSIM_BWD(2)
+        GSX_SSIM_BWD(3)
+        GSX_SSIM_BWD(4)
+        GSX_SSIM_BWD(5)
+        GSX_SSIM_BWD(6)
+        GSX_SSIM_BWD(7)
+#undef GSX_SSIM_BWD
+        default:
+            return GSX_ERR_INVALID;
+    }
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_adam_step(int32_t num_groups, const gsx_adam_group* groups, float beta1, float beta2,
+                  float eps, void* stream) {
+    if (num_groups < 0 || num_groups > kAdamMaxGroups) return GSX_ERR_INVALID;
+    if (num_groups > 0 && !groups) return GSX_ERR_INVALID;
+    AdamArgs a{};
+    int64_t blocks = 0;
+    int count = 0;
+    for (int i = 0; i < num_groups; ++i) {
+        const gsx_adam_group& g = groups[i];
+        if (g.n < 0) return GSX_ERR_INVALID;
+        if (g.n == 0) continue;
+        if (!g.param || !g.grad || !g.m || !g.v) return GSX_ERR_INVALID;
+        a.p[count] = g.param;
+        a.g[count] = g.grad;
+        a.m[count] = g.m;
+        a.v[count] = g.v;
+        a.n[count] = g.n;
+        a.lr[count] = g.lr;
+        const uintptr_t any = (uintptr_t)g.param | (uintptr_t)g.grad | (uintptr_t)g.m |
+                              (uintptr_t)g.v;
+        a.vec[count] = (any & 15u) == 0;
+        a.blk[count] = blocks;
+        blocks += (g.n + kAdamPerBlock - 1) / kAdamPerBlock;
+        ++count;
+    }
+    a.blk[count] = blocks;
+    a.count = count;
+    if (blocks == 0) return GSX_OK;
+    if (blocks > 0x7fffffff) return GSX_ERR_TOO_LARGE;
+    // (1 - b1) and (1 - b2) are formed in double and rounded once, as the
+    // Python scalars of the reference reach the float32 arithmetic.
+    const float omb1 = (float)(1.0 - (double)beta1), omb2 = (float)(1.0 - (double)beta2);
+    hipLaunchKernelGGL(k_adam, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, a,
+                       beta1, omb1, beta2, omb2, eps);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_accum_screen_grads(int64_t n, const float* g_means2d, const float* radii, int32_t width,
+                           int32_t height, float* grad_accum, float* grad_count, void* stream) {
+    if (n < 0 || width <= 0 || height <= 0) return GSX_ERR_INVALID;
+    if (n == 0) return GSX_OK;
+    if (!g_means2d || !radii || !grad_accum || !grad_count) return GSX_ERR_INVALID;
+    if (((uintptr_t)g_means2d & 7u) != 0) return GSX_ERR_INVALID;
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    hipLaunchKernelGGL(k_accum_screen_grads, dim3(blocks), dim3(256), 0, (hipStream_t)stream, n,
+                       (const float2*)g_means2d, radii, (float)(width / 2.0),
+                       (float)(height / 2.0), grad_accum, grad_count);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+}  // extern "C"

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -166,3 +167,181 @@ class GaussianModel:
                                         self.scales_act, self.opacities_act, features,
                                         background=background, normalize=normalize,
                                         antialias=antialias, projection=projection)
+
+    # ------------------------------------------------------------ table edits
+    # Row edits run on the device; each returns new leaf tensors that keep the
+    # requires_grad flag of the ones they replace.
+    def _replace(self, params: dict[str, torch.Tensor]) -> None:
+        self.params = {k: v.detach().contiguous().requires_grad_(self.params[k].requires_grad)
+                       for k, v in params.items()}
+
+    def copy(self) -> "GaussianModel":
+        """A detached copy of the table (model.py:273-277)."""
+        out = GaussianModel({k: v.detach().clone() for k, v in self.params.items()},
+                            self.sh_degree)
+        out.active_sh_degree = self.active_sh_degree
+        return out
+
+    def select(self, keep_idx) -> None:
+        """Keep only the rows ``keep_idx`` (model.py:395-398)."""
+        idx = torch.as_tensor(np.asarray(keep_idx), dtype=torch.int64,
+                              device=self.params["means"].device)
+        with torch.no_grad():
+            self._replace({k: v[idx] for k, v in self.params.items()})
+
+    def append(self, new_params: dict[str, torch.Tensor]) -> None:
+        """Concatenate rows (model.py:400-404)."""
+        with torch.no_grad():
+            self._replace({k: torch.cat([v, torch.as_tensor(new_params[k]).to(v)], dim=0)
+                           for k, v in self.params.items()})
+
+    def apply_2dgs_constraints(self, max_thickness: float) -> None:
+        """Cap the third log-scale at log(max(thickness, 1e-8)) (model.py:128-143)."""
+        lim = float(np.log(max(float(max_thickness), 1e-8)))
+        with torch.no_grad():
+            s = self.params["scales"]
+            z = torch.clamp(s[:, 2:3], max=lim)
+            params = dict(self.params)
+            params["scales"] = torch.cat([s[:, :2], z], dim=1)
+            self._replace(params)
+
+    def reset_opacities(self, max_opacity: float = 0.01) -> None:
+        """Clamp opacity logits to logit(max_opacity) (model.py:533-538)."""
+        logit = float(np.log(max_opacity / (1 - max_opacity)))
+        with torch.no_grad():
+            params = dict(self.params)
+            params["opacities"] = torch.clamp(self.params["opacities"], max=logit)
+            self._replace(params)
+
+    def compact(self, min_opacity: float = 0.0, max_gaussians: int | None = None,
+                target_sh_degree: int | None = None) -> "GaussianModel":
+        """A pruned copy ranked by sigmoid(opacity) max(scale)^2 (model.py:279-335)."""
+        if max_gaussians is not None and max_gaussians <= 0:
+            raise ValueError("max_gaussians must be positive when provided.")
+        if target_sh_degree is not None and not (0 <= target_sh_degree <= self.sh_degree):
+            raise ValueError("target_sh_degree must be between 0 and the model sh_degree.")
+        n = self.num_gaussians
+        if n == 0:
+            return self.copy()
+        with torch.no_grad():
+            opacity = self.opacities_act
+            max_scale = self.scales_act.max(dim=1).values
+            importance = opacity * max_scale * max_scale
+            keep = opacity >= float(min_opacity)
+            if not bool(keep.any()):
+                keep[int(torch.argmax(importance))] = True
+            keep_idx = torch.nonzero(keep).flatten()
+            if max_gaussians is not None and keep_idx.numel() > max_gaussians:
+                top = torch.topk(importance[keep_idx], max_gaussians).indices
+                keep_idx = torch.sort(keep_idx[top]).values
+            params = {k: v.detach()[keep_idx].clone() for k, v in self.params.items()}
+        sh_degree = self.sh_degree
+        if target_sh_degree is not None:
+            sh_degree = int(target_sh_degree)
+            params["sh_rest"] = params["sh_rest"][:, :max(0, num_sh_bases(sh_degree) - 1), :]
+        out = GaussianModel({k: v.contiguous() for k, v in params.items()}, sh_degree=sh_degree)
+        out.active_sh_degree = min(self.active_sh_degree, sh_degree)
+        return out
+
+    def densify_and_prune(self, grad_accum: torch.Tensor, grad_count: torch.Tensor,
+                          grad_threshold: float = 0.0002, scene_extent: float = 1.0,
+                          percent_dense: float = 0.01, min_opacity: float = 0.005,
+                          return_optimizer_state: bool = False) -> dict:
+        """Adaptive density control of the 3DGS paper (model.py:406-480).
+
+        High average screen gradient: clone if max(scale) <= percent_dense
+        extent, else split into two samples N(0, diag(s^2)) rotated by the
+        Gaussian's rotation, log-scales reduced by log 1.6.  Prune split
+        sources, sigmoid(opacity) < min_opacity and max(scale) > 0.5 extent.
+        The split samples come from ``np.random.normal`` (the global NumPy
+        generator, as the reference draws them).  Rows end up ordered
+        [kept originals, clones, split pairs].
+        """
+        from ..transforms import quaternion_to_matrix
+
+        with torch.no_grad():
+            p = {k: v.detach() for k, v in self.params.items()}
+            dev = p["means"].device
+            avg_grad = grad_accum / torch.clamp(grad_count, min=1.0)
+            scales = torch.exp(p["scales"])
+            max_scale = scales.max(dim=1).values
+            high_grad = avg_grad > grad_threshold
+            dense = percent_dense * scene_extent
+            clone_mask = high_grad & (max_scale <= dense)
+            split_mask = high_grad & (max_scale > dense)
+            clone_idx = torch.nonzero(clone_mask).flatten()
+            split_idx = torch.nonzero(split_mask).flatten()
+            opac = 1.0 / (1.0 + torch.exp(-torch.clamp(p["opacities"], -50.0, 50.0)))
+            prune_mask = (opac < min_opacity) | split_mask | (max_scale > 0.5 * scene_extent)
+            keep_idx = torch.nonzero(~prune_mask).flatten()
+            parts = {k: [v[keep_idx], v[clone_idx]] for k, v in p.items()}
+            n_split = int(split_idx.numel())
+            if n_split > 0:
+                q = p["quats"][split_idx]
+                R = quaternion_to_matrix(q / torch.linalg.norm(q, dim=1, keepdim=True))
+                s = scales[split_idx].cpu().numpy()
+                samples = np.random.normal(size=(2 * n_split, 3)) * np.repeat(s, 2, axis=0)
+                offsets = np.einsum("nij,nj->ni", np.repeat(R.cpu().numpy(), 2, axis=0), samples)
+                for k, v in p.items():
+                    rows = torch.repeat_interleave(v[split_idx], 2, dim=0)
+                    if k == "means":
+                        rows = rows + torch.from_numpy(offsets.astype(np.float32)).to(dev)
+                    elif k == "scales":
+                        rows = rows - float(np.log(1.6))
+                    parts[k].append(rows)
+            self._replace({k: torch.cat(v, dim=0) for k, v in parts.items()})
+        stats: dict = {"cloned": int(clone_idx.numel()), "split": n_split,
+                       "pruned": int(prune_mask.sum())}
+        if return_optimizer_state:
+            stats["_keep_idx"] = keep_idx.cpu().numpy().astype(np.int32)
+            stats["_new_count"] = int(clone_idx.numel() + 2 * n_split)
+        return stats
+
+    def relocate_mcmc(self, grad_accum: torch.Tensor, grad_count: torch.Tensor,
+                      relocate_frac: float = 0.02, min_opacity: float = 0.01,
+                      jitter_scale: float = 0.25,
+                      generator: torch.Generator | None = None) -> dict:
+        """Fixed-budget relocation (model.py:482-531): the k best relocation
+        targets (never-seen or sigmoid(opacity) < min_opacity rows first, then
+        the least opaque) take jittered copies of the k rows with the highest
+        average screen gradient among the rest; opacity resets to 0.05 and
+        log-scales shrink by log 1.6.  Rows are rewritten as
+        ``a[dst] + (new - a[dst])``, the reference's scatter-add."""
+        n = self.num_gaussians
+        max_relocate = int(max(0, min(relocate_frac, 1.0)) * n)
+        if max_relocate <= 0 or n <= 1:
+            return {"relocated": 0}
+        with torch.no_grad():
+            p = {k: v.detach() for k, v in self.params.items()}
+            avg_grad = grad_accum / torch.clamp(grad_count, min=1.0)
+            opac = torch.sigmoid(p["opacities"])
+            underused = (opac < min_opacity) | (grad_count <= 0)
+            underused_count = int(underused.sum())
+            k = max_relocate if underused_count == 0 else min(max_relocate, underused_count)
+            k = min(k, n - 1)
+            if k == 0:
+                return {"relocated": 0}
+            target_score = torch.where(underused, 2.0 - opac, -opac)
+            dst = torch.topk(target_score, k).indices
+            source_score = avg_grad.clone()
+            source_score[dst] = source_score[dst] + (-1e30 - avg_grad[dst])
+            src = torch.topk(source_score, k).indices
+            source_scales = torch.exp(p["scales"][src])
+            reset_opacity = float(np.log(0.05 / 0.95))
+            shrink = float(np.log(1.6))
+            out = {}
+            for name, arr in p.items():
+                values = arr[src]
+                if name == "means" and jitter_scale > 0:
+                    gdev = generator.device if generator is not None else values.device
+                    noise = torch.randn(values.shape, generator=generator, device=gdev)
+                    values = values + noise.to(values.device) * source_scales * float(jitter_scale)
+                elif name == "opacities":
+                    values = torch.full_like(values, reset_opacity)
+                elif name == "scales":
+                    values = values - shrink
+                arr = arr.clone()
+                arr[dst] = arr[dst] + (values - arr[dst])
+                out[name] = arr
+            self._replace(out)
+        return {"relocated": int(k), "_moved_idx": dst}

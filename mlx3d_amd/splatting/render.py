@@ -39,6 +39,9 @@ class _Cfg:
     sh_mode: str | None  # "packed" (N,K,3) tensor, "split" (dc, rest) tensors, None = colours
     return_depth: bool
     refine: bool = False  # refine_tiles: drop bbox tiles the conic never reaches
+    # (grad_accum, grad_count): the backward adds the density-control
+    # statistics of dL/dmeans2d (trainer.py:357-365) to these in place.
+    screen_stats: tuple | None = None
 
 
 def _sh_views(cfg: _Cfg, sh_a, sh_b):
@@ -104,7 +107,7 @@ class _RenderFn(torch.autograd.Function):
         ctx.cfg = cfg
         ctx.save_for_backward(means, quats, scales, opacities, sh_a, sh_b, r["feats"],
                               r["means2d"], r["conic_opac"], r["sorted_ids"], r["tile_ranges"],
-                              r["final_T"], r["n_contrib"], background)
+                              r["final_T"], r["n_contrib"], background, r["radii"])
         depth = r["depth"] if r["depth"] is not None else r["final_T"].new_empty((0,))
         ctx.mark_non_differentiable(r["radii"], r["n_contrib"], depth, r["sorted_ids"],
                                     r["tile_ranges"])
@@ -116,7 +119,7 @@ class _RenderFn(torch.autograd.Function):
     def backward(ctx, g_image, g_final_T, _g_nc, g_means2d, g_depths, _g_radii, g_comp, _g_depth,
                  _g_ids, _g_ranges):
         (means, quats, scales, opacities, sh_a, sh_b, feats, means2d, co, ids, ranges, final_T,
-         n_contrib, background) = ctx.saved_tensors
+         n_contrib, background, radii) = ctx.saved_tensors
         cfg = ctx.cfg
         dev = means.device
         n = means.shape[0]
@@ -124,6 +127,11 @@ class _RenderFn(torch.autograd.Function):
             g_m2, g_con, g_feat, g_op = raster_backward(means2d, co, feats, ids, ranges,
                                                         background, cfg.width, cfg.height,
                                                         final_T, n_contrib, g_image, g_final_T)
+        if cfg.screen_stats is not None:
+            acc, cnt = cfg.screen_stats
+            _lib.check(_lib.load().gsx_accum_screen_grads(
+                n, _lib.ptr(g_m2), _lib.ptr(radii), cfg.width, cfg.height, _lib.ptr(acc),
+                _lib.ptr(cnt), _lib.stream_handle(dev)), "gsx_accum_screen_grads")
         f = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)  # noqa: E731
         g_means, g_quats, g_scales, g_opac = f(n, 3), f(n, 4), f(n, 3), f(n)
         g_sh_a = g_sh_b = None
@@ -164,9 +172,20 @@ def _background(background, channels, dev):
     return bg.contiguous()
 
 
+def _stats(screen_stats, n, dev):
+    if screen_stats is None:
+        return None
+    acc, cnt = screen_stats
+    for t in (acc, cnt):
+        if t.shape != (n,) or t.dtype != torch.float32 or not t.is_contiguous() or t.device != dev:
+            raise ValueError("screen_stats tensors must be contiguous float32 (N,) on the "
+                             "render device")
+    return acc, cnt
+
+
 def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=None,
          sh_mode=None, K=0, degree=0, colors=None, background=None, flags=0, antialias=False,
-         blur=0.3, return_depth=False, refine_tiles=False):
+         blur=0.3, return_depth=False, refine_tiles=False, screen_stats=None):
     n = means.shape[0]
     if means.ndim != 2 or means.shape[1] != 3:
         raise ValueError("means must have shape (N, 3).")
@@ -178,7 +197,8 @@ def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=Non
         flags |= _lib.ANTIALIAS
     cfg = _Cfg(cam=camera.to_gsx(), width=int(camera.width), height=int(camera.height),
                flags=flags, blur=float(blur), degree=int(degree), K=int(K), sh_mode=sh_mode,
-               return_depth=bool(return_depth), refine=bool(refine_tiles))
+               return_depth=bool(return_depth), refine=bool(refine_tiles),
+               screen_stats=_stats(screen_stats, n, dev))
     c = _lib.f32c
     (image, final_T, n_contrib, means2d, depths, radii, comp, depth, ids,
      ranges) = _RenderFn.apply(c(means), c(quats), c(scales), c(opacities),

@@ -15,6 +15,7 @@
  *                          when conics are given)
  *   orc_raster_fwd      -- rasterize.py:28-98 (+ depth rasterize.py:223-290)
  *   orc_raster_bwd      -- rasterize.py:100-221, vjp wiring :364-403
+ *   orc_photometric, orc_adam, orc_accum_screen_grads -- train_oracle.c
  *   orc_project_bwd /
  *   orc_preprocess_bwd  -- hand-derived VJP of projection.py:56-138,
  *                          sh.py:52-78, render.py:75-80, model.py:116-122
@@ -116,6 +117,23 @@ void orc_raster_bwd(int64_t n, int C, const float* means2d,
                     const float* grad_final_T, float* g_means2d,
                     float* g_conics, float* g_feats, float* g_opac,
                     int nthreads);
+
+/* ------------------------------------------------ training step (train_oracle.c) */
+
+/* Mean L1 and mean SSIM of pred vs target (H,W,C), double precision, direct
+ * 2D window; out[2] = {mean L1, mean SSIM}.  grad (H,W,C) or NULL receives
+ * g_l1 d(mean L1)/dpred + g_ssim d(mean SSIM)/dpred. */
+void orc_photometric(int H, int W, int C, const float* pred, const float* target, int window,
+                     double sigma, double max_val, double g_l1, double g_ssim, double* out,
+                     double* grad);
+
+/* One Adam update in place (mlx.optimizers.Adam, bias_correction off). */
+void orc_adam(int64_t n, float* p, const float* g, float* m, float* v, float lr, float b1,
+              float b2, float eps);
+
+/* Density-control statistics of trainer.py:357-365, in place. */
+void orc_accum_screen_grads(int64_t n, const float* g, const float* radii, int W, int H,
+                            float* accum, float* count);
 
 #ifdef __cplusplus
 }

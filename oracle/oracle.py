@@ -85,6 +85,10 @@ def _declare(L):
                                  _P, _P, _P, _P, _P, _I64, _I]
     L.orc_raster_bwd.argtypes = [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P,
                                  _P, _P, _P, _P, _P, _P, _I]
+    _D = ctypes.c_double
+    L.orc_photometric.argtypes = [_I, _I, _I, _P, _P, _I, _D, _D, _D, _D, _P, _P]
+    L.orc_adam.argtypes = [_I64, _P, _P, _P, _P, _F, _F, _F, _F]
+    L.orc_accum_screen_grads.argtypes = [_I64, _P, _P, _I, _I, _P, _P]
 
 
 def _f32(a):
@@ -271,3 +275,40 @@ def raster_bwd(means2d, conics, opacities, feats, sorted_ids, tile_ranges, width
                          _ptr(final_T), _ptr(n_contrib), _ptr(grad_out), _ptr(grad_final_T),
                          _ptr(g_m), _ptr(g_c), _ptr(g_f), _ptr(g_o), threads)
     return dict(means2d=g_m, conics=g_c, features=g_f, opacities=g_o)
+
+
+# ------------------------------------------------------------ training step
+
+
+def photometric(pred, target, window_size=11, sigma=1.5, max_val=1.0, g_l1=0.0, g_ssim=0.0,
+                grad=False):
+    """(mean L1, mean SSIM[, gradient]) of (H, W, C) images in float64
+    (losses/image_metrics.py:23-55, 66-85; trainer.py:303)."""
+    pred, target = _f32(pred), _f32(target)
+    if pred.ndim == 2:
+        pred, target = pred[..., None], target[..., None]
+    H, W, C = pred.shape
+    out = np.zeros(2, np.float64)
+    g = np.zeros(pred.shape, np.float64) if grad else None
+    lib().orc_photometric(H, W, C, _ptr(pred), _ptr(target), int(window_size), float(sigma),
+                          float(max_val), float(g_l1), float(g_ssim), _ptr(out), _ptr(g))
+    return (out[0], out[1], g) if grad else (out[0], out[1])
+
+
+def adam(param, grad, m, v, lr, beta1=0.9, beta2=0.999, eps=1e-15):
+    """One mlx.optimizers.Adam update (bias_correction off); returns new
+    (param, m, v) as float32 arrays."""
+    p, m, v = _f32(param).copy(), _f32(m).copy(), _f32(v).copy()
+    g = _f32(grad)
+    lib().orc_adam(p.size, _ptr(p), _ptr(g), _ptr(m), _ptr(v), float(np.float32(lr)),
+                   float(np.float32(beta1)), float(np.float32(beta2)), float(np.float32(eps)))
+    return p, m, v
+
+
+def accum_screen_grads(g_means2d, radii, width, height, accum, count):
+    """trainer.py:357-365; returns new (accum, count)."""
+    g, r = _f32(g_means2d), _f32(radii)
+    a, c = _f32(accum).copy(), _f32(count).copy()
+    lib().orc_accum_screen_grads(r.size, _ptr(g), _ptr(r), int(width), int(height), _ptr(a),
+                                 _ptr(c))
+    return a, c

@@ -1,0 +1,270 @@
+"""GPU parity of the training step: photometric loss kernels, multi-group
+Adam, screen-gradient statistics, density control and GaussianTrainer.step,
+each against the CPU oracle (oracle/train_oracle.c, oracle/density.py,
+oracle/gsx_oracle.c).
+
+Tolerances: Adam and the screen-gradient statistics are float32 in the
+reference's operation order and must match bit for bit; the loss values
+(float32 on the GPU vs float64 in the oracle) within 2e-6 absolute; loss
+and parameter gradients within max|d| / max|ref| < 1e-4 (loss) and 1e-3
+(parameters, the rasterizer's bar).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_bits, cu, host, oracle_backward, oracle_forward, rel_err, say
+from mlx3d_amd import _lib
+from mlx3d_amd.losses import photometric, ssim
+from mlx3d_amd.optim import Adam, adam_step, exponential_decay
+from mlx3d_amd.splatting import GaussianModel
+from mlx3d_amd.splatting.trainer import GaussianTrainer, TrainerConfig
+from oracle import density as DN
+from oracle import oracle as O
+from refimpl import random_scene
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("H,W,C,ws,sigma", [(64, 80, 3, 11, 1.5), (37, 53, 3, 11, 1.5),
+                                            (5, 7, 3, 11, 1.5), (48, 40, 1, 3, 0.7),
+                                            (33, 29, 2, 15, 2.5), (20, 24, 3, 1, 1.0)])
+def test_photometric_matches_oracle(H, W, C, ws, sigma):
+    say(f"photometric H={H} W={W} C={C} ws={ws}")
+    rng = np.random.default_rng(H + W + ws)
+    p = rng.random((H, W, C), dtype=np.float32)
+    t = rng.random((H, W, C), dtype=np.float32)
+    pt = cu(p).requires_grad_(True)
+    l1, s = photometric(pt, cu(t), ws, sigma)
+    (0.8 * l1 - 0.2 * s).backward()
+    rl1, rs, rg = O.photometric(p, t, ws, sigma, g_l1=0.8, g_ssim=-0.2, grad=True)
+    say(f"  l1 {float(l1):.8f} vs {rl1:.8f}; ssim {float(s):.8f} vs {rs:.8f}")
+    assert abs(float(l1) - rl1) < 2e-6 and abs(float(s) - rs) < 2e-6
+    e = rel_err(host(pt.grad), rg)
+    say(f"  grad rel {e:.2e}")
+    assert e < 1e-4
+
+
+def test_photometric_full_size_properties():
+    """1920x1080x3: SSIM(x, x) = 1 with zero SSIM gradient; L1 against torch."""
+    say("photometric 1080p properties")
+    rng = np.random.default_rng(9)
+    p = cu(rng.random((1080, 1920, 3), dtype=np.float32)).requires_grad_(True)
+    t = cu(rng.random((1080, 1920, 3), dtype=np.float32))
+    l1, s = photometric(p, p.detach().clone())
+    assert float(l1) == 0.0 and abs(float(s) - 1.0) < 1e-6
+    s.backward()
+    assert float(p.grad.abs().max()) < 1e-9
+    p.grad = None
+    l1, s = photometric(p, t)
+    ref = (p.detach().double() - t.double()).abs().mean()
+    assert abs(float(l1) - float(ref)) < 1e-6
+    l1.backward()
+    np.testing.assert_array_equal(host(p.grad), host(torch.sign(p.detach() - t) / p.numel()))
+
+
+def test_ssim_batched_and_errors():
+    rng = np.random.default_rng(2)
+    a = rng.random((2, 24, 30, 3), dtype=np.float32)
+    b = rng.random((2, 24, 30, 3), dtype=np.float32)
+    s = float(ssim(cu(a), cu(b)))
+    ref = 0.5 * (O.photometric(a[0], b[0])[1] + O.photometric(a[1], b[1])[1])
+    assert abs(s - ref) < 2e-6
+    with pytest.raises(ValueError):
+        ssim(cu(a[0]), cu(b[0]), window_size=10)
+    with pytest.raises(ValueError):
+        photometric(cu(a[0]), cu(b[1, :20]))
+
+
+def test_adam_bitexact_multi_group():
+    say("adam groups")
+    rng = np.random.default_rng(4)
+    sizes = [5, 1024, 4099, 3, 0, 100_003, 7, 64, 12, 999]  # > 8 groups: two launches
+    ps = [rng.normal(size=n).astype(np.float32) for n in sizes]
+    opts, params, ref = [], [], []
+    for i, n in enumerate(sizes):
+        base = cu(np.concatenate([[0.0], ps[i]]).astype(np.float32))
+        # odd groups start one float into their buffer: the scalar path
+        p = base[1:] if i % 2 else cu(ps[i])
+        params.append(p)
+        lr = exponential_decay(1e-2 * (i + 1), 0.97) if i == 0 else 1e-3 * (i + 1)
+        opts.append(Adam(learning_rate=lr, eps=1e-15))
+        ref.append([ps[i].copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)])
+    for step in range(3):
+        grads = [rng.normal(size=n).astype(np.float32) for n in sizes]
+        adam_step([(opts[i], {"w": cu(grads[i])}, {"w": params[i]}) for i in range(len(sizes))])
+        for i in range(len(sizes)):
+            lr = 1e-2 * 0.97 ** step if i == 0 else 1e-3 * (i + 1)
+            ref[i] = list(O.adam(ref[i][0], grads[i], ref[i][1], ref[i][2], lr, eps=1e-15))
+    for i in range(len(sizes)):
+        assert_bits(host(params[i]), ref[i][0], f"adam param {i}")
+        assert_bits(host(opts[i].state["w"]["m"]), ref[i][1], f"adam m {i}")
+        assert_bits(host(opts[i].state["w"]["v"]), ref[i][2], f"adam v {i}")
+    assert abs(opts[0].learning_rate - 1e-2 * 0.97 ** 2) < 1e-12
+
+
+def test_accum_screen_grads_bitexact():
+    rng = np.random.default_rng(8)
+    n = 100_001
+    g = (rng.normal(size=(n, 2)) * 1e-4).astype(np.float32)
+    radii = np.where(rng.random(n) < 0.3, 0.0, rng.integers(1, 50, n)).astype(np.float32)
+    acc0 = rng.random(n).astype(np.float32)
+    cnt0 = rng.integers(0, 5, n).astype(np.float32)
+    acc, cnt = cu(acc0), cu(cnt0)
+    gd, rd = cu(g), cu(radii)  # alive until the kernel has run
+    _lib.check(_lib.load().gsx_accum_screen_grads(
+        n, _lib.ptr(gd), _lib.ptr(rd), 1279, 720, _lib.ptr(acc), _lib.ptr(cnt),
+        _lib.stream_handle(acc.device)), "accum")
+    ra, rc = O.accum_screen_grads(g, radii, 1279, 720, acc0, cnt0)
+    assert_bits(host(acc), ra, "grad_accum")
+    assert_bits(host(cnt), rc, "grad_count")
+
+
+def _model(seed, n, degree=3):
+    cam, means, quats, scales, opac, _ = random_scene(seed, n=n, width=160, height=112)
+    rng = np.random.default_rng(100 + seed)
+    sh = (rng.standard_normal((n, 16, 3)) * 0.2).astype(np.float32)
+    ls = np.log(scales).astype(np.float32)
+    lo = np.clip(rng.standard_normal(n), -4, 3).astype(np.float32)
+    raw = dict(means=means, quats=quats, scales=ls, opacities=lo, sh_dc=sh[:, :1].copy(),
+               sh_rest=sh[:, 1:].copy())
+    model = GaussianModel({k: cu(v) for k, v in raw.items()}, sh_degree=3)
+    model.active_sh_degree = degree
+    return cam, model, raw, sh
+
+
+@pytest.mark.parametrize("degree", [0, 3])
+def test_trainer_step_matches_oracle(degree):
+    say(f"trainer step degree {degree}")
+    cam, model, raw, sh = _model(21 + degree, 4000, degree)
+    rng = np.random.default_rng(7)
+    target = rng.random((cam.height, cam.width, 3), dtype=np.float32)
+    cfg = TrainerConfig(densify_from=1, densify_until=100, densify_every=50)
+    tr = GaussianTrainer(model, cfg)
+    p0 = {k: v.copy() for k, v in raw.items()}
+    info = tr.step(cam, cu(target))
+
+    flags = O.LOG_SCALES | O.LOGIT_OPACITY
+    pre, feats, ids, ranges, r = oracle_forward(cam, raw["means"], raw["quats"], raw["scales"],
+                                                raw["opacities"], sh=sh, degree=degree,
+                                                flags=flags)
+    lam = cfg.lambda_dssim
+    l1, s, g_img = O.photometric(r["image"], target, g_l1=1 - lam, g_ssim=-lam, grad=True)
+    loss = (1 - lam) * l1 + lam * (1 - s)
+    say(f"  loss {info['loss']:.8f} vs oracle {loss:.8f}")
+    assert abs(info["loss"] - loss) < 2e-6
+    g = oracle_backward(cam, raw["means"], raw["quats"], raw["scales"], raw["opacities"], pre,
+                        feats, ids, ranges, r, g_img.astype(np.float32), None, sh=sh,
+                        degree=degree, flags=flags)
+    g["sh_dc"], g["sh_rest"] = g["sh"][:, :1], g["sh"][:, 1:]
+    for k in ("means", "quats", "scales", "opacities", "sh_dc", "sh_rest"):
+        st = tr.optimizers[k].state[k]
+        m1, v1 = host(st["m"]), host(st["v"])
+        # first step from zero moments: m = 0.1 g
+        e = rel_err(m1 / np.float32(0.1), g[k])
+        say(f"  grad {k}: rel {e:.2e}")
+        assert e < 1e-3
+        # the update the kernel applied, recomputed in float32 from its moments
+        lr = np.float32(tr.optimizers[k].learning_rate)
+        expect = p0[k] - (lr * m1) / (np.sqrt(v1) + np.float32(1e-15))
+        assert_bits(host(model.params[k]), expect.astype(np.float32), f"update {k}")
+    # screen-space statistics of the rasterizer's dL/dmeans2d
+    ra, rc = O.accum_screen_grads(g["raster"]["means2d"], pre["radii"], cam.width, cam.height,
+                                  np.zeros(4000), np.zeros(4000))
+    np.testing.assert_array_equal(host(tr.grad_count), rc)
+    e = rel_err(host(tr.grad_accum), ra)
+    say(f"  grad_accum rel {e:.2e}")
+    assert e < 1e-3
+
+
+def test_densify_and_prune_matches_oracle():
+    say("densify_and_prune")
+    _, model, raw, _ = _model(31, 3000)
+    # scales are about 0.08: extent 8 puts percent_dense * extent mid-range
+    # (clones and splits); 50 rows below the opacity floor
+    raw["opacities"][:50] = -7.0
+    model.params["opacities"][:50] = -7.0
+    rng = np.random.default_rng(3)
+    acc = (rng.random(3000) * 4e-3).astype(np.float32)
+    cnt = rng.integers(0, 10, 3000).astype(np.float32)
+    np.random.seed(11)
+    stats = model.densify_and_prune(cu(acc), cu(cnt), scene_extent=8.0,
+                                    return_optimizer_state=True)
+    np.random.seed(11)
+    ref, rstats, keep = DN.densify_and_prune(raw, acc, cnt, scene_extent=8.0)
+    say(f"  {stats['cloned']} cloned, {stats['split']} split, {stats['pruned']} pruned")
+    assert {k: stats[k] for k in ("cloned", "split", "pruned")} == rstats
+    assert stats["cloned"] > 0 and stats["split"] > 0 and stats["pruned"] > 0
+    np.testing.assert_array_equal(stats["_keep_idx"], keep)
+    assert stats["_new_count"] == rstats["cloned"] + 2 * rstats["split"]
+    for k, v in ref.items():
+        a = host(model.params[k])
+        assert a.shape == v.shape, k
+        np.testing.assert_allclose(a, v, rtol=2e-6, atol=2e-6, err_msg=k)
+
+
+def test_relocate_mcmc_moves_rows():
+    say("relocate_mcmc")
+    _, model, raw, _ = _model(32, 2000)
+    rng = np.random.default_rng(5)
+    acc = rng.random(2000).astype(np.float32)
+    cnt = rng.integers(0, 4, 2000).astype(np.float32)
+    k, dst, src = DN.relocate_select(raw, acc, cnt, relocate_frac=0.05, min_opacity=0.1)
+    out = model.relocate_mcmc(cu(acc), cu(cnt), relocate_frac=0.05, min_opacity=0.1,
+                              generator=torch.Generator(device="cuda").manual_seed(0))
+    assert out["relocated"] == k == 100
+    np.testing.assert_array_equal(np.sort(host(out["_moved_idx"])), dst)
+    p = {kk: host(v) for kk, v in model.params.items()}
+    moved = np.zeros(2000, bool)
+    moved[dst] = True
+    for kk in raw:
+        np.testing.assert_array_equal(p[kk][~moved], raw[kk][~moved], err_msg=kk)
+    np.testing.assert_allclose(p["opacities"][dst], np.log(0.05 / 0.95), rtol=1e-6)
+    # every moved row is a copy of a source row, up to the rounding of the
+    # reference's scatter-add a + (v - a); log-scales shrink by log 1.6
+    srcv = raw["sh_rest"][src].reshape(len(src), -1)
+    srcs = raw["scales"][src] - np.float32(np.log(1.6))
+    for i in dst:
+        d = np.abs(srcv - p["sh_rest"][i].ravel()).max(axis=1)
+        j = int(np.argmin(d))
+        assert d[j] < 1e-6
+        np.testing.assert_allclose(p["scales"][i], srcs[j], rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("method", ["vanilla", "mcmc", "2dgs"])
+def test_trainer_loop(method):
+    """Fits a random scene to the render of another for 40 steps: the loss
+    falls, density control fires, Adam state follows the table size."""
+    say(f"trainer loop {method}")
+    cam, gt, _, _ = _model(41, 3000)
+    with torch.no_grad():
+        target = gt.render(cam)["image"].detach()
+    _, model, _, _ = _model(42, 2000, degree=0)
+    cfg = TrainerConfig(method=method, densify_from=5, densify_until=30, densify_every=10,
+                        densify_grad_threshold=1e-5, opacity_reset_every=1000,
+                        sh_increase_every=15,
+                        lambda_2d_depth_variance=0.1 if method == "2dgs" else 0.0,
+                        lambda_2d_normal_consistency=0.05 if method == "2dgs" else 0.0)
+    tr = GaussianTrainer(model, cfg, scene_extent=2.0,
+                         generator=torch.Generator(device="cuda").manual_seed(1))
+    losses, events = [], 0
+    for _ in range(40):
+        info = tr.step(cam, target)
+        losses.append(info["loss"])
+        events += info["densify"] is not None
+        n = model.num_gaussians
+        for k, opt in tr.optimizers.items():
+            assert opt.state[k]["m"].shape[0] == n
+        assert np.isfinite(info["loss"])
+    say(f"  loss {losses[0]:.4f} -> {losses[-1]:.4f}, N {model.num_gaussians}, events {events}")
+    assert losses[-1] < 0.9 * losses[0]
+    assert events == 3 and model.active_sh_degree == 2
+    if method == "mcmc":
+        assert model.num_gaussians == 2000
+    else:
+        assert model.num_gaussians != 2000
+    if method == "2dgs":
+        assert float(model.params["scales"][:, 2].max()) <= np.log(1e-4 * 2.0) + 1e-6
