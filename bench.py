@@ -27,6 +27,8 @@ Profiling helpers (used to produce profiles/):
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import math
 import os
@@ -46,6 +48,8 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-stages", action="store_true",
                     help="print per-stage times to stderr")
+    ap.add_argument("--train-steps", type=int, default=12,
+                    help="also time GaussianTrainer.step (SH configs with a backward); 0 = off")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB")
     ap.add_argument("--summarize-prof", metavar="DIR", nargs="+")
     ap.add_argument("--workload", default="c3_1m_sh3_aa_1080p_8views")
@@ -237,6 +241,68 @@ def cpu_baseline(scene, views, cfg_name: str):
             "cpu_model": cpu}
 
 
+@contextlib.contextmanager
+def _no_gc():
+    """Python's cyclic garbage collector off inside a timed region (as timeit
+    does): a collection pass over the autograd objects of earlier steps can
+    stall the host for tens of milliseconds at an arbitrary step."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+
+
+def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool) -> dict:
+    """Times GaussianTrainer.step (trainer.py:319-421): fused render forward and
+    backward, L1 + D-SSIM, Adam over the six groups.  Density control, opacity
+    reset and SH growth are outside the measured steps, so the table keeps
+    its size; the step's own loss readback (float(loss)) is included."""
+    import torch
+
+    from mlx3d_amd.profiling import StageTimer
+    from mlx3d_amd.splatting.trainer import GaussianTrainer, TrainerConfig
+
+    big = 1 << 30
+    cfg = TrainerConfig(densify_from=big, densify_until=big, opacity_reset_every=big,
+                        sh_increase_every=big, antialias=antialias)
+    tr = GaussianTrainer(model, cfg)
+    nviews = len(cams)
+    for i in range(max(warmup, nviews)):
+        tr.step(cams[i % nviews], targets[i % nviews])
+    timer = StageTimer()
+    with timer, _no_gc():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            tr.step(cams[i % nviews], targets[i % nviews])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / steps
+    N = model.num_gaussians
+    P = cams[0].width * cams[0].height
+    floats = sum(int(v[0].numel()) for v in model.params.values())  # per Gaussian
+    algo = {"photometric_fwd": 20 * P * 3, "photometric_bwd": 24 * P * 3,
+            "adam": 28 * N * floats}
+    stages = {}
+    for name in ("preprocess_fwd", "binning", "raster_fwd", "photometric_fwd",
+                 "photometric_bwd", "raster_bwd", "preprocess_bwd", "adam"):
+        t = timer.mean_ms(name)
+        if math.isnan(t):
+            continue
+        stages[name] = {"ms": round(t, 4)}
+        if name in algo:
+            gbs = algo[name] / (t * 1e-3) / 1e9
+            stages[name].update({"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                 "algorithmic_bytes": int(algo[name])})
+    return {"ms": round(ms, 4), "it_s": round(1e3 / ms, 3), "steps": steps,
+            "what": "GaussianTrainer.step: render fwd+bwd, L1 + 0.2 D-SSIM, Adam (6 groups)",
+            "stages": stages}
+
+
 def main():
     args = _parse()
     if args.summarize_prof:
@@ -311,7 +377,7 @@ def main():
     torch.cuda.synchronize()
 
     timer = StageTimer()
-    with timer:
+    with timer, _no_gc():
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(args.steps):
@@ -321,7 +387,7 @@ def main():
     ms_step = (t1 - t0) * 1e3 / args.steps
 
     # forward-only frames per second over the same views
-    with torch.no_grad():
+    with torch.no_grad(), _no_gc():
         torch.cuda.synchronize()
         f0 = time.perf_counter()
         for i in range(args.steps):
@@ -389,6 +455,9 @@ def main():
                      "algorithmic_bytes": int(B[dom]), "mean_ms": stages[dom]["ms"]},
         "stages": stages,
     }
+    if args.train_steps > 0 and scene.backward and not feat_mode:
+        out["train_step"] = train_step(model, cams, targets, args.train_steps, args.warmup,
+                                       scene.antialias)
     if not args.no_cpu_baseline:
         print("bench: timing CPU oracle baseline ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(scene, list(range(nviews)), workload)

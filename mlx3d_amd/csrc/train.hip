@@ -248,7 +248,8 @@ __global__ __launch_bounds__(kSsT * kSsT) void k_ssim_bwd(
 // in float32, each operation rounded once, in this order.
 
 constexpr int kAdamMaxGroups = GSX_ADAM_MAX_GROUPS;
-constexpr int kAdamPerBlock = 1024;  // 256 threads x 4 elements
+constexpr int kAdamThreads = 512;
+constexpr int kAdamPerBlock = kAdamThreads * 4;  // four floats per thread
 
 struct AdamArgs {
     float* p[kAdamMaxGroups];
@@ -269,8 +270,13 @@ __device__ __forceinline__ void adam_one(float& p, float g, float& m, float& v, 
     p = p - (lr * m) / (sqrtf(v) + eps);
 }
 
-__global__ __launch_bounds__(256) void k_adam(AdamArgs a, float b1, float omb1, float b2,
-                                              float omb2, float eps) {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Every element is read and written once per step, far more data than the
+// caches hold: non-temporal loads and stores keep the stream from evicting
+// other data (measured on MI355X: 5.4 -> 5.7-6.1 TB/s on 59M-float groups).
+__global__ __launch_bounds__(kAdamThreads) void k_adam(AdamArgs a, float b1, float omb1, float b2,
+                                                       float omb2, float eps) {
     const int64_t b = blockIdx.x;
     int gi = 0;
     while (gi + 1 < a.count && b >= a.blk[gi + 1]) ++gi;
@@ -283,17 +289,20 @@ __global__ __launch_bounds__(256) void k_adam(AdamArgs a, float b1, float omb1, 
     float* __restrict__ V = a.v[gi];
     const float lr = a.lr[gi];
     if (a.vec[gi] && i0 + 4 <= n) {
-        float4 p = *reinterpret_cast<const float4*>(P + i0);
-        const float4 g = *reinterpret_cast<const float4*>(G + i0);
-        float4 m = *reinterpret_cast<const float4*>(M + i0);
-        float4 v = *reinterpret_cast<const float4*>(V + i0);
-        adam_one(p.x, g.x, m.x, v.x, lr, b1, omb1, b2, omb2, eps);
-        adam_one(p.y, g.y, m.y, v.y, lr, b1, omb1, b2, omb2, eps);
-        adam_one(p.z, g.z, m.z, v.z, lr, b1, omb1, b2, omb2, eps);
-        adam_one(p.w, g.w, m.w, v.w, lr, b1, omb1, b2, omb2, eps);
-        *reinterpret_cast<float4*>(P + i0) = p;
-        *reinterpret_cast<float4*>(M + i0) = m;
-        *reinterpret_cast<float4*>(V + i0) = v;
+        const f32x4 p4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(P + i0));
+        const f32x4 g4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(G + i0));
+        const f32x4 m4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(M + i0));
+        const f32x4 v4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(V + i0));
+        float p[4] = {p4.x, p4.y, p4.z, p4.w}, m[4] = {m4.x, m4.y, m4.z, m4.w};
+        float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        const float g[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) adam_one(p[k], g[k], m[k], v[k], lr, b1, omb1, b2, omb2, eps);
+        const f32x4 po = {p[0], p[1], p[2], p[3]}, mo = {m[0], m[1], m[2], m[3]};
+        const f32x4 vo = {v[0], v[1], v[2], v[3]};
+        __builtin_nontemporal_store(po, reinterpret_cast<f32x4*>(P + i0));
+        __builtin_nontemporal_store(mo, reinterpret_cast<f32x4*>(M + i0));
+        __builtin_nontemporal_store(vo, reinterpret_cast<f32x4*>(V + i0));
         return;
     }
     const int64_t i1 = std::min<int64_t>(i0 + 4, n);
@@ -475,7 +484,7 @@ int gsx_adam_step(int32_t num_groups, const gsx_adam_group* groups, float beta1,
     // (1 - b1) and (1 - b2) are formed in double and rounded once, as the
     // Python scalars of the reference reach the float32 arithmetic.
     const float omb1 = (float)(1.0 - (double)beta1), omb2 = (float)(1.0 - (double)beta2);
-    hipLaunchKernelGGL(k_adam, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, a,
+    hipLaunchKernelGGL(k_adam, dim3((unsigned)blocks), dim3(kAdamThreads), 0, (hipStream_t)stream, a,
                        beta1, omb1, beta2, omb2, eps);
     GSX_LAUNCH_CHECK();
     return GSX_OK;

@@ -12,6 +12,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .profiling import stage
 
 __all__ = ["l1_loss", "photometric", "psnr", "ssim"]
 
@@ -24,11 +25,12 @@ class _PhotometricFn(torch.autograd.Function):
         nbytes = int(L.gsx_photometric_workspace_bytes(H, W, C))
         ws = torch.empty((nbytes,), dtype=torch.uint8, device=pred.device)
         out = torch.empty((2,), dtype=torch.float32, device=pred.device)
-        _lib.check(L.gsx_photometric_fwd(H, W, C, _lib.ptr(pred), _lib.ptr(target),
-                                         int(window_size), float(sigma), float(max_val),
-                                         _lib.ptr(ws), nbytes, _lib.ptr(out),
-                                         _lib.stream_handle(pred.device)),
-                   "gsx_photometric_fwd")
+        with stage("photometric_fwd"):
+            _lib.check(L.gsx_photometric_fwd(H, W, C, _lib.ptr(pred), _lib.ptr(target),
+                                             int(window_size), float(sigma), float(max_val),
+                                             _lib.ptr(ws), nbytes, _lib.ptr(out),
+                                             _lib.stream_handle(pred.device)),
+                       "gsx_photometric_fwd")
         ctx.save_for_backward(pred, target, ws)
         ctx.window = (int(window_size), float(sigma))
         return out
@@ -39,10 +41,11 @@ class _PhotometricFn(torch.autograd.Function):
         H, W, C = pred.shape
         g = _lib.f32c(g_out)
         grad = torch.empty_like(pred)
-        _lib.check(_lib.load().gsx_photometric_bwd(
-            H, W, C, _lib.ptr(pred), _lib.ptr(target), ctx.window[0], ctx.window[1],
-            _lib.ptr(ws), ws.numel(), _lib.ptr(g), _lib.ptr(grad),
-            _lib.stream_handle(pred.device)), "gsx_photometric_bwd")
+        with stage("photometric_bwd"):
+            _lib.check(_lib.load().gsx_photometric_bwd(
+                H, W, C, _lib.ptr(pred), _lib.ptr(target), ctx.window[0], ctx.window[1],
+                _lib.ptr(ws), ws.numel(), _lib.ptr(g), _lib.ptr(grad),
+                _lib.stream_handle(pred.device)), "gsx_photometric_bwd")
         return grad, None, None, None, None
 
 

@@ -24,6 +24,7 @@ from typing import Callable
 import torch
 
 from . import _lib
+from .profiling import stage
 
 __all__ = ["Adam", "adam_step", "exponential_decay"]
 
@@ -116,5 +117,6 @@ def adam_step(updates) -> None:
             arr[k] = _lib.GsxAdamGroup(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
                                        p.numel(), lr)
             keep.append(g)
-        _lib.check(L.gsx_adam_step(len(chunk), ctypes.cast(arr, ctypes.c_void_p), b1, b2, eps,
-                                   _lib.stream_handle(dev)), "gsx_adam_step")
+        with stage("adam"):
+            _lib.check(L.gsx_adam_step(len(chunk), ctypes.cast(arr, ctypes.c_void_p), b1, b2,
+                                       eps, _lib.stream_handle(dev)), "gsx_adam_step")
