@@ -59,7 +59,9 @@ def _parse():
 
 # stage name -> device kernel symbol prefix (as rocprofv3 reports it)
 KERNEL_SYMBOL = {"raster_fwd": "k_raster_fwd", "raster_bwd": "k_raster_bwd",
-                 "preprocess_fwd": "k_preprocess_fwd", "preprocess_bwd": "k_preprocess_bwd"}
+                 "preprocess_fwd": "k_preprocess_fwd", "preprocess_bwd": "k_preprocess_bwd",
+                 "photometric_fwd": "k_ssim_fwd", "photometric_bwd": "k_ssim_bwd",
+                 "adam": "k_adam"}
 COPY_PROBE_KERNEL = "k_debug_expf"
 
 
@@ -256,7 +258,8 @@ def _no_gc():
             gc.enable()
 
 
-def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool) -> dict:
+def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool,
+               workload: str) -> dict:
     """Times GaussianTrainer.step (trainer.py:319-421): fused render forward and
     backward, L1 + D-SSIM, Adam over the six groups.  Density control, opacity
     reset and SH growth are outside the measured steps, so the table keeps
@@ -297,7 +300,8 @@ def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool) -
         if name in algo:
             gbs = algo[name] / (t * 1e-3) / 1e9
             stages[name].update({"GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                                 "algorithmic_bytes": int(algo[name])})
+                                 "algorithmic_bytes": int(algo[name]),
+                                 "traffic": _traffic(name, workload)})
     return {"ms": round(ms, 4), "it_s": round(1e3 / ms, 3), "steps": steps,
             "what": "GaussianTrainer.step: render fwd+bwd, L1 + 0.2 D-SSIM, Adam (6 groups)",
             "stages": stages}
@@ -457,7 +461,7 @@ def main():
     }
     if args.train_steps > 0 and scene.backward and not feat_mode:
         out["train_step"] = train_step(model, cams, targets, args.train_steps, args.warmup,
-                                       scene.antialias)
+                                       scene.antialias, scene.name)
     if not args.no_cpu_baseline:
         print("bench: timing CPU oracle baseline ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(scene, list(range(nviews)), workload)

@@ -41,7 +41,9 @@ using gsx::kWave;
 //   dS_mean/dp = (F(dS/dmu_p) + 2 p F(dS/dE_pp) + t F(dS/dE_pt)) / n.
 
 constexpr int kSsT = 16;                  // output tile edge (16 x 16 threads)
+constexpr int kSsThreads = kSsT * kSsT;
 constexpr int kSsMaxR = 7;                // window radius up to 7 (15 taps)
+constexpr int kSsMaxCh = 4;               // channels per launch
 
 struct SsimWindow {
     float g[2 * kSsMaxR + 1];
@@ -52,51 +54,67 @@ struct SsimTile {
     static constexpr int kSpan = kSsT + 2 * R;
 };
 
-// Loads the (16 + 2R)^2 window of channel c of `src` around the tile into
-// `dst`, zero outside the image.
-template <int R>
-__device__ __forceinline__ void load_halo(float (*dst)[kSsT + 2 * R + 1], const float* __restrict__ src,
-                                          int H, int W, int C, int c, int x0, int y0) {
+// Tile of this workgroup: linear ids go round-robin over the XCDs, and the
+// remap gives each XCD a contiguous band of tiles, so the halo rows that
+// neighbouring tiles share are fetched into one L2.
+__device__ __forceinline__ void ssim_tile(int tiles_x, int& x0, int& y0) {
+    const int t = (int)gsx::xcd_remap(blockIdx.x, gridDim.x);
+    x0 = (t % tiles_x) * kSsT;
+    y0 = (t / tiles_x) * kSsT;
+}
+
+// Loads channels [c0, c0 + CH) of the (16 + 2R)^2 window around the tile into
+// dst[c][y][x], zero outside the image.  Consecutive threads read consecutive
+// floats of the interleaved (H, W, C) rows.
+template <int R, int CH>
+__device__ __forceinline__ void load_halo(float (*dst)[SsimTile<R>::kSpan][SsimTile<R>::kSpan + 1],
+                                          const float* __restrict__ src, int H, int W, int C,
+                                          int c0, int x0, int y0) {
     constexpr int S = SsimTile<R>::kSpan;
-    for (int i = threadIdx.x; i < S * S; i += kSsT * kSsT) {
-        const int ly = i / S, lx = i - ly * S;
+    for (int i = threadIdx.x; i < S * S * CH; i += kSsThreads) {
+        const int ly = i / (S * CH);
+        const int rem = i - ly * (S * CH);
+        const int lx = rem / CH, c = rem - lx * CH;
         const int gy = y0 - R + ly, gx = x0 - R + lx;
         float v = 0.0f;
-        if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = src[((int64_t)gy * W + gx) * C + c];
-        dst[ly][lx] = v;
+        if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = src[((int64_t)gy * W + gx) * C + c0 + c];
+        dst[c][ly][lx] = v;
     }
 }
 
-template <int R>
-__global__ __launch_bounds__(kSsT * kSsT) void k_ssim_fwd(
-    const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C,
-    SsimWindow win, float c1, float c2, float* __restrict__ maps, float* __restrict__ partials) {
+template <int R, int CH>
+__global__ __launch_bounds__(kSsThreads) void k_ssim_fwd(
+    const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C, int c0,
+    int tiles_x, SsimWindow win, float c1, float c2, float* __restrict__ maps,
+    float* __restrict__ partials) {
     constexpr int S = SsimTile<R>::kSpan;
     constexpr int K = 2 * R + 1;
-    __shared__ float s_p[S][S + 1];
-    __shared__ float s_t[S][S + 1];
+    __shared__ float s_p[CH][S][S + 1];
+    __shared__ float s_t[CH][S][S + 1];
     __shared__ float s_h[5][S][kSsT + 1];
-    __shared__ float s_red[2][kSsT * kSsT / kWave];
+    __shared__ float s_red[2][kSsThreads / kWave];
 
     const int tid = threadIdx.x;
     const int tx = tid & (kSsT - 1), ty = tid / kSsT;
-    const int x0 = blockIdx.x * kSsT, y0 = blockIdx.y * kSsT;
+    int x0, y0;
+    ssim_tile(tiles_x, x0, y0);
     const int x = x0 + tx, y = y0 + ty;
     const bool inside = x < W && y < H;
     const int64_t plane = (int64_t)H * W * C;
-    const int64_t pix = ((int64_t)y * W + x) * C;
+    const int64_t pix = ((int64_t)y * W + x) * C + c0;
     float l1 = 0.0f, ssum = 0.0f;
 
-    for (int c = 0; c < C; ++c) {
-        load_halo<R>(s_p, pred, H, W, C, c, x0, y0);
-        load_halo<R>(s_t, tgt, H, W, C, c, x0, y0);
-        __syncthreads();
-        for (int i = tid; i < S * kSsT; i += kSsT * kSsT) {
+    load_halo<R, CH>(s_p, pred, H, W, C, c0, x0, y0);
+    load_halo<R, CH>(s_t, tgt, H, W, C, c0, x0, y0);
+    __syncthreads();
+#pragma unroll 1
+    for (int c = 0; c < CH; ++c) {
+        for (int i = tid; i < S * kSsT; i += kSsThreads) {
             const int ly = i / kSsT, lx = i - ly * kSsT;
             float a = 0.0f, b = 0.0f, pp = 0.0f, tt = 0.0f, pt = 0.0f;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-                const float w = win.g[k], p = s_p[ly][lx + k], t = s_t[ly][lx + k];
+                const float w = win.g[k], p = s_p[c][ly][lx + k], t = s_t[c][ly][lx + k];
                 a = fmaf(w, p, a);
                 b = fmaf(w, t, b);
                 pp = fmaf(w, p * p, pp);
@@ -121,7 +139,7 @@ __global__ __launch_bounds__(kSsT * kSsT) void k_ssim_fwd(
             ept = fmaf(w, s_h[4][ty + k][tx], ept);
         }
         if (inside) {
-            const float p = s_p[ty + R][tx + R], t = s_t[ty + R][tx + R];
+            const float p = s_p[c][ty + R][tx + R], t = s_t[c][ty + R][tx + R];
             const float mpp = mp * mp, mtt = mt * mt, mpt = mp * mt;
             const float A = 2.0f * mpt + c1, B = mpp + mtt + c1;
             const float Cn = 2.0f * (ept - mpt) + c2, D = (epp - mpp) + (ett - mtt) + c2;
@@ -147,13 +165,12 @@ __global__ __launch_bounds__(kSsT * kSsT) void k_ssim_fwd(
     if (tid == 0) {
         float a = 0.0f, b = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kSsT * kSsT / kWave; ++w) {
+        for (int w = 0; w < kSsThreads / kWave; ++w) {
             a += s_red[0][w];
             b += s_red[1][w];
         }
-        const int64_t blk = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-        partials[2 * blk] = a;
-        partials[2 * blk + 1] = b;
+        partials[2 * (int64_t)blockIdx.x] = a;
+        partials[2 * (int64_t)blockIdx.x + 1] = b;
     }
 }
 
@@ -185,38 +202,40 @@ __global__ __launch_bounds__(256) void k_loss_reduce(const float* __restrict__ p
 }
 
 // grad_pred = g_l1 sign(p - t) / n + g_ssim (F(dmu) + 2 p F(dpp) + t F(dpt)) / n
-template <int R>
-__global__ __launch_bounds__(kSsT * kSsT) void k_ssim_bwd(
-    const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C,
-    SsimWindow win, const float* __restrict__ maps, const float* __restrict__ grad_in,
+template <int R, int CH>
+__global__ __launch_bounds__(kSsThreads) void k_ssim_bwd(
+    const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C, int c0,
+    int tiles_x, SsimWindow win, const float* __restrict__ maps, const float* __restrict__ grad_in,
     float inv_n, float* __restrict__ grad) {
     constexpr int S = SsimTile<R>::kSpan;
     constexpr int K = 2 * R + 1;
-    __shared__ float s_m[3][S][S + 1];
+    __shared__ float s_m[3][CH][S][S + 1];
     __shared__ float s_h[3][S][kSsT + 1];
 
     const int tid = threadIdx.x;
     const int tx = tid & (kSsT - 1), ty = tid / kSsT;
-    const int x0 = blockIdx.x * kSsT, y0 = blockIdx.y * kSsT;
+    int x0, y0;
+    ssim_tile(tiles_x, x0, y0);
     const int x = x0 + tx, y = y0 + ty;
     const bool inside = x < W && y < H;
     const int64_t plane = (int64_t)H * W * C;
-    const int64_t pix = ((int64_t)y * W + x) * C;
+    const int64_t pix = ((int64_t)y * W + x) * C + c0;
     const float gl = grad_in[0] * inv_n, gs = grad_in[1] * inv_n;
 
-    for (int c = 0; c < C; ++c) {
 #pragma unroll
-        for (int q = 0; q < 3; ++q) load_halo<R>(s_m[q], maps + q * plane, H, W, C, c, x0, y0);
-        __syncthreads();
-        for (int i = tid; i < S * kSsT; i += kSsT * kSsT) {
+    for (int q = 0; q < 3; ++q) load_halo<R, CH>(s_m[q], maps + q * plane, H, W, C, c0, x0, y0);
+    __syncthreads();
+#pragma unroll 1
+    for (int c = 0; c < CH; ++c) {
+        for (int i = tid; i < S * kSsT; i += kSsThreads) {
             const int ly = i / kSsT, lx = i - ly * kSsT;
             float a = 0.0f, b = 0.0f, d = 0.0f;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
                 const float w = win.g[k];
-                a = fmaf(w, s_m[0][ly][lx + k], a);
-                b = fmaf(w, s_m[1][ly][lx + k], b);
-                d = fmaf(w, s_m[2][ly][lx + k], d);
+                a = fmaf(w, s_m[0][c][ly][lx + k], a);
+                b = fmaf(w, s_m[1][c][ly][lx + k], b);
+                d = fmaf(w, s_m[2][c][ly][lx + k], d);
             }
             s_h[0][ly][lx] = a;
             s_h[1][ly][lx] = b;
@@ -359,6 +378,8 @@ int64_t photometric_blocks(int32_t H, int32_t W) {
     return (int64_t)((W + kSsT - 1) / kSsT) * ((H + kSsT - 1) / kSsT);
 }
 
+int64_t photometric_groups(int32_t C) { return (C + kSsMaxCh - 1) / kSsMaxCh; }
+
 inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
 }  // namespace
@@ -368,7 +389,8 @@ extern "C" {
 int64_t gsx_photometric_workspace_bytes(int32_t height, int32_t width, int32_t channels) {
     if (height <= 0 || width <= 0 || channels <= 0) return 0;
     const int64_t maps = 3 * (int64_t)height * width * channels * (int64_t)sizeof(float);
-    return align256(maps) + align256(2 * photometric_blocks(height, width) * (int64_t)sizeof(float));
+    return align256(maps) + align256(2 * photometric_groups(channels) *
+                                     photometric_blocks(height, width) * (int64_t)sizeof(float));
 }
 
 int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const float* pred,
@@ -387,30 +409,39 @@ int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const f
     float* maps = (float*)workspace;
     float* partials = (float*)((char*)workspace +
                                align256(3 * (int64_t)height * width * channels * 4));
-    const dim3 grid((unsigned)((width + kSsT - 1) / kSsT), (unsigned)((height + kSsT - 1) / kSsT));
+    const int tiles_x = (width + kSsT - 1) / kSsT;
+    const int64_t nblk = photometric_blocks(height, width);
     hipStream_t st = (hipStream_t)stream;
-    switch (window_size / 2) {
-#define GSX_SSIM_FWD(RR)                                                                       \
-    case RR:                                                                                   \
-        hipLaunchKernelGGL(k_ssim_fwd<RR>, grid, dim3(kSsT * kSsT), 0, st, pred, target,      \
-                           height, width, channels, win, c1, c2, maps, partials);              \
+    for (int c0 = 0; c0 < channels; c0 += kSsMaxCh) {
+        const int nc = std::min(kSsMaxCh, channels - c0);
+        float* part = partials + 2 * (c0 / kSsMaxCh) * nblk;
+        const int key = (window_size / 2) * 8 + nc;
+        switch (key) {
+#define GSX_SSIM_FWD(RR, CC)                                                                   \
+    case RR * 8 + CC:                                                                          \
+        hipLaunchKernelGGL((k_ssim_fwd<RR, CC>), dim3((unsigned)nblk), dim3(kSsThreads), 0, st, \
+                           pred, target, height, width, channels, c0, tiles_x, win, c1, c2,     \
+                           maps, part);                                                        \
         break;
-        GSX_SSIM_FWD(0)
-        GSX_SSIM_FWD(1)
-        GSX_SSIM_FWD(2)
-        GSX_SSIM_FWD(3)
-        GSX_SSIM_FWD(4)
-        GSX_SSIM_FWD(5)
-        GSX_SSIM_FWD(6)
-        GSX_SSIM_FWD(7)
+#define GSX_SSIM_FWD_R(RR) GSX_SSIM_FWD(RR, 1) GSX_SSIM_FWD(RR, 2) GSX_SSIM_FWD(RR, 3) GSX_SSIM_FWD(RR, 4)
+            GSX_SSIM_FWD_R(0)
+            GSX_SSIM_FWD_R(1)
+            GSX_SSIM_FWD_R(2)
+            GSX_SSIM_FWD_R(3)
+            GSX_SSIM_FWD_R(4)
+            GSX_SSIM_FWD_R(5)
+            GSX_SSIM_FWD_R(6)
+            GSX_SSIM_FWD_R(7)
+#undef GSX_SSIM_FWD_R
 #undef GSX_SSIM_FWD
-        default:
-            return GSX_ERR_INVALID;
+            default:
+                return GSX_ERR_INVALID;
+        }
+        GSX_LAUNCH_CHECK();
     }
-    GSX_LAUNCH_CHECK();
     const double inv_n = 1.0 / ((double)height * width * channels);
     hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, partials,
-                       photometric_blocks(height, width), inv_n, out);
+                       photometric_groups(channels) * nblk, inv_n, out);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
@@ -427,28 +458,36 @@ int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const f
     if (workspace_bytes < gsx_photometric_workspace_bytes(height, width, channels))
         return GSX_ERR_WORKSPACE;
     const float inv_n = (float)(1.0 / ((double)height * width * channels));
-    const dim3 grid((unsigned)((width + kSsT - 1) / kSsT), (unsigned)((height + kSsT - 1) / kSsT));
+    const int tiles_x = (width + kSsT - 1) / kSsT;
+    const int64_t nblk = photometric_blocks(height, width);
     hipStream_t st = (hipStream_t)stream;
     const float* maps = (const float*)workspace;
-    switch (window_size / 2) {
-#define GSX_SSIM_BWD(RR)                                                                       \
-    case RR:                                                                                   \
-        hipLaunchKernelGGL(k_ssim_bwd<RR>, grid, dim3(kSsT * kSsT), 0, st, pred, target,      \
-                           height, width, channels, win, maps, grad_out, inv_n, grad_pred);    \
+    for (int c0 = 0; c0 < channels; c0 += kSsMaxCh) {
+        const int nc = std::min(kSsMaxCh, channels - c0);
+        const int key = (window_size / 2) * 8 + nc;
+        switch (key) {
+#define GSX_SSIM_BWD(RR, CC)                                                                   \
+    case RR * 8 + CC:                                                                          \
+        hipLaunchKernelGGL((k_ssim_bwd<RR, CC>), dim3((unsigned)nblk), dim3(kSsThreads), 0, st, \
+                           pred, target, height, width, channels, c0, tiles_x, win, maps,       \
+                           grad_out, inv_n, grad_pred);                                        \
         break;
-        GSX_SSIM_BWD(0)
-        GSX_SSIM_BWD(1)
-        GSX_SSIM_BWD(2)
-        GSX_SSIM_BWD(3)
-        GSX_SSIM_BWD(4)
-        GSX_SSIM_BWD(5)
-        GSX_SSIM_BWD(6)
-        GSX_SSIM_BWD(7)
+#define GSX_SSIM_BWD_R(RR) GSX_SSIM_BWD(RR, 1) GSX_SSIM_BWD(RR, 2) GSX_SSIM_BWD(RR, 3) GSX_SSIM_BWD(RR, 4)
+            GSX_SSIM_BWD_R(0)
+            GSX_SSIM_BWD_R(1)
+            GSX_SSIM_BWD_R(2)
+            GSX_SSIM_BWD_R(3)
+            GSX_SSIM_BWD_R(4)
+            GSX_SSIM_BWD_R(5)
+            GSX_SSIM_BWD_R(6)
+            GSX_SSIM_BWD_R(7)
+#undef GSX_SSIM_BWD_R
 #undef GSX_SSIM_BWD
-        default:
-            return GSX_ERR_INVALID;
+            default:
+                return GSX_ERR_INVALID;
+        }
+        GSX_LAUNCH_CHECK();
     }
-    GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
 

@@ -31,7 +31,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("H,W,C,ws,sigma", [(64, 80, 3, 11, 1.5), (37, 53, 3, 11, 1.5),
                                             (5, 7, 3, 11, 1.5), (48, 40, 1, 3, 0.7),
-                                            (33, 29, 2, 15, 2.5), (20, 24, 3, 1, 1.0)])
+                                            (33, 29, 2, 15, 2.5), (20, 24, 3, 1, 1.0),
+                                            (24, 20, 5, 11, 1.5), (17, 35, 8, 7, 1.0)])
 def test_photometric_matches_oracle(H, W, C, ws, sigma):
     say(f"photometric H={H} W={W} C={C} ws={ws}")
     rng = np.random.default_rng(H + W + ws)
