@@ -168,6 +168,90 @@ class GaussianModel:
                                         background=background, normalize=normalize,
                                         antialias=antialias, projection=projection)
 
+    # ------------------------------------------------------------ checkpoints
+    def ply_properties(self) -> list[str]:
+        """Vertex properties of the standard 3DGS PLY layout, in file order
+        (model.py:338-361): x y z nx ny nz f_dc_0..2 f_rest_* opacity
+        scale_0..2 rot_0..3."""
+        n_rest = 3 * self.params["sh_rest"].shape[1]
+        return (["x", "y", "z", "nx", "ny", "nz", "f_dc_0", "f_dc_1", "f_dc_2"]
+                + [f"f_rest_{i}" for i in range(n_rest)] + ["opacity"]
+                + [f"scale_{i}" for i in range(3)] + [f"rot_{i}" for i in range(4)])
+
+    def save_ply(self, path: str) -> None:
+        """Save in the standard 3DGS PLY layout, binary little-endian
+        (model.py:338-361): zero normals, ``f_rest`` channel-major.  The
+        (N, P) float32 table is assembled on the device and written with one
+        device-to-host copy; the bytes are those of ``io.save_ply`` with
+        these properties."""
+        import os
+
+        p = {k: v.detach() for k, v in self.params.items()}
+        n = self.num_gaussians
+        rest = p["sh_rest"].transpose(1, 2).reshape(n, -1)  # channel-major (N, 3 (K-1))
+        cols = [p["means"].reshape(n, 3), torch.zeros_like(p["means"]).reshape(n, 3),
+                p["sh_dc"].reshape(n, 3), rest, p["opacities"].reshape(n, 1),
+                p["scales"].reshape(n, 3), p["quats"].reshape(n, 4)]
+        table = torch.cat([c.to(torch.float32) for c in cols], dim=1).cpu().numpy()
+        header = ["ply", "format binary_little_endian 1.0", f"element vertex {n}"]
+        header += [f"property float {k}" for k in self.ply_properties()]
+        header.append("end_header")
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "wb") as f:
+            f.write(("\n".join(header) + "\n").encode("ascii"))
+            f.write(np.ascontiguousarray(table, dtype="<f4").tobytes())
+
+    @classmethod
+    def load_ply(cls, path: str, sh_degree: int = 3, device=None) -> "GaussianModel":
+        """Load a 3DGS-format PLY checkpoint (model.py:363-392); the SH degree
+        follows the file when its f_rest count disagrees with ``sh_degree``,
+        and the active degree is set to the full degree.  An all-float32
+        binary file goes to ``device`` (default: the GPU when present) as one
+        (N, P) copy and is split there; other files take the generic path."""
+        from ..io import load_ply, read_ply_vertices
+
+        if device is None:
+            device = "cuda" if torch.cuda.is_available() else "cpu"
+        try:
+            names, table = read_ply_vertices(path)
+            t = torch.from_numpy(table).to(device)
+            idx = {k: i for i, k in enumerate(names)}
+
+            def col(k):
+                return t[:, idx[k]]
+        except ValueError:
+            data = load_ply(path)
+            cols = dict(data.extra)
+            cols["x"], cols["y"], cols["z"] = data.verts.unbind(-1)
+            idx = cols
+
+            def col(k):
+                return cols[k].to(device)
+        n_rest = len([k for k in idx if k.startswith("f_rest_")])
+        K = num_sh_bases(sh_degree)
+        if n_rest != 3 * (K - 1):
+            K = n_rest // 3 + 1
+            sh_degree = int(np.sqrt(K)) - 1
+        stack = lambda ks: torch.stack([col(k) for k in ks], dim=-1)  # noqa: E731
+        n = col("x").shape[0]
+        if n_rest > 0:
+            rest = stack([f"f_rest_{i}" for i in range(n_rest)])
+            sh_rest = rest.reshape(n, 3, K - 1).transpose(1, 2)
+        else:
+            sh_rest = torch.zeros((n, K - 1, 3), device=device)
+        params = {
+            "means": stack(["x", "y", "z"]),
+            "scales": stack([f"scale_{i}" for i in range(3)]),
+            "quats": stack([f"rot_{i}" for i in range(4)]),
+            "opacities": col("opacity"),
+            "sh_dc": stack(["f_dc_0", "f_dc_1", "f_dc_2"])[:, None, :],
+            "sh_rest": sh_rest,
+        }
+        model = cls({k: v.to(torch.float32).contiguous() for k, v in params.items()},
+                    sh_degree=sh_degree)
+        model.active_sh_degree = sh_degree
+        return model
+
     # ------------------------------------------------------------ table edits
     # Row edits run on the device; each returns new leaf tensors that keep the
     # requires_grad flag of the ones they replace.
