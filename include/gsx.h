@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define GSX_ABI_VERSION 1
+#define GSX_ABI_VERSION 2
 #define GSX_TILE_SIZE 16 /* tiles.py:14 */
 
 enum gsx_status {
@@ -54,7 +54,16 @@ enum gsx_bin_error {
 enum gsx_flags {
     GSX_LOG_SCALES = 1,     /* scales are log-sigma: exp applied (model.py:116-118)  */
     GSX_LOGIT_OPACITY = 2,  /* opacities are logits: sigmoid (model.py:120-122)      */
-    GSX_ANTIALIAS = 4       /* Mip-Splatting compensation (projection.py:125-129)    */
+    GSX_ANTIALIAS = 4,      /* Mip-Splatting compensation (projection.py:125-129)    */
+    GSX_PROJECT_UT = 8      /* unscented-transform projection (projection.py:149-205)
+                               instead of EWA                                       */
+};
+
+/* Lens model of a gsx_camera (cameras.py:154-172). */
+enum gsx_lens {
+    GSX_LENS_NONE = 0,
+    GSX_LENS_BROWN = 1,     /* Brown-Conrady k1 k2 p1 p2 [k3] (cameras.py:42-51)      */
+    GSX_LENS_FISHEYE = 2    /* OpenCV equidistant k1..k4 (cameras.py:69-77)           */
 };
 
 /* Pinhole camera, OpenCV convention, X_cam = R X_world + t
@@ -70,6 +79,16 @@ typedef struct gsx_camera {
     float lim_x, lim_y;
     float znear;
     int32_t width, height;
+    /* Lens model, used by the UT projection only (the EWA projection is a
+     * pinhole model, as in the reference; cameras.py:290-325).
+     * orthographic != 0: u = fx x_cam + cx, v = fy y_cam + cy.
+     * lens = GSX_LENS_BROWN: dist = {k1, k2, p1, p2, k3, 2 p1, 2 p2} (the
+     * doubled constants formed in double and rounded once, as the
+     * reference's Python scalars reach its float32 arithmetic);
+     * GSX_LENS_FISHEYE: dist = {k1, k2, k3, k4}; unused entries zero. */
+    int32_t orthographic;
+    int32_t lens;
+    float dist[8];
 } gsx_camera;
 
 const char* gsx_strerror(int status);
@@ -95,6 +114,28 @@ int gsx_project_bwd(const gsx_camera* cam, int64_t n, const float* means,
                     const float* g_conics, const float* g_depths,
                     const float* g_compensation, float* g_means,
                     float* g_quats, float* g_scales, void* stream);
+
+/* Replaces project_gaussians_ut (splatting/projection.py:149-205): six
+ * sigma points mean +- sqrt(3) R diag(s) e_k through the camera's
+ * project_points (cameras.py:290-311: perspective or orthographic, with
+ * Brown-Conrady or fisheye distortion), their mean and covariance, then the
+ * EWA path's blur, conic, compensation, radius and validity; depths are the
+ * centres' camera z.  Same arguments and outputs as gsx_project_fwd. */
+int gsx_project_ut_fwd(const gsx_camera* cam, int64_t n, const float* means,
+                       const float* quats, const float* scales, float blur,
+                       int32_t antialias, float* means2d, float* conics,
+                       float* depths, float* radii, float* compensation,
+                       void* stream);
+
+/* VJP of project_gaussians_ut (what MLX autodiff computes through
+ * projection.py:149-205 and cameras.py:42-77, 290-311).  Any cotangent may
+ * be NULL (= zero). */
+int gsx_project_ut_bwd(const gsx_camera* cam, int64_t n, const float* means,
+                       const float* quats, const float* scales, float blur,
+                       int32_t antialias, const float* g_means2d,
+                       const float* g_conics, const float* g_depths,
+                       const float* g_compensation, float* g_means,
+                       float* g_quats, float* g_scales, void* stream);
 
 /* ------------------------------------------------------------------ SH --
  * Replaces eval_sh (splatting/sh.py:41-78): sh (N,K,C), dirs (N,3) ->
@@ -313,6 +354,11 @@ int gsx_accum_screen_grads(int64_t n, const float* g_means2d,
  * metal::exp at rasterize.py:80,171,274) on n inputs; tests check it
  * bit-for-bit against the CPU oracle. */
 int gsx_debug_expf(int64_t n, const float* x, float* y, void* stream);
+
+/* Evaluates the device arctan of the fisheye lens model (the stand-in for
+ * the arctan at cameras.py:72) on n inputs >= 0; tests check it bit for bit
+ * against the CPU oracle. */
+int gsx_debug_atanf(int64_t n, const float* x, float* y, void* stream);
 
 #ifdef __cplusplus
 }

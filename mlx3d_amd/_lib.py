@@ -20,6 +20,7 @@ GSX_OK = 0
 LOG_SCALES = 1
 LOGIT_OPACITY = 2
 ANTIALIAS = 4
+PROJECT_UT = 8
 
 
 class GsxError(RuntimeError):
@@ -42,6 +43,9 @@ class GsxCamera(ctypes.Structure):
         ("znear", ctypes.c_float),
         ("width", ctypes.c_int32),
         ("height", ctypes.c_int32),
+        ("orthographic", ctypes.c_int32),
+        ("lens", ctypes.c_int32),
+        ("dist", ctypes.c_float * 8),
     ]
 
 
@@ -76,6 +80,10 @@ SIGNATURES = {
     "gsx_project_fwd": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _F, _I32, _P, _P, _P, _P, _P, _P]),
     "gsx_project_bwd": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _F, _I32, _P, _P, _P, _P, _P, _P,
                                        _P, _P]),
+    "gsx_project_ut_fwd": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _F, _I32, _P, _P, _P, _P, _P,
+                                          _P]),
+    "gsx_project_ut_bwd": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _F, _I32, _P, _P, _P, _P, _P,
+                                          _P, _P, _P]),
     "gsx_eval_sh_fwd": (ctypes.c_int, [_I64, _I32, _I32, _I32, _P, _P, _P, _P]),
     "gsx_eval_sh_bwd": (ctypes.c_int, [_I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
     "gsx_preprocess_fwd": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _P, _P, _I64, _P, _I64, _I32,
@@ -104,6 +112,7 @@ SIGNATURES = {
     "gsx_adam_step": (ctypes.c_int, [_I32, ctypes.c_void_p, _F, _F, _F, _P]),
     "gsx_accum_screen_grads": (ctypes.c_int, [_I64, _P, _P, _I32, _I32, _P, _P, _P]),
     "gsx_debug_expf": (ctypes.c_int, [_I64, _P, _P, _P]),
+    "gsx_debug_atanf": (ctypes.c_int, [_I64, _P, _P, _P]),
 }
 
 _lib = None

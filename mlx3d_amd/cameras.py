@@ -1,10 +1,13 @@
-"""Pinhole cameras in the OpenCV convention (x right, y down, z forward).
+"""Cameras in the OpenCV convention (x right, y down, z forward).
 
 Mirrors the parts of ``mlx3d.cameras`` the splatting path consumes
-(``src/mlx3d/cameras/cameras.py:32-34, 94-113, 139-273``): ``Camera``,
-``look_at``, ``fov_to_focal``, ``Camera.from_fov``, ``Camera.look_at`` and
-``camera_center``.  ``R`` and ``t`` are float32 CPU tensors, as the
-reference keeps them as float32 arrays; the intrinsics are Python floats.
+(``src/mlx3d/cameras/cameras.py:32-34, 42-113, 139-336``): ``Camera`` with
+its lens model (orthographic, Brown-Conrady or fisheye distortion, used by
+the UT projection), ``look_at``, ``fov_to_focal``, ``Camera.from_fov``,
+``Camera.look_at``, ``Camera.orthographic_camera``, ``camera_center``,
+``project_points`` and ``unproject_points``.  ``R`` and ``t`` are float32
+CPU tensors, as the reference keeps them as float32 arrays; the intrinsics
+are Python floats.
 """
 
 from __future__ import annotations
@@ -40,6 +43,56 @@ def _norm32(v: np.ndarray) -> np.float32:
     return np.float32(np.sqrt(s))
 
 
+def _brown_distort(x, y, c):
+    """Brown-Conrady distortion of normalised coordinates, c = (k1, k2, p1, p2[, k3])
+    (cameras.py:42-51)."""
+    k1, k2, p1, p2 = c[0], c[1], c[2], c[3]
+    k3 = c[4] if len(c) > 4 else 0.0
+    r2 = x * x + y * y
+    radial = 1.0 + r2 * (k1 + r2 * (k2 + r2 * k3))
+    xd = x * radial + 2.0 * p1 * x * y + p2 * (r2 + 2.0 * x * x)
+    yd = y * radial + p1 * (r2 + 2.0 * y * y) + 2.0 * p2 * x * y
+    return xd, yd
+
+
+def _brown_undistort(xd, yd, c, iters: int = 8):
+    """Fixed-point inversion of the Brown-Conrady model (cameras.py:54-66)."""
+    k1, k2, p1, p2 = c[0], c[1], c[2], c[3]
+    k3 = c[4] if len(c) > 4 else 0.0
+    x, y = xd, yd
+    for _ in range(iters):
+        r2 = x * x + y * y
+        radial = 1.0 + r2 * (k1 + r2 * (k2 + r2 * k3))
+        dx = 2.0 * p1 * x * y + p2 * (r2 + 2.0 * x * x)
+        dy = p1 * (r2 + 2.0 * y * y) + 2.0 * p2 * x * y
+        x = (xd - dx) / radial
+        y = (yd - dy) / radial
+    return x, y
+
+
+def _fisheye_distort(x, y, c, eps: float = 1e-9):
+    """OpenCV equidistant fisheye, c = (k1, k2, k3, k4) (cameras.py:69-77)."""
+    k1, k2, k3, k4 = (list(c) + [0.0, 0.0, 0.0, 0.0])[:4]
+    r = torch.sqrt(x * x + y * y)
+    theta = torch.atan(r)
+    th2 = theta * theta
+    theta_d = theta * (1.0 + th2 * (k1 + th2 * (k2 + th2 * (k3 + th2 * k4))))
+    scale = theta_d / torch.clamp(r, min=eps)
+    return x * scale, y * scale
+
+
+def _fisheye_undistort(xd, yd, c, iters: int = 8, eps: float = 1e-9):
+    """Fixed-point inversion of the fisheye model (cameras.py:80-91)."""
+    k1, k2, k3, k4 = (list(c) + [0.0, 0.0, 0.0, 0.0])[:4]
+    theta_d = torch.sqrt(xd * xd + yd * yd)
+    theta = theta_d
+    for _ in range(iters):
+        th2 = theta * theta
+        theta = theta_d / (1.0 + th2 * (k1 + th2 * (k2 + th2 * (k3 + th2 * k4))))
+    scale = torch.tan(theta) / torch.clamp(theta_d, min=eps)
+    return xd * scale, yd * scale
+
+
 def look_at(eye, at, up) -> tuple[torch.Tensor, torch.Tensor]:
     """OpenCV extrinsics ``(R, t)`` with ``X_cam = R X_world + t`` (cameras.py:94-113).
 
@@ -59,12 +112,17 @@ def look_at(eye, at, up) -> tuple[torch.Tensor, torch.Tensor]:
 
 @dataclass
 class Camera:
-    """A pinhole camera (cameras.py:139-173).
+    """A camera (cameras.py:139-173).
 
     Attributes:
         R: (3, 3) world-to-camera rotation.  t: (3,) translation.
         fx, fy, cx, cy: intrinsics in pixels.  width, height: image size.
         znear, zfar: clipping range (only ``znear`` culls Gaussians).
+        orthographic: parallel projection, ``fx``/``fy`` in pixels per world
+            unit.  distortion: Brown-Conrady ``(k1, k2, p1, p2[, k3])``, or
+            fisheye ``(k1, k2, k3, k4)`` with ``fisheye=True``.  The lens
+            model is honoured by ``project_points`` and the UT projection;
+            the EWA projection is pinhole, as in the reference.
     """
 
     R: torch.Tensor
@@ -77,10 +135,32 @@ class Camera:
     height: int
     znear: float = 0.01
     zfar: float = 100.0
+    orthographic: bool = False
+    distortion: tuple | None = None
+    fisheye: bool = False
 
     def __post_init__(self):
         self.R = torch.as_tensor(_as_f32(self.R)).reshape(3, 3)
         self.t = torch.as_tensor(_as_f32(self.t)).reshape(3)
+        if self.distortion is not None:
+            self.distortion = tuple(float(v) for v in self.distortion)
+            n = len(self.distortion)
+            if (self.fisheye and n > 4) or (not self.fisheye and n not in (4, 5)):
+                raise ValueError("distortion must be (k1, k2, p1, p2[, k3]) or, with "
+                                 "fisheye=True, up to (k1, k2, k3, k4).")
+
+    @classmethod
+    def orthographic_camera(cls, scale: float, width: int, height: int, R=None, t=None,
+                            **kwargs) -> "Camera":
+        """Orthographic camera whose view spans [-scale, scale] world units
+        vertically (cameras.py:174-207)."""
+        ppwu = (height / 2.0) / float(scale)
+        if R is None:
+            R = torch.eye(3)
+        if t is None:
+            t = torch.zeros(3)
+        return cls(R=R, t=t, fx=ppwu, fy=ppwu, cx=width / 2.0, cy=height / 2.0, width=width,
+                   height=height, orthographic=True, **kwargs)
 
     @classmethod
     def from_fov(cls, fov: float, width: int, height: int, R=None, t=None, degrees: bool = True,
@@ -138,11 +218,41 @@ class Camera:
         """(X_cam - t) R (cameras.py:286-288)."""
         return (points - self.t.to(points.device)) @ self.R.to(points.device)
 
+    def _distort(self, x, y):
+        if self.distortion is None:
+            return x, y
+        if self.fisheye:
+            return _fisheye_distort(x, y, self.distortion)
+        return _brown_distort(x, y, self.distortion)
+
+    def _undistort(self, x, y):
+        if self.distortion is None:
+            return x, y
+        if self.fisheye:
+            return _fisheye_undistort(x, y, self.distortion)
+        return _brown_undistort(x, y, self.distortion)
+
+    def project_points(self, points: torch.Tensor, eps: float = 1e-8):
+        """World points (..., 3) to (pixel coordinates (..., 2), camera z (...,))
+        (cameras.py:290-311)."""
+        pc = self.world_to_camera(points)
+        z = pc[..., 2]
+        if self.orthographic:
+            u = self.fx * pc[..., 0] + self.cx
+            v = self.fy * pc[..., 1] + self.cy
+            return torch.stack([u, v], dim=-1), z
+        inv_z = 1.0 / torch.where(z.abs() < eps, torch.full_like(z, eps), z)
+        x, y = self._distort(pc[..., 0] * inv_z, pc[..., 1] * inv_z)
+        return torch.stack([self.fx * x + self.cx, self.fy * y + self.cy], dim=-1), z
+
     def unproject_points(self, xy: torch.Tensor, depth: torch.Tensor) -> torch.Tensor:
         """Pixel coordinates (..., 2) with z-depths (...,) to world points
-        (cameras.py:327-336, pinhole)."""
+        (cameras.py:327-336)."""
         x = (xy[..., 0] - self.cx) / self.fx
         y = (xy[..., 1] - self.cy) / self.fy
+        if self.orthographic:
+            return self.camera_to_world(torch.stack([x, y, depth], dim=-1))
+        x, y = self._undistort(x, y)
         return self.camera_to_world(torch.stack([x * depth, y * depth, depth], dim=-1))
 
     def gsx_fields(self) -> dict:
@@ -166,7 +276,30 @@ class Camera:
             znear=float(np.float32(self.znear)),
             width=int(self.width),
             height=int(self.height),
+            orthographic=int(bool(self.orthographic)),
+            lens=self._lens_code(),
+            dist=self._lens_coefficients(),
         )
+
+    def _lens_code(self) -> int:
+        if self.distortion is None:
+            return 0
+        return 2 if self.fisheye else 1
+
+    def _lens_coefficients(self) -> list[float]:
+        """The float32 constants of the lens formulas: Brown k1 k2 p1 p2 k3 and
+        2 p1, 2 p2 (products of Python floats, rounded once); fisheye k1..k4."""
+        d = [0.0] * 8
+        if self.distortion is None:
+            return d
+        c = list(self.distortion)
+        if self.fisheye:
+            c = (c + [0.0] * 4)[:4]
+            d[:4] = c
+        else:
+            k3 = c[4] if len(c) > 4 else 0.0
+            d[:7] = [c[0], c[1], c[2], c[3], k3, 2.0 * c[2], 2.0 * c[3]]
+        return [float(np.float32(v)) for v in d]
 
     def to_gsx(self):
         """ctypes ``gsx_camera`` for the C ABI."""
@@ -177,6 +310,8 @@ class Camera:
         cam.R[:] = [float(v) for v in f["R"]]
         cam.t[:] = [float(v) for v in f["t"]]
         cam.center[:] = [float(v) for v in f["center"]]
-        for k in ("fx", "fy", "cx", "cy", "lim_x", "lim_y", "znear", "width", "height"):
+        for k in ("fx", "fy", "cx", "cy", "lim_x", "lim_y", "znear", "width", "height",
+                  "orthographic", "lens"):
             setattr(cam, k, f[k])
+        cam.dist[:] = f["dist"]
         return cam

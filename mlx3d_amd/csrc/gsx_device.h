@@ -150,6 +150,56 @@ __device__ __forceinline__ void project(const gsx_camera& cam, float m0, float m
     }
 }
 
+// Gradient of the raw quaternion from the gradient G of the rotation matrix
+// of its normalisation qn = q / |q| (rotations.py:30-49, projection.py:94-105).
+__device__ __forceinline__ void quat_vjp(const float* qn, float qnorm, const float* G,
+                                         float* g_q) {
+    const float w = qn[0], x = qn[1], y = qn[2], z = qn[3];
+    float gqn[4];
+    gqn[0] = 2.0f * (-z * G[1] + y * G[2] + z * G[3] - x * G[5] - y * G[6] + x * G[7]);
+    gqn[1] = 2.0f * (y * G[1] + z * G[2] + y * G[3] - 2.0f * x * G[4] - w * G[5] + z * G[6] +
+                     w * G[7] - 2.0f * x * G[8]);
+    gqn[2] = 2.0f * (-2.0f * y * G[0] + x * G[1] + w * G[2] + x * G[3] + z * G[5] - w * G[6] +
+                     z * G[7] - 2.0f * y * G[8]);
+    gqn[3] = 2.0f * (-2.0f * z * G[0] - w * G[1] + x * G[2] + w * G[3] - 2.0f * z * G[4] +
+                     y * G[5] + x * G[6] + y * G[7]);
+    const float dot = w * gqn[0] + x * gqn[1] + y * gqn[2] + z * gqn[3];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) g_q[k] = (gqn[k] - qn[k] * dot) / qnorm;
+}
+
+// Gradient of the screen covariance (a0, b, c0) (before blur) from the
+// cotangents of the conic (A, B, C) = (c, -b, a) / max(det, 1e-12) and of the
+// antialiasing compensation sqrt(max(a0 c0 - b^2, 0) / max(det, 1e-12))
+// (projection.py:115-129); max passes gradient only strictly inside.
+__device__ __forceinline__ void cov2d_vjp(float a0, float b, float c0, float a, float c,
+                                          float det, float ds, float A, float B, float C,
+                                          float comp, bool valid, bool aa, float gA, float gB,
+                                          float gC, float gcomp, float& g_a0_out,
+                                          float& g_b_out, float& g_c0_out) {
+    float g_a = gC / ds, g_b = -gB / ds, g_c = gA / ds;
+    float g_a0 = 0.0f, g_c0 = 0.0f;
+    float g_ds = -(gA * A + gB * B + gC * C) / ds;
+    if (aa && valid) {
+        const float det0 = a0 * c0 - b * b;
+        if (det0 > 0.0f && comp > 0.0f) {
+            const float g_r = gcomp * 0.5f / comp;
+            const float g_det0 = g_r / ds;
+            g_ds += -g_r * (det0 / ds) / ds;
+            g_a0 += g_det0 * c0;
+            g_c0 += g_det0 * a0;
+            g_b += -2.0f * b * g_det0;
+        }
+    }
+    const float g_det = (det > 1e-12f) ? g_ds : 0.0f;
+    g_a += g_det * c;
+    g_c += g_det * a;
+    g_b += -2.0f * b * g_det;
+    g_a0_out = g_a0 + g_a;
+    g_c0_out = g_c0 + g_c;
+    g_b_out = g_b;
+}
+
 // Reverse-mode derivative of project(): cotangents of (u, v), conic
 // (A, B, C), z and comp -> gradients of the mean, raw quaternion and
 // (activated) scales.  max/clip pass gradient strictly inside their active
@@ -159,26 +209,9 @@ __device__ __forceinline__ void project_vjp(const gsx_camera& cam, const Proj& p
                                             float gz_in, float gcomp, float* g_m, float* g_q,
                                             float* g_s) {
     const float* R = cam.R;
-    float g_a = gC / p.ds, g_b = -gB / p.ds, g_c = gA / p.ds;
-    float g_a0 = 0.0f, g_c0 = 0.0f;
-    float g_ds = -(gA * p.A + gB * p.B + gC * p.C) / p.ds;
-    if (aa && p.valid) {
-        const float det0 = p.a0 * p.c0 - p.b * p.b;
-        if (det0 > 0.0f && p.comp > 0.0f) {
-            const float g_r = gcomp * 0.5f / p.comp;
-            const float g_det0 = g_r / p.ds;
-            g_ds += -g_r * (det0 / p.ds) / p.ds;
-            g_a0 += g_det0 * p.c0;
-            g_c0 += g_det0 * p.a0;
-            g_b += -2.0f * p.b * g_det0;
-        }
-    }
-    const float g_det = (p.det > 1e-12f) ? g_ds : 0.0f;
-    g_a += g_det * p.c;
-    g_c += g_det * p.a;
-    g_b += -2.0f * p.b * g_det;
-    g_a0 += g_a;
-    g_c0 += g_c;
+    float g_a0, g_b, g_c0;
+    cov2d_vjp(p.a0, p.b, p.c0, p.a, p.c, p.det, p.ds, p.A, p.B, p.C, p.comp, p.valid, aa, gA,
+              gB, gC, gcomp, g_a0, g_b, g_c0);
     float gM[6], gP[6];
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
@@ -232,19 +265,315 @@ __device__ __forceinline__ void project_vjp(const gsx_camera& cam, const Proj& p
     const float g_z = gz_in + ((p.z > 1e-6f) ? g_zs : 0.0f);
 #pragma unroll
     for (int j = 0; j < 3; ++j) g_m[j] = R[j] * g_x + R[3 + j] * g_y + R[6 + j] * g_z;
-    const float w = p.qn[0], x = p.qn[1], y = p.qn[2], z = p.qn[3];
-    const float* G = gRq;
-    float gqn[4];
-    gqn[0] = 2.0f * (-z * G[1] + y * G[2] + z * G[3] - x * G[5] - y * G[6] + x * G[7]);
-    gqn[1] = 2.0f * (y * G[1] + z * G[2] + y * G[3] - 2.0f * x * G[4] - w * G[5] + z * G[6] +
-                     w * G[7] - 2.0f * x * G[8]);
-    gqn[2] = 2.0f * (-2.0f * y * G[0] + x * G[1] + w * G[2] + x * G[3] + z * G[5] - w * G[6] +
-                     z * G[7] - 2.0f * y * G[8]);
-    gqn[3] = 2.0f * (-2.0f * z * G[0] - w * G[1] + x * G[2] + w * G[3] - 2.0f * z * G[4] +
-                     y * G[5] + x * G[6] + y * G[7]);
-    const float dot = w * gqn[0] + x * gqn[1] + y * gqn[2] + z * gqn[3];
+    quat_vjp(p.qn, p.qnorm, gRq, g_q);
+}
+
+// ----------------------------------------------------------------- UT --
+// project_gaussians_ut (projection.py:149-205) with the camera's
+// project_points (cameras.py:290-311) and lens models (cameras.py:42-77).
+// World-to-camera products are summed left to right as in project();
+// means over the six sigma points are sums (in point order) times
+// float32(1/6).  The CPU oracle evaluates the same operations.
+
+constexpr float kSqrt3 = 1.73205077648162841796875f;  // float32(sqrt(3))
+constexpr float kSixth = 0.16666667163372039794921875f;  // float32(1/6)
+
+// arctan(r), r >= 0, from the Taylor series: arctan r = pi/2 - arctan(1/r)
+// above 1 and arctan x = pi/4 + arctan((x - 1)/(x + 1)) above tan(pi/8) leave
+// |y| <= tan(pi/8), where y - y^3/3 + ... - y^19/19 + y^21/21 (truncation
+// below 2e-10 relative) is evaluated in Horner form with fused
+// multiply-adds.  Stands in for the arctan of the fisheye model
+// (cameras.py:72); the CPU oracle uses the same sequence.
+__device__ __forceinline__ float datan_pos(float r) {
+    const bool big = r > 1.0f;
+    const float x = big ? 1.0f / r : r;
+    const bool mid = x > 0.414213562373095049f;
+    const float y = mid ? (x - 1.0f) / (x + 1.0f) : x;
+    const float y2 = y * y;
+    float q = 4.76190476190476191e-02f;
+    q = fmaf(q, y2, -5.26315789473684211e-02f);
+    q = fmaf(q, y2, 5.88235294117647059e-02f);
+    q = fmaf(q, y2, -6.66666666666666667e-02f);
+    q = fmaf(q, y2, 7.69230769230769231e-02f);
+    q = fmaf(q, y2, -9.09090909090909091e-02f);
+    q = fmaf(q, y2, 1.11111111111111111e-01f);
+    q = fmaf(q, y2, -1.42857142857142857e-01f);
+    q = fmaf(q, y2, 2.0e-01f);
+    q = fmaf(q, y2, -3.33333333333333333e-01f);
+    float a = fmaf(y * y2, q, y);
+    // pi/4 and pi/2 as float32 head + tail: the tail joins the small term first
+    if (mid) a = 0.785398185253143310546875f + (a + -2.18556950752568e-08f);
+    return big ? 1.57079637050628662109375f + (-4.37113900018624e-08f - a) : a;
+}
+
+__device__ __forceinline__ void cam_point(const gsx_camera& cam, float px, float py, float pz,
+                                          float& x, float& y, float& z) {
+    const float* R = cam.R;
+    x = px * R[0] + py * R[1] + pz * R[2] + cam.t[0];
+    y = px * R[3] + py * R[4] + pz * R[5] + cam.t[1];
+    z = px * R[6] + py * R[7] + pz * R[8] + cam.t[2];
+}
+
+// Lens distortion of normalised coordinates (cameras.py:42-51, 69-77).
+__device__ __forceinline__ void distort(const gsx_camera& cam, float x, float y, float& xd,
+                                        float& yd) {
+    const float* d = cam.dist;
+    if (cam.lens == GSX_LENS_BROWN) {
+        const float r2 = x * x + y * y;
+        const float radial = 1.0f + r2 * (d[0] + r2 * (d[1] + r2 * d[4]));
+        xd = x * radial + d[5] * x * y + d[3] * (r2 + 2.0f * x * x);
+        yd = y * radial + d[2] * (r2 + 2.0f * y * y) + d[6] * x * y;
+    } else if (cam.lens == GSX_LENS_FISHEYE) {
+        const float r = sqrtf(x * x + y * y);
+        const float th = datan_pos(r);
+        const float th2 = th * th;
+        const float thd = th * (1.0f + th2 * (d[0] + th2 * (d[1] + th2 * (d[2] + th2 * d[3]))));
+        const float scale = thd / fmaxf(r, 1e-9f);
+        xd = x * scale;
+        yd = y * scale;
+    } else {
+        xd = x;
+        yd = y;
+    }
+}
+
+// Cotangent of (x, y) from that of the distorted (xd, yd).
+__device__ __forceinline__ void distort_vjp(const gsx_camera& cam, float x, float y, float gxd,
+                                            float gyd, float& gx, float& gy) {
+    const float* d = cam.dist;
+    if (cam.lens == GSX_LENS_BROWN) {
+        const float r2 = x * x + y * y;
+        const float radial = 1.0f + r2 * (d[0] + r2 * (d[1] + r2 * d[4]));
+        const float dr = d[0] + r2 * (2.0f * d[1] + 3.0f * d[4] * r2);  // d radial / d r2
+        const float xy2 = 2.0f * x * y * dr;
+        const float dxdx = radial + 2.0f * x * x * dr + 2.0f * d[2] * y + 6.0f * d[3] * x;
+        const float dxdy = xy2 + 2.0f * d[2] * x + 2.0f * d[3] * y;
+        const float dydy = radial + 2.0f * y * y * dr + 6.0f * d[2] * y + 2.0f * d[3] * x;
+        gx = gxd * dxdx + gyd * dxdy;
+        gy = gxd * dxdy + gyd * dydy;
+    } else if (cam.lens == GSX_LENS_FISHEYE) {
+        const float r = sqrtf(x * x + y * y);
+        const float th = datan_pos(r);
+        const float th2 = th * th;
+        const float thd = th * (1.0f + th2 * (d[0] + th2 * (d[1] + th2 * (d[2] + th2 * d[3]))));
+        const float rs = fmaxf(r, 1e-9f);
+        const float scale = thd / rs;
+        const float dthd = 1.0f + th2 * (3.0f * d[0] + th2 * (5.0f * d[1] +
+                                         th2 * (7.0f * d[2] + th2 * 9.0f * d[3])));
+        float ds_dr = dthd / (1.0f + r * r) / rs;
+        if (r > 1e-9f) ds_dr -= thd / (rs * rs);
+        gx = gxd * scale;
+        gy = gyd * scale;
+        if (r > 0.0f) {
+            const float g_r = (gxd * x + gyd * y) * ds_dr;
+            gx += g_r * x / r;
+            gy += g_r * y / r;
+        }
+    } else {
+        gx = gxd;
+        gy = gyd;
+    }
+}
+
+// Camera.project_points of one world point (cameras.py:290-311).
+__device__ __forceinline__ void ut_point(const gsx_camera& cam, float px, float py, float pz,
+                                         float& u, float& v) {
+    float x, y, z;
+    cam_point(cam, px, py, pz, x, y, z);
+    if (cam.orthographic) {
+        u = cam.fx * x + cam.cx;
+        v = cam.fy * y + cam.cy;
+        return;
+    }
+    const float inv = 1.0f / (fabsf(z) < 1e-8f ? 1e-8f : z);
+    float xd, yd;
+    distort(cam, x * inv, y * inv, xd, yd);
+    u = cam.fx * xd + cam.cx;
+    v = cam.fy * yd + cam.cy;
+}
+
+// Cotangent of the world point from that of its pixel coordinates.
+__device__ __forceinline__ void ut_point_vjp(const gsx_camera& cam, float px, float py, float pz,
+                                             float gu, float gv, float* gp) {
+    float x, y, z;
+    cam_point(cam, px, py, pz, x, y, z);
+    float gcx, gcy, gcz = 0.0f;
+    if (cam.orthographic) {
+        gcx = cam.fx * gu;
+        gcy = cam.fy * gv;
+    } else {
+        const bool tiny = fabsf(z) < 1e-8f;
+        const float inv = 1.0f / (tiny ? 1e-8f : z);
+        float gx, gy;
+        distort_vjp(cam, x * inv, y * inv, cam.fx * gu, cam.fy * gv, gx, gy);
+        gcx = gx * inv;
+        gcy = gy * inv;
+        if (!tiny) gcz = -(gx * x + gy * y) * inv * inv;
+    }
+    const float* R = cam.R;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) g_q[k] = (gqn[k] - p.qn[k] * dot) / p.qnorm;
+    for (int j = 0; j < 3; ++j) gp[j] = R[j] * gcx + R[3 + j] * gcy + R[6 + j] * gcz;
+}
+
+struct ProjUT {
+    float u, v, z, A, B, C, comp, radius;
+    bool valid;
+    float qnorm, qn[4], Rq[9], s[3];
+    float a0, b, c0, a, c, det, ds;
+    float du[6], dv[6];
+};
+
+// Sigma point k of the mean m: m + sqrt(3) (+-) column (k mod 3) of R diag(s).
+__device__ __forceinline__ void ut_sigma(const ProjUT& p, float m0, float m1, float m2, int k,
+                                         float* q) {
+    const int j = k % 3;
+    const float sg = k < 3 ? 1.0f : -1.0f;
+    q[0] = m0 + kSqrt3 * (sg * (p.Rq[j] * p.s[j]));
+    q[1] = m1 + kSqrt3 * (sg * (p.Rq[3 + j] * p.s[j]));
+    q[2] = m2 + kSqrt3 * (sg * (p.Rq[6 + j] * p.s[j]));
+}
+
+__device__ __forceinline__ void project_ut(const gsx_camera& cam, float m0, float m1, float m2,
+                                           float q0, float q1, float q2, float q3, float s0,
+                                           float s1, float s2, float blur, bool aa, ProjUT& p) {
+    p.qnorm = sqrtf(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3);
+    const float w = q0 / p.qnorm, x = q1 / p.qnorm, y = q2 / p.qnorm, z = q3 / p.qnorm;
+    p.qn[0] = w;
+    p.qn[1] = x;
+    p.qn[2] = y;
+    p.qn[3] = z;
+    p.Rq[0] = 1.0f - 2.0f * (y * y + z * z);
+    p.Rq[1] = 2.0f * (x * y - w * z);
+    p.Rq[2] = 2.0f * (x * z + w * y);
+    p.Rq[3] = 2.0f * (x * y + w * z);
+    p.Rq[4] = 1.0f - 2.0f * (x * x + z * z);
+    p.Rq[5] = 2.0f * (y * z - w * x);
+    p.Rq[6] = 2.0f * (x * z - w * y);
+    p.Rq[7] = 2.0f * (y * z + w * x);
+    p.Rq[8] = 1.0f - 2.0f * (x * x + y * y);
+    p.s[0] = s0;
+    p.s[1] = s1;
+    p.s[2] = s2;
+    float us[6], vs[6];
+    float su = 0.0f, sv = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        float q[3];
+        ut_sigma(p, m0, m1, m2, k, q);
+        ut_point(cam, q[0], q[1], q[2], us[k], vs[k]);
+        su = k ? su + us[k] : us[k];
+        sv = k ? sv + vs[k] : vs[k];
+    }
+    p.u = su * kSixth;
+    p.v = sv * kSixth;
+    float saa = 0.0f, sab = 0.0f, scc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        p.du[k] = us[k] - p.u;
+        p.dv[k] = vs[k] - p.v;
+        const float aa_k = p.du[k] * p.du[k], ab_k = p.du[k] * p.dv[k], cc_k = p.dv[k] * p.dv[k];
+        saa = k ? saa + aa_k : aa_k;
+        sab = k ? sab + ab_k : ab_k;
+        scc = k ? scc + cc_k : cc_k;
+    }
+    p.a0 = saa * kSixth;
+    p.b = sab * kSixth;
+    p.c0 = scc * kSixth;
+    p.a = p.a0 + blur;
+    p.c = p.c0 + blur;
+    p.det = p.a * p.c - p.b * p.b;
+    p.ds = fmaxf(p.det, 1e-12f);
+    p.A = p.c / p.ds;
+    p.B = -p.b / p.ds;
+    p.C = p.a / p.ds;
+    p.comp = aa ? sqrtf(fmaxf(p.a0 * p.c0 - p.b * p.b, 0.0f) / p.ds) : 1.0f;
+    const float mid = 0.5f * (p.a + p.c);
+    const float lam1 = mid + sqrtf(fmaxf(mid * mid - p.det, 0.01f));
+    p.radius = ceilf(3.0f * sqrtf(fmaxf(lam1, 0.0f)));
+    const float* R = cam.R;
+    p.z = m0 * R[6] + m1 * R[7] + m2 * R[8] + cam.t[2];
+    p.valid = (p.z > cam.znear) && (p.det > 0.0f);
+    if (!p.valid) {
+        p.radius = 0.0f;
+        p.comp = 0.0f;
+    }
+}
+
+// Reverse-mode derivative of project_ut().  The sigma-point covariance
+// is differentiated as (1/6) sum du dv^T with du = u_k - mean: the terms
+// through the mean drop out because sum_k du_k = 0.
+__device__ __forceinline__ void project_ut_vjp(const gsx_camera& cam, const ProjUT& p, float m0,
+                                               float m1, float m2, bool aa, float gu, float gv,
+                                               float gA, float gB, float gC, float gz_in,
+                                               float gcomp, float* g_m, float* g_q,
+                                               float* g_s) {
+    float g_a0, g_b, g_c0;
+    cov2d_vjp(p.a0, p.b, p.c0, p.a, p.c, p.det, p.ds, p.A, p.B, p.C, p.comp, p.valid, aa, gA,
+              gB, gC, gcomp, g_a0, g_b, g_c0);
+    float gM[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) gM[i] = 0.0f;
+    g_m[0] = g_m[1] = g_m[2] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const float guk = (gu + 2.0f * p.du[k] * g_a0 + p.dv[k] * g_b) * kSixth;
+        const float gvk = (gv + p.du[k] * g_b + 2.0f * p.dv[k] * g_c0) * kSixth;
+        float q[3], gp[3];
+        ut_sigma(p, m0, m1, m2, k, q);
+        ut_point_vjp(cam, q[0], q[1], q[2], guk, gvk, gp);
+        const int j = k % 3;
+        const float sg = k < 3 ? kSqrt3 : -kSqrt3;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            g_m[i] += gp[i];
+            gM[3 * i + j] += sg * gp[i];
+        }
+    }
+    const float* R = cam.R;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) g_m[j] += R[6 + j] * gz_in;
+    float gRq[9];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        g_s[j] = gM[j] * p.Rq[j] + gM[3 + j] * p.Rq[3 + j] + gM[6 + j] * p.Rq[6 + j];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) gRq[3 * i + j] = gM[3 * i + j] * p.s[j];
+    }
+    quat_vjp(p.qn, p.qnorm, gRq, g_q);
+}
+
+// Projection selected at compile time: EWA (project) or UT (project_ut).
+template <bool UT>
+struct ProjOf {
+    using T = Proj;
+};
+template <>
+struct ProjOf<true> {
+    using T = ProjUT;
+};
+
+template <bool UT>
+__device__ __forceinline__ void project_any(const gsx_camera& cam, float m0, float m1, float m2,
+                                            float q0, float q1, float q2, float q3, float s0,
+                                            float s1, float s2, float blur, bool aa,
+                                            typename ProjOf<UT>::T& p) {
+    if constexpr (UT)
+        project_ut(cam, m0, m1, m2, q0, q1, q2, q3, s0, s1, s2, blur, aa, p);
+    else
+        project(cam, m0, m1, m2, q0, q1, q2, q3, s0, s1, s2, blur, aa, p);
+}
+
+template <bool UT>
+__device__ __forceinline__ void project_any_vjp(const gsx_camera& cam,
+                                                const typename ProjOf<UT>::T& p, float m0,
+                                                float m1, float m2, bool aa, float gu, float gv,
+                                                float gA, float gB, float gC, float gz,
+                                                float gcomp, float* g_m, float* g_q,
+                                                float* g_s) {
+    if constexpr (UT)
+        project_ut_vjp(cam, p, m0, m1, m2, aa, gu, gv, gA, gB, gC, gz, gcomp, g_m, g_q, g_s);
+    else
+        project_vjp(cam, p, aa, gu, gv, gA, gB, gC, gz, gcomp, g_m, g_q, g_s);
 }
 
 // ----------------------------------------------------------------- SH --

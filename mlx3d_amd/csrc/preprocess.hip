@@ -78,6 +78,7 @@ __device__ __forceinline__ void lds_to_rows(const float* s, int pad, float* __re
     }
 }
 
+template <bool UT>
 __global__ __launch_bounds__(kThreads) void k_project_fwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, float blur, bool aa, float2* __restrict__ means2d,
@@ -86,9 +87,9 @@ __global__ __launch_bounds__(kThreads) void k_project_fwd(
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
     const float4 q = quats[i];
-    Proj p;
-    project(cam, means[3 * i], means[3 * i + 1], means[3 * i + 2], q.x, q.y, q.z, q.w,
-            scales[3 * i], scales[3 * i + 1], scales[3 * i + 2], blur, aa, p);
+    typename ProjOf<UT>::T p;
+    project_any<UT>(cam, means[3 * i], means[3 * i + 1], means[3 * i + 2], q.x, q.y, q.z, q.w,
+                    scales[3 * i], scales[3 * i + 1], scales[3 * i + 2], blur, aa, p);
     means2d[i] = make_float2(p.u, p.v);
     conics[3 * i] = p.A;
     conics[3 * i + 1] = p.B;
@@ -98,6 +99,7 @@ __global__ __launch_bounds__(kThreads) void k_project_fwd(
     comp[i] = p.comp;
 }
 
+template <bool UT>
 __global__ __launch_bounds__(kThreads) void k_project_bwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, float blur, bool aa, const float2* __restrict__ g_means2d,
@@ -107,14 +109,16 @@ __global__ __launch_bounds__(kThreads) void k_project_bwd(
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
     const float4 q = quats[i];
-    Proj p;
-    project(cam, means[3 * i], means[3 * i + 1], means[3 * i + 2], q.x, q.y, q.z, q.w,
-            scales[3 * i], scales[3 * i + 1], scales[3 * i + 2], blur, aa, p);
+    const float m0 = means[3 * i], m1 = means[3 * i + 1], m2 = means[3 * i + 2];
+    typename ProjOf<UT>::T p;
+    project_any<UT>(cam, m0, m1, m2, q.x, q.y, q.z, q.w, scales[3 * i], scales[3 * i + 1],
+                    scales[3 * i + 2], blur, aa, p);
     const float2 gm2 = g_means2d ? g_means2d[i] : make_float2(0.0f, 0.0f);
     float gm[3], gq[4], gs[3];
-    project_vjp(cam, p, aa, gm2.x, gm2.y, g_conics ? g_conics[3 * i] : 0.0f,
-                g_conics ? g_conics[3 * i + 1] : 0.0f, g_conics ? g_conics[3 * i + 2] : 0.0f,
-                g_depths ? g_depths[i] : 0.0f, g_comp ? g_comp[i] : 0.0f, gm, gq, gs);
+    project_any_vjp<UT>(cam, p, m0, m1, m2, aa, gm2.x, gm2.y,
+                        g_conics ? g_conics[3 * i] : 0.0f, g_conics ? g_conics[3 * i + 1] : 0.0f,
+                        g_conics ? g_conics[3 * i + 2] : 0.0f, g_depths ? g_depths[i] : 0.0f,
+                        g_comp ? g_comp[i] : 0.0f, gm, gq, gs);
     g_means[3 * i] = gm[0];
     g_means[3 * i + 1] = gm[1];
     g_means[3 * i + 2] = gm[2];
@@ -228,6 +232,7 @@ __global__ __launch_bounds__(kThreads) void k_eval_sh_bwd(int64_t n, int K, int 
 // binning rectangle/count and depth key for one Gaussian per lane.  SH
 // coefficients come through LDS (sh_mode: split = rest rows staged, DC read
 // directly; packed = whole rows of 3 Ka floats staged; direct = no staging).
+template <bool UT>
 __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities,
@@ -254,8 +259,8 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     const float sy = act_scale(scales[3 * i + 1], flags);
     const float sz = act_scale(scales[3 * i + 2], flags);
     const float o = act_opacity(opacities[i], flags);
-    Proj p;
-    project(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
+    typename ProjOf<UT>::T p;
+    project_any<UT>(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
     means2d[i] = make_float2(p.u, p.v);
     depths[i] = p.z;
     radii[i] = p.radius;
@@ -297,6 +302,7 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
 // VJP of k_preprocess_fwd, one Gaussian per lane.  SH gradients (zero for
 // coefficients >= Ka) are written through LDS rows in the same sh_mode
 // layouts as the forward reads.
+template <bool UT>
 __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities,
@@ -319,8 +325,8 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
         const float sy = act_scale(scales[3 * i + 1], flags);
         const float sz = act_scale(scales[3 * i + 2], flags);
         const float o = act_opacity(opacities[i], flags);
-        Proj p;
-        project(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
+        typename ProjOf<UT>::T p;
+        project_any<UT>(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
         const float goe = g_opac_eff[i];
         const float g_o = goe * p.comp;
         const float g_comp_total = (g_comp ? g_comp[i] : 0.0f) + goe * o;
@@ -331,8 +337,9 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
             gm2.y += e.y;
         }
         float gm[3], gq[4], gs[3];
-        project_vjp(cam, p, aa, gm2.x, gm2.y, g_conics[3 * i], g_conics[3 * i + 1],
-                    g_conics[3 * i + 2], g_depths ? g_depths[i] : 0.0f, g_comp_total, gm, gq, gs);
+        project_any_vjp<UT>(cam, p, m0, m1, m2, aa, gm2.x, gm2.y, g_conics[3 * i],
+                            g_conics[3 * i + 1], g_conics[3 * i + 2],
+                            g_depths ? g_depths[i] : 0.0f, g_comp_total, gm, gq, gs);
         g_means[3 * i] = gm[0];
         g_means[3 * i + 1] = gm[1];
         g_means[3 * i + 2] = gm[2];
@@ -403,6 +410,12 @@ __global__ __launch_bounds__(kThreads) void k_pack_conic_opacity(int64_t n,
     out[i] = make_float4(conics[3 * i], conics[3 * i + 1], conics[3 * i + 2], opac[i]);
 }
 
+__global__ __launch_bounds__(kThreads) void k_debug_atanf(int64_t n, const float* __restrict__ x,
+                                                         float* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) y[i] = datan_pos(x[i]);
+}
+
 __global__ __launch_bounds__(kThreads) void k_debug_expf(int64_t n, const float* __restrict__ x,
                                                          float* __restrict__ y) {
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
@@ -412,6 +425,47 @@ __global__ __launch_bounds__(kThreads) void k_debug_expf(int64_t n, const float*
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
 
+inline bool lens_ok(const gsx_camera* cam) {
+    return cam->lens == GSX_LENS_NONE || cam->lens == GSX_LENS_BROWN ||
+           cam->lens == GSX_LENS_FISHEYE;
+}
+
+template <bool UT>
+int project_fwd_impl(const gsx_camera* cam, int64_t n, const float* means, const float* quats,
+                     const float* scales, float blur, int32_t antialias, float* means2d,
+                     float* conics, float* depths, float* radii, float* compensation,
+                     void* stream) {
+    if (!cam || n < 0 || !lens_ok(cam)) return GSX_ERR_INVALID;
+    if (n == 0) return GSX_OK;
+    if (!means || !quats || !scales || !means2d || !conics || !depths || !radii || !compensation)
+        return GSX_ERR_INVALID;
+    if (!aligned16(quats) || !aligned8(means2d)) return GSX_ERR_INVALID;
+    hipLaunchKernelGGL(k_project_fwd<UT>, dim3(grid_for(n)), dim3(kThreads), 0,
+                       (hipStream_t)stream, *cam, n, means, (const float4*)quats, scales, blur,
+                       antialias != 0 && blur > 0.0f, (float2*)means2d, conics, depths, radii,
+                       compensation);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+template <bool UT>
+int project_bwd_impl(const gsx_camera* cam, int64_t n, const float* means, const float* quats,
+                     const float* scales, float blur, int32_t antialias, const float* g_means2d,
+                     const float* g_conics, const float* g_depths, const float* g_compensation,
+                     float* g_means, float* g_quats, float* g_scales, void* stream) {
+    if (!cam || n < 0 || !lens_ok(cam)) return GSX_ERR_INVALID;
+    if (n == 0) return GSX_OK;
+    if (!means || !quats || !scales || !g_means || !g_quats || !g_scales) return GSX_ERR_INVALID;
+    if (!aligned16(quats) || !aligned16(g_quats) || (g_means2d && !aligned8(g_means2d)))
+        return GSX_ERR_INVALID;
+    hipLaunchKernelGGL(k_project_bwd<UT>, dim3(grid_for(n)), dim3(kThreads), 0,
+                       (hipStream_t)stream, *cam, n, means, (const float4*)quats, scales, blur,
+                       antialias != 0 && blur > 0.0f, (const float2*)g_means2d, g_conics,
+                       g_depths, g_compensation, g_means, (float4*)g_quats, g_scales);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -420,34 +474,35 @@ int gsx_project_fwd(const gsx_camera* cam, int64_t n, const float* means, const 
                     const float* scales, float blur, int32_t antialias, float* means2d,
                     float* conics, float* depths, float* radii, float* compensation,
                     void* stream) {
-    if (!cam || n < 0) return GSX_ERR_INVALID;
-    if (n == 0) return GSX_OK;
-    if (!means || !quats || !scales || !means2d || !conics || !depths || !radii || !compensation)
-        return GSX_ERR_INVALID;
-    if (!aligned16(quats) || !aligned8(means2d)) return GSX_ERR_INVALID;
-    hipLaunchKernelGGL(k_project_fwd, dim3(grid_for(n)), dim3(kThreads), 0, (hipStream_t)stream,
-                       *cam, n, means, (const float4*)quats, scales, blur,
-                       antialias != 0 && blur > 0.0f, (float2*)means2d, conics, depths, radii,
-                       compensation);
-    GSX_LAUNCH_CHECK();
-    return GSX_OK;
+    return project_fwd_impl<false>(cam, n, means, quats, scales, blur, antialias, means2d,
+                                   conics, depths, radii, compensation, stream);
 }
 
 int gsx_project_bwd(const gsx_camera* cam, int64_t n, const float* means, const float* quats,
                     const float* scales, float blur, int32_t antialias, const float* g_means2d,
                     const float* g_conics, const float* g_depths, const float* g_compensation,
                     float* g_means, float* g_quats, float* g_scales, void* stream) {
-    if (!cam || n < 0) return GSX_ERR_INVALID;
-    if (n == 0) return GSX_OK;
-    if (!means || !quats || !scales || !g_means || !g_quats || !g_scales) return GSX_ERR_INVALID;
-    if (!aligned16(quats) || !aligned16(g_quats) || (g_means2d && !aligned8(g_means2d)))
-        return GSX_ERR_INVALID;
-    hipLaunchKernelGGL(k_project_bwd, dim3(grid_for(n)), dim3(kThreads), 0, (hipStream_t)stream,
-                       *cam, n, means, (const float4*)quats, scales, blur,
-                       antialias != 0 && blur > 0.0f, (const float2*)g_means2d, g_conics,
-                       g_depths, g_compensation, g_means, (float4*)g_quats, g_scales);
-    GSX_LAUNCH_CHECK();
-    return GSX_OK;
+    return project_bwd_impl<false>(cam, n, means, quats, scales, blur, antialias, g_means2d,
+                                   g_conics, g_depths, g_compensation, g_means, g_quats,
+                                   g_scales, stream);
+}
+
+int gsx_project_ut_fwd(const gsx_camera* cam, int64_t n, const float* means, const float* quats,
+                       const float* scales, float blur, int32_t antialias, float* means2d,
+                       float* conics, float* depths, float* radii, float* compensation,
+                       void* stream) {
+    return project_fwd_impl<true>(cam, n, means, quats, scales, blur, antialias, means2d,
+                                  conics, depths, radii, compensation, stream);
+}
+
+int gsx_project_ut_bwd(const gsx_camera* cam, int64_t n, const float* means, const float* quats,
+                       const float* scales, float blur, int32_t antialias,
+                       const float* g_means2d, const float* g_conics, const float* g_depths,
+                       const float* g_compensation, float* g_means, float* g_quats,
+                       float* g_scales, void* stream) {
+    return project_bwd_impl<true>(cam, n, means, quats, scales, blur, antialias, g_means2d,
+                                  g_conics, g_depths, g_compensation, g_means, g_quats,
+                                  g_scales, stream);
 }
 
 int gsx_eval_sh_fwd(int64_t n, int32_t K, int32_t C, int32_t degree, const float* sh,
@@ -482,7 +537,8 @@ int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means, con
                        float* depths, float* radii, float* compensation, float* conic_opacity,
                        float* colors_out, uint32_t* tile_counts, uint32_t* depth_keys,
                        uint32_t* tile_rects, void* stream) {
-    if (!cam || n < 0 || cam->width <= 0 || cam->height <= 0) return GSX_ERR_INVALID;
+    if (!cam || n < 0 || cam->width <= 0 || cam->height <= 0 || !lens_ok(cam))
+        return GSX_ERR_INVALID;
     if (n == 0) return GSX_OK;
     if (!means || !quats || !scales || !opacities || !means2d || !depths || !radii ||
         !compensation || !conic_opacity || !tile_counts || !depth_keys || !tile_rects)
@@ -509,7 +565,8 @@ int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means, con
             sh_cols = 3 * (Ka - 1);
         }
     }
-    hipLaunchKernelGGL(k_preprocess_fwd, dim3(grid_for(n)), dim3(kThreads), 0,
+    auto kern = (flags & GSX_PROJECT_UT) ? k_preprocess_fwd<true> : k_preprocess_fwd<false>;
+    hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(kThreads), 0,
                        (hipStream_t)stream, *cam, n, means, (const float4*)quats, scales,
                        opacities, sh0, sh0_stride, sh_rest, sh_rest_stride, K, degree, sh_mode,
                        sh_cols, flags, blur, (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f,
@@ -529,7 +586,7 @@ int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means, con
                        float* g_quats, float* g_scales, float* g_opacities, float* g_sh0,
                        int64_t sh0_stride, float* g_sh_rest, int64_t sh_rest_stride,
                        void* stream) {
-    if (!cam || n < 0) return GSX_ERR_INVALID;
+    if (!cam || n < 0 || !lens_ok(cam)) return GSX_ERR_INVALID;
     if (n == 0) return GSX_OK;
     if (!means || !quats || !scales || !opacities || !g_means2d || !g_conics || !g_opac_eff ||
         !g_means || !g_quats || !g_scales || !g_opacities)
@@ -554,7 +611,8 @@ int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means, con
             sh_cols = 3 * (K - 1);
         }
     }
-    hipLaunchKernelGGL(k_preprocess_bwd, dim3(grid_for(n)), dim3(kThreads), 0,
+    auto kern = (flags & GSX_PROJECT_UT) ? k_preprocess_bwd<true> : k_preprocess_bwd<false>;
+    hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(kThreads), 0,
                        (hipStream_t)stream, *cam, n, means, (const float4*)quats, scales,
                        opacities, colors_out, K, degree, sh_mode, sh_cols, flags, blur,
                        (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, (const float2*)g_means2d,
@@ -590,6 +648,16 @@ int gsx_pack_conic_opacity(int64_t n, const float* conics, const float* opacitie
         return GSX_ERR_INVALID;
     hipLaunchKernelGGL(k_pack_conic_opacity, dim3(grid_for(n)), dim3(kThreads), 0,
                        (hipStream_t)stream, n, conics, opacities, (float4*)conic_opacity);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_debug_atanf(int64_t n, const float* x, float* y, void* stream) {
+    if (n < 0) return GSX_ERR_INVALID;
+    if (n == 0) return GSX_OK;
+    if (!x || !y) return GSX_ERR_INVALID;
+    hipLaunchKernelGGL(k_debug_atanf, dim3(grid_for(n)), dim3(kThreads), 0, (hipStream_t)stream,
+                       n, x, y);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }

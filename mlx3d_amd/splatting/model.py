@@ -135,24 +135,24 @@ class GaussianModel:
     def render(self, camera: Camera, background=None, antialias: bool = False,
                projection: str = "ewa", return_depth: bool = False) -> dict:
         """Render with the active SH degree (model.py:146-164)."""
-        _check_common(projection)
+        pflags = _check_common(projection)
         means, quats, scales, opac = self._raw()
         K = self.params["sh_dc"].shape[1] + self.params["sh_rest"].shape[1]
         return _run(camera, means, quats, scales, opac, sh_a=self.params["sh_dc"],
                     sh_b=self.params["sh_rest"], sh_mode="split", K=K,
                     degree=self.active_sh_degree, background=background,
-                    flags=_lib.LOG_SCALES | _lib.LOGIT_OPACITY, antialias=antialias,
+                    flags=_lib.LOG_SCALES | _lib.LOGIT_OPACITY | pflags, antialias=antialias,
                     return_depth=return_depth)
 
     def render_depth(self, camera: Camera, antialias: bool = False,
                      projection: str = "ewa") -> dict:
         """Expected depth, forward only (model.py:166-180)."""
-        _check_common(projection)
+        pflags = _check_common(projection)
         means, quats, scales, opac = self._raw()
         with torch.no_grad():
             zeros = torch.zeros((means.shape[0], 1), dtype=torch.float32, device=means.device)
             out = _run(camera, means, quats, scales, opac, colors=zeros,
-                       flags=_lib.LOG_SCALES | _lib.LOGIT_OPACITY, antialias=antialias,
+                       flags=_lib.LOG_SCALES | _lib.LOGIT_OPACITY | pflags, antialias=antialias,
                        return_depth=True)
         return {"depth": out["depth"], "alpha": out["alpha"], "final_T": out["final_T"],
                 "means2d": out["means2d"], "depths": out["depths"], "radii": out["radii"],

@@ -154,11 +154,11 @@ class _RenderFn(torch.autograd.Function):
         return g_means, g_quats, g_scales, g_opac, g_sh_a, g_sh_b, g_colors, None, None
 
 
-def _check_common(projection: str):
+def _check_common(projection: str) -> int:
+    """Flag bits of the projection (render.py:14-26)."""
     if projection not in ("ewa", "ut"):
         raise ValueError("projection must be 'ewa' or 'ut'.")
-    if projection == "ut":
-        raise NotImplementedError("projection='ut' is not implemented; use 'ewa'")
+    return _lib.PROJECT_UT if projection == "ut" else 0
 
 
 def _background(background, channels, dev):
@@ -228,7 +228,7 @@ def render_gaussians(camera: Camera, means, quats, scales, opacities, colors=Non
     """
     if (colors is None) == (sh is None):
         raise ValueError("Provide exactly one of `colors` or `sh`.")
-    _check_common(projection)
+    pflags = _check_common(projection)
     if sh is not None:
         if sh.ndim != 3 or sh.shape[2] != 3 or sh.shape[1] < num_sh_bases(sh_degree):
             raise ValueError(f"sh must have shape (N, K>={num_sh_bases(sh_degree)}, 3).")
@@ -236,23 +236,24 @@ def render_gaussians(camera: Camera, means, quats, scales, opacities, colors=Non
             raise ValueError("sh_degree must be in [0, 3].")
         return _run(camera, means, quats, scales, opacities, sh_a=sh, sh_mode="packed",
                     K=sh.shape[1], degree=sh_degree, background=background, antialias=antialias,
-                    return_depth=return_depth, refine_tiles=refine_tiles)
+                    return_depth=return_depth, refine_tiles=refine_tiles, flags=pflags)
     if colors.ndim != 2 or colors.shape != (means.shape[0], 3):
         raise ValueError("colors must have shape (N, 3).")
     return _run(camera, means, quats, scales, opacities, colors=colors, background=background,
-                antialias=antialias, return_depth=return_depth, refine_tiles=refine_tiles)
+                antialias=antialias, return_depth=return_depth, refine_tiles=refine_tiles,
+                flags=pflags)
 
 
 def render_gaussian_depth(camera: Camera, means, quats, scales, opacities,
                           refine_tiles: bool = False, antialias: bool = False,
                           projection: str = "ewa") -> dict:
     """Expected depth and alpha, forward only (render.py:115-161)."""
-    _check_common(projection)
+    pflags = _check_common(projection)
     with torch.no_grad():
         dev = _lib.require_device(means)
         ones = torch.zeros((means.shape[0], 1), dtype=torch.float32, device=dev)
         out = _run(camera, means, quats, scales, opacities, colors=ones, antialias=antialias,
-                   return_depth=True, refine_tiles=refine_tiles)
+                   return_depth=True, refine_tiles=refine_tiles, flags=pflags)
     return {"depth": out["depth"], "alpha": out["alpha"], "final_T": out["final_T"],
             "means2d": out["means2d"], "depths": out["depths"], "radii": out["radii"],
             "compensation": out["compensation"]}
@@ -274,10 +275,11 @@ def render_gaussian_features(camera: Camera, means, quats, scales, opacities, fe
     channels = int(features.shape[1])
     if channels <= 0:
         raise ValueError("features must contain at least one channel.")
-    _check_common(projection)
+    pflags = _check_common(projection)
     bg = None if normalize else background
     out = _run(camera, means, quats, scales, opacities, colors=features, background=bg,
-               antialias=antialias, return_depth=return_depth, refine_tiles=refine_tiles)
+               antialias=antialias, return_depth=return_depth, refine_tiles=refine_tiles,
+               flags=pflags)
     feat = out.pop("image")
     if normalize:
         a = out["alpha"][..., None]

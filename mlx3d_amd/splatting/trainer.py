@@ -33,9 +33,9 @@ from ..optim import Adam, adam_step, exponential_decay
 from ..transforms import quaternion_to_matrix
 from .. import _lib
 from .model import GaussianModel
-from .projection import project_gaussians
+from .projection import project_gaussians, project_gaussians_ut
 from .rasterize import rasterize, rasterize_features
-from .render import _run
+from .render import _check_common, _run
 from .sh import eval_sh
 from .tiles import bin_gaussians
 
@@ -93,8 +93,6 @@ class GaussianTrainer:
             raise ValueError("TrainerConfig.method must be 'vanilla', 'mcmc', or '2dgs'")
         if self.config.projection not in {"ewa", "ut"}:
             raise ValueError("TrainerConfig.projection must be 'ewa' or 'ut'")
-        if self.config.projection == "ut":
-            raise NotImplementedError("projection='ut' is not implemented; use 'ewa'")
         self.scene_extent = scene_extent
         self.step_count = 0
         # Random draws of the MCMC method (relocation jitter, position noise).
@@ -234,7 +232,9 @@ class GaussianTrainer:
         K = p["sh_dc"].shape[1] + p["sh_rest"].shape[1]
         out = _run(camera, p["means"], p["quats"], p["scales"], p["opacities"], sh_a=p["sh_dc"],
                    sh_b=p["sh_rest"], sh_mode="split", K=K, degree=self.model.active_sh_degree,
-                   background=background, flags=_lib.LOG_SCALES | _lib.LOGIT_OPACITY,
+                   background=background,
+                   flags=(_lib.LOG_SCALES | _lib.LOGIT_OPACITY
+                          | _check_common(self.config.projection)),
                    antialias=self.config.antialias, screen_stats=stats)
         img = out["image"]
         return self._photometric(img, target), img, out["radii"], None
@@ -242,8 +242,9 @@ class GaussianTrainer:
     def _render_loss_staged(self, params, probe, camera: Camera, target, background):
         """trainer.py:261-316 stage by stage, with the reference's means2d probe."""
         p = params
-        proj = project_gaussians(camera, p["means"], p["quats"], torch.exp(p["scales"]),
-                                 antialias=self.config.antialias)
+        project = project_gaussians_ut if self.config.projection == "ut" else project_gaussians
+        proj = project(camera, p["means"], p["quats"], torch.exp(p["scales"]),
+                       antialias=self.config.antialias)
         means2d = proj["means2d"] + probe
         opacities = torch.sigmoid(p["opacities"]) * proj["compensation"]
         sh = torch.cat([p["sh_dc"], p["sh_rest"]], dim=1)

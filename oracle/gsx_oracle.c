@@ -471,7 +471,20 @@ void orc_preprocess_fwd(const orc_camera* cam, int64_t n, const float* means,
         for (int k = 0; k < 3; ++k) s[k] = act_scale(scales[3 * i + k], flags);
         const float o = act_opacity(opacities[i], flags);
         proj_t p;
-        project_one(cam, means + 3 * i, quats + 4 * i, s, blur, aa, &p);
+        if (flags & ORC_PROJECT_UT) { /* render.py:14-26 */
+            float r[8];
+            orc_ut_project_one(cam, means + 3 * i, quats + 4 * i, s, blur, aa, r);
+            p.u = r[0];
+            p.v = r[1];
+            p.A = r[2];
+            p.B = r[3];
+            p.C = r[4];
+            p.z = r[5];
+            p.radius = r[6];
+            p.comp = r[7];
+        } else {
+            project_one(cam, means + 3 * i, quats + 4 * i, s, blur, aa, &p);
+        }
         means2d[2 * i] = p.u;
         means2d[2 * i + 1] = p.v;
         conics[3 * i] = p.A;
@@ -507,18 +520,34 @@ void orc_preprocess_bwd(const orc_camera* cam, int64_t n, const float* means,
         float s[3];
         for (int k = 0; k < 3; ++k) s[k] = act_scale(scales[3 * i + k], flags);
         const float o = act_opacity(opacities[i], flags);
+        const int ut = (flags & ORC_PROJECT_UT) != 0;
+        float comp_i;
         proj_t p;
-        project_one(cam, means + 3 * i, quats + 4 * i, s, blur, aa, &p);
+        if (ut) {
+            float r[8];
+            orc_ut_project_one(cam, means + 3 * i, quats + 4 * i, s, blur, aa, r);
+            comp_i = r[7];
+        } else {
+            project_one(cam, means + 3 * i, quats + 4 * i, s, blur, aa, &p);
+            comp_i = p.comp;
+        }
         const float goe = g_opac_eff ? g_opac_eff[i] : 0.0f;
         /* opac_eff = o * comp */
-        const float g_o = goe * p.comp;
+        const float g_o = goe * comp_i;
         const float g_comp_total = (g_comp ? g_comp[i] : 0.0f) + goe * o;
         float gs[3];
-        project_vjp(cam, &p, aa, g_means2d ? g_means2d[2 * i] : 0.0f,
-                    g_means2d ? g_means2d[2 * i + 1] : 0.0f,
-                    g_conics ? g_conics[3 * i] : 0.0f, g_conics ? g_conics[3 * i + 1] : 0.0f,
-                    g_conics ? g_conics[3 * i + 2] : 0.0f, g_depths ? g_depths[i] : 0.0f,
-                    g_comp_total, g_means + 3 * i, g_quats + 4 * i, gs);
+        const float g_in[7] = {g_means2d ? g_means2d[2 * i] : 0.0f,
+                               g_means2d ? g_means2d[2 * i + 1] : 0.0f,
+                               g_conics ? g_conics[3 * i] : 0.0f,
+                               g_conics ? g_conics[3 * i + 1] : 0.0f,
+                               g_conics ? g_conics[3 * i + 2] : 0.0f,
+                               g_depths ? g_depths[i] : 0.0f, g_comp_total};
+        if (ut)
+            orc_ut_project_vjp_one(cam, means + 3 * i, quats + 4 * i, s, blur, aa, g_in,
+                                   g_means + 3 * i, g_quats + 4 * i, gs);
+        else
+            project_vjp(cam, &p, aa, g_in[0], g_in[1], g_in[2], g_in[3], g_in[4], g_in[5],
+                        g_in[6], g_means + 3 * i, g_quats + 4 * i, gs);
         for (int k = 0; k < 3; ++k)
             g_scales[3 * i + k] = (flags & ORC_LOG_SCALES) ? gs[k] * s[k] : gs[k];
         g_opacities[i] = (flags & ORC_LOGIT_OPACITY) ? g_o * o * (1.0f - o) : g_o;

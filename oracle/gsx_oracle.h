@@ -15,6 +15,8 @@
  *                          when conics are given)
  *   orc_raster_fwd      -- rasterize.py:28-98 (+ depth rasterize.py:223-290)
  *   orc_raster_bwd      -- rasterize.py:100-221, vjp wiring :364-403
+ *   orc_project_ut      -- projection.py:149-205 + cameras.py:42-77, 290-311
+ *                          (ut_oracle.c; orc_preprocess_* under ORC_PROJECT_UT)
  *   orc_photometric, orc_adam, orc_accum_screen_grads -- train_oracle.c
  *   orc_project_bwd /
  *   orc_preprocess_bwd  -- hand-derived VJP of projection.py:56-138,
@@ -42,13 +44,19 @@ typedef struct orc_camera {
     float lim_x, lim_y;
     float znear;
     int32_t width, height;
+    int32_t orthographic;   /* UT projection only (cameras.py:158-160)   */
+    int32_t lens;           /* ORC_LENS_*                                 */
+    float dist[8];          /* Brown: k1 k2 p1 p2 k3 2p1 2p2; fisheye k1..k4 */
 } orc_camera;
 
 enum {
     ORC_LOG_SCALES = 1,     /* scales given as log-sigma: apply exp      */
     ORC_LOGIT_OPACITY = 2,  /* opacities given as logits: apply sigmoid  */
-    ORC_ANTIALIAS = 4       /* Mip-Splatting compensation (blur > 0)     */
+    ORC_ANTIALIAS = 4,      /* Mip-Splatting compensation (blur > 0)     */
+    ORC_PROJECT_UT = 8      /* unscented-transform projection            */
 };
+
+enum { ORC_LENS_NONE = 0, ORC_LENS_BROWN = 1, ORC_LENS_FISHEYE = 2 };
 
 float orc_expf(float x);
 void orc_expf_array(int64_t n, const float* x, float* y);
@@ -117,6 +125,29 @@ void orc_raster_bwd(int64_t n, int C, const float* means2d,
                     const float* grad_final_T, float* g_means2d,
                     float* g_conics, float* g_feats, float* g_opac,
                     int nthreads);
+
+/* ------------------------------------------------ UT projection (ut_oracle.c) */
+
+float orc_atanf(float r);  /* r >= 0 */
+
+void orc_project_ut(const orc_camera* cam, int64_t n, const float* means, const float* quats,
+                    const float* scales, float blur, int antialias, float* means2d,
+                    float* conics, float* depths, float* radii, float* comp, int nthreads);
+
+void orc_project_ut_bwd(const orc_camera* cam, int64_t n, const float* means,
+                        const float* quats, const float* scales, float blur, int antialias,
+                        const float* g_means2d, const float* g_conics, const float* g_depths,
+                        const float* g_comp, float* g_means, float* g_quats, float* g_scales,
+                        int nthreads);
+
+/* One Gaussian (used by orc_preprocess_* under ORC_PROJECT_UT):
+ * out = {u, v, A, B, C, z, radius, comp};
+ * g_in = cotangents {u, v, A, B, C, z, comp}. */
+void orc_ut_project_one(const orc_camera* cam, const float* m, const float* q, const float* s,
+                        float blur, int aa, float* out);
+void orc_ut_project_vjp_one(const orc_camera* cam, const float* m, const float* q,
+                            const float* s, float blur, int aa, const float* g_in, float* g_m,
+                            float* g_q, float* g_s);
 
 /* ------------------------------------------------ training step (train_oracle.c) */
 

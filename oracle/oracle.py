@@ -23,6 +23,7 @@ _lib = None
 LOG_SCALES = 1
 LOGIT_OPACITY = 2
 ANTIALIAS = 4
+PROJECT_UT = 8
 
 
 class OrcCamera(ctypes.Structure):
@@ -39,6 +40,9 @@ class OrcCamera(ctypes.Structure):
         ("znear", ctypes.c_float),
         ("width", ctypes.c_int32),
         ("height", ctypes.c_int32),
+        ("orthographic", ctypes.c_int32),
+        ("lens", ctypes.c_int32),
+        ("dist", ctypes.c_float * 8),
     ]
 
 
@@ -85,6 +89,11 @@ def _declare(L):
                                  _P, _P, _P, _P, _P, _I64, _I]
     L.orc_raster_bwd.argtypes = [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P,
                                  _P, _P, _P, _P, _P, _P, _I]
+    L.orc_atanf.argtypes = [_F]
+    L.orc_atanf.restype = _F
+    L.orc_project_ut.argtypes = [_P, _I64, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P, _I]
+    L.orc_project_ut_bwd.argtypes = [_P, _I64, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P, _P, _P,
+                                     _I]
     _D = ctypes.c_double
     L.orc_photometric.argtypes = [_I, _I, _I, _P, _P, _I, _D, _D, _D, _D, _P, _P]
     L.orc_adam.argtypes = [_I64, _P, _P, _P, _P, _F, _F, _F, _F]
@@ -110,7 +119,8 @@ def default_threads() -> int:
         return os.cpu_count() or 1
 
 
-def make_camera(R, t, center, fx, fy, cx, cy, lim_x, lim_y, znear, width, height) -> OrcCamera:
+def make_camera(R, t, center, fx, fy, cx, cy, lim_x, lim_y, znear, width, height,
+                orthographic=0, lens=0, dist=None) -> OrcCamera:
     cam = OrcCamera()
     cam.R[:] = [float(v) for v in np.asarray(R, np.float32).reshape(9)]
     cam.t[:] = [float(v) for v in np.asarray(t, np.float32).reshape(3)]
@@ -118,6 +128,8 @@ def make_camera(R, t, center, fx, fy, cx, cy, lim_x, lim_y, znear, width, height
     cam.fx, cam.fy, cam.cx, cam.cy = fx, fy, cx, cy
     cam.lim_x, cam.lim_y, cam.znear = lim_x, lim_y, znear
     cam.width, cam.height = int(width), int(height)
+    cam.orthographic, cam.lens = int(orthographic), int(lens)
+    cam.dist[:] = [float(v) for v in (dist if dist is not None else [0.0] * 8)]
     return cam
 
 
@@ -146,17 +158,41 @@ def project(cam, means, quats, scales, blur=0.3, antialias=False, threads=1):
 
 
 def project_bwd(cam, means, quats, scales, g_means2d=None, g_conics=None, g_depths=None,
-                g_comp=None, blur=0.3, antialias=False, threads=1):
+                g_comp=None, blur=0.3, antialias=False, threads=1, ut=False):
     means, quats, scales = _f32(means), _f32(quats), _f32(scales)
     n = means.shape[0]
     gm = np.empty((n, 3), np.float32)
     gq = np.empty((n, 4), np.float32)
     gs = np.empty((n, 3), np.float32)
     conv = [None if a is None else _f32(a) for a in (g_means2d, g_conics, g_depths, g_comp)]
-    lib().orc_project_bwd(ctypes.byref(cam), n, _ptr(means), _ptr(quats), _ptr(scales), blur,
-                          int(antialias), *[_ptr(a) for a in conv], _ptr(gm), _ptr(gq),
-                          _ptr(gs), threads)
+    fn = lib().orc_project_ut_bwd if ut else lib().orc_project_bwd
+    fn(ctypes.byref(cam), n, _ptr(means), _ptr(quats), _ptr(scales), blur, int(antialias),
+       *[_ptr(a) for a in conv], _ptr(gm), _ptr(gq), _ptr(gs), threads)
     return gm, gq, gs
+
+
+def atanf(r):
+    """The oracle's arctan (r >= 0), element by element."""
+    return np.array([lib().orc_atanf(float(v)) for v in np.asarray(r, np.float32).ravel()],
+                    np.float32).reshape(np.shape(r))
+
+
+def project_ut(cam, means, quats, scales, blur=0.3, antialias=False, threads=1):
+    """project_gaussians_ut (projection.py:149-205)."""
+    means, quats, scales = _f32(means), _f32(quats), _f32(scales)
+    n = means.shape[0]
+    out = dict(
+        means2d=np.empty((n, 2), np.float32),
+        conics=np.empty((n, 3), np.float32),
+        depths=np.empty((n,), np.float32),
+        radii=np.empty((n,), np.float32),
+        compensation=np.empty((n,), np.float32),
+    )
+    lib().orc_project_ut(ctypes.byref(cam), n, _ptr(means), _ptr(quats), _ptr(scales), blur,
+                         int(antialias), _ptr(out["means2d"]), _ptr(out["conics"]),
+                         _ptr(out["depths"]), _ptr(out["radii"]), _ptr(out["compensation"]),
+                         threads)
+    return out
 
 
 def eval_sh(degree, sh, dirs, threads=1):

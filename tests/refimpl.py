@@ -41,7 +41,8 @@ def oracle_camera(cam: Camera):
 
     f = cam.gsx_fields()
     return O.make_camera(f["R"], f["t"], f["center"], f["fx"], f["fy"], f["cx"], f["cy"],
-                         f["lim_x"], f["lim_y"], f["znear"], f["width"], f["height"])
+                         f["lim_x"], f["lim_y"], f["znear"], f["width"], f["height"],
+                         f["orthographic"], f["lens"], f["dist"])
 
 
 # -------------------------------------------------------------- projection
@@ -95,6 +96,85 @@ def project_matrix_f64(cam: Camera, means, quats, scales, blur=0.3, antialias=Fa
     comp = torch.where(valid, comp, torch.zeros_like(comp))
     return dict(means2d=torch.stack([u, v], -1), conics=conics, depths=z, radii=radii,
                 compensation=comp, lam1=lam1)
+
+
+def project_points_f64(cam: Camera, pts: torch.Tensor, eps: float = 1e-8):
+    """Camera.project_points (cameras.py:290-311) with its lens models
+    (cameras.py:42-77), float64, differentiable."""
+    R = torch.tensor(cam.R.numpy(), dtype=torch.float64)
+    t = torch.tensor(cam.t.numpy(), dtype=torch.float64)
+    pc = pts @ R.T + t
+    if cam.orthographic:
+        return torch.stack([cam.fx * pc[..., 0] + cam.cx, cam.fy * pc[..., 1] + cam.cy], -1)
+    z = pc[..., 2]
+    inv = 1.0 / torch.where(z.abs() < eps, torch.full_like(z, eps), z)
+    x, y = pc[..., 0] * inv, pc[..., 1] * inv
+    if cam.distortion is not None:
+        c = list(cam.distortion)
+        if cam.fisheye:
+            k1, k2, k3, k4 = (c + [0.0] * 4)[:4]
+            r = torch.sqrt(x * x + y * y)
+            th = torch.atan(r)
+            th2 = th * th
+            thd = th * (1 + th2 * (k1 + th2 * (k2 + th2 * (k3 + th2 * k4))))
+            scale = thd / torch.clamp(r, min=1e-9)
+            x, y = x * scale, y * scale
+        else:
+            k1, k2, p1, p2 = c[:4]
+            k3 = c[4] if len(c) > 4 else 0.0
+            r2 = x * x + y * y
+            radial = 1 + r2 * (k1 + r2 * (k2 + r2 * k3))
+            x, y = (x * radial + 2 * p1 * x * y + p2 * (r2 + 2 * x * x),
+                    y * radial + p1 * (r2 + 2 * y * y) + 2 * p2 * x * y)
+    return torch.stack([cam.fx * x + cam.cx, cam.fy * y + cam.cy], -1)
+
+
+def project_ut_f64(cam: Camera, means, quats, scales, blur=0.3, antialias=False):
+    """project_gaussians_ut (projection.py:149-205) in float64, differentiable."""
+    Rq = quat_to_rot_f64(quats)
+    sq = Rq * scales[:, None, :]
+    offsets = torch.cat([sq.transpose(1, 2), -sq.transpose(1, 2)], 1)
+    sigma = means[:, None, :] + math.sqrt(3.0) * offsets
+    xy = project_points_f64(cam, sigma.reshape(-1, 3)).reshape(means.shape[0], 6, 2)
+    m2 = xy.mean(1)
+    d = xy - m2[:, None, :]
+    a0 = (d[..., 0] * d[..., 0]).mean(1)
+    b = (d[..., 0] * d[..., 1]).mean(1)
+    c0 = (d[..., 1] * d[..., 1]).mean(1)
+    a, c = a0 + blur, c0 + blur
+    det = a * c - b * b
+    ds = torch.clamp(det, min=1e-12)
+    conics = torch.stack([c / ds, -b / ds, a / ds], -1)
+    if antialias and blur > 0:
+        comp = torch.sqrt(torch.clamp(a0 * c0 - b * b, min=0.0) / ds)
+    else:
+        comp = torch.ones_like(det)
+    mid = 0.5 * (a + c)
+    lam1 = mid + torch.sqrt(torch.clamp(mid * mid - det, min=0.01))
+    radii = torch.ceil(3.0 * torch.sqrt(torch.clamp(lam1, min=0.0)))
+    R = torch.tensor(cam.R.numpy(), dtype=torch.float64)
+    t = torch.tensor(cam.t.numpy(), dtype=torch.float64)
+    z = (means @ R.T + t)[:, 2]
+    valid = (z > cam.znear) & (det > 0)
+    radii = torch.where(valid, radii, torch.zeros_like(radii))
+    comp = torch.where(valid, comp, torch.zeros_like(comp))
+    return dict(means2d=m2, conics=conics, depths=z, radii=radii, compensation=comp, lam1=lam1)
+
+
+def lens_cameras(width=96, height=64):
+    """Pinhole, Brown-Conrady (4 and 5 coefficients), fisheye and orthographic
+    variants of one pose, for the UT projection."""
+    base = Camera.look_at(eye=(0.3, -0.2, -3.0), at=(0, 0, 0), fov=55.0, width=width,
+                          height=height)
+    kw = dict(R=base.R, t=base.t, fx=base.fx, fy=base.fy, cx=base.cx, cy=base.cy, width=width,
+              height=height)
+    return {
+        "pinhole": base,
+        "brown4": Camera(**kw, distortion=(-0.35, 0.12, 0.002, -0.001)),
+        "brown5": Camera(**kw, distortion=(0.08, -0.03, -0.004, 0.003, 0.01)),
+        "fisheye": Camera(**kw, distortion=(0.05, -0.02, 0.004, -0.001), fisheye=True),
+        "ortho": Camera.orthographic_camera(1.6, width, height, R=base.R, t=base.t),
+    }
 
 
 # ---------------------------------------------------------------------- SH

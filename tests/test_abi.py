@@ -32,15 +32,19 @@ def test_python_binding_covers_header():
 
 def test_status_strings_and_version():
     L = _lib.load()
-    assert L.gsx_abi_version() == 1
+    assert L.gsx_abi_version() == 2
     assert _lib.strerror(0) == "ok"
     assert "invalid" in _lib.strerror(-1)
     assert "capacity" in _lib.strerror(1)
 
 
 def test_camera_struct_layout():
-    # 9 + 3 + 3 + 4 + 2 + 1 floats, 2 int32
-    assert ctypes.sizeof(_lib.GsxCamera) == 4 * 24
+    # 9 + 3 + 3 + 4 + 2 + 1 floats, 2 int32; lens: 2 int32 + 8 floats
+    assert ctypes.sizeof(_lib.GsxCamera) == 4 * 34
+    from oracle import oracle as O
+
+    assert ctypes.sizeof(O.OrcCamera) == ctypes.sizeof(_lib.GsxCamera)
+    assert [f[0] for f in O.OrcCamera._fields_] == [f[0] for f in _lib.GsxCamera._fields_]
 
 
 def test_workspace_query_is_host_only():
