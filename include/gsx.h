@@ -349,6 +349,21 @@ int gsx_accum_screen_grads(int64_t n, const float* g_means2d,
                            const float* radii, int32_t width, int32_t height,
                            float* grad_accum, float* grad_count, void* stream);
 
+/* --------------------------------------------------------- mesh raster --
+ * Replaces the hard z-buffer kernel of rasterize_meshes
+ * (renderer/rasterizer.py:29-87), the mesh consumer of bin_gaussians: the
+ * caller bins faces by centroid, bounding-circle radius and mean depth
+ * (rasterizer.py:140-146) and passes the screen-space vertices tri_xy
+ * (F,6) = (ax, ay, bx, by, cx, cy), camera depths tri_z (F,3), sorted ids
+ * and tile ranges.  Per pixel (centre +0.5) the nearest face with all
+ * barycentrics >= -1e-5 and interpolated depth > znear wins (first in list
+ * order on ties); pix_to_face (H,W) int32 (-1 = empty), zbuf (H,W) (0 where
+ * empty). */
+int gsx_mesh_raster(int64_t n_faces, const float* tri_xy, const float* tri_z,
+                    const int32_t* sorted_ids, int64_t num_ids,
+                    const int32_t* tile_ranges, int32_t width, int32_t height,
+                    float znear, int32_t* pix_to_face, float* zbuf, void* stream);
+
 /* ---------------------------------------------------------- diagnostics --
  * Evaluates the device exp used by the rasterizer (the stand-in for
  * metal::exp at rasterize.py:80,171,274) on n inputs; tests check it

@@ -17,6 +17,7 @@
  *   orc_raster_bwd      -- rasterize.py:100-221, vjp wiring :364-403
  *   orc_project_ut      -- projection.py:149-205 + cameras.py:42-77, 290-311
  *                          (ut_oracle.c; orc_preprocess_* under ORC_PROJECT_UT)
+ *   orc_mesh_raster     -- renderer/rasterizer.py:29-87 (mesh_oracle.c)
  *   orc_photometric, orc_adam, orc_accum_screen_grads -- train_oracle.c
  *   orc_project_bwd /
  *   orc_preprocess_bwd  -- hand-derived VJP of projection.py:56-138,
@@ -148,6 +149,15 @@ void orc_ut_project_one(const orc_camera* cam, const float* m, const float* q, c
 void orc_ut_project_vjp_one(const orc_camera* cam, const float* m, const float* q,
                             const float* s, float blur, int aa, const float* g_in, float* g_m,
                             float* g_q, float* g_s);
+
+/* -------------------------------------------------- mesh raster (mesh_oracle.c) */
+
+/* renderer/rasterizer.py:29-87: nearest face per pixel over its tile's
+ * list; tri_xy (F,6), tri_z (F,3); pix_to_face (H*W) (-1 empty), zbuf. */
+void orc_mesh_raster(int64_t n_faces, const float* tri_xy, const float* tri_z,
+                     const int32_t* sorted_ids, const int32_t* tile_ranges, int width,
+                     int height, float znear, int32_t* pix_to_face, float* zbuf,
+                     int nthreads);
 
 /* ------------------------------------------------ training step (train_oracle.c) */
 

@@ -94,6 +94,7 @@ def _declare(L):
     L.orc_project_ut.argtypes = [_P, _I64, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P, _I]
     L.orc_project_ut_bwd.argtypes = [_P, _I64, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P, _P, _P,
                                      _I]
+    L.orc_mesh_raster.argtypes = [_I64, _P, _P, _P, _P, _I, _I, _F, _P, _P, _I]
     _D = ctypes.c_double
     L.orc_photometric.argtypes = [_I, _I, _I, _P, _P, _I, _D, _D, _D, _D, _P, _P]
     L.orc_adam.argtypes = [_I64, _P, _P, _P, _P, _F, _F, _F, _F]
@@ -348,3 +349,18 @@ def accum_screen_grads(g_means2d, radii, width, height, accum, count):
     lib().orc_accum_screen_grads(r.size, _ptr(g), _ptr(r), int(width), int(height), _ptr(a),
                                  _ptr(c))
     return a, c
+
+
+# ------------------------------------------------------------- mesh raster
+
+
+def mesh_raster(tri_xy, tri_z, sorted_ids, tile_ranges, width, height, znear=0.01, threads=1):
+    """(pix_to_face (H, W) int32, zbuf (H, W)) of renderer/rasterizer.py:29-87."""
+    tri_xy, tri_z = _f32(tri_xy).reshape(-1, 6), _f32(tri_z).reshape(-1, 3)
+    ids, ranges = _i32(sorted_ids), _i32(tile_ranges)
+    p2f = np.empty((height, width), np.int32)
+    zb = np.empty((height, width), np.float32)
+    lib().orc_mesh_raster(tri_xy.shape[0], _ptr(tri_xy), _ptr(tri_z), _ptr(ids), _ptr(ranges),
+                          int(width), int(height), float(np.float32(znear)), _ptr(p2f),
+                          _ptr(zb), threads)
+    return p2f, zb

@@ -373,3 +373,68 @@ def render_f64(cam: Camera, means, quats, scales, opac, colors=None, sh=None, de
     img, T, _ = dense_composite_f64(p["means2d"], p["conics"], oe, colors, order, cam.width,
                                     cam.height, bg=bg, mask=mask, kernel_stop=kernel_stop)
     return img, T, p
+
+
+# ------------------------------------------------------------------- meshes
+def ico_sphere(level: int = 1, radius: float = 1.0):
+    """(verts (V, 3) float32, faces (F, 3) int32) of a subdivided icosahedron
+    (the test mesh of the reference's rasterizer tests)."""
+    t = (1.0 + 5 ** 0.5) / 2.0
+    v = [(-1, t, 0), (1, t, 0), (-1, -t, 0), (1, -t, 0), (0, -1, t), (0, 1, t), (0, -1, -t),
+         (0, 1, -t), (t, 0, -1), (t, 0, 1), (-t, 0, -1), (-t, 0, 1)]
+    verts = [np.array(p, np.float64) / np.linalg.norm(p) for p in v]
+    faces = [(0, 11, 5), (0, 5, 1), (0, 1, 7), (0, 7, 10), (0, 10, 11), (1, 5, 9), (5, 11, 4),
+             (11, 10, 2), (10, 7, 6), (7, 1, 8), (3, 9, 4), (3, 4, 2), (3, 2, 6), (3, 6, 8),
+             (3, 8, 9), (4, 9, 5), (2, 4, 11), (6, 2, 10), (8, 6, 7), (9, 8, 1)]
+    for _ in range(level):
+        cache, nf = {}, []
+
+        def mid(a, b):
+            key = (min(a, b), max(a, b))
+            if key not in cache:
+                m = verts[a] + verts[b]
+                verts.append(m / np.linalg.norm(m))
+                cache[key] = len(verts) - 1
+            return cache[key]
+
+        for a, b, c in faces:
+            ab, bc, ca = mid(a, b), mid(b, c), mid(c, a)
+            nf += [(a, ab, ca), (b, bc, ab), (c, ca, bc), (ab, bc, ca)]
+        faces = nf
+    return (np.array(verts) * radius).astype(np.float32), np.array(faces, np.int32)
+
+
+def mesh_zbuffer_f64(tri_xy, tri_z, width, height, znear=0.01):
+    """All-faces float64 z-buffer: (nearest face, its depth, depth margin to
+    the runner-up, coverage ambiguous) per pixel, for checking the binned
+    rasterizer."""
+    txy = np.asarray(tri_xy, np.float64).reshape(-1, 3, 2)
+    tz = np.asarray(tri_z, np.float64).reshape(-1, 3)
+    px = (np.arange(width) + 0.5)[None, :, None]
+    py = (np.arange(height) + 0.5)[:, None, None]
+    ax, ay = txy[:, 0, 0], txy[:, 0, 1]
+    bx, by = txy[:, 1, 0], txy[:, 1, 1]
+    cx, cy = txy[:, 2, 0], txy[:, 2, 1]
+    den = (by - cy) * (ax - cx) + (cx - bx) * (ay - cy)
+    ok = np.abs(den) >= 1e-12
+    den = np.where(ok, den, 1.0)
+    l0 = ((by - cy) * (px - cx) + (cx - bx) * (py - cy)) / den
+    l1 = ((cy - ay) * (px - cx) + (ax - cx) * (py - cy)) / den
+    l2 = 1.0 - l0 - l1
+    z = l0 * tz[:, 0] + l1 * tz[:, 1] + l2 * tz[:, 2]
+    hit = ok & (l0 >= -1e-5) & (l1 >= -1e-5) & (l2 >= -1e-5) & (z > znear)
+    zz = np.where(hit, z, np.inf)
+    best = np.argmin(zz, axis=-1)
+    bz = np.take_along_axis(zz, best[..., None], -1)[..., 0]
+    srt = np.sort(zz, axis=-1)
+    margin = np.full(bz.shape, np.inf)
+    if zz.shape[-1] > 1:
+        with np.errstate(invalid="ignore"):
+            gap = srt[..., 1] - srt[..., 0]
+        margin = np.where(np.isfinite(srt[..., 0]), gap, np.inf)
+    # a face's coverage of a pixel is ambiguous when its smallest barycentric
+    # sits within rounding distance of the -1e-5 threshold
+    lmin = np.minimum(np.minimum(l0, l1), l2)
+    amb = (ok & (z > znear) & (np.abs(lmin + 1e-5) < 1e-4)).any(axis=-1)
+    return (np.where(np.isfinite(bz), best, -1).astype(np.int32),
+            np.where(np.isfinite(bz), bz, 0.0), margin, amb)
