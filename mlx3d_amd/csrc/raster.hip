@@ -35,25 +35,39 @@ namespace {
 constexpr int kThreads = kTilePixels;
 constexpr int kWaves = kThreads / kWave;  // 4 quadrant waves
 
-// exp with the range handling of dexp done by selects instead of branches;
-// identical results to dexp for every input.
-__device__ __forceinline__ float dexp_sel(float x) {
-    const float xc = fminf(fmaxf(x, -86.0f), 88.0f);
-    const float k = rintf(xc * 1.44269504088896341f);
-    float r = fmaf(k, -0.693145751953125f, xc);
-    r = fmaf(k, -1.42860682030941723e-06f, r);
-    float p = 1.98412698412698413e-04f;
-    p = fmaf(p, r, 1.38888888888888889e-03f);
-    p = fmaf(p, r, 8.33333333333333333e-03f);
-    p = fmaf(p, r, 4.16666666666666667e-02f);
-    p = fmaf(p, r, 1.66666666666666667e-01f);
-    p = fmaf(p, r, 0.5f);
-    p = fmaf(p, r, 1.0f);
-    p = fmaf(p, r, 1.0f);
-    float e = ldexpf(p, (int)k);
+// The compositing loops' exp (stands in for metal::exp at rasterize.py:80,
+// 171): k = rint(x log2 e), r = x - k ln2 with ln2 rounded to float32 (one
+// multiply-add), e^r by the degree-5 polynomial 1 + r q(r) whose
+// coefficients were fitted for least maximum relative error on |r| <= ln2/2,
+// then exact scaling by 2^k.  At most 2.02 ulp from exp for x in [-6, 0]
+// (every power that can pass the alpha test), 4.75 ulp on [-87, 0], and
+// exp(0) = 1.  splat_exp_core is the sequence without range handling
+// (callers that know x lies in [-86, 88]); splat_exp_sel adds it with
+// selects: 0 below -86, +inf above 88, NaN unchanged.
+__device__ __forceinline__ float splat_exp_core(float x) {
+    const float k = rintf(x * 1.44269504088896341f);
+    const float r = fmaf(k, -0.693147182464599609375f, x);
+    float q = 8.290260538610955e-03f;
+    q = fmaf(q, r, 4.189814578274823e-02f);
+    q = fmaf(q, r, 1.6667638172664237e-01f);
+    q = fmaf(q, r, 4.9999147944277167e-01f);
+    q = fmaf(q, r, 9.999997063356061e-01f);
+    return ldexpf(fmaf(q, r, 1.0f), (int)k);
+}
+
+__device__ __forceinline__ float splat_exp_sel(float x) {
+    float e = splat_exp_core(fminf(fmaxf(x, -86.0f), 88.0f));
     e = (x < -86.0f) ? 0.0f : e;
     e = (x > 88.0f) ? __builtin_huge_valf() : e;
     return (x != x) ? x : e;
+}
+
+// rasterize.py:77-78, power = -0.5 (a dx^2 + c dy^2) - b dx dy, with the
+// conic staged pre-scaled to (A, B, C) = (-a/2, -b, -c/2) (exact scalings)
+// and the two multiply-adds a contracting compiler forms from that
+// expression: power = (B dx) dy + ((C dy) dy + (A dx) dx).
+__device__ __forceinline__ float splat_power(float A, float B, float C, float dx, float dy) {
+    return fmaf(B * dx, dy, fmaf(C * dy, dy, (A * dx) * dx));
 }
 
 // Power below which o * exp(power) < 1/255 for certain.  +inf when the
@@ -75,9 +89,10 @@ __device__ __forceinline__ float alpha_floor_power(float o) {
 // kept when the minimum of q over its rectangle of pixel centres (float64:
 // zero if the mean is inside, else the least of the four clipped edge
 // minimisers) is within that bound.  With b^2 < 0.999 a c the float32
-// evaluation of the power is within 7.2e-4 relative of the exact value, so
-// tau is inflated by 1% (+1e-3); the float32 log of the bound and float32
-// reciprocals for the minimisers add errors of ~1e-7, well inside that.
+// evaluation of the power (splat_power) is within 7.2e-4 relative of the
+// exact value, so tau is inflated by 1% (+1e-3); the float32 log of the
+// bound, the float32 reciprocals for the minimisers and the <= 5 ulp of
+// splat_exp add errors of ~1e-6, well inside that.
 // Ill-conditioned, non-positive or non-finite conics get no culling (all
 // four bits).
 __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, int px0, int py0) {
@@ -133,56 +148,59 @@ __device__ __forceinline__ bool plain_gaussian(float x, float y, float4 c, float
     return ok;
 }
 
-// exp for arguments known to lie in [-86, 88]: the dexp sequence without its
-// range checks (identical results there).
-__device__ __forceinline__ float dexp_inrange(float x) {
-    const float k = rintf(x * 1.44269504088896341f);
-    float r = fmaf(k, -0.693145751953125f, x);
-    r = fmaf(k, -1.42860682030941723e-06f, r);
-    float p = 1.98412698412698413e-04f;
-    p = fmaf(p, r, 1.38888888888888889e-03f);
-    p = fmaf(p, r, 8.33333333333333333e-03f);
-    p = fmaf(p, r, 4.16666666666666667e-02f);
-    p = fmaf(p, r, 1.66666666666666667e-01f);
-    p = fmaf(p, r, 0.5f);
-    p = fmaf(p, r, 1.0f);
-    p = fmaf(p, r, 1.0f);
-    return ldexpf(p, (int)k);
-}
-
 template <int CTRL, int ROW_MASK, int BANK_MASK>
 __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK,
                                                        BANK_MASK, false));
 }
 
+// In-place v_permlane32_swap (upper 32 lanes of a <-> lower 32 lanes of b)
+// and v_permlane16_swap (odd rows of a <-> even rows of b).  Written as asm
+// so the operands are swapped where they live (the builtins' two results
+// made the register allocator copy both operands first); the leading
+// s_nop 1 supplies the two wait states a swap needs after a VALU write of
+// its operands, since the compiler's hazard check cannot see into the asm.
+__device__ __forceinline__ void swap_rows32(float& a, float& b) {
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
 // Sums of NVP per-lane values (NVP a multiple of 4) over the 64 lanes of
 // the wave, spread over the four 16-lane rows: afterwards every lane of row
 // r holds in q[m] the total of value 4m + row_value(r).  Step 1 swaps the
-// upper half of value 2k with the lower half of value 2k + 1
-// (v_permlane32_swap) and adds, so each half carries one of the two values;
-// step 2 does the same between rows (v_permlane16_swap); step 3 sums each
-// row with four DPP steps.  NVP + NVP/2 + NVP exchanges/adds instead of 6 NVP
-// for a separate 64-lane reduction of every value.  All lanes must be active.
+// upper half of value 2k with the lower half of value 2k + 1 and adds, so
+// each half carries one of the two values; step 2 does the same between
+// rows; step 3 sums each row with four DPP steps.  NVP + NVP/2 + NVP
+// exchanges/adds instead of 6 NVP for a separate 64-lane reduction of every
+// value.  Values from index NZ on are known zeros: pairs of them skip their
+// exchange.  All lanes must be active.
 __device__ __forceinline__ int row_value(int row) { return ((row & 1) << 1) | (row >> 1); }
 
-template <int NVP>
+template <int NVP, int NZ = NVP>
 __device__ __forceinline__ void wave_reduce_rows(const float (&v)[NVP], float (&q)[NVP / 4]) {
-    static_assert(NVP % 4 == 0, "values come in groups of four");
+    static_assert(NVP % 4 == 0 && NZ <= NVP, "values come in groups of four");
     float h[NVP / 2];
 #pragma unroll
     for (int k = 0; k < NVP / 2; ++k) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2 * k]),
-                                                        __float_as_uint(v[2 * k + 1]), false,
-                                                        false);
-        h[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        if (2 * k >= NZ) {
+            h[k] = 0.0f;
+            continue;
+        }
+        float a = v[2 * k], b = 2 * k + 1 < NZ ? v[2 * k + 1] : 0.0f;
+        swap_rows32(a, b);
+        h[k] = a + b;
     }
 #pragma unroll
     for (int m = 0; m < NVP / 4; ++m) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(h[2 * m]),
-                                                        __float_as_uint(h[2 * m + 1]), false,
-                                                        false);
-        float t = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        if (4 * m >= NZ) {
+            q[m] = 0.0f;
+            continue;
+        }
+        float a = h[2 * m], b = h[2 * m + 1];
+        swap_rows16(a, b);
+        float t = a + b;
         t += dpp_f<0xB1, 0xF, 0xF>(t);   // quad_perm [1,0,3,2]
         t += dpp_f<0x4E, 0xF, 0xF>(t);   // quad_perm [2,3,0,1]
         t += dpp_f<0x141, 0xF, 0xF>(t);  // row_half_mirror
@@ -283,9 +301,9 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
 #pragma unroll
     for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
     const float dx = r0.x - pxf, dy = r0.y - pyf;
-    const float power = -0.5f * (r1.x * dx * dx + r1.z * dy * dy) - r1.y * dx * dy;
+    const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
     const bool live = !done && !(power > 0.0f) && !(power < r0.z);
-    const float e = PLAIN ? dexp_inrange(power) : dexp_sel(power);
+    const float e = PLAIN ? splat_exp_core(power) : splat_exp_sel(power);
     const float alpha = fminf(0.99f, r0.w * e);
     const bool pass = live && !(alpha < 1.0f / 255.0f);
     const float next_T = T * (1.0f - alpha);
@@ -356,7 +374,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     int* __restrict__ n_contrib, float* __restrict__ depth_out) {
     constexpr int F4 = (CH + 3) / 4;
     __shared__ float4 s_r0[kThreads];      // mean x, mean y, log-alpha bound, opacity
-    __shared__ float4 s_r1[kThreads];      // conic a, b, c, depth
+    __shared__ float4 s_r1[kThreads];      // -a/2, -b, -c/2 (conic), depth
     __shared__ float4 s_f[kThreads][F4];   // channels, zero padded
     __shared__ uint64_t s_mask[kWaves][kWaves];  // [quadrant][loader wave]
 
@@ -392,7 +410,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
                 const float thr = alpha_floor_power(c.w);
                 s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
                 const float dz = DEPTH ? depths[g] : 0.0f;
-                s_r1[tid] = make_float4(c.x, c.y, c.z, dz);
+                s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, dz);
                 stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                 qm = quadrant_mask(m.x, m.y, c, px0, py0);
                 plain = plain_gaussian<CH>(m.x, m.y, c, thr, s_f[tid]) && fabsf(dz) < 1e30f;
@@ -451,36 +469,45 @@ struct BwdPixel {
 };
 
 // One (pixel, Gaussian) step of the back-to-front replay
-// (rasterize.py:162-219).  When any lane of the wave contributes, the wave
-// sums of
+// (rasterize.py:162-219).  Returns whether any lane of the wave contributes
+// and writes each lane's values to out[S q + O] (all zeros when none does):
 //   u = G dx dL/dG, w = G dy dL/dG, u dx, u dy, w dy, G dL/dalpha, alpha T g_c
-// go into the wave's slot for Gaussian j; the flush turns them into the
-// reference's means2d, conic, opacity and colour gradients (linear in these
-// sums).  alpha and the skip tests repeat the forward's float32 arithmetic
-// exactly (the replay must take the forward's decisions); the gradient
-// arithmetic itself uses fused multiply-adds.  T is recovered with one
-// reciprocal of (1 - alpha) per pair.  PLAIN: inputs are finite, so a lane
-// that does not contribute can run the same update with a zero weight.
-template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
-                                         const float4* __restrict__ fsrc, int j, int gj,
-                                         float4 (*part)[((CH + 6) + 3) / 4], float pxf, float pyf,
-                                         int lane, BwdPixel<CH>& px, uint64_t& wrote0,
-                                         uint64_t& wrote1) {
+// (zero for lanes that do not contribute), whose wave sums the flush turns
+// into the reference's means2d, conic, opacity and colour gradients (linear
+// in these sums).  power, alpha and the skip tests repeat the forward's
+// float32 arithmetic exactly (the replay must take the forward's
+// decisions); the gradient arithmetic itself uses fused multiply-adds.  T is
+// recovered with one reciprocal of (1 - alpha) per pair.  PLAIN: inputs are
+// finite, so a lane that does not contribute can run the same update with a
+// zero weight.
+template <int CH, bool PLAIN, int S = 1, int O = 0, int NW>
+__device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
+                                           const float4* __restrict__ fsrc, int gj, float pxf,
+                                           float pyf, BwdPixel<CH>& px, float (&out)[NW]) {
+    static_assert(S * (CH + 5) + O < NW, "strided values fit the output array");
     constexpr int F4 = (CH + 3) / 4;
     constexpr int NV = CH + 6;
-    constexpr int NVP = 4 * ((NV + 3) / 4);
     const float dx = r0.x - pxf, dy = r0.y - pyf;
-    const float power = -0.5f * (r1.x * dx * dx + r1.z * dy * dy) - r1.y * dx * dy;
+    const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
     bool ok = gj < px.last && !(power > 0.0f) && !(power < r0.z);
-    if (__ballot(ok) == 0ull) return;
+    if (__ballot(ok) == 0ull) {
+#pragma unroll
+        for (int q = 0; q < NV; ++q) out[S * q + O] = 0.0f;
+        return false;
+    }
     // PLAIN: lanes that pass have power in [-86, 0]; clamping leaves them
     // unchanged and keeps G finite (so zero weights stay zero) elsewhere.
-    const float G = PLAIN ? dexp_inrange(__builtin_amdgcn_fmed3f(power, -87.0f, 0.0f))
-                          : dexp_sel(power);
+    const float G = PLAIN ? splat_exp_core(__builtin_amdgcn_fmed3f(power, -86.0f, 0.0f))
+                          : splat_exp_sel(power);
     const float alpha = fminf(0.99f, r0.w * G);
     ok = ok && !(alpha < 1.0f / 255.0f);
-    if (__ballot(ok) == 0ull) return;
+    if (__ballot(ok) == 0ull) {
+        // every output is written on every path, so callers hold no stale
+        // values across iterations
+#pragma unroll
+        for (int q = 0; q < NV; ++q) out[S * q + O] = 0.0f;
+        return false;
+    }
     float4 fv[F4];
 #pragma unroll
     for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
@@ -496,8 +523,8 @@ __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
     const float qn = fmaf(aT, cg, px.Q);
     px.Q = (PLAIN || ok) ? qn : px.Q;
     const float gd = G * (r0.w * dL_dalpha);  // G dL/dG
-    float v[NVP];
     const float u = gd * dx, w = gd * dy;
+    float v[NV];
     v[0] = u;
     v[1] = w;
     v[2] = u * dx;
@@ -507,30 +534,69 @@ __device__ __forceinline__ void bwd_pair(const float4& r0, const float4& r1,
 #pragma unroll
     for (int ch = 0; ch < CH; ++ch) v[6 + ch] = aT * px.gpix[ch];
 #pragma unroll
-    for (int q = NV; q < NVP; ++q) v[q] = 0.0f;
-    if (!PLAIN) {
+    for (int q = 0; q < NV; ++q) out[S * q + O] = (PLAIN || ok) ? v[q] : 0.0f;
+    return true;
+}
+
+__device__ __forceinline__ void mark_written(int j, uint64_t& wrote0, uint64_t& wrote1) {
+    if (j < kWave) wrote0 |= 1ull << j;
+    else wrote1 |= 1ull << (j - kWave);
+}
+
+// Wave sums of one Gaussian's values into its slot: row r of the wave ends
+// with the totals of values 4m + row_value(r), which lane 15 of the row
+// stores at those positions.
+template <int CH>
+__device__ __forceinline__ void bwd_reduce1(const float (&v)[CH + 6], int j,
+                                            float4 (*part)[((CH + 6) + 3) / 4], int lane,
+                                            uint64_t& wrote0, uint64_t& wrote1) {
+    constexpr int NV = CH + 6;
+    constexpr int NVP = 4 * ((NV + 3) / 4);
+    float w[NVP];
 #pragma unroll
-        for (int q = 0; q < NV; ++q) v[q] = ok ? v[q] : 0.0f;
-    }
+    for (int q = 0; q < NVP; ++q) w[q] = q < NV ? v[q] : 0.0f;
     float tot[NVP / 4];
-    wave_reduce_rows<NVP>(v, tot);
+    wave_reduce_rows<NVP, NV>(w, tot);
     if ((lane & 15) == 15) {
         float* dst = reinterpret_cast<float*>(part[j]) + row_value(lane >> 4);
 #pragma unroll
         for (int m = 0; m < NVP / 4; ++m) dst[4 * m] = tot[m];
     }
-    if (j < kWave) wrote0 |= 1ull << j;
-    else wrote1 |= 1ull << (j - kWave);
+    mark_written(j, wrote0, wrote1);
+}
+
+// The same for two Gaussians in one reduction (fewer padding values and
+// shared exchange steps): value i of Gaussian a sits at 2i and of Gaussian b
+// at 2i + 1 of the combined array, so the first exchange pairs a's and b's
+// value i; rows with row_value 0 and 2 then finish a's values 2m and 2m + 1,
+// rows with 1 and 3 b's, each stored at slot position 2m + (row_value >> 1).
+template <int CH>
+__device__ __forceinline__ void bwd_reduce2(float (&w)[4 * ((CH + 7) / 2)], int ja, bool ha,
+                                            int jb, bool hb, float4 (*part)[((CH + 6) + 3) / 4],
+                                            int lane, uint64_t& wrote0, uint64_t& wrote1) {
+    constexpr int NV = CH + 6;
+    constexpr int NH = (NV + 1) / 2;  // value pairs per Gaussian
+    static_assert(2 * NH <= 4 * ((NV + 3) / 4), "a Gaussian's slot holds its padded pairs");
+    float tot[NH];
+    wave_reduce_rows<4 * NH, 2 * NV>(w, tot);
+    if ((lane & 15) == 15) {
+        const int rv = row_value(lane >> 4);
+        float* dst = reinterpret_cast<float*>(part[(rv & 1) ? jb : ja]) + (rv >> 1);
+#pragma unroll
+        for (int m = 0; m < NH; ++m) dst[2 * m] = tot[m];
+    }
+    if (ha) mark_written(ja, wrote0, wrote1);
+    if (hb) mark_written(jb, wrote0, wrote1);
 }
 
 // Back-to-front walk of one quadrant wave over its staged Gaussians, two
-// records in flight.
+// records in flight, one reduction per contributing Gaussian.
 template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_walk(BitWalkDown& walk, const float4* s_r0,
-                                         const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
-                                         float4 (*part)[((CH + 6) + 3) / 4], float pxf, float pyf,
-                                         int bbase, int lane, BwdPixel<CH>& px, uint64_t& wrote0,
-                                         uint64_t& wrote1) {
+__device__ __forceinline__ void bwd_walk1(BitWalkDown& walk, const float4* s_r0,
+                                          const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+                                          float4 (*part)[((CH + 6) + 3) / 4], float pxf,
+                                          float pyf, int bbase, int lane, BwdPixel<CH>& px,
+                                          uint64_t& wrote0, uint64_t& wrote1) {
     int ja = walk.next();
     if (ja < 0) return;
     float4 a0 = s_r0[ja], a1 = s_r1[ja];
@@ -538,25 +604,87 @@ __device__ __forceinline__ void bwd_walk(BitWalkDown& walk, const float4* s_r0,
         const int jb = walk.next();
         const int lb = jb >= 0 ? jb : ja;
         const float4 b0 = s_r0[lb], b1 = s_r1[lb];
-        bwd_pair<CH, PLAIN>(a0, a1, s_f[ja], ja, bbase + ja, part, pxf, pyf, lane, px, wrote0,
-                            wrote1);
+        {
+            float v[CH + 6];
+            if (bwd_values<CH, PLAIN>(a0, a1, s_f[ja], bbase + ja, pxf, pyf, px, v))
+                bwd_reduce1<CH>(v, ja, part, lane, wrote0, wrote1);
+        }
         if (jb < 0) return;
         ja = walk.next();
         const int la = ja >= 0 ? ja : jb;
         a0 = s_r0[la];
         a1 = s_r1[la];
-        bwd_pair<CH, PLAIN>(b0, b1, s_f[jb], jb, bbase + jb, part, pxf, pyf, lane, px, wrote0,
-                            wrote1);
+        {
+            float v[CH + 6];
+            if (bwd_values<CH, PLAIN>(b0, b1, s_f[jb], bbase + jb, pxf, pyf, px, v))
+                bwd_reduce1<CH>(v, jb, part, lane, wrote0, wrote1);
+        }
         if (ja < 0) return;
     }
 }
 
+// The same walk with the two Gaussians of each step sharing one reduction
+// (a Gaussian without contributions enters it as zeros and is not marked):
+// their values are written interleaved, a's at even and b's at odd
+// positions, which is the layout bwd_reduce2 sums.
+template <int CH, bool PLAIN>
+__device__ __forceinline__ void bwd_walk2(BitWalkDown& walk, const float4* s_r0,
+                                          const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+                                          float4 (*part)[((CH + 6) + 3) / 4], float pxf,
+                                          float pyf, int bbase, int lane, BwdPixel<CH>& px,
+                                          uint64_t& wrote0, uint64_t& wrote1) {
+    constexpr int NV = CH + 6;
+    constexpr int NW = 4 * ((NV + 1) / 2);
+    int ja = walk.next();
+    if (ja < 0) return;
+    float4 a0 = s_r0[ja], a1 = s_r1[ja];
+    while (true) {
+        const int jb = walk.next();
+        const int lb = jb >= 0 ? jb : ja;
+        const float4 b0 = s_r0[lb], b1 = s_r1[lb];
+        if (jb < 0) {
+            float v[NV];
+            if (bwd_values<CH, PLAIN>(a0, a1, s_f[ja], bbase + ja, pxf, pyf, px, v))
+                bwd_reduce1<CH>(v, ja, part, lane, wrote0, wrote1);
+            return;
+        }
+        float w[NW];
+#pragma unroll
+        for (int q = 2 * NV; q < NW; ++q) w[q] = 0.0f;
+        const bool ha = bwd_values<CH, PLAIN, 2, 0>(a0, a1, s_f[ja], bbase + ja, pxf, pyf, px, w);
+        const int jc = ja;
+        ja = walk.next();
+        const int la = ja >= 0 ? ja : jb;
+        a0 = s_r0[la];
+        a1 = s_r1[la];
+        const bool hb = bwd_values<CH, PLAIN, 2, 1>(b0, b1, s_f[jb], bbase + jb, pxf, pyf, px, w);
+        if (ha || hb) bwd_reduce2<CH>(w, jc, ha, jb, hb, part, lane, wrote0, wrote1);
+        if (ja < 0) return;
+    }
+}
+
+// Paired reductions up to four channels (at most 20 values per pair); wider
+// channel blocks reduce one Gaussian at a time, where padding is a small
+// share and two value sets would not fit the register budget.
+template <int CH, bool PLAIN>
+__device__ __forceinline__ void bwd_walk(BitWalkDown& walk, const float4* s_r0,
+                                         const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+                                         float4 (*part)[((CH + 6) + 3) / 4], float pxf, float pyf,
+                                         int bbase, int lane, BwdPixel<CH>& px, uint64_t& wrote0,
+                                         uint64_t& wrote1) {
+    if constexpr (CH <= 4)
+        bwd_walk2<CH, PLAIN>(walk, s_r0, s_r1, s_f, part, pxf, pyf, bbase, lane, px, wrote0,
+                             wrote1);
+    else
+        bwd_walk1<CH, PLAIN>(walk, s_r0, s_r1, s_f, part, pxf, pyf, bbase, lane, px, wrote0,
+                             wrote1);
+}
+
 // Waves per SIMD the backward asks for (more waves hide LDS and ballot
-// latencies): five up to eight channels (96 VGPRs; the 31.6 KB of LDS of
-// the 128-Gaussian batches also caps the one- to four-channel variants at
-// five blocks per CU), four at 16 channels (112), three at 32 (145), all
-// without spills.
-constexpr int bwd_min_waves(int ch) { return ch <= 8 ? 5 : (ch <= 16 ? 4 : 3); }
+// latencies): five up to four channels (<= 96 VGPRs; the 31.6 KB of LDS of
+// the 128-Gaussian batches also caps them at five blocks per CU), four up
+// to 16 channels, three at 32, all without spills.
+constexpr int bwd_min_waves(int ch) { return ch <= 4 ? 5 : (ch <= 16 ? 4 : 3); }
 
 template <int CH>
 __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
@@ -574,7 +702,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     constexpr int NLW = BB / kWave;
     static_assert(NLW == 1 || NLW == 2, "the written-mask words are held as two scalars");
     __shared__ float4 s_r0[BB];
-    __shared__ float4 s_r1[BB];
+    __shared__ float4 s_r1[BB];  // -a/2, -b, -c/2 (conic), unused
     __shared__ float4 s_f[BB][F4];
     __shared__ int s_id[BB];
     __shared__ float4 s_part[kWaves][BB][NV4];  // per-wave gradient sums per Gaussian
@@ -638,7 +766,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
                     const float4 c = co[g];
                     const float thr = alpha_floor_power(c.w);
                     s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
-                    s_r1[tid] = make_float4(c.x, c.y, c.z, 0.0f);
+                    s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, 0.0f);
                     stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                     qm = quadrant_mask(m.x, m.y, c, px0, py0);
 #pragma unroll
@@ -700,10 +828,11 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
                     e[4 * q + 2] = sum[q].z;
                     e[4 * q + 3] = sum[q].w;
                 }
-                // rasterize.py:197-218 in terms of the sums
+                // rasterize.py:197-218 in terms of the sums; the staged conic
+                // is (-a/2, -b, -c/2)
                 const float4 c = s_r1[tid];
-                const float gx = -(c.x * e[0] + c.y * e[1]);
-                const float gy = -(c.y * e[0] + c.z * e[1]);
+                const float gx = 2.0f * c.x * e[0] + c.y * e[1];
+                const float gy = c.y * e[0] + 2.0f * c.z * e[1];
                 const float ga = -0.5f * e[2], gb = -e[3], gc = -0.5f * e[4];
                 if (gx != 0.0f) atomicAdd(&g_xy[2 * g], gx);
                 if (gy != 0.0f) atomicAdd(&g_xy[2 * g + 1], gy);

@@ -6,8 +6,10 @@
  *
  * Every function restates one piece of the reference (paths relative to the
  * reference repository root):
- *   orc_expf            -- own exp (Cody-Waite reduction + degree-7 Taylor);
- *                          stands in for metal::exp at rasterize.py:80,171,274
+ *   orc_expf            -- own exp (Cody-Waite reduction + degree-7 Taylor)
+ *                          for the activations of model.py:116-122
+ *   orc_splat_expf,     -- the compositing loops' exp and power (metal::exp
+ *   orc_splat_power        and the power of rasterize.py:77-80,169-171)
  *   orc_project         -- src/mlx3d/splatting/projection.py:24-146
  *   orc_eval_sh         -- src/mlx3d/splatting/sh.py:41-78
  *   orc_preprocess_fwd  -- render.py:73-80 + projection + model.py:116-126
@@ -25,7 +27,9 @@
  *                          (what MLX autodiff computes for the reference)
  *
  * Arithmetic is IEEE float32 in the reference's operation order, compiled
- * with -ffp-contract=off so no multiply-add is fused behind our back.
+ * with -ffp-contract=off so no multiply-add is fused behind our back; the
+ * explicit fmaf calls (the compositing power and accumulation) are the
+ * contractions a fast-math compiler applies to the reference's expressions.
  *
  * The camera struct has the same layout as gsx_camera in include/gsx.h.
  */
@@ -61,6 +65,9 @@ enum { ORC_LENS_NONE = 0, ORC_LENS_BROWN = 1, ORC_LENS_FISHEYE = 2 };
 
 float orc_expf(float x);
 void orc_expf_array(int64_t n, const float* x, float* y);
+float orc_splat_expf(float x);
+void orc_splat_expf_array(int64_t n, const float* x, float* y);
+float orc_splat_power(float a, float b, float c, float dx, float dy);
 
 void orc_project(const orc_camera* cam, int64_t n, const float* means,
                  const float* quats, const float* scales, float blur,

@@ -75,6 +75,9 @@ def _declare(L):
     L.orc_expf.argtypes = [_F]
     L.orc_expf.restype = _F
     L.orc_expf_array.argtypes = [_I64, _P, _P]
+    L.orc_splat_expf_array.argtypes = [_I64, _P, _P]
+    L.orc_splat_power.argtypes = [_F, _F, _F, _F, _F]
+    L.orc_splat_power.restype = _F
     L.orc_project.argtypes = [_P, _I64, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P, _I]
     L.orc_project_bwd.argtypes = [_P, _I64, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P, _P, _P, _I]
     L.orc_eval_sh.argtypes = [_I64, _I, _I, _I, _P, _P, _P, _I]
@@ -139,6 +142,19 @@ def expf(x):
     y = np.empty_like(x)
     lib().orc_expf_array(x.size, _ptr(x), _ptr(y))
     return y
+
+
+def splat_expf(x):
+    """The compositing loops' exp (orc_splat_expf)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().orc_splat_expf_array(x.size, _ptr(x), _ptr(y))
+    return y
+
+
+def splat_power(a, b, c, dx, dy):
+    """The compositing loops' power for one (conic, offset) (orc_splat_power)."""
+    return float(lib().orc_splat_power(a, b, c, dx, dy))
 
 
 def project(cam, means, quats, scales, blur=0.3, antialias=False, threads=1):
