@@ -5,13 +5,15 @@
 // pixel quadrant (w&1, w>>1).  The tile's depth-sorted Gaussians are staged
 // through LDS in batches (two 16-byte records per Gaussian plus its
 // channels, read as broadcasts).  While staging, each lane tests its
-// Gaussian's alpha >= 1/255 ellipse (bounding box, float64, with a margin
-// that covers the float32 rounding of the per-pixel power) against the four
-// quadrants, and the workgroup publishes per quadrant a bit mask of the
-// Gaussians that can touch it.  Each wave walks only its own set bits, in
-// list order, prefetching the next record while it evaluates the current
-// one.  Skipped pairs are exactly pairs whose alpha is below 1/255, which
-// the reference also skips, so every output is unchanged.
+// Gaussian's alpha >= 1/255 ellipse against the four quadrants (exact
+// minimum of the conic form over each quadrant's pixel centres, with a
+// margin that covers the float32 rounding of the per-pixel power), and the
+// workgroup publishes per quadrant a bit mask of the Gaussians that can
+// touch it.  Each wave compacts its quadrant's bits into a list of record
+// offsets and walks it in list order, reading each Gaussian's records while
+// the previous one is evaluated.  Skipped pairs are exactly pairs whose
+// alpha is below 1/255, which the reference also skips, so every output is
+// unchanged.
 //
 // Forward: per-pixel front-to-back compositing as rasterize.py:60-96 (same
 // skips, same termination before compositing the splat that would drop T
@@ -19,11 +21,12 @@
 // terminated and the workgroup stops loading once all 256 have.
 // Backward: back-to-front replay (rasterize.py:147-220) from the largest
 // n_contrib of each quadrant.  A pair's gradient terms are summed over the
-// wave with DPP row operations; lane 63 stores the sums in the wave's own
-// LDS slot for that Gaussian (no LDS atomics), and after the batch one lane
-// per Gaussian adds the four waves' slots and issues one global atomic per
-// (Gaussian, tile, component) -- the reference issues one per (pixel,
-// Gaussian, component).
+// wave with cross-row swaps and DPP row operations (two Gaussians per
+// reduction up to four channels); lane 15 of each row stores its share of
+// the sums in the wave's own LDS slot for that Gaussian (no LDS atomics),
+// and after the batch one lane per Gaussian adds the four waves' slots and
+// issues one global atomic per (Gaussian, tile, component) -- the reference
+// issues one per (pixel, Gaussian, component).
 #include <algorithm>
 
 #include "gsx_device.h"
@@ -86,49 +89,56 @@ __device__ __forceinline__ float alpha_floor_power(float o) {
 // Which of the tile's four 8x8 quadrants (bit q = quadrant (q&1, q>>1)) the
 // pixels with alpha >= 1/255 of this Gaussian can lie in.  alpha >= 1/255
 // needs q(d) = a dx^2 + 2 b dx dy + c dy^2 <= 2 ln(255 o); a quadrant is
-// kept when the minimum of q over its rectangle of pixel centres (float64:
-// zero if the mean is inside, else the least of the four clipped edge
-// minimisers) is within that bound.  With b^2 < 0.999 a c the float32
+// kept when the minimum of q over its rectangle of pixel centres is within
+// that bound: zero if the mean is inside, else the least of the four edge
+// minima.  On a row dy = k, q = a (dx + b k / a)^2 + k^2 det / a, so the
+// edge minimum is that expression at dx clamped to the edge (columns alike
+// with a and c exchanged), and the eight edge lines are shared by the
+// quadrants.  Float32 throughout: with det > 1e-3 a c every term carries a
+// relative error below 1e-4, and with b^2 < 0.999 a c the float32
 // evaluation of the power (splat_power) is within 7.2e-4 relative of the
 // exact value, so tau is inflated by 1% (+1e-3); the float32 log of the
-// bound, the float32 reciprocals for the minimisers and the <= 5 ulp of
-// splat_exp add errors of ~1e-6, well inside that.
-// Ill-conditioned, non-positive or non-finite conics get no culling (all
-// four bits).
+// bound and the <= 5 ulp of splat_exp add errors of ~1e-6, well inside
+// that.  Ill-conditioned, non-positive or non-finite conics get no culling
+// (all four bits).
 __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, int px0, int py0) {
     const float o = c.w;
     if (!(o >= 0.0039215f)) return (o == o) ? 0u : 0xFu;  // alpha < 1/255 everywhere
-    const double A = c.x, B = c.y, C = c.z;
-    const double det = A * C - B * B;
-    if (!(A > 0.0 && C > 0.0 && det > 1e-3 * A * C)) return 0xFu;
-    // log and the reciprocals in float32: their errors (~1e-7) are far inside
-    // the margin, and an inexact minimiser only over-estimates the minimum
-    const double t2 = 2.0 * ((double)__logf(255.0f * o) * 1.01 + 1e-3);
-    const double xd = x, yd = y;
-    if (!(t2 < 1e30 && A < 1e30 && C < 1e30 && fabs(xd) < 1e30 && fabs(yd) < 1e30)) return 0xFu;
-    const double ia = (double)__builtin_amdgcn_rcpf(c.x), ic = (double)__builtin_amdgcn_rcpf(c.z);
-    uint32_t m = 0;
-#pragma unroll 1
-    for (int q = 0; q < 4; ++q) {
-        const double x0 = px0 + (q & 1) * 8 + 0.5 - xd, x1 = x0 + 7.0;
-        const double y0 = py0 + (q >> 1) * 8 + 0.5 - yd, y1 = y0 + 7.0;
-        double qmin;
-        if (x0 <= 0.0 && x1 >= 0.0 && y0 <= 0.0 && y1 >= 0.0) {
-            qmin = 0.0;
-        } else {
-            qmin = 1e300;
-#pragma unroll 1
-            for (int e = 0; e < 2; ++e) {
-                const double xe = e ? x1 : x0, ye = e ? y1 : y0;
-                const double ys = fmin(fmax(-B * xe * ic, y0), y1);
-                const double xs = fmin(fmax(-B * ye * ia, x0), x1);
-                qmin = fmin(qmin, A * xe * xe + 2.0 * B * xe * ys + C * ys * ys);
-                qmin = fmin(qmin, A * xs * xs + 2.0 * B * xs * ye + C * ye * ye);
-            }
-        }
-        m |= (qmin <= t2) ? (1u << q) : 0u;
-    }
-    return m;
+    const float A = c.x, B = c.y, C = c.z;
+    const float det = fmaf(A, C, -B * B);
+    if (!(A > 0.0f && C > 0.0f && det > 1e-3f * A * C)) return 0xFu;
+    const float t2 = 2.0f * fmaf(__logf(255.0f * o), 1.01f, 1e-3f);
+    if (!(t2 < 1e30f && A < 1e30f && C < 1e30f && fabsf(x) < 1e30f && fabsf(y) < 1e30f))
+        return 0xFu;
+    const float ia = __builtin_amdgcn_rcpf(A), ic = __builtin_amdgcn_rcpf(C);
+    const float ba = -B * ia, bc = -B * ic, da = det * ia, dc = det * ic;
+    // pixel-centre offsets from the mean: columns [xl0, xl0 + 7] (left
+    // quadrants) and [xl0 + 8, xl0 + 15] (right), rows likewise
+    const float xl0 = ((float)px0 + 0.5f) - x, xl1 = xl0 + 7.0f;
+    const float xr0 = xl0 + 8.0f, xr1 = xl0 + 15.0f;
+    const float yt0 = ((float)py0 + 0.5f) - y, yt1 = yt0 + 7.0f;
+    const float yb0 = yt0 + 8.0f, yb1 = yt0 + 15.0f;
+    // minimum of q on row dy = k over dx in [lo, hi], and on columns
+    auto row = [&](float k, float lo, float hi) {
+        const float xs = ba * k, u = fminf(fmaxf(xs, lo), hi) - xs;
+        return fmaf(A * u, u, k * k * da);
+    };
+    auto col = [&](float k, float lo, float hi) {
+        const float ys = bc * k, u = fminf(fmaxf(ys, lo), hi) - ys;
+        return fmaf(C * u, u, k * k * dc);
+    };
+    const bool inl = xl0 <= 0.0f && xl1 >= 0.0f, inr = xr0 <= 0.0f && xr1 >= 0.0f;
+    const bool intp = yt0 <= 0.0f && yt1 >= 0.0f, inb = yb0 <= 0.0f && yb1 >= 0.0f;
+    const float q0 = fminf(fminf(row(yt0, xl0, xl1), row(yt1, xl0, xl1)),
+                           fminf(col(xl0, yt0, yt1), col(xl1, yt0, yt1)));
+    const float q1 = fminf(fminf(row(yt0, xr0, xr1), row(yt1, xr0, xr1)),
+                           fminf(col(xr0, yt0, yt1), col(xr1, yt0, yt1)));
+    const float q2 = fminf(fminf(row(yb0, xl0, xl1), row(yb1, xl0, xl1)),
+                           fminf(col(xl0, yb0, yb1), col(xl1, yb0, yb1)));
+    const float q3 = fminf(fminf(row(yb0, xr0, xr1), row(yb1, xr0, xr1)),
+                           fminf(col(xr0, yb0, yb1), col(xr1, yb0, yb1)));
+    return ((inl && intp) || q0 <= t2 ? 1u : 0u) | ((inr && intp) || q1 <= t2 ? 2u : 0u) |
+           ((inl && inb) || q2 <= t2 ? 4u : 0u) | ((inr && inb) || q3 <= t2 ? 8u : 0u);
 }
 
 // A staged Gaussian is "plain" when every quantity the per-pixel loop reads
@@ -154,17 +164,38 @@ __device__ __forceinline__ float dpp_f(float v) {
                                                        BANK_MASK, false));
 }
 
-// In-place v_permlane32_swap (upper 32 lanes of a <-> lower 32 lanes of b)
-// and v_permlane16_swap (odd rows of a <-> even rows of b).  Written as asm
-// so the operands are swapped where they live (the builtins' two results
-// made the register allocator copy both operands first); the leading
-// s_nop 1 supplies the two wait states a swap needs after a VALU write of
-// its operands, since the compiler's hazard check cannot see into the asm.
-__device__ __forceinline__ void swap_rows32(float& a, float& b) {
-    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+// In-place v_permlane32_swap (upper 32 lanes of a[k] <-> lower 32 lanes of
+// b[k]) and v_permlane16_swap (odd rows of a[k] <-> even rows of b[k]) for
+// K register pairs, up to four per asm block.  Written as asm so the
+// operands are swapped where they live (the builtins' two results made the
+// register allocator copy both operands first); each block starts with
+// s_nop 1, the two wait states a swap needs after a VALU write of its
+// operands, since the compiler's hazard check cannot see into the asm (the
+// swaps inside a block touch disjoint registers).
+#define GSX_SWAP_BLOCK(OP, K, a, b)                                                          \
+    do {                                                                                     \
+        if constexpr (K >= 4) {                                                              \
+            asm("s_nop 1\n\t" OP " %0, %1\n\t" OP " %2, %3\n\t" OP " %4, %5\n\t" OP " %6, %7" \
+                : "+v"(a[0]), "+v"(b[0]), "+v"(a[1]), "+v"(b[1]), "+v"(a[2]), "+v"(b[2]),    \
+                  "+v"(a[3]), "+v"(b[3]));                                                   \
+        } else if constexpr (K == 3) {                                                       \
+            asm("s_nop 1\n\t" OP " %0, %1\n\t" OP " %2, %3\n\t" OP " %4, %5"                \
+                : "+v"(a[0]), "+v"(b[0]), "+v"(a[1]), "+v"(b[1]), "+v"(a[2]), "+v"(b[2]));   \
+        } else if constexpr (K == 2) {                                                       \
+            asm("s_nop 1\n\t" OP " %0, %1\n\t" OP " %2, %3"                                 \
+                : "+v"(a[0]), "+v"(b[0]), "+v"(a[1]), "+v"(b[1]));                           \
+        } else if constexpr (K == 1) {                                                       \
+            asm("s_nop 1\n\t" OP " %0, %1" : "+v"(a[0]), "+v"(b[0]));                        \
+        }                                                                                    \
+    } while (0)
+
+template <int K>
+__device__ __forceinline__ void swap_rows32(float (&a)[K], float (&b)[K]) {
+    GSX_SWAP_BLOCK("v_permlane32_swap_b32", K, a, b);
 }
-__device__ __forceinline__ void swap_rows16(float& a, float& b) {
-    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+template <int K>
+__device__ __forceinline__ void swap_rows16(float (&a)[K], float (&b)[K]) {
+    GSX_SWAP_BLOCK("v_permlane16_swap_b32", K, a, b);
 }
 
 // Sums of NVP per-lane values (NVP a multiple of 4) over the 64 lanes of
@@ -178,35 +209,63 @@ __device__ __forceinline__ void swap_rows16(float& a, float& b) {
 // exchange.  All lanes must be active.
 __device__ __forceinline__ int row_value(int row) { return ((row & 1) << 1) | (row >> 1); }
 
+// Step 1 for value pairs K0..K1-1: h[k] = swap32-sum of v[2k], v[2k + 1]
+// (values from NZ on are zeros), four pairs per asm block.
+template <int K0, int K1, int NVP, int NZ>
+__device__ __forceinline__ void reduce_step1(const float (&v)[NVP], float (&h)[NVP / 2]) {
+    if constexpr (K0 < K1) {
+        constexpr int N = (K1 - K0) < 4 ? (K1 - K0) : 4;
+        float a[N], b[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            a[k] = v[2 * (K0 + k)];
+            b[k] = 2 * (K0 + k) + 1 < NZ ? v[2 * (K0 + k) + 1] : 0.0f;
+        }
+        swap_rows32<N>(a, b);
+#pragma unroll
+        for (int k = 0; k < N; ++k) h[K0 + k] = a[k] + b[k];
+        reduce_step1<K0 + N, K1, NVP, NZ>(v, h);
+    }
+}
+
+// Steps 2 and 3 for row groups M0..M1-1: swap16-sum of h[2m], h[2m + 1],
+// then the four DPP steps within each row.
+template <int M0, int M1, int NVP>
+__device__ __forceinline__ void reduce_step23(const float (&h)[NVP / 2], float (&q)[NVP / 4]) {
+    if constexpr (M0 < M1) {
+        constexpr int N = (M1 - M0) < 4 ? (M1 - M0) : 4;
+        float a[N], b[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            a[k] = h[2 * (M0 + k)];
+            b[k] = h[2 * (M0 + k) + 1];
+        }
+        swap_rows16<N>(a, b);
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            float t = a[k] + b[k];
+            t += dpp_f<0xB1, 0xF, 0xF>(t);   // quad_perm [1,0,3,2]
+            t += dpp_f<0x4E, 0xF, 0xF>(t);   // quad_perm [2,3,0,1]
+            t += dpp_f<0x141, 0xF, 0xF>(t);  // row_half_mirror
+            t += dpp_f<0x140, 0xF, 0xF>(t);  // row_mirror
+            q[M0 + k] = t;
+        }
+        reduce_step23<M0 + N, M1, NVP>(h, q);
+    }
+}
+
 template <int NVP, int NZ = NVP>
 __device__ __forceinline__ void wave_reduce_rows(const float (&v)[NVP], float (&q)[NVP / 4]) {
     static_assert(NVP % 4 == 0 && NZ <= NVP, "values come in groups of four");
+    constexpr int K1 = (NZ + 1) / 2;  // value pairs with a non-zero member
+    constexpr int K2 = (K1 + 1) / 2;  // row groups with a non-zero member
     float h[NVP / 2];
 #pragma unroll
-    for (int k = 0; k < NVP / 2; ++k) {
-        if (2 * k >= NZ) {
-            h[k] = 0.0f;
-            continue;
-        }
-        float a = v[2 * k], b = 2 * k + 1 < NZ ? v[2 * k + 1] : 0.0f;
-        swap_rows32(a, b);
-        h[k] = a + b;
-    }
+    for (int k = K1; k < NVP / 2; ++k) h[k] = 0.0f;
+    reduce_step1<0, K1, NVP, NZ>(v, h);
 #pragma unroll
-    for (int m = 0; m < NVP / 4; ++m) {
-        if (4 * m >= NZ) {
-            q[m] = 0.0f;
-            continue;
-        }
-        float a = h[2 * m], b = h[2 * m + 1];
-        swap_rows16(a, b);
-        float t = a + b;
-        t += dpp_f<0xB1, 0xF, 0xF>(t);   // quad_perm [1,0,3,2]
-        t += dpp_f<0x4E, 0xF, 0xF>(t);   // quad_perm [2,3,0,1]
-        t += dpp_f<0x141, 0xF, 0xF>(t);  // row_half_mirror
-        t += dpp_f<0x140, 0xF, 0xF>(t);  // row_mirror
-        q[m] = t;
-    }
+    for (int m = K2; m < NVP / 4; ++m) q[m] = 0.0f;
+    reduce_step23<0, K2, NVP>(h, q);
 }
 
 __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
@@ -224,49 +283,34 @@ __device__ __forceinline__ void tile_span(int2 rg, int64_t n_ids, int& start, in
     num = (int)(s1 - s0);
 }
 
-// Walk over the set bits of a quadrant's staged-Gaussian mask (NW 64-bit
-// words in LDS), ascending or descending.  Only the current word is held
-// (in scalar registers); the next word is read from LDS when it runs out.
-struct BitWalkUp {
-    const uint64_t* words;  // LDS
-    int nw, w;
-    uint64_t cur;
-    __device__ __forceinline__ void init(const uint64_t* p, int n) {
-        words = p;
-        nw = n;
-        w = 0;
-        cur = uniform64(p[0]);
+// A quadrant wave's walk list: the staged Gaussians whose bit is set in the
+// quadrant's NW mask words (loader wave lw, lane l <-> staged index
+// 64 lw + l), compacted in LDS as 16-bit record byte offsets (16 x index)
+// so the walk is a counted loop over uniform offsets.  Built by the wave
+// itself after the workgroup barrier that publishes the masks; ascending
+// index order (REV: descending).  list[cnt] and list[cnt + 1] are set to 0,
+// a valid offset, for the walks' look-ahead.  Returns cnt (uniform).
+template <int NW, bool REV>
+__device__ __forceinline__ int build_list(const uint64_t* words, uint16_t* list, int lane) {
+    int total = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
+    const uint64_t above = lane == 63 ? 0ull : ~((2ull << lane) - 1ull);
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+        const int lw = REV ? NW - 1 - k : k;
+        const uint64_t m = uniform64(words[lw]);
+        if ((m >> lane) & 1ull)
+            list[total + __popcll(m & (REV ? above : below))] = (uint16_t)((lw * kWave + lane) * 16);
+        total += __popcll(m);
     }
-    __device__ __forceinline__ int next() {
-        while (cur == 0ull) {
-            if (++w >= nw) return -1;
-            cur = uniform64(words[w]);
-        }
-        const int b = __builtin_ctzll(cur);
-        cur &= cur - 1ull;
-        return w * kWave + b;
-    }
-};
+    if (lane < 2) list[total + lane] = 0;
+    return total;
+}
 
-struct BitWalkDown {
-    const uint64_t* words;  // LDS
-    int w;
-    uint64_t cur;
-    __device__ __forceinline__ void init(const uint64_t* p, int n) {
-        words = p;
-        w = n - 1;
-        cur = uniform64(p[w]);
-    }
-    __device__ __forceinline__ int next() {
-        while (cur == 0ull) {
-            if (--w < 0) return -1;
-            cur = uniform64(words[w]);
-        }
-        const int b = 63 - __builtin_clzll(cur);
-        cur &= ~(1ull << b);
-        return w * kWave + b;
-    }
-};
+// The staged record at a byte offset from a list (16 x staged index).
+__device__ __forceinline__ const float4& rec_at(const float4* base, int off) {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(base) + off);
+}
 
 template <int CH>
 __device__ __forceinline__ void stage_features(float4* dst, const float* f, int nc) {
@@ -293,9 +337,9 @@ __device__ __forceinline__ float comp4(const float4& v, int e) {
 // range handling and a non-compositing lane can add a zero weight.
 template <int CH, bool DEPTH, bool PLAIN>
 __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
-                                         const float4* __restrict__ fsrc, int jlast, float pxf,
-                                         float pyf, float& T, float* acc, float& dacc, int& last,
-                                         bool& done) {
+                                         const float4* __restrict__ fsrc, int off, float pxf,
+                                         float pyf, float& T, float* acc, float& dacc,
+                                         int& last_off, bool& done) {
     constexpr int F4 = (CH + 3) / 4;
     float4 fv[F4];
 #pragma unroll
@@ -329,35 +373,41 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
         }
     }
     T = add ? next_T : T;
-    last = add ? jlast : last;
+    last_off = add ? off : last_off;
     done = done || stop;
 }
 
-// Front-to-back walk of one quadrant wave over its staged Gaussians, two
-// records in flight (the next one is read from LDS while the current one is
-// evaluated; a finished walk re-reads its last index, which is harmless).
+// Front-to-back walk of one quadrant wave over its list, two Gaussians per
+// round: each Gaussian's records are read while the one before it is
+// evaluated, and list entries two places ahead (list[cnt] and
+// list[cnt + 1] are valid padding; later entries may be stale and are
+// never used).  The wave stops once its 64 pixels have terminated.
+// last_off gets the offset of each pixel's last composited Gaussian of this
+// batch.
 template <int CH, bool DEPTH, bool PLAIN>
-__device__ __forceinline__ void fwd_walk(BitWalkUp& walk, const float4* s_r0, const float4* s_r1,
-                                         const float4 (*s_f)[(CH + 3) / 4], float pxf, float pyf,
-                                         int base, float& T, float* acc, float& dacc, int& last,
-                                         bool& done) {
-    int ja = walk.next();
-    if (ja < 0) return;
-    float4 a0 = s_r0[ja], a1 = s_r1[ja];
-    while (true) {
-        const int jb = walk.next();
-        const int lb = jb >= 0 ? jb : ja;
-        const float4 b0 = s_r0[lb], b1 = s_r1[lb];
-        fwd_pair<CH, DEPTH, PLAIN>(a0, a1, s_f[ja], base + ja + 1, pxf, pyf, T, acc, dacc, last,
-                                   done);
-        if (jb < 0 || __ballot(!done) == 0ull) return;
-        ja = walk.next();
-        const int la = ja >= 0 ? ja : jb;
-        a0 = s_r0[la];
-        a1 = s_r1[la];
-        fwd_pair<CH, DEPTH, PLAIN>(b0, b1, s_f[jb], base + jb + 1, pxf, pyf, T, acc, dacc, last,
-                                   done);
-        if (ja < 0 || __ballot(!done) == 0ull) return;
+__device__ __forceinline__ void fwd_walk(const uint16_t* list, int cnt, const float4* s_r0,
+                                         const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+                                         float pxf, float pyf, float& T, float* acc, float& dacc,
+                                         int& last_off, bool& done) {
+    constexpr int F4 = (CH + 3) / 4;
+    const float4* sf = &s_f[0][0];
+    if (cnt <= 0) return;
+    int oa = list[0], ob = list[1];
+    float4 a0 = rec_at(s_r0, oa), a1 = rec_at(s_r1, oa);
+    for (int i = 0;; i += 2) {
+        const int na = list[i + 2];
+        const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
+        fwd_pair<CH, DEPTH, PLAIN>(a0, a1, &rec_at(sf, oa * F4), oa, pxf, pyf, T, acc, dacc,
+                                   last_off, done);
+        if (i + 1 >= cnt) return;
+        const int nb = list[i + 3];
+        a0 = rec_at(s_r0, na);
+        a1 = rec_at(s_r1, na);
+        fwd_pair<CH, DEPTH, PLAIN>(b0, b1, &rec_at(sf, ob * F4), ob, pxf, pyf, T, acc, dacc,
+                                   last_off, done);
+        if (i + 2 >= cnt || __ballot(!done) == 0ull) return;
+        oa = na;
+        ob = nb;
     }
 }
 
@@ -377,6 +427,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     __shared__ float4 s_r1[kThreads];      // -a/2, -b, -c/2 (conic), depth
     __shared__ float4 s_f[kThreads][F4];   // channels, zero padded
     __shared__ uint64_t s_mask[kWaves][kWaves];  // [quadrant][loader wave]
+    __shared__ uint16_t s_list[kWaves][kThreads + 4];  // walk lists (+ look-ahead room)
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tile = (int)xcd_remap(blockIdx.x, gridDim.x);
@@ -423,14 +474,15 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
         }
         const bool batch_plain = __syncthreads_and(plain);
         if (__ballot(!done) == 0ull) continue;
-        BitWalkUp walk;
-        walk.init(s_mask[wave], kWaves);
+        const int cnt = build_list<kWaves, false>(s_mask[wave], s_list[wave], lane);
+        int last_off = -1;
         if (batch_plain)
-            fwd_walk<CH, DEPTH, true>(walk, s_r0, s_r1, s_f, pxf, pyf, base, T, acc, dacc, last,
-                                      done);
+            fwd_walk<CH, DEPTH, true>(s_list[wave], cnt, s_r0, s_r1, s_f, pxf, pyf, T, acc, dacc,
+                                      last_off, done);
         else
-            fwd_walk<CH, DEPTH, false>(walk, s_r0, s_r1, s_f, pxf, pyf, base, T, acc, dacc, last,
-                                       done);
+            fwd_walk<CH, DEPTH, false>(s_list[wave], cnt, s_r0, s_r1, s_f, pxf, pyf, T, acc,
+                                       dacc, last_off, done);
+        if (last_off >= 0) last = base + (last_off >> 4) + 1;
     }
     if (inside) {
         const int64_t pid = (int64_t)py * W + px;
@@ -477,19 +529,22 @@ struct BwdPixel {
 // in these sums).  power, alpha and the skip tests repeat the forward's
 // float32 arithmetic exactly (the replay must take the forward's
 // decisions); the gradient arithmetic itself uses fused multiply-adds.  T is
-// recovered with one reciprocal of (1 - alpha) per pair.  PLAIN: inputs are
-// finite, so a lane that does not contribute can run the same update with a
-// zero weight.
+// recovered with one reciprocal of (1 - alpha) per pair.  off is the
+// Gaussian's record offset (16 x its staged index) and lim = 16 (n_contrib -
+// batch base): the pixel's forward composited it only if off < lim.  PLAIN:
+// inputs are finite, so a lane that does not contribute can run the same
+// update with a zero weight.
 template <int CH, bool PLAIN, int S = 1, int O = 0, int NW>
 __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
-                                           const float4* __restrict__ fsrc, int gj, float pxf,
-                                           float pyf, BwdPixel<CH>& px, float (&out)[NW]) {
+                                           const float4* __restrict__ fsrc, int off, int lim,
+                                           float pxf, float pyf, BwdPixel<CH>& px,
+                                           float (&out)[NW]) {
     static_assert(S * (CH + 5) + O < NW, "strided values fit the output array");
     constexpr int F4 = (CH + 3) / 4;
     constexpr int NV = CH + 6;
     const float dx = r0.x - pxf, dy = r0.y - pyf;
     const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
-    bool ok = gj < px.last && !(power > 0.0f) && !(power < r0.z);
+    bool ok = off < lim && !(power > 0.0f) && !(power < r0.z);
     if (__ballot(ok) == 0ull) {
 #pragma unroll
         for (int q = 0; q < NV; ++q) out[S * q + O] = 0.0f;
@@ -538,18 +593,19 @@ __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
     return true;
 }
 
-__device__ __forceinline__ void mark_written(int j, uint64_t& wrote0, uint64_t& wrote1) {
-    if (j < kWave) wrote0 |= 1ull << j;
-    else wrote1 |= 1ull << (j - kWave);
+// A Gaussian's slot in the wave's LDS sums, from its record offset.
+template <int CH>
+__device__ __forceinline__ float* slot_at(float4 (*part)[((CH + 6) + 3) / 4], int off) {
+    constexpr int NV4 = ((CH + 6) + 3) / 4;
+    return reinterpret_cast<float*>(reinterpret_cast<char*>(part) + off * NV4);
 }
 
 // Wave sums of one Gaussian's values into its slot: row r of the wave ends
 // with the totals of values 4m + row_value(r), which lane 15 of the row
 // stores at those positions.
 template <int CH>
-__device__ __forceinline__ void bwd_reduce1(const float (&v)[CH + 6], int j,
-                                            float4 (*part)[((CH + 6) + 3) / 4], int lane,
-                                            uint64_t& wrote0, uint64_t& wrote1) {
+__device__ __forceinline__ void bwd_reduce1(const float (&v)[CH + 6], int off,
+                                            float4 (*part)[((CH + 6) + 3) / 4], int lane) {
     constexpr int NV = CH + 6;
     constexpr int NVP = 4 * ((NV + 3) / 4);
     float w[NVP];
@@ -558,22 +614,21 @@ __device__ __forceinline__ void bwd_reduce1(const float (&v)[CH + 6], int j,
     float tot[NVP / 4];
     wave_reduce_rows<NVP, NV>(w, tot);
     if ((lane & 15) == 15) {
-        float* dst = reinterpret_cast<float*>(part[j]) + row_value(lane >> 4);
+        float* dst = slot_at<CH>(part, off) + row_value(lane >> 4);
 #pragma unroll
         for (int m = 0; m < NVP / 4; ++m) dst[4 * m] = tot[m];
     }
-    mark_written(j, wrote0, wrote1);
 }
 
-// The same for two Gaussians in one reduction (fewer padding values and
-// shared exchange steps): value i of Gaussian a sits at 2i and of Gaussian b
-// at 2i + 1 of the combined array, so the first exchange pairs a's and b's
-// value i; rows with row_value 0 and 2 then finish a's values 2m and 2m + 1,
-// rows with 1 and 3 b's, each stored at slot position 2m + (row_value >> 1).
+// The same for two different Gaussians in one reduction (fewer padding
+// values and shared exchange steps): value i of Gaussian a sits at 2i and of
+// Gaussian b at 2i + 1 of the combined array, so the first exchange pairs
+// a's and b's value i; rows with row_value 0 and 2 then finish a's values
+// 2m and 2m + 1, rows with 1 and 3 b's, each stored at slot position
+// 2m + (row_value >> 1).
 template <int CH>
-__device__ __forceinline__ void bwd_reduce2(float (&w)[4 * ((CH + 7) / 2)], int ja, bool ha,
-                                            int jb, bool hb, float4 (*part)[((CH + 6) + 3) / 4],
-                                            int lane, uint64_t& wrote0, uint64_t& wrote1) {
+__device__ __forceinline__ void bwd_reduce2(float (&w)[4 * ((CH + 7) / 2)], int oa, int ob,
+                                            float4 (*part)[((CH + 6) + 3) / 4], int lane) {
     constexpr int NV = CH + 6;
     constexpr int NH = (NV + 1) / 2;  // value pairs per Gaussian
     static_assert(2 * NH <= 4 * ((NV + 3) / 4), "a Gaussian's slot holds its padded pairs");
@@ -581,85 +636,88 @@ __device__ __forceinline__ void bwd_reduce2(float (&w)[4 * ((CH + 7) / 2)], int 
     wave_reduce_rows<4 * NH, 2 * NV>(w, tot);
     if ((lane & 15) == 15) {
         const int rv = row_value(lane >> 4);
-        float* dst = reinterpret_cast<float*>(part[(rv & 1) ? jb : ja]) + (rv >> 1);
+        float* dst = slot_at<CH>(part, (rv & 1) ? ob : oa) + (rv >> 1);
 #pragma unroll
         for (int m = 0; m < NH; ++m) dst[2 * m] = tot[m];
     }
-    if (ha) mark_written(ja, wrote0, wrote1);
-    if (hb) mark_written(jb, wrote0, wrote1);
 }
 
-// Back-to-front walk of one quadrant wave over its staged Gaussians, two
-// records in flight, one reduction per contributing Gaussian.
+// Back-to-front walk of one quadrant wave over its list (descending staged
+// index), records and list entries read ahead as in fwd_walk, one
+// reduction per contributing Gaussian.
 template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_walk1(BitWalkDown& walk, const float4* s_r0,
-                                          const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+__device__ __forceinline__ void bwd_walk1(const uint16_t* list, int cnt, int lim,
+                                          const float4* s_r0, const float4* s_r1,
+                                          const float4 (*s_f)[(CH + 3) / 4],
                                           float4 (*part)[((CH + 6) + 3) / 4], float pxf,
-                                          float pyf, int bbase, int lane, BwdPixel<CH>& px,
-                                          uint64_t& wrote0, uint64_t& wrote1) {
-    int ja = walk.next();
-    if (ja < 0) return;
-    float4 a0 = s_r0[ja], a1 = s_r1[ja];
-    while (true) {
-        const int jb = walk.next();
-        const int lb = jb >= 0 ? jb : ja;
-        const float4 b0 = s_r0[lb], b1 = s_r1[lb];
+                                          float pyf, int lane, BwdPixel<CH>& px) {
+    constexpr int F4 = (CH + 3) / 4;
+    const float4* sf = &s_f[0][0];
+    if (cnt <= 0) return;
+    int oa = list[0], ob = list[1];
+    float4 a0 = rec_at(s_r0, oa), a1 = rec_at(s_r1, oa);
+    for (int i = 0;; i += 2) {
+        const int na = list[i + 2];
+        const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
         {
             float v[CH + 6];
-            if (bwd_values<CH, PLAIN>(a0, a1, s_f[ja], bbase + ja, pxf, pyf, px, v))
-                bwd_reduce1<CH>(v, ja, part, lane, wrote0, wrote1);
+            if (bwd_values<CH, PLAIN>(a0, a1, &rec_at(sf, oa * F4), oa, lim, pxf, pyf, px, v))
+                bwd_reduce1<CH>(v, oa, part, lane);
         }
-        if (jb < 0) return;
-        ja = walk.next();
-        const int la = ja >= 0 ? ja : jb;
-        a0 = s_r0[la];
-        a1 = s_r1[la];
+        if (i + 1 >= cnt) return;
+        const int nb = list[i + 3];
+        a0 = rec_at(s_r0, na);
+        a1 = rec_at(s_r1, na);
         {
             float v[CH + 6];
-            if (bwd_values<CH, PLAIN>(b0, b1, s_f[jb], bbase + jb, pxf, pyf, px, v))
-                bwd_reduce1<CH>(v, jb, part, lane, wrote0, wrote1);
+            if (bwd_values<CH, PLAIN>(b0, b1, &rec_at(sf, ob * F4), ob, lim, pxf, pyf, px, v))
+                bwd_reduce1<CH>(v, ob, part, lane);
         }
-        if (ja < 0) return;
+        if (i + 2 >= cnt) return;
+        oa = na;
+        ob = nb;
     }
 }
 
-// The same walk with the two Gaussians of each step sharing one reduction
-// (a Gaussian without contributions enters it as zeros and is not marked):
-// their values are written interleaved, a's at even and b's at odd
-// positions, which is the layout bwd_reduce2 sums.
+// The same walk two Gaussians at a time, the pair sharing one reduction (a
+// Gaussian without contributions enters it as zeros): their values are
+// written interleaved, a's at even and b's at odd positions, which is the
+// layout bwd_reduce2 sums.  b's records are read before a is evaluated and
+// the next a's before b is; a lone last Gaussian is reduced by itself.
 template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_walk2(BitWalkDown& walk, const float4* s_r0,
-                                          const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+__device__ __forceinline__ void bwd_walk2(const uint16_t* list, int cnt, int lim,
+                                          const float4* s_r0, const float4* s_r1,
+                                          const float4 (*s_f)[(CH + 3) / 4],
                                           float4 (*part)[((CH + 6) + 3) / 4], float pxf,
-                                          float pyf, int bbase, int lane, BwdPixel<CH>& px,
-                                          uint64_t& wrote0, uint64_t& wrote1) {
+                                          float pyf, int lane, BwdPixel<CH>& px) {
+    constexpr int F4 = (CH + 3) / 4;
     constexpr int NV = CH + 6;
     constexpr int NW = 4 * ((NV + 1) / 2);
-    int ja = walk.next();
-    if (ja < 0) return;
-    float4 a0 = s_r0[ja], a1 = s_r1[ja];
-    while (true) {
-        const int jb = walk.next();
-        const int lb = jb >= 0 ? jb : ja;
-        const float4 b0 = s_r0[lb], b1 = s_r1[lb];
-        if (jb < 0) {
-            float v[NV];
-            if (bwd_values<CH, PLAIN>(a0, a1, s_f[ja], bbase + ja, pxf, pyf, px, v))
-                bwd_reduce1<CH>(v, ja, part, lane, wrote0, wrote1);
-            return;
-        }
-        float w[NW];
+    const float4* sf = &s_f[0][0];
+    int oa = list[0], ob = list[1];
+    float4 a0 = rec_at(s_r0, oa), a1 = rec_at(s_r1, oa);
+    for (int i = 0; i < cnt; i += 2) {
+        const int na = list[i + 2], nb = list[i + 3];
+        const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
+        if (i + 1 < cnt) {
+            float w[NW];
 #pragma unroll
-        for (int q = 2 * NV; q < NW; ++q) w[q] = 0.0f;
-        const bool ha = bwd_values<CH, PLAIN, 2, 0>(a0, a1, s_f[ja], bbase + ja, pxf, pyf, px, w);
-        const int jc = ja;
-        ja = walk.next();
-        const int la = ja >= 0 ? ja : jb;
-        a0 = s_r0[la];
-        a1 = s_r1[la];
-        const bool hb = bwd_values<CH, PLAIN, 2, 1>(b0, b1, s_f[jb], bbase + jb, pxf, pyf, px, w);
-        if (ha || hb) bwd_reduce2<CH>(w, jc, ha, jb, hb, part, lane, wrote0, wrote1);
-        if (ja < 0) return;
+            for (int q = 2 * NV; q < NW; ++q) w[q] = 0.0f;
+            const bool ha = bwd_values<CH, PLAIN, 2, 0>(a0, a1, &rec_at(sf, oa * F4), oa, lim,
+                                                        pxf, pyf, px, w);
+            const float4 n0 = rec_at(s_r0, na), n1 = rec_at(s_r1, na);
+            const bool hb = bwd_values<CH, PLAIN, 2, 1>(b0, b1, &rec_at(sf, ob * F4), ob, lim,
+                                                        pxf, pyf, px, w);
+            if (ha || hb) bwd_reduce2<CH>(w, oa, ob, part, lane);
+            a0 = n0;
+            a1 = n1;
+        } else {
+            float v[NV];
+            if (bwd_values<CH, PLAIN>(a0, a1, &rec_at(sf, oa * F4), oa, lim, pxf, pyf, px, v))
+                bwd_reduce1<CH>(v, oa, part, lane);
+        }
+        oa = na;
+        ob = nb;
     }
 }
 
@@ -667,17 +725,15 @@ __device__ __forceinline__ void bwd_walk2(BitWalkDown& walk, const float4* s_r0,
 // channel blocks reduce one Gaussian at a time, where padding is a small
 // share and two value sets would not fit the register budget.
 template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_walk(BitWalkDown& walk, const float4* s_r0,
-                                         const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
+__device__ __forceinline__ void bwd_walk(const uint16_t* list, int cnt, int lim,
+                                         const float4* s_r0, const float4* s_r1,
+                                         const float4 (*s_f)[(CH + 3) / 4],
                                          float4 (*part)[((CH + 6) + 3) / 4], float pxf, float pyf,
-                                         int bbase, int lane, BwdPixel<CH>& px, uint64_t& wrote0,
-                                         uint64_t& wrote1) {
+                                         int lane, BwdPixel<CH>& px) {
     if constexpr (CH <= 4)
-        bwd_walk2<CH, PLAIN>(walk, s_r0, s_r1, s_f, part, pxf, pyf, bbase, lane, px, wrote0,
-                             wrote1);
+        bwd_walk2<CH, PLAIN>(list, cnt, lim, s_r0, s_r1, s_f, part, pxf, pyf, lane, px);
     else
-        bwd_walk1<CH, PLAIN>(walk, s_r0, s_r1, s_f, part, pxf, pyf, bbase, lane, px, wrote0,
-                             wrote1);
+        bwd_walk1<CH, PLAIN>(list, cnt, lim, s_r0, s_r1, s_f, part, pxf, pyf, lane, px);
 }
 
 // Waves per SIMD the backward asks for (more waves hide LDS and ballot
@@ -699,15 +755,14 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     constexpr int NV = CH + 6;             // u, w, u dx, u dy, w dy, opacity term, channels
     constexpr int NV4 = (NV + 3) / 4;
     constexpr int BB = (CH <= 4) ? 128 : 64;  // Gaussians per batch (bounded by slot LDS)
-    constexpr int NLW = BB / kWave;
-    static_assert(NLW == 1 || NLW == 2, "the written-mask words are held as two scalars");
+    constexpr int NLW = BB / kWave;  // mask words per quadrant
     __shared__ float4 s_r0[BB];
     __shared__ float4 s_r1[BB];  // -a/2, -b, -c/2 (conic), unused
     __shared__ float4 s_f[BB][F4];
     __shared__ int s_id[BB];
     __shared__ float4 s_part[kWaves][BB][NV4];  // per-wave gradient sums per Gaussian
     __shared__ uint64_t s_mask[kWaves][NLW];
-    __shared__ uint64_t s_wrote[kWaves][NLW];
+    __shared__ uint16_t s_list[kWaves][BB + 4];  // walk lists (+ look-ahead room)
     __shared__ int s_last[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -785,41 +840,42 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
             }
         }
         const bool batch_plain = __syncthreads_and(plain);
-        BitWalkDown walk;
-        walk.init(s_mask[wave], NLW);
-        uint64_t wrote0 = 0ull, wrote1 = 0ull;
-        if (batch_plain)
-            bwd_walk<CH, true>(walk, s_r0, s_r1, s_f, s_part[wave], pxf, pyf, b * BB, lane, st,
-                               wrote0, wrote1);
-        else
-            bwd_walk<CH, false>(walk, s_r0, s_r1, s_f, s_part[wave], pxf, pyf, b * BB, lane, st,
-                                wrote0, wrote1);
-        if (lane == 0) {
-            s_wrote[wave][0] = wrote0;
-            if (NLW > 1) s_wrote[wave][NLW - 1] = wrote1;
+        // the wave's slots start at zero: Gaussians it does not walk, or
+        // whose sums it does not store, then add nothing in the flush
+        {
+            float4* p = &s_part[wave][0][0];
+#pragma unroll
+            for (int k = 0; k < BB * NV4 / kWave; ++k)
+                p[k * kWave + lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
+        const int cnt = build_list<NLW, true>(s_mask[wave], s_list[wave], lane);
+        const int lim = 16 * max(0, min(st.last - b * BB, BB));
+        if (batch_plain)
+            bwd_walk<CH, true>(s_list[wave], cnt, lim, s_r0, s_r1, s_f, s_part[wave], pxf, pyf,
+                               lane, st);
+        else
+            bwd_walk<CH, false>(s_list[wave], cnt, lim, s_r0, s_r1, s_f, s_part[wave], pxf, pyf,
+                                lane, st);
         __syncthreads();
         if (tid < BB) {
             const int g = s_id[tid];
             float4 sum[NV4];
 #pragma unroll
-            for (int q = 0; q < NV4; ++q) sum[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            bool any = false;
+            for (int q = 0; q < NV4; ++q) sum[q] = s_part[0][tid][q];
+            // one wave's slot at a time (all four in flight would need
+            // 4 NV4 float4 registers)
+#pragma unroll 1
+            for (int w = 1; w < kWaves; ++w) {
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                if ((s_wrote[w][tid >> 6] >> (tid & 63)) & 1ull) {
-                    any = true;
-#pragma unroll
-                    for (int q = 0; q < NV4; ++q) {
-                        const float4 p = s_part[w][tid][q];
-                        sum[q].x += p.x;
-                        sum[q].y += p.y;
-                        sum[q].z += p.z;
-                        sum[q].w += p.w;
-                    }
+                for (int q = 0; q < NV4; ++q) {
+                    const float4 p = s_part[w][tid][q];
+                    sum[q].x += p.x;
+                    sum[q].y += p.y;
+                    sum[q].z += p.z;
+                    sum[q].w += p.w;
                 }
             }
-            if (any && g >= 0) {
+            if (g >= 0) {
                 float e[4 * NV4];
 #pragma unroll
                 for (int q = 0; q < NV4; ++q) {

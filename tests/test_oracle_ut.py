@@ -50,11 +50,15 @@ def _f64(*a):
     return [torch.tensor(x, dtype=torch.float64) for x in a]
 
 
+# fixed per-camera scene seeds (str hash() changes from process to process)
+_SEEDS = {"pinhole": 11, "brown4": 12, "brown5": 13, "fisheye": 14, "ortho": 15}
+
+
 @pytest.mark.parametrize("name", ["pinhole", "brown4", "brown5", "fisheye", "ortho"])
 @pytest.mark.parametrize("antialias", [False, True])
 def test_ut_forward_matches_f64(name, antialias):
     cam = lens_cameras()[name]
-    means, quats, scales = _scene(seed=hash(name) % 1000)
+    means, quats, scales = _scene(seed=_SEEDS[name])
     out = O.project_ut(oracle_camera(cam), means, quats, scales, antialias=antialias)
     ref = project_ut_f64(cam, *_f64(means, quats, scales), antialias=antialias)
     valid = ref["radii"].numpy() > 0
