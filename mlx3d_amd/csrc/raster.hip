@@ -73,12 +73,21 @@ __device__ __forceinline__ float splat_power(float A, float B, float C, float dx
     return fmaf(B * dx, dy, fmaf(C * dy, dy, (A * dx) * dx));
 }
 
+// ln x from the hardware base-2 logarithm (about 1 ulp of log2 x, plus the
+// rounding of the product): the culling bounds below carry margins of
+// 1e-3 + 1e-4 |L| (alpha_floor_power) and 1% + 1e-3 (quadrant_mask), far
+// above that error.  x must be a positive normal number.
+__device__ __forceinline__ float ln_fast(float x) {
+    return __builtin_amdgcn_logf(x) * 0.693147180559945309f;
+}
+
 // Power below which o * exp(power) < 1/255 for certain.  +inf when the
 // opacity can never reach 1/255 (o <= 0 or tiny), -inf when no bound is safe
 // (o NaN or +inf).
 __device__ __forceinline__ float alpha_floor_power(float o) {
     if (o > 0.0f) {
-        float L = -__logf(255.0f * o);  // ln(1 / (255 o))
+        // ln(1 / (255 o)); below the normal range the bound is 200 anyway
+        float L = 255.0f * o >= 1.17549435e-38f ? -ln_fast(255.0f * o) : 200.0f;
         L = fminf(L, 200.0f);
         return L - (1e-3f + 1e-4f * fabsf(L));
     }
@@ -107,7 +116,7 @@ __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, in
     const float A = c.x, B = c.y, C = c.z;
     const float det = fmaf(A, C, -B * B);
     if (!(A > 0.0f && C > 0.0f && det > 1e-3f * A * C)) return 0xFu;
-    const float t2 = 2.0f * fmaf(__logf(255.0f * o), 1.01f, 1e-3f);
+    const float t2 = 2.0f * fmaf(ln_fast(255.0f * o), 1.01f, 1e-3f);
     if (!(t2 < 1e30f && A < 1e30f && C < 1e30f && fabsf(x) < 1e30f && fabsf(y) < 1e30f))
         return 0xFu;
     const float ia = __builtin_amdgcn_rcpf(A), ic = __builtin_amdgcn_rcpf(C);
@@ -288,10 +297,12 @@ __device__ __forceinline__ void tile_span(int2 rg, int64_t n_ids, int& start, in
 // 64 lw + l), compacted in LDS as 16-bit record byte offsets (16 x index)
 // so the walk is a counted loop over uniform offsets.  Built by the wave
 // itself after the workgroup barrier that publishes the masks; ascending
-// index order (REV: descending).  list[cnt] and list[cnt + 1] are set to 0,
-// a valid offset, for the walks' look-ahead.  Returns cnt (uniform).
+// index order (REV: descending).  list[cnt] and list[cnt + 1] are set to
+// pad, a valid record offset, for the walks' look-ahead.  Returns cnt
+// (uniform).
 template <int NW, bool REV>
-__device__ __forceinline__ int build_list(const uint64_t* words, uint16_t* list, int lane) {
+__device__ __forceinline__ int build_list(const uint64_t* words, uint16_t* list, int lane,
+                                          int pad) {
     int total = 0;
     const uint64_t below = (1ull << lane) - 1ull;
     const uint64_t above = lane == 63 ? 0ull : ~((2ull << lane) - 1ull);
@@ -303,7 +314,7 @@ __device__ __forceinline__ int build_list(const uint64_t* words, uint16_t* list,
             list[total + __popcll(m & (REV ? above : below))] = (uint16_t)((lw * kWave + lane) * 16);
         total += __popcll(m);
     }
-    if (lane < 2) list[total + lane] = 0;
+    if (lane < 2) list[total + lane] = (uint16_t)pad;
     return total;
 }
 
@@ -474,7 +485,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
         }
         const bool batch_plain = __syncthreads_and(plain);
         if (__ballot(!done) == 0ull) continue;
-        const int cnt = build_list<kWaves, false>(s_mask[wave], s_list[wave], lane);
+        const int cnt = build_list<kWaves, false>(s_mask[wave], s_list[wave], lane, 0);
         int last_off = -1;
         if (batch_plain)
             fwd_walk<CH, DEPTH, true>(s_list[wave], cnt, s_r0, s_r1, s_f, pxf, pyf, T, acc, dacc,
@@ -523,7 +534,8 @@ struct BwdPixel {
 // One (pixel, Gaussian) step of the back-to-front replay
 // (rasterize.py:162-219).  Returns whether any lane of the wave contributes
 // and writes each lane's values to out[S q + O] (all zeros when none does):
-//   u = G dx dL/dG, w = G dy dL/dG, u dx, u dy, w dy, G dL/dalpha, alpha T g_c
+//   u = G dx dL/dalpha, w = G dy dL/dalpha, u dx, u dy, w dy, G dL/dalpha,
+//   alpha T g_c
 // (zero for lanes that do not contribute), whose wave sums the flush turns
 // into the reference's means2d, conic, opacity and colour gradients (linear
 // in these sums).  power, alpha and the skip tests repeat the forward's
@@ -544,8 +556,13 @@ __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
     constexpr int NV = CH + 6;
     const float dx = r0.x - pxf, dy = r0.y - pyf;
     const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
-    bool ok = off < lim && !(power > 0.0f) && !(power < r0.z);
-    if (__ballot(ok) == 0ull) {
+    // the wave-wide tests ballot each comparison on its own: a ballot of a
+    // single comparison is its lane mask, one of a combined condition is
+    // first materialised in a vector register
+    const bool c1 = off < lim, c2 = !(power > 0.0f), c3 = !(power < r0.z);
+    bool ok = c1 && c2 && c3;
+    const uint64_t m123 = __ballot(c1) & __ballot(c2) & __ballot(c3);
+    if (m123 == 0ull) {
 #pragma unroll
         for (int q = 0; q < NV; ++q) out[S * q + O] = 0.0f;
         return false;
@@ -555,8 +572,9 @@ __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
     const float G = PLAIN ? splat_exp_core(__builtin_amdgcn_fmed3f(power, -86.0f, 0.0f))
                           : splat_exp_sel(power);
     const float alpha = fminf(0.99f, r0.w * G);
-    ok = ok && !(alpha < 1.0f / 255.0f);
-    if (__ballot(ok) == 0ull) {
+    const bool c4 = !(alpha < 1.0f / 255.0f);
+    ok = ok && c4;
+    if ((m123 & __ballot(c4)) == 0ull) {
         // every output is written on every path, so callers hold no stale
         // values across iterations
 #pragma unroll
@@ -577,15 +595,17 @@ __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
     // PLAIN: cg is finite, so aT = 0 leaves Q unchanged without a select.
     const float qn = fmaf(aT, cg, px.Q);
     px.Q = (PLAIN || ok) ? qn : px.Q;
-    const float gd = G * (r0.w * dL_dalpha);  // G dL/dG
-    const float u = gd * dx, w = gd * dy;
+    // G dL/dalpha; the opacity factor of G dL/dG = o G dL/dalpha is applied
+    // to the sums in the flush
+    const float ga = G * dL_dalpha;
+    const float u = ga * dx, w = ga * dy;
     float v[NV];
     v[0] = u;
     v[1] = w;
     v[2] = u * dx;
     v[3] = u * dy;
     v[4] = w * dy;
-    v[5] = G * dL_dalpha;
+    v[5] = ga;
 #pragma unroll
     for (int ch = 0; ch < CH; ++ch) v[6 + ch] = aT * px.gpix[ch];
 #pragma unroll
@@ -683,7 +703,8 @@ __device__ __forceinline__ void bwd_walk1(const uint16_t* list, int cnt, int lim
 // Gaussian without contributions enters it as zeros): their values are
 // written interleaved, a's at even and b's at odd positions, which is the
 // layout bwd_reduce2 sums.  b's records are read before a is evaluated and
-// the next a's before b is; a lone last Gaussian is reduced by itself.
+// the next a's before b is.  An odd count pairs the last Gaussian with the
+// padding record, which contributes nothing and owns a slot of its own.
 template <int CH, bool PLAIN>
 __device__ __forceinline__ void bwd_walk2(const uint16_t* list, int cnt, int lim,
                                           const float4* s_r0, const float4* s_r1,
@@ -699,23 +720,16 @@ __device__ __forceinline__ void bwd_walk2(const uint16_t* list, int cnt, int lim
     for (int i = 0; i < cnt; i += 2) {
         const int na = list[i + 2], nb = list[i + 3];
         const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
-        if (i + 1 < cnt) {
-            float w[NW];
+        float w[NW];
 #pragma unroll
-            for (int q = 2 * NV; q < NW; ++q) w[q] = 0.0f;
-            const bool ha = bwd_values<CH, PLAIN, 2, 0>(a0, a1, &rec_at(sf, oa * F4), oa, lim,
-                                                        pxf, pyf, px, w);
-            const float4 n0 = rec_at(s_r0, na), n1 = rec_at(s_r1, na);
-            const bool hb = bwd_values<CH, PLAIN, 2, 1>(b0, b1, &rec_at(sf, ob * F4), ob, lim,
-                                                        pxf, pyf, px, w);
-            if (ha || hb) bwd_reduce2<CH>(w, oa, ob, part, lane);
-            a0 = n0;
-            a1 = n1;
-        } else {
-            float v[NV];
-            if (bwd_values<CH, PLAIN>(a0, a1, &rec_at(sf, oa * F4), oa, lim, pxf, pyf, px, v))
-                bwd_reduce1<CH>(v, oa, part, lane);
-        }
+        for (int q = 2 * NV; q < NW; ++q) w[q] = 0.0f;
+        const bool ha = bwd_values<CH, PLAIN, 2, 0>(a0, a1, &rec_at(sf, oa * F4), oa, lim, pxf,
+                                                    pyf, px, w);
+        a0 = rec_at(s_r0, na);
+        a1 = rec_at(s_r1, na);
+        const bool hb = bwd_values<CH, PLAIN, 2, 1>(b0, b1, &rec_at(sf, ob * F4), ob, lim, pxf,
+                                                    pyf, px, w);
+        if (ha || hb) bwd_reduce2<CH>(w, oa, ob, part, lane);
         oa = na;
         ob = nb;
     }
@@ -756,11 +770,13 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     constexpr int NV4 = (NV + 3) / 4;
     constexpr int BB = (CH <= 4) ? 128 : 64;  // Gaussians per batch (bounded by slot LDS)
     constexpr int NLW = BB / kWave;  // mask words per quadrant
-    __shared__ float4 s_r0[BB];
-    __shared__ float4 s_r1[BB];  // -a/2, -b, -c/2 (conic), unused
-    __shared__ float4 s_f[BB][F4];
+    // entry BB of the records and slots is the walk lists' padding: a record
+    // no pixel can take (alpha bound +inf) whose slot the flush never reads
+    __shared__ float4 s_r0[BB + 1];
+    __shared__ float4 s_r1[BB + 1];  // -a/2, -b, -c/2 (conic), unused
+    __shared__ float4 s_f[BB + 1][F4];
     __shared__ int s_id[BB];
-    __shared__ float4 s_part[kWaves][BB][NV4];  // per-wave gradient sums per Gaussian
+    __shared__ float4 s_part[kWaves][BB + 1][NV4];  // per-wave gradient sums per Gaussian
     __shared__ uint64_t s_mask[kWaves][NLW];
     __shared__ uint16_t s_list[kWaves][BB + 4];  // walk lists (+ look-ahead room)
     __shared__ int s_last[kWaves];
@@ -791,6 +807,14 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     // The alpha output's cotangent enters once, with the first channel block.
     if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + grad_T[pid];
     st.Q = T_final * bg_dot;
+
+    // the padding record (written before the barrier below)
+    if (tid == 0) {
+        s_r0[BB] = make_float4(0.0f, 0.0f, __builtin_huge_valf(), 0.0f);
+        s_r1[BB] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int q = 0; q < F4; ++q) s_f[BB][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
 
     // Largest n_contrib of each quadrant: later list entries changed no pixel.
     {
@@ -848,7 +872,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
             for (int k = 0; k < BB * NV4 / kWave; ++k)
                 p[k * kWave + lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-        const int cnt = build_list<NLW, true>(s_mask[wave], s_list[wave], lane);
+        const int cnt = build_list<NLW, true>(s_mask[wave], s_list[wave], lane, BB * 16);
         const int lim = 16 * max(0, min(st.last - b * BB, BB));
         if (batch_plain)
             bwd_walk<CH, true>(s_list[wave], cnt, lim, s_r0, s_r1, s_f, s_part[wave], pxf, pyf,
@@ -857,8 +881,10 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
             bwd_walk<CH, false>(s_list[wave], cnt, lim, s_r0, s_r1, s_f, s_part[wave], pxf, pyf,
                                 lane, st);
         __syncthreads();
+        // 1. one thread per Gaussian adds the four waves' slots and turns the
+        //    sums into the reference's gradient components, kept in its own
+        //    wave-0 slot
         if (tid < BB) {
-            const int g = s_id[tid];
             float4 sum[NV4];
 #pragma unroll
             for (int q = 0; q < NV4; ++q) sum[q] = s_part[0][tid][q];
@@ -875,32 +901,42 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
                     sum[q].w += p.w;
                 }
             }
-            if (g >= 0) {
-                float e[4 * NV4];
+            float e[4 * NV4];
 #pragma unroll
-                for (int q = 0; q < NV4; ++q) {
-                    e[4 * q] = sum[q].x;
-                    e[4 * q + 1] = sum[q].y;
-                    e[4 * q + 2] = sum[q].z;
-                    e[4 * q + 3] = sum[q].w;
-                }
-                // rasterize.py:197-218 in terms of the sums; the staged conic
-                // is (-a/2, -b, -c/2)
-                const float4 c = s_r1[tid];
-                const float gx = 2.0f * c.x * e[0] + c.y * e[1];
-                const float gy = c.y * e[0] + 2.0f * c.z * e[1];
-                const float ga = -0.5f * e[2], gb = -e[3], gc = -0.5f * e[4];
-                if (gx != 0.0f) atomicAdd(&g_xy[2 * g], gx);
-                if (gy != 0.0f) atomicAdd(&g_xy[2 * g + 1], gy);
-                if (ga != 0.0f) atomicAdd(&g_conic[3 * g], ga);
-                if (gb != 0.0f) atomicAdd(&g_conic[3 * g + 1], gb);
-                if (gc != 0.0f) atomicAdd(&g_conic[3 * g + 2], gc);
-                if (e[5] != 0.0f) atomicAdd(&g_opac[g], e[5]);
-#pragma unroll
-                for (int ch = 0; ch < CH; ++ch)
-                    if (ch < nc && e[6 + ch] != 0.0f)
-                        atomicAdd(&g_feat[(int64_t)g * C + c0 + ch], e[6 + ch]);
+            for (int q = 0; q < NV4; ++q) {
+                e[4 * q] = sum[q].x;
+                e[4 * q + 1] = sum[q].y;
+                e[4 * q + 2] = sum[q].z;
+                e[4 * q + 3] = sum[q].w;
             }
+            // rasterize.py:197-218 in terms of the sums (dL/dG = o dL/dalpha);
+            // the staged conic is (-a/2, -b, -c/2)
+            const float4 c = s_r1[tid];
+            const float o = s_r0[tid].w;
+            float* fin = reinterpret_cast<float*>(s_part[0][tid]);
+            fin[0] = o * (2.0f * c.x * e[0] + c.y * e[1]);
+            fin[1] = o * (c.y * e[0] + 2.0f * c.z * e[1]);
+            fin[2] = -0.5f * o * e[2];
+            fin[3] = -o * e[3];
+            fin[4] = -0.5f * o * e[4];
+#pragma unroll
+            for (int q = 5; q < NV; ++q) fin[q] = e[q];
+        }
+        __syncthreads();
+        // 2. the global atomics, component-major across the lanes: a wave's
+        //    atomic instruction covers about 64 / NV Gaussians, each touching
+        //    one cache line per gradient array, instead of 64 Gaussians with
+        //    one line each per component
+        for (int item = tid; item < BB * NV; item += kThreads) {
+            const int j = item / NV, k = item - j * NV;
+            const int g = s_id[j];
+            const float v = reinterpret_cast<const float*>(s_part[0][j])[k];
+            if (g < 0 || v == 0.0f || (k >= 6 && k - 6 >= nc)) continue;
+            float* dst = k < 2 ? g_xy + 2 * (int64_t)g + k
+                       : k < 5 ? g_conic + 3 * (int64_t)g + (k - 2)
+                       : k == 5 ? g_opac + g
+                                : g_feat + (int64_t)g * C + c0 + (k - 6);
+            atomicAdd(dst, v);
         }
     }
 }
