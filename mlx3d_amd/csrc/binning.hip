@@ -120,16 +120,24 @@ __device__ __forceinline__ int64_t live_count(int64_t n_host, const uint32_t* n_
     return d < n_host ? d : n_host;
 }
 
-// Lanes of the wave (among `valid` ones) holding the same 8-bit digit.
-__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
-    uint64_t m = __ballot(valid);
+// Lanes of the wave (among `valid` ones) holding the same digit, whose
+// significant bits are the low `nbits` (<= 8, uniform; the others are zero
+// in every key).  Per bit, the lanes whose bit differs from this lane's are
+// the ballot XOR this lane's bit replicated (a sign-extended bit field), and
+// the differing masks are OR-ed: four to five 32-bit operations per bit
+// instead of selecting between the ballot and its complement in 64 bits.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid, int nbits) {
+    uint32_t lo = 0u, hi = 0u;
 #pragma unroll
     for (int b = 0; b < kRadixBits; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t bb = __ballot(bit);
-        m &= bit ? bb : ~bb;
+        if (b >= nbits) break;
+        const int s = __builtin_amdgcn_sbfe((int)d, b, 1);  // 0 or -1
+        const uint64_t bb = __ballot(s != 0);
+        lo |= (uint32_t)bb ^ (uint32_t)s;
+        hi |= (uint32_t)(bb >> 32) ^ (uint32_t)s;
     }
-    return valid ? m : 0ull;
+    const uint64_t same = ~(((uint64_t)hi << 32) | lo) & __ballot(valid);
+    return valid ? same : 0ull;
 }
 
 // LDS histogram add of one digit per valid lane.  Lanes sharing the digit
@@ -256,7 +264,7 @@ __global__ __launch_bounds__(kHistThreads) void k_depth_hist(const uint32_t* __r
 template <int THREADS, int ITEMS>
 __global__ __launch_bounds__(THREADS) void k_onesweep(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n_host,
-    const uint32_t* __restrict__ n_dev, int shift, const uint32_t* __restrict__ hist,
+    const uint32_t* __restrict__ n_dev, int shift, int nbits, const uint32_t* __restrict__ hist,
     uint32_t* __restrict__ status, uint32_t* __restrict__ counter,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ err) {
     constexpr int kWaves = THREADS / 64;
@@ -295,7 +303,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     for (int r = 0; r < ITEMS; ++r) {
         const bool valid = base + r * 64 + lane < n;
         const uint32_t d = (key[r] >> shift) & (kRadix - 1);
-        const uint64_t m = match_digit(d, valid);
+        const uint64_t m = match_digit(d, valid, nbits);
         const uint32_t before = s_cnt[wave][d];
         rank[r] = before + (uint32_t)__popcll(m & lt);
         if (valid && (m & lt) == 0ull) s_cnt[wave][d] = before + (uint32_t)__popcll(m);
@@ -724,7 +732,7 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     for (int p = 0; p < 4; ++p) {
         hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems>), dim3((unsigned)L.depth_chunks),
                            dim3(kDepthThreads), 0, st, kin, vin, n, (const uint32_t*)nullptr,
-                           p * kRadixBits, depth_hist + p * kRadix,
+                           p * kRadixBits, kRadixBits, depth_hist + p * kRadix,
                            status + (size_t)p * L.depth_chunks * kRadix, misc + p, kbuf[p & 1],
                            vbuf[p & 1], err);
         kin = kbuf[p & 1];
@@ -737,6 +745,8 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     //    histograms) into the buffers from which the tile passes end in
     //    sorted_ids; 4. tile sort over the device-side D
     const int passes = refine ? L.tile_passes : passes_for(T);
+    // significant bits of the tile ids (the refine_tiles sentinel T included)
+    const int tile_bits = bits_for(std::max<int64_t>(refine ? T + 1 : T, 1));
     uint32_t* tk[2] = {at<uint32_t>(ws, L.tk0), at<uint32_t>(ws, L.tk1)};
     uint32_t* tv[2] = {(uint32_t*)sorted_ids, at<uint32_t>(ws, L.tv)};
     int cur = passes & 1;
@@ -756,7 +766,8 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     for (int p = 0; p < passes; ++p) {
         hipLaunchKernelGGL((k_onesweep<kTileThreads, kTileItems>), dim3((unsigned)L.tile_chunks),
                            dim3(kTileThreads), 0, st, tk[cur], tv[cur], capacity,
-                           (const uint32_t*)d_total, p * kRadixBits, tile_hist + p * kRadix,
+                           (const uint32_t*)d_total, p * kRadixBits,
+                           std::min(kRadixBits, tile_bits - p * kRadixBits), tile_hist + p * kRadix,
                            tstatus + (size_t)p * L.tile_chunks * kRadix, misc + 4 + p,
                            tk[cur ^ 1], tv[cur ^ 1], err);
         cur ^= 1;
