@@ -355,11 +355,14 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
 }
 
 // Exclusive scan of the tile counts in depth order: offs[i] = sum of the
-// counts of depth-ordered Gaussians 0..i-1, offs[n] = D, *d_total = D.
+// counts of depth-ordered Gaussians 0..i-1, offs[n] = D, *d_total = D; and
+// owner[b] for every emission workgroup b that has duplicates: the
+// depth-ordered Gaussian that owns its first duplicate b * kEmitDups.
 __global__ __launch_bounds__(kScanThreads) void k_count_scan(
     int64_t n, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ gids,
     uint32_t* __restrict__ status, uint32_t* __restrict__ counter, uint32_t* __restrict__ offs,
-    uint32_t* __restrict__ d_total, uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ owner, int64_t n_owner, uint32_t* __restrict__ d_total,
+    uint32_t* __restrict__ err) {
     __shared__ uint32_t s_w[kScanThreads / 64];
     __shared__ uint32_t s_chunk, s_prefix;
     const int tid = threadIdx.x;
@@ -396,7 +399,13 @@ __global__ __launch_bounds__(kScanThreads) void k_count_scan(
     uint32_t run = s_prefix + excl;
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) {
-        if (i0 + j < n) offs[i0 + j] = run;
+        if (i0 + j < n) {
+            offs[i0 + j] = run;
+            // owner[b] = the Gaussian whose duplicates include b * kEmitDups
+            for (int64_t b = ceil_div((int64_t)run, kEmitDups);
+                 b * kEmitDups < (int64_t)run + c[j] && b < n_owner; ++b)
+                owner[b] = (uint32_t)(i0 + j);
+        }
         run += c[j];
     }
 }
@@ -445,7 +454,8 @@ __device__ __forceinline__ bool refine_keep(uint32_t tx, uint32_t ty, int W, int
 // (passes x 256) go into copy blockIdx % kHistCopies of tile_hist.
 __global__ __launch_bounds__(kEmitThreads) void k_emit(
     int64_t n, int64_t cap, const uint32_t* __restrict__ d_total,
-    const uint32_t* __restrict__ offs, const uint32_t* __restrict__ gids,
+    const uint32_t* __restrict__ offs, const uint32_t* __restrict__ owner,
+    const uint32_t* __restrict__ gids,
     const uint2* __restrict__ rects, int tiles_x, int passes, const float2* __restrict__ xy,
     const float* __restrict__ con, int64_t cstride, int W, int H, uint32_t sentinel,
     uint32_t* __restrict__ dropped, uint32_t* __restrict__ keys_out,
@@ -462,8 +472,11 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit(
     const int64_t d1 = min(d0 + kEmitDups, nd);
     for (int k = tid; k < kMaxPasses * kRadix; k += kEmitThreads) (&s_h[0][0])[k] = 0u;
     if (tid == 0) s_drop = 0u;
-    const int64_t lo = block_find_owner<kEmitThreads>(offs, n, (uint32_t)d0);
-    const int64_t hi = block_find_owner<kEmitThreads>(offs, n, (uint32_t)(d1 - 1));
+    // owner of the first duplicate, and a bound on the owner of the last:
+    // the next workgroup's first owner, or a search for the last workgroup
+    const int64_t lo = owner[blockIdx.x];
+    const int64_t hi = d1 < nd ? (int64_t)owner[blockIdx.x + 1]
+                               : block_find_owner<kEmitThreads>(offs, n, (uint32_t)(d1 - 1));
     const int64_t w = hi - lo + 1;
     const bool staged = w <= kEmitDups;  // uniform
     if (staged) {
@@ -608,7 +621,7 @@ constexpr int kSyncStatusWord = 12;
 constexpr int kMiscWords = kMiscCounters + 2 * kHistCopies * kHistStride;
 
 struct Layout {
-    size_t dk0, dk1, dv0, dv1, offs, tk0, tk1, tv, status, misc, total;
+    size_t dk0, dk1, dv0, dv1, offs, owner, tk0, tk1, tv, status, misc, total;
     int64_t depth_chunks, tile_chunks, scan_chunks, emit_blocks, hist_blocks, status_words;
     int tile_passes;
 };
@@ -638,6 +651,7 @@ Layout make_layout(int64_t n, int64_t cap, int64_t num_tiles) {
     L.dv0 = take(4 * nn);
     L.dv1 = take(4 * nn);
     L.offs = take(4 * (nn + 1));
+    L.owner = take(4 * (size_t)L.emit_blocks);
     L.tk0 = take(4 * cc);
     L.tk1 = take(4 * cc);
     L.tv = take(4 * cc);
@@ -753,12 +767,15 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     uint32_t* tstatus = status + (size_t)4 * L.depth_chunks * kRadix;
     uint32_t* sstatus = tstatus + (size_t)L.tile_passes * L.tile_chunks * kRadix;
     uint32_t* offs = at<uint32_t>(ws, L.offs);
+    uint32_t* owner = at<uint32_t>(ws, L.owner);
     hipLaunchKernelGGL(k_count_scan, dim3((unsigned)L.scan_chunks), dim3(kScanThreads), 0, st, n,
-                       tile_counts, gids, sstatus, misc + 8, offs, d_total, err);
+                       tile_counts, gids, sstatus, misc + 8, offs, owner, L.emit_blocks, d_total,
+                       err);
     GSX_LAUNCH_CHECK();
     if (capacity == 0) return GSX_OK;
     hipLaunchKernelGGL(k_emit, dim3((unsigned)L.emit_blocks), dim3(kEmitThreads), 0, st, n,
-                       capacity, (const uint32_t*)d_total, (const uint32_t*)offs, gids,
+                       capacity, (const uint32_t*)d_total, (const uint32_t*)offs,
+                       (const uint32_t*)owner, gids,
                        (const uint2*)tile_rects, tiles_x, passes, (const float2*)means2d,
                        conics, conic_stride, (int)width, (int)height, (uint32_t)T, dropped,
                        tk[cur], tv[cur], tile_hist);
