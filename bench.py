@@ -325,6 +325,7 @@ def main():
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from mlx3d_amd import _lib, scenes
     from mlx3d_amd.profiling import StageTimer
+    from mlx3d_amd.losses import l1_loss
     from mlx3d_amd.splatting import GaussianModel, render_gaussian_features
 
     if not torch.cuda.is_available():
@@ -373,7 +374,7 @@ def main():
                 render(i)
             return
         img = render(i)
-        loss = (img - targets[i % nviews]).abs().mean()
+        loss = l1_loss(img, targets[i % nviews])
         loss.backward()
 
     for i in range(args.warmup):

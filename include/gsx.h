@@ -322,6 +322,20 @@ int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels,
                         const void* workspace, int64_t workspace_bytes,
                         const float* grad_out, float* grad_pred, void* stream);
 
+/* Replaces l1_loss(pred, target) = mean |pred - target|
+ * (losses/image_metrics.py:13-14) for n contiguous floats: out (1 float,
+ * device); partial sums in double, added in a fixed order.  The workspace
+ * holds the partials (gsx_l1_workspace_bytes). */
+int64_t gsx_l1_workspace_bytes(int64_t n);
+int gsx_l1_fwd(int64_t n, const float* pred, const float* target,
+               void* workspace, int64_t workspace_bytes, float* out,
+               void* stream);
+
+/* Its gradient: grad_pred = sign(pred - target) grad_out[0] / n (sign(0) =
+ * 0), grad_out (1 float) on the device. */
+int gsx_l1_bwd(int64_t n, const float* pred, const float* target,
+               const float* grad_out, float* grad_pred, void* stream);
+
 #define GSX_ADAM_MAX_GROUPS 8
 
 /* One parameter group of gsx_adam_step: n floats each (host struct). */

@@ -380,6 +380,72 @@ int64_t photometric_blocks(int32_t H, int32_t W) {
 
 int64_t photometric_groups(int32_t C) { return (C + kSsMaxCh - 1) / kSsMaxCh; }
 
+// ------------------------------------------------------------------ L1 --
+// mean |pred - target| (image_metrics.py:13-14): each workgroup sums 4096
+// elements (float4 loads) in double into its partial (k_loss_reduce adds
+// the partials in a fixed order), and the gradient sign(pred - target) g/n
+// in one elementwise pass.
+constexpr int kL1Threads = 256, kL1Per = 16, kL1Block = kL1Threads * kL1Per;
+
+template <bool VEC>
+__global__ __launch_bounds__(kL1Threads) void k_l1_partial(int64_t n,
+                                                           const float* __restrict__ p,
+                                                           const float* __restrict__ t,
+                                                           float* __restrict__ partials) {
+    __shared__ double s[kL1Threads];
+    const int64_t base = (int64_t)blockIdx.x * kL1Block;
+    double acc = 0.0;
+#pragma unroll
+    for (int k = 0; k < kL1Per / 4; ++k) {
+        const int64_t i = base + 4 * ((int64_t)k * kL1Threads + threadIdx.x);
+        if (VEC && i + 3 < n) {
+            const float4 a = *reinterpret_cast<const float4*>(p + i);
+            const float4 b = *reinterpret_cast<const float4*>(t + i);
+            acc += (double)fabsf(a.x - b.x) + (double)fabsf(a.y - b.y) +
+                   (double)fabsf(a.z - b.z) + (double)fabsf(a.w - b.w);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (i + e < n) acc += (double)fabsf(p[i + e] - t[i + e]);
+        }
+    }
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = kL1Threads / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) s[threadIdx.x] += s[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        partials[2 * blockIdx.x] = (float)s[0];
+        partials[2 * blockIdx.x + 1] = 0.0f;
+    }
+}
+
+// grad = sign(pred - target) * (g / n); sign(0) = 0, NaN differences give NaN
+template <bool VEC>
+__global__ __launch_bounds__(kL1Threads) void k_l1_bwd(int64_t n, const float* __restrict__ p,
+                                                       const float* __restrict__ t,
+                                                       const float* __restrict__ g, float nf,
+                                                       float* __restrict__ grad) {
+    const float sc = g[0] / nf;
+    auto sgn = [&](float d) { return d > 0.0f ? sc : (d < 0.0f ? -sc : (d == 0.0f ? 0.0f : d)); };
+    const int64_t base = (int64_t)blockIdx.x * kL1Block;
+#pragma unroll
+    for (int k = 0; k < kL1Per / 4; ++k) {
+        const int64_t i = base + 4 * ((int64_t)k * kL1Threads + threadIdx.x);
+        if (VEC && i + 3 < n) {
+            const float4 a = *reinterpret_cast<const float4*>(p + i);
+            const float4 b = *reinterpret_cast<const float4*>(t + i);
+            *reinterpret_cast<float4*>(grad + i) =
+                make_float4(sgn(a.x - b.x), sgn(a.y - b.y), sgn(a.z - b.z), sgn(a.w - b.w));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (i + e < n) grad[i + e] = sgn(p[i + e] - t[i + e]);
+        }
+    }
+}
+
 inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
 }  // namespace
@@ -488,6 +554,50 @@ int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const f
         }
         GSX_LAUNCH_CHECK();
     }
+    return GSX_OK;
+}
+
+int64_t gsx_l1_workspace_bytes(int64_t n) {
+    if (n <= 0) return 0;
+    return align256(2 * ((n + kL1Block - 1) / kL1Block) * (int64_t)sizeof(float));
+}
+
+int gsx_l1_fwd(int64_t n, const float* pred, const float* target, void* workspace,
+               int64_t workspace_bytes, float* out, void* stream) {
+    if (n <= 0 || !pred || !target || !workspace || !out) return GSX_ERR_INVALID;
+    if (workspace_bytes < gsx_l1_workspace_bytes(n)) return GSX_ERR_WORKSPACE;
+    const int64_t nblk = (n + kL1Block - 1) / kL1Block;
+    if (nblk > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
+    hipStream_t st = (hipStream_t)stream;
+    float* partials = (float*)workspace;
+    const bool vec = (((uintptr_t)pred | (uintptr_t)target) & 15u) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_l1_partial<true>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
+                           pred, target, partials);
+    else
+        hipLaunchKernelGGL(k_l1_partial<false>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
+                           pred, target, partials);
+    GSX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, (const float*)partials, nblk,
+                       1.0 / (double)n, out);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_l1_bwd(int64_t n, const float* pred, const float* target, const float* grad_out,
+               float* grad_pred, void* stream) {
+    if (n <= 0 || !pred || !target || !grad_out || !grad_pred) return GSX_ERR_INVALID;
+    const int64_t nblk = (n + kL1Block - 1) / kL1Block;
+    if (nblk > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
+    hipStream_t st = (hipStream_t)stream;
+    const bool vec = (((uintptr_t)pred | (uintptr_t)target | (uintptr_t)grad_pred) & 15u) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_l1_bwd<true>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n, pred,
+                           target, grad_out, (float)n, grad_pred);
+    else
+        hipLaunchKernelGGL(k_l1_bwd<false>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
+                           pred, target, grad_out, (float)n, grad_pred);
+    GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
 

@@ -4,7 +4,8 @@
 one fused kernel pass (``gsx_photometric_fwd``), and the gradient of any
 combination of the two from a second (``gsx_photometric_bwd``); the trainer's
 ``(1 - lambda) L1 + lambda (1 - SSIM)`` (trainer.py:303-305) is formed from
-the two scalars.  ``ssim`` is the reference's function on top of it.
+the two scalars.  ``ssim`` is the reference's function on top of it, and
+``l1_loss`` the L1 term alone (``gsx_l1_fwd`` / ``gsx_l1_bwd``).
 """
 
 from __future__ import annotations
@@ -84,9 +85,42 @@ def ssim(pred: torch.Tensor, target: torch.Tensor, max_val: float = 1.0, window_
     return torch.stack(vals).mean()
 
 
+class _L1Fn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, pred, target):
+        n = pred.numel()
+        L = _lib.load()
+        nbytes = int(L.gsx_l1_workspace_bytes(n))
+        ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=pred.device)
+        out = torch.empty((1,), dtype=torch.float32, device=pred.device)
+        with stage("l1_fwd"):
+            _lib.check(L.gsx_l1_fwd(n, _lib.ptr(pred), _lib.ptr(target), _lib.ptr(ws), nbytes,
+                                    _lib.ptr(out), _lib.stream_handle(pred.device)), "gsx_l1_fwd")
+        ctx.save_for_backward(pred, target)
+        return out[0]
+
+    @staticmethod
+    def backward(ctx, g_out):
+        pred, target = ctx.saved_tensors
+        g = _lib.f32c(g_out.reshape(1))
+        grad = torch.empty_like(pred)
+        with stage("l1_bwd"):
+            _lib.check(_lib.load().gsx_l1_bwd(pred.numel(), _lib.ptr(pred), _lib.ptr(target),
+                                              _lib.ptr(g), _lib.ptr(grad),
+                                              _lib.stream_handle(pred.device)), "gsx_l1_bwd")
+        return grad, None
+
+
 def l1_loss(pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
-    """Mean absolute error (image_metrics.py:13-14)."""
-    return (pred - target).abs().mean()
+    """Mean absolute error (image_metrics.py:13-14), differentiable with
+    respect to ``pred``: one reduction kernel forward, one elementwise
+    gradient kernel backward (gsx_l1_fwd / gsx_l1_bwd)."""
+    if pred.shape != target.shape:
+        raise ValueError("pred and target must have the same shape.")
+    if pred.numel() == 0:
+        raise ValueError("l1_loss of empty tensors.")
+    _lib.require_device(pred, target)
+    return _L1Fn.apply(_lib.f32c(pred), _lib.f32c(target).detach())
 
 
 def psnr(pred: torch.Tensor, target: torch.Tensor, max_val: float = 1.0) -> torch.Tensor:

@@ -18,7 +18,7 @@ import torch
 
 from gpu_util import assert_bits, cu, host, oracle_backward, oracle_forward, rel_err, say
 from mlx3d_amd import _lib
-from mlx3d_amd.losses import photometric, ssim
+from mlx3d_amd.losses import l1_loss, photometric, ssim
 from mlx3d_amd.optim import Adam, adam_step, exponential_decay
 from mlx3d_amd.splatting import GaussianModel
 from mlx3d_amd.splatting.trainer import GaussianTrainer, TrainerConfig
@@ -78,6 +78,35 @@ def test_ssim_batched_and_errors():
         ssim(cu(a[0]), cu(b[0]), window_size=10)
     with pytest.raises(ValueError):
         photometric(cu(a[0]), cu(b[1, :20]))
+
+
+@pytest.mark.parametrize("n,offset", [(1, 0), (7, 0), (4101, 0), (4101, 1),
+                                      (1080 * 1920 * 3, 0), (65537, 3)])
+def test_l1_loss_matches_closed_form(n, offset):
+    """mean |p - t| against float64, and the gradient bit for bit against
+    sign(p - t) * (g / n) in float32; offset views take the unvectorised
+    path."""
+    say(f"l1 n={n} offset={offset}")
+    rng = np.random.default_rng(n + offset)
+    p = rng.random(n + offset, dtype=np.float32)
+    t = rng.random(n + offset, dtype=np.float32)
+    t[offset::5] = p[offset::5]  # equal entries: sign 0
+    base = cu(p).requires_grad_(True)
+    loss = l1_loss(base[offset:], cu(t)[offset:])  # offset > 0: unaligned contiguous view
+    ref = np.abs(p[offset:].astype(np.float64) - t[offset:].astype(np.float64)).mean()
+    assert abs(float(loss) - ref) <= 2e-7 * max(ref, 1e-30) + 1e-12
+    (2.5 * loss).backward()
+    g = base.grad[offset:]
+    sc = np.float32(2.5) / np.float32(n)
+    want = (np.sign(p[offset:] - t[offset:]).astype(np.float32) * sc).astype(np.float32)
+    assert_bits(host(g), want, "l1 grad")
+
+
+def test_l1_loss_errors():
+    with pytest.raises(ValueError):
+        l1_loss(torch.zeros(3), torch.zeros(3))  # host tensors
+    with pytest.raises(ValueError):
+        l1_loss(cu(np.zeros(3, np.float32)), cu(np.zeros(4, np.float32)))
 
 
 def test_adam_bitexact_multi_group():
