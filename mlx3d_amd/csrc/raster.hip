@@ -67,10 +67,11 @@ __device__ __forceinline__ float splat_exp_sel(float x) {
 
 // rasterize.py:77-78, power = -0.5 (a dx^2 + c dy^2) - b dx dy, with the
 // conic staged pre-scaled to (A, B, C) = (-a/2, -b, -c/2) (exact scalings)
-// and the two multiply-adds a contracting compiler forms from that
-// expression: power = (B dx) dy + ((C dy) dy + (A dx) dx).
+// and factored as power = (A dx + B dy) dx + (C dy) dy: three products and
+// two multiply-adds, five roundings whose error is at most
+// 2 eps (|A| dx^2 + |B dx dy| + |C| dy^2) + eps |power| (eps = 2^-24).
 __device__ __forceinline__ float splat_power(float A, float B, float C, float dx, float dy) {
-    return fmaf(B * dx, dy, fmaf(C * dy, dy, (A * dx) * dx));
+    return fmaf(fmaf(B, dy, A * dx), dx, (C * dy) * dy);
 }
 
 // ln x from the hardware base-2 logarithm (about 1 ulp of log2 x, plus the
@@ -105,7 +106,7 @@ __device__ __forceinline__ float alpha_floor_power(float o) {
 // with a and c exchanged), and the eight edge lines are shared by the
 // quadrants.  Float32 throughout: with det > 1e-3 a c every term carries a
 // relative error below 1e-4, and with b^2 < 0.999 a c the float32
-// evaluation of the power (splat_power) is within 7.2e-4 relative of the
+// evaluation of the power (splat_power) is within 4.8e-4 relative of the
 // exact value, so tau is inflated by 1% (+1e-3); the float32 log of the
 // bound and the <= 5 ulp of splat_exp add errors of ~1e-6, well inside
 // that.  Ill-conditioned, non-positive or non-finite conics get no culling
@@ -198,6 +199,37 @@ __device__ __forceinline__ float dpp_f(float v) {
         }                                                                                    \
     } while (0)
 
+// The last two steps of a 16-lane row sum for K registers, up to four per
+// asm block: t[k] += t[k] of the mirrored lane of its 8-lane half-row (DPP
+// row_half_mirror), then += that of the mirrored lane of its row
+// (row_mirror), after which every lane of a row holds the row's total.
+// asm (volatile) so the adds are not sunk into the following one-lane store
+// branch, where each would become a DPP move with a zero fill plus a
+// separate add; s_nop 1 gives the two wait states a DPP read needs after a
+// VALU write of its operand.
+#define GSX_DPP_ADD(r, ctl) "v_add_f32_dpp " r ", " r ", " r " " ctl " row_mask:0xf bank_mask:0xf\n\t"
+#define GSX_ROW_TAIL1(ctl) GSX_DPP_ADD("%0", ctl)
+#define GSX_ROW_TAIL2(ctl) GSX_DPP_ADD("%0", ctl) GSX_DPP_ADD("%1", ctl)
+#define GSX_ROW_TAIL3(ctl) GSX_DPP_ADD("%0", ctl) GSX_DPP_ADD("%1", ctl) GSX_DPP_ADD("%2", ctl)
+#define GSX_ROW_TAIL4(ctl) \
+    GSX_DPP_ADD("%0", ctl) GSX_DPP_ADD("%1", ctl) GSX_DPP_ADD("%2", ctl) GSX_DPP_ADD("%3", ctl)
+#define GSX_ROW_TAIL(N)                                                                   \
+    "s_nop 1\n\t" GSX_ROW_TAIL##N("row_half_mirror") "s_nop 1\n\t" GSX_ROW_TAIL##N("row_mirror")
+
+template <int K>
+__device__ __forceinline__ void row_tail_add(float (&t)[K]) {
+    static_assert(K >= 1 && K <= 4, "one to four registers per block");
+    if constexpr (K == 4) {
+        asm volatile(GSX_ROW_TAIL(4) : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]));
+    } else if constexpr (K == 3) {
+        asm volatile(GSX_ROW_TAIL(3) : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]));
+    } else if constexpr (K == 2) {
+        asm volatile(GSX_ROW_TAIL(2) : "+v"(t[0]), "+v"(t[1]));
+    } else {
+        asm volatile(GSX_ROW_TAIL(1) : "+v"(t[0]));
+    }
+}
+
 template <int K>
 __device__ __forceinline__ void swap_rows32(float (&a)[K], float (&b)[K]) {
     GSX_SWAP_BLOCK("v_permlane32_swap_b32", K, a, b);
@@ -253,12 +285,13 @@ __device__ __forceinline__ void reduce_step23(const float (&h)[NVP / 2], float (
 #pragma unroll
         for (int k = 0; k < N; ++k) {
             float t = a[k] + b[k];
-            t += dpp_f<0xB1, 0xF, 0xF>(t);   // quad_perm [1,0,3,2]
-            t += dpp_f<0x4E, 0xF, 0xF>(t);   // quad_perm [2,3,0,1]
-            t += dpp_f<0x141, 0xF, 0xF>(t);  // row_half_mirror
-            t += dpp_f<0x140, 0xF, 0xF>(t);  // row_mirror
-            q[M0 + k] = t;
+            t += dpp_f<0xB1, 0xF, 0xF>(t);  // quad_perm [1,0,3,2]
+            t += dpp_f<0x4E, 0xF, 0xF>(t);  // quad_perm [2,3,0,1]
+            a[k] = t;
         }
+        row_tail_add<N>(a);
+#pragma unroll
+        for (int k = 0; k < N; ++k) q[M0 + k] = a[k];
         reduce_step23<M0 + N, M1, NVP>(h, q);
     }
 }
@@ -391,8 +424,9 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
 // Front-to-back walk of one quadrant wave over its list, two Gaussians per
 // round: each Gaussian's records are read while the one before it is
 // evaluated, and list entries two places ahead (list[cnt] and
-// list[cnt + 1] are valid padding; later entries may be stale and are
-// never used).  The wave stops once its 64 pixels have terminated.
+// list[cnt + 1] are the padding record, which no pixel takes, so an odd
+// count needs no exit in the middle of a round; later entries may be stale
+// and are never used).  The wave stops once its 64 pixels have terminated.
 // last_off gets the offset of each pixel's last composited Gaussian of this
 // batch.
 template <int CH, bool DEPTH, bool PLAIN>
@@ -402,21 +436,18 @@ __device__ __forceinline__ void fwd_walk(const uint16_t* list, int cnt, const fl
                                          int& last_off, bool& done) {
     constexpr int F4 = (CH + 3) / 4;
     const float4* sf = &s_f[0][0];
-    if (cnt <= 0) return;
     int oa = list[0], ob = list[1];
     float4 a0 = rec_at(s_r0, oa), a1 = rec_at(s_r1, oa);
-    for (int i = 0;; i += 2) {
-        const int na = list[i + 2];
+    for (int i = 0; i < cnt; i += 2) {
+        const int na = list[i + 2], nb = list[i + 3];
         const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
         fwd_pair<CH, DEPTH, PLAIN>(a0, a1, &rec_at(sf, oa * F4), oa, pxf, pyf, T, acc, dacc,
                                    last_off, done);
-        if (i + 1 >= cnt) return;
-        const int nb = list[i + 3];
         a0 = rec_at(s_r0, na);
         a1 = rec_at(s_r1, na);
         fwd_pair<CH, DEPTH, PLAIN>(b0, b1, &rec_at(sf, ob * F4), ob, pxf, pyf, T, acc, dacc,
                                    last_off, done);
-        if (i + 2 >= cnt || __ballot(!done) == 0ull) return;
+        if (__ballot(!done) == 0ull) return;
         oa = na;
         ob = nb;
     }
@@ -434,11 +465,19 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     int W, int H, int tiles_x, float* __restrict__ out, float* __restrict__ final_T,
     int* __restrict__ n_contrib, float* __restrict__ depth_out) {
     constexpr int F4 = (CH + 3) / 4;
-    __shared__ float4 s_r0[kThreads];      // mean x, mean y, log-alpha bound, opacity
-    __shared__ float4 s_r1[kThreads];      // -a/2, -b, -c/2 (conic), depth
-    __shared__ float4 s_f[kThreads][F4];   // channels, zero padded
+    // entry kThreads of the records is the walk lists' padding: a record no
+    // pixel can take (alpha bound +inf)
+    __shared__ float4 s_r0[kThreads + 1];     // mean x, mean y, log-alpha bound, opacity
+    __shared__ float4 s_r1[kThreads + 1];     // -a/2, -b, -c/2 (conic), depth
+    __shared__ float4 s_f[kThreads + 1][F4];  // channels, zero padded
     __shared__ uint64_t s_mask[kWaves][kWaves];  // [quadrant][loader wave]
     __shared__ uint16_t s_list[kWaves][kThreads + 4];  // walk lists (+ look-ahead room)
+    // one word per wave, written before a barrier and read by every thread
+    // after it (a 16-byte read): some pixel of the wave still composites /
+    // every Gaussian the wave staged is plain.  Each batch's reads come
+    // before the next barrier, and the next batch writes only after it.
+    __shared__ __align__(16) uint32_t s_alive[kWaves];
+    __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tile = (int)xcd_remap(blockIdx.x, gridDim.x);
@@ -458,9 +497,20 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     for (int k = 0; k < CH; ++k) acc[k] = 0.0f;
     int last = 0;
     bool done = !inside;
+    // the padding record (written before the first barrier)
+    if (tid == 0) {
+        s_r0[kThreads] = make_float4(0.0f, 0.0f, __builtin_huge_valf(), 0.0f);
+        s_r1[kThreads] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int q = 0; q < F4; ++q) s_f[kThreads][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
 
     for (int base = 0; base < num; base += kThreads) {
-        if (__syncthreads_count(done) == kThreads) break;
+        const uint64_t alive = __ballot(!done);
+        if (lane == 0) s_alive[wave] = alive != 0ull;
+        __syncthreads();
+        const uint4 al = *reinterpret_cast<const uint4*>(s_alive);
+        if ((al.x | al.y | al.z | al.w) == 0u) break;  // all 256 pixels done
         const int k = base + tid;
         uint32_t qm = 0;
         bool plain = true;
@@ -483,9 +533,14 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
             const uint64_t b = __ballot((qm >> q) & 1u);
             if (lane == 0) s_mask[q][wave] = b;
         }
-        const bool batch_plain = __syncthreads_and(plain);
-        if (__ballot(!done) == 0ull) continue;
-        const int cnt = build_list<kWaves, false>(s_mask[wave], s_list[wave], lane, 0);
+        const uint64_t np = __ballot(!plain);
+        if (lane == 0) s_plain[wave] = np == 0ull;
+        __syncthreads();
+        const uint4 pl = *reinterpret_cast<const uint4*>(s_plain);
+        const bool batch_plain = (pl.x & pl.y & pl.z & pl.w) != 0u;
+        if (alive == 0ull) continue;
+        const int cnt =
+            build_list<kWaves, false>(s_mask[wave], s_list[wave], lane, kThreads * 16);
         int last_off = -1;
         if (batch_plain)
             fwd_walk<CH, DEPTH, true>(s_list[wave], cnt, s_r0, s_r1, s_f, pxf, pyf, T, acc, dacc,
@@ -567,10 +622,9 @@ __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
         for (int q = 0; q < NV; ++q) out[S * q + O] = 0.0f;
         return false;
     }
-    // PLAIN: lanes that pass have power in [-86, 0]; clamping leaves them
-    // unchanged and keeps G finite (so zero weights stay zero) elsewhere.
-    const float G = PLAIN ? splat_exp_core(__builtin_amdgcn_fmed3f(power, -86.0f, 0.0f))
-                          : splat_exp_sel(power);
+    // PLAIN: lanes that pass have power in [-86, 0]; the others' G is
+    // replaced by zero below, whatever its value.
+    const float G = PLAIN ? splat_exp_core(power) : splat_exp_sel(power);
     const float alpha = fminf(0.99f, r0.w * G);
     const bool c4 = !(alpha < 1.0f / 255.0f);
     ok = ok && c4;
@@ -584,20 +638,35 @@ __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
     float4 fv[F4];
 #pragma unroll
     for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
-    const float rcp = __builtin_amdgcn_rcpf(1.0f - alpha);
-    px.T = ok ? px.T * rcp : px.T;
     float cg = 0.0f;  // c_i . g
+    // ga = G dL/dalpha (the opacity factor of G dL/dG = o G dL/dalpha is
+    // applied to the sums in the flush), aT = alpha T
+    float ga, aT;
+    if constexpr (PLAIN) {
+        // a lane that does not contribute runs the update with G = alpha = 0:
+        // its rcp is 1 (T, Q unchanged) and its dL/dalpha is finite, so
+        // every value below is zero for it without further selects
+        const float Gs = ok ? G : 0.0f;
+        const float as = ok ? alpha : 0.0f;
+        const float rcp = __builtin_amdgcn_rcpf(1.0f - as);
+        px.T = px.T * rcp;
 #pragma unroll
-    for (int ch = 0; ch < CH; ++ch) cg = fmaf(comp4(fv[ch >> 2], ch & 3), px.gpix[ch], cg);
-    float dL_dalpha = fmaf(cg, px.T, -(px.Q * rcp));
-    dL_dalpha = ok ? dL_dalpha : 0.0f;
-    const float aT = ok ? alpha * px.T : 0.0f;
-    // PLAIN: cg is finite, so aT = 0 leaves Q unchanged without a select.
-    const float qn = fmaf(aT, cg, px.Q);
-    px.Q = (PLAIN || ok) ? qn : px.Q;
-    // G dL/dalpha; the opacity factor of G dL/dG = o G dL/dalpha is applied
-    // to the sums in the flush
-    const float ga = G * dL_dalpha;
+        for (int ch = 0; ch < CH; ++ch) cg = fmaf(comp4(fv[ch >> 2], ch & 3), px.gpix[ch], cg);
+        const float dL_dalpha = fmaf(cg, px.T, -(px.Q * rcp));
+        aT = as * px.T;
+        px.Q = fmaf(aT, cg, px.Q);
+        ga = Gs * dL_dalpha;
+    } else {
+        const float rcp = __builtin_amdgcn_rcpf(1.0f - alpha);
+        px.T = ok ? px.T * rcp : px.T;
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) cg = fmaf(comp4(fv[ch >> 2], ch & 3), px.gpix[ch], cg);
+        float dL_dalpha = fmaf(cg, px.T, -(px.Q * rcp));
+        dL_dalpha = ok ? dL_dalpha : 0.0f;
+        aT = ok ? alpha * px.T : 0.0f;
+        px.Q = ok ? fmaf(aT, cg, px.Q) : px.Q;
+        ga = G * dL_dalpha;
+    }
     const float u = ga * dx, w = ga * dy;
     float v[NV];
     v[0] = u;
@@ -773,13 +842,15 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     // entry BB of the records and slots is the walk lists' padding: a record
     // no pixel can take (alpha bound +inf) whose slot the flush never reads
     __shared__ float4 s_r0[BB + 1];
-    __shared__ float4 s_r1[BB + 1];  // -a/2, -b, -c/2 (conic), unused
+    __shared__ float4 s_r1[BB + 1];  // -a/2, -b, -c/2 (conic), Gaussian id (int bits)
     __shared__ float4 s_f[BB + 1][F4];
-    __shared__ int s_id[BB];
     __shared__ float4 s_part[kWaves][BB + 1][NV4];  // per-wave gradient sums per Gaussian
     __shared__ uint64_t s_mask[kWaves][NLW];
     __shared__ uint16_t s_list[kWaves][BB + 4];  // walk lists (+ look-ahead room)
     __shared__ int s_last[kWaves];
+    // per wave: every Gaussian it staged is plain (written before the staging
+    // barrier, read by all after it; the loop-top barrier orders batches)
+    __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tile = (int)xcd_remap(blockIdx.x, gridDim.x);
@@ -836,16 +907,15 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
         bool plain = true;
         if (tid < BB) {
             const int k = b * BB + tid;
-            int gid = -1;
+            float4 r1 = make_float4(0.0f, 0.0f, 0.0f, __int_as_float(-1));
             if (k < num) {
                 const int g = ids[start + k];
                 if ((uint32_t)g < (uint64_t)n) {
-                    gid = g;
                     const float2 m = xy[g];
                     const float4 c = co[g];
                     const float thr = alpha_floor_power(c.w);
                     s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
-                    s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, 0.0f);
+                    r1 = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, __int_as_float(g));
                     stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                     qm = quadrant_mask(m.x, m.y, c, px0, py0);
 #pragma unroll
@@ -854,7 +924,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
                     plain = plain_gaussian<CH>(m.x, m.y, c, thr, s_f[tid]);
                 }
             }
-            s_id[tid] = gid;
+            s_r1[tid] = r1;
         }
         if (wave < NLW) {
 #pragma unroll
@@ -863,7 +933,11 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
                 if (lane == 0) s_mask[q][wave] = bq;
             }
         }
-        const bool batch_plain = __syncthreads_and(plain);
+        const uint64_t np = __ballot(!plain);
+        if (lane == 0) s_plain[wave] = np == 0ull;
+        __syncthreads();
+        const uint4 pl = *reinterpret_cast<const uint4*>(s_plain);
+        const bool batch_plain = (pl.x & pl.y & pl.z & pl.w) != 0u;
         // the wave's slots start at zero: Gaussians it does not walk, or
         // whose sums it does not store, then add nothing in the flush
         {
@@ -929,7 +1003,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
         //    one line each per component
         for (int item = tid; item < BB * NV; item += kThreads) {
             const int j = item / NV, k = item - j * NV;
-            const int g = s_id[j];
+            const int g = __float_as_int(s_r1[j].w);
             const float v = reinterpret_cast<const float*>(s_part[0][j])[k];
             if (g < 0 || v == 0.0f || (k >= 6 && k - 6 >= nc)) continue;
             float* dst = k < 2 ? g_xy + 2 * (int64_t)g + k

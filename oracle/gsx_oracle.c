@@ -83,12 +83,13 @@ void orc_splat_expf_array(int64_t n, const float* x, float* y) {
 }
 
 /* rasterize.py:77-78, power = -0.5 (a dx^2 + c dy^2) - b dx dy, evaluated
- * with the conic pre-scaled to (A, B, C) = (-a/2, -b, -c/2) (exact) and the
- * two multiply-adds a contracting compiler forms from that expression:
- * power = (B dx) dy + ((C dy) dy + (A dx) dx). */
+ * with the conic pre-scaled to (A, B, C) = (-a/2, -b, -c/2) (exact) and
+ * factored as power = (A dx + B dy) dx + (C dy) dy (three products, two
+ * multiply-adds; error <= 2 eps (|A| dx^2 + |B dx dy| + |C| dy^2) + eps |power|,
+ * eps = 2^-24). */
 float orc_splat_power(float a, float b, float c, float dx, float dy) {
     const float A = -0.5f * a, B = -b, C = -0.5f * c;
-    return fmaf(B * dx, dy, fmaf(C * dy, dy, (A * dx) * dx));
+    return fmaf(fmaf(B, dy, A * dx), dx, (C * dy) * dy);
 }
 
 /* model.py:116-122 activations. */

@@ -92,8 +92,30 @@ def test_splat_power_against_float64():
         exact = -0.5 * (a * dx * dx + c * dy * dy) - b * dx * dy
         scale = 0.5 * (a * dx * dx + c * dy * dy) + abs(b * dx * dy)
         worst = max(worst, abs(p - exact) / scale)
-    # three roundings of terms bounded by scale: a few float32 epsilons
-    assert worst < 4 * 2.0**-23
+    # (A dx + B dy) dx + (C dy) dy with five roundings: the error is at most
+    # 2 eps scale + eps |power| <= 3 eps scale (eps = 2^-24)
+    assert worst <= 3 * 2.0**-24
+
+
+def test_splat_power_relative_bound_for_culling():
+    # the quadrant culling assumes the float32 power is within 4.8e-4 of the
+    # exact value, relative, when b^2 < 0.999 a c (nearly degenerate conics)
+    rng = np.random.default_rng(12)
+    worst = 0.0
+    for _ in range(20000):
+        s1, s2 = np.exp(rng.normal(0, 1.5, 2))
+        rho = rng.uniform(-1, 1) * 0.9994
+        a, c = 1 / s1**2, 1 / s2**2
+        b = rho * np.sqrt(a * c)
+        a, b, c = (float(np.float32(v)) for v in (a, b, c))
+        if not b * b < 0.999 * a * c:
+            continue
+        dx, dy = (float(np.float32(v)) for v in rng.normal(0, 3 * max(s1, s2), 2))
+        exact = -0.5 * (a * dx * dx + c * dy * dy) - b * dx * dy
+        if exact == 0.0:
+            continue
+        worst = max(worst, abs(O.splat_power(a, b, c, dx, dy) - exact) / abs(exact))
+    assert worst <= 4.8e-4
 
 
 def test_splat_power_closed_forms():
