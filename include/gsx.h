@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define GSX_ABI_VERSION 2
+#define GSX_ABI_VERSION 3
 #define GSX_TILE_SIZE 16 /* tiles.py:14 */
 
 enum gsx_status {
@@ -230,8 +230,9 @@ int gsx_bin_sort(int64_t n, const uint32_t* tile_counts,
                  int64_t* num_dups, void* stream);
 
 /* The same pipeline without the readback: bin_status (4 device words) gets
- * the number of duplicates emitted, the gsx_bin_error bits and the number
- * refine_tiles dropped (they sort after all kept ones).  If the emitted
+ * the number of duplicates emitted, the gsx_bin_error bits, the number
+ * refine_tiles dropped (they sort after all kept ones) and the sum of the
+ * tile counts (see gsx_bin_count_async).  If the emitted
  * duplicates exceed capacity, sorted_ids/tile_ranges hold an incomplete
  * (but in-bounds: ids < n, ranges within [0, capacity]) binning, so kernels
  * enqueued behind it stay safe; the caller copies bin_status to the host
@@ -245,6 +246,53 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts,
                        int64_t capacity, int32_t* sorted_ids,
                        int32_t* tile_ranges, uint32_t* bin_status,
                        void* stream);
+
+/* The same pipeline in three calls, for callers that size the duplicate
+ * buffers exactly instead of guessing a capacity.
+ *
+ * gsx_bin_count_async: zeroes tile_ranges and bin_status words 0, 2 and 3,
+ * builds the depth keys' digit histograms in depth_ws
+ * (gsx_bin_depth_workspace_bytes(n)) and adds the tile counts into
+ * bin_status[3]: the number of duplicates emission will write (before
+ * refine_tiles drops any), with GSX_BIN_ERR_OVERFLOW in bin_status[1] past
+ * 2^30 - 1.  bin_status[1] is not cleared: the error bits of every call on
+ * one bin_status accumulate until the caller clears the word, so a copy
+ * made behind this call also reports the checks of earlier calls' tile
+ * phases.  A caller that copies bin_status to the host right behind it and
+ * enqueues gsx_bin_depth_async before waiting for that copy reads the count
+ * while the device sorts.
+ *
+ * gsx_bin_depth_async: the stable depth sort (tiles.py:67-72) of the same
+ * n depth keys in the same depth_ws.
+ *
+ * gsx_bin_tiles_async: the rest of tiles.py:73-182 (scan of the counts in
+ * depth order, emission, tile sort, ranges) on the depth sort's output,
+ * with the same n, tile_counts, width and height and the same depth_ws,
+ * plus tile_ws (gsx_bin_tile_workspace_bytes(capacity, num_tiles)).
+ * bin_status then holds what gsx_bin_sort_async documents; with capacity =
+ * bin_status[3] the duplicates always fit.
+ *
+ * gsx_bin_sort_async is the three in sequence on one workspace (depth part
+ * first, all four bin_status words cleared); gsx_bin_workspace_bytes is the
+ * sum of the two sizes. */
+int64_t gsx_bin_depth_workspace_bytes(int64_t n);
+int64_t gsx_bin_tile_workspace_bytes(int64_t capacity, int32_t num_tiles);
+int gsx_bin_count_async(int64_t n, const uint32_t* tile_counts,
+                        const uint32_t* depth_keys, int32_t width,
+                        int32_t height, void* depth_ws,
+                        int64_t depth_ws_bytes, int32_t* tile_ranges,
+                        uint32_t* bin_status, void* stream);
+int gsx_bin_depth_async(int64_t n, const uint32_t* depth_keys, void* depth_ws,
+                        int64_t depth_ws_bytes, uint32_t* bin_status,
+                        void* stream);
+int gsx_bin_tiles_async(int64_t n, const uint32_t* tile_counts,
+                        const uint32_t* tile_rects, const float* means2d,
+                        const float* conics, int64_t conic_stride,
+                        int32_t width, int32_t height, void* depth_ws,
+                        int64_t depth_ws_bytes, void* tile_ws,
+                        int64_t tile_ws_bytes, int64_t capacity,
+                        int32_t* sorted_ids, int32_t* tile_ranges,
+                        uint32_t* bin_status, void* stream);
 
 /* Host-side: interprets a host copy of the 4 bin_status words.  Returns
  * GSX_OK with *num_dups = D (duplicates kept), 1 with *num_dups = the
@@ -266,14 +314,16 @@ int gsx_pack_conic_opacity(int64_t n, const float* conics,
  * (num_ids); tile ranges are clamped to [0, num_ids] and ids outside [0, n)
  * are treated as transparent, so malformed inputs cannot read out of
  * bounds; background (C) or NULL (zeros); out (H,W,C); final_T (H,W);
- * n_contrib (H,W) int32; depth_out (H,W) when depths != NULL. */
+ * n_contrib (H,W) int32; depth_out (H,W) when depths != NULL; alpha_out
+ * (H,W) = 1 - final_T (rasterize.py:443) or NULL. */
 int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
                    const float* depths, const int32_t* sorted_ids,
                    int64_t num_ids, const int32_t* tile_ranges,
                    const float* background,
                    int32_t width, int32_t height, float* out, float* final_T,
-                   int32_t* n_contrib, float* depth_out, void* stream);
+                   int32_t* n_contrib, float* depth_out, float* alpha_out,
+                   void* stream);
 
 /* Replaces gs_rasterize_backward (rasterize.py:100-221) and the vjp wiring
  * of _rasterize_core (rasterize.py:364-403).  grad_out (H,W,C);

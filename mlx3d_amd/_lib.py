@@ -98,10 +98,16 @@ SIGNATURES = {
                                     _P, _P, ctypes.POINTER(_I64), _P]),
     "gsx_bin_sort_async": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I64,
                                           _I64, _P, _P, _P, _P]),
+    "gsx_bin_depth_workspace_bytes": (_I64, [_I64]),
+    "gsx_bin_tile_workspace_bytes": (_I64, [_I64, _I32]),
+    "gsx_bin_count_async": (ctypes.c_int, [_I64, _P, _P, _I32, _I32, _P, _I64, _P, _P, _P]),
+    "gsx_bin_depth_async": (ctypes.c_int, [_I64, _P, _P, _I64, _P, _P]),
+    "gsx_bin_tiles_async": (ctypes.c_int, [_I64, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I64, _P,
+                                           _I64, _I64, _P, _P, _P, _P]),
     "gsx_bin_status_check": (ctypes.c_int, [_P, _I64, ctypes.POINTER(_I64)]),
     "gsx_pack_conic_opacity": (ctypes.c_int, [_I64, _P, _P, _P, _P]),
     "gsx_raster_fwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32,
-                                      _P, _P, _P, _P, _P]),
+                                      _P, _P, _P, _P, _P, _P]),
     "gsx_raster_bwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32, _P,
                                       _P, _P, _P, _P, _P, _P, _P, _P]),
     "gsx_photometric_workspace_bytes": (_I64, [_I32, _I32, _I32]),

@@ -214,39 +214,63 @@ __device__ __forceinline__ int64_t block_find_owner(const uint32_t* __restrict__
     return a;
 }
 
+constexpr int kZeroRanges = 5;
 struct ZeroRanges {
-    uint32_t* p[4];
-    int64_t n[4];
+    uint32_t* p[kZeroRanges];
+    int64_t n[kZeroRanges];
 };
 
 __global__ __launch_bounds__(256) void k_zero_ranges(ZeroRanges z) {
     const int64_t stride = (int64_t)gridDim.x * 256;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < kZeroRanges; ++r)
         for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < z.n[r]; i += stride)
             z.p[r][i] = 0u;
 }
 
 // Digit histograms of the 4 bytes of every depth key from one read, added
-// into copy blockIdx % kHistCopies of hist[copy][pass][digit].
+// into copy blockIdx % kHistCopies of hist[copy][pass][digit], and the sum
+// of the tile counts (the number of duplicates emission will write) added
+// to *total, with the overflow bit once it passes kCountMask.
 __global__ __launch_bounds__(kHistThreads) void k_depth_hist(const uint32_t* __restrict__ keys,
+                                                             const uint32_t* __restrict__ counts,
                                                              int64_t n,
-                                                             uint32_t* __restrict__ hist) {
+                                                             uint32_t* __restrict__ hist,
+                                                             uint32_t* __restrict__ total,
+                                                             uint32_t* __restrict__ err) {
     __shared__ uint32_t s_h[kMaxPasses][kRadix];
+    __shared__ uint64_t s_sum[kHistThreads / 64];
     const int tid = threadIdx.x, wave = tid >> 6;
     for (int k = tid; k < kMaxPasses * kRadix; k += kHistThreads) (&s_h[0][0])[k] = 0u;
     __syncthreads();
     const int64_t base =
         (int64_t)blockIdx.x * (kHistThreads * kHistItems) + wave * (64 * kHistItems);
+    uint64_t sum = 0;
     for (int r = 0; r < kHistItems; ++r) {
         const int64_t i = base + r * 64 + (tid & 63);
         const bool valid = i < n;
         const uint32_t key = valid ? keys[i] : 0u;
+        sum += valid ? counts[i] : 0u;
 #pragma unroll
         for (int p = 0; p < kMaxPasses; ++p)
             hist_add(s_h[p], (key >> (p * kRadixBits)) & (kRadix - 1), valid);
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if ((tid & 63) == 0) s_sum[wave] = sum;
     __syncthreads();
+    if (tid == 0) {
+        uint64_t t = 0;
+#pragma unroll
+        for (int w = 0; w < kHistThreads / 64; ++w) t += s_sum[w];
+        if (t > 0) {
+            // each add is at most 2^30, so the word cannot wrap before the
+            // bit is set
+            const uint32_t add = (uint32_t)(t > kCountMask ? kCountMask + 1u : t);
+            const uint32_t old = atomicAdd(total, add);
+            if ((uint64_t)old + add > kCountMask) atomicOr(err, GSX_BIN_ERR_OVERFLOW);
+        }
+    }
     uint32_t* h = hist + (blockIdx.x % kHistCopies) * kHistStride;
     for (int k = tid; k < kMaxPasses * kRadix; k += kHistThreads) {
         const uint32_t v = (&s_h[0][0])[k];
@@ -362,10 +386,15 @@ __global__ __launch_bounds__(kScanThreads) void k_count_scan(
     int64_t n, const uint32_t* __restrict__ counts, const uint32_t* __restrict__ gids,
     uint32_t* __restrict__ status, uint32_t* __restrict__ counter, uint32_t* __restrict__ offs,
     uint32_t* __restrict__ owner, int64_t n_owner, uint32_t* __restrict__ d_total,
-    uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ err, uint32_t* __restrict__ clear, int64_t n_clear) {
     __shared__ uint32_t s_w[kScanThreads / 64];
     __shared__ uint32_t s_chunk, s_prefix;
     const int tid = threadIdx.x;
+    // the tile passes' look-back status words start at zero (they run after
+    // this kernel and emission)
+    for (int64_t k = (int64_t)blockIdx.x * kScanThreads + tid; k < n_clear;
+         k += (int64_t)gridDim.x * kScanThreads)
+        clear[k] = 0u;
     if (tid == 0) s_chunk = atomicAdd(counter, 1u);
     __syncthreads();
     const int64_t chunk = s_chunk;
@@ -620,44 +649,64 @@ constexpr int kMiscCounters = 16;
 constexpr int kSyncStatusWord = 12;
 constexpr int kMiscWords = kMiscCounters + 2 * kHistCopies * kHistStride;
 
-struct Layout {
-    size_t dk0, dk1, dv0, dv1, offs, owner, tk0, tk1, tv, status, misc, total;
-    int64_t depth_chunks, tile_chunks, scan_chunks, emit_blocks, hist_blocks, status_words;
+// Workspace of the depth phase (sized by n alone) and of the tile phase
+// (sized by the duplicate capacity); gsx_bin_sort(_async) places the tile
+// part right after the depth part of one workspace.
+struct DepthLayout {
+    size_t dk0, dk1, dv0, dv1, offs, status, misc, total;
+    int64_t depth_chunks, scan_chunks, hist_blocks, status_words;
+};
+struct TileLayout {
+    size_t owner, tk0, tk1, tv, status, total;
+    int64_t tile_chunks, emit_blocks, status_words;
     int tile_passes;
 };
 
 inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
-Layout make_layout(int64_t n, int64_t cap, int64_t num_tiles) {
-    Layout L{};
+struct Taker {
     size_t o = 0;
-    auto take = [&](size_t bytes) {
+    size_t operator()(size_t bytes) {
         const size_t at = o;
         o = align_up(o + bytes);
         return at;
-    };
-    const size_t nn = (size_t)std::max<int64_t>(n, 1), cc = (size_t)std::max<int64_t>(cap, 1);
+    }
+};
+
+DepthLayout make_depth_layout(int64_t n) {
+    DepthLayout L{};
+    Taker take;
+    const size_t nn = (size_t)std::max<int64_t>(n, 1);
     L.depth_chunks = ceil_div((int64_t)nn, kDepthThreads * kDepthItems);
-    L.tile_chunks = ceil_div((int64_t)cc, kTileThreads * kTileItems);
     L.scan_chunks = ceil_div((int64_t)nn, kScanChunk);
-    L.emit_blocks = ceil_div((int64_t)cc, kEmitDups);
     L.hist_blocks = ceil_div((int64_t)nn, kHistThreads * kHistItems);
-    // room for the refine_tiles sentinel id (= num_tiles)
-    L.tile_passes = passes_for(num_tiles + 1);
-    L.status_words =
-        (4 * L.depth_chunks + L.tile_passes * L.tile_chunks) * kRadix + L.scan_chunks;
+    L.status_words = 4 * L.depth_chunks * kRadix + L.scan_chunks;
     L.dk0 = take(4 * nn);
     L.dk1 = take(4 * nn);
     L.dv0 = take(4 * nn);
     L.dv1 = take(4 * nn);
     L.offs = take(4 * (nn + 1));
+    L.status = take(4 * (size_t)L.status_words);
+    L.misc = take(4 * (size_t)kMiscWords);
+    L.total = take.o;
+    return L;
+}
+
+TileLayout make_tile_layout(int64_t cap, int64_t num_tiles) {
+    TileLayout L{};
+    Taker take;
+    const size_t cc = (size_t)std::max<int64_t>(cap, 1);
+    L.tile_chunks = ceil_div((int64_t)cc, kTileThreads * kTileItems);
+    L.emit_blocks = ceil_div((int64_t)cc, kEmitDups);
+    // room for the refine_tiles sentinel id (= num_tiles)
+    L.tile_passes = passes_for(num_tiles + 1);
+    L.status_words = (int64_t)L.tile_passes * L.tile_chunks * kRadix;
     L.owner = take(4 * (size_t)L.emit_blocks);
     L.tk0 = take(4 * cc);
     L.tk1 = take(4 * cc);
     L.tv = take(4 * cc);
     L.status = take(4 * (size_t)L.status_words);
-    L.misc = take(4 * (size_t)kMiscWords);
-    L.total = o;
+    L.total = take.o;
     return L;
 }
 
@@ -672,7 +721,7 @@ inline unsigned grid_for(int64_t n, int64_t per) {
 
 int zero(ZeroRanges z, hipStream_t st) {
     int64_t most = 0;
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kZeroRanges; ++r) {
         if (!z.p[r]) z.n[r] = 0;
         most = std::max(most, z.n[r]);
     }
@@ -690,24 +739,102 @@ int check_args(int64_t n, int32_t width, int32_t height, int64_t capacity) {
     return GSX_OK;
 }
 
+int count_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
+                int32_t width, int32_t height, void* depth_ws, int64_t depth_ws_bytes,
+                int32_t* tile_ranges, uint32_t* bin_status, bool clear_errors,
+                hipStream_t st) {
+    int rc = check_args(n, width, height, 0);
+    if (rc != GSX_OK) return rc;
+    if (!tile_ranges || !bin_status) return GSX_ERR_INVALID;
+    if (n > 0 && (!tile_counts || !depth_keys || !depth_ws)) return GSX_ERR_INVALID;
+    const int64_t T = (int64_t)((width + kTile - 1) / kTile) * ((height + kTile - 1) / kTile);
+    const DepthLayout L = make_depth_layout(n);
+    if (n > 0 && depth_ws_bytes < (int64_t)L.total) return GSX_ERR_WORKSPACE;
+    uint32_t* status = n > 0 ? at<uint32_t>(depth_ws, L.status) : nullptr;
+    uint32_t* misc = n > 0 ? at<uint32_t>(depth_ws, L.misc) : nullptr;
+    // ranges, the bin_status counts (and, when asked, its error bits),
+    // look-back status words, counters and histograms all start at zero
+    rc = zero(ZeroRanges{{(uint32_t*)tile_ranges, bin_status + (clear_errors ? 0 : 2),
+                          bin_status, status, misc},
+                         {2 * T, clear_errors ? 4 : 2, 1, L.status_words, kMiscWords}},
+              st);
+    if (rc != GSX_OK || n == 0) return rc;
+    // digit histograms of the depth keys; the tile counts summed into
+    // bin_status[3]
+    hipLaunchKernelGGL(k_depth_hist, dim3((unsigned)L.hist_blocks), dim3(kHistThreads), 0, st,
+                       depth_keys, tile_counts, n, misc + kMiscCounters, bin_status + 3,
+                       bin_status + 1);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles) {
-    if (n < 0 || capacity < 0 || num_tiles <= 0) return -1;
-    return (int64_t)make_layout(n, capacity, num_tiles).total;
+int64_t gsx_bin_depth_workspace_bytes(int64_t n) {
+    if (n < 0) return -1;
+    return (int64_t)make_depth_layout(n).total;
 }
 
-int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
-                       const uint32_t* tile_rects, const float* means2d, const float* conics,
-                       int64_t conic_stride, int32_t width, int32_t height, void* workspace,
-                       int64_t workspace_bytes, int64_t capacity, int32_t* sorted_ids,
-                       int32_t* tile_ranges, uint32_t* bin_status, void* stream) {
+int64_t gsx_bin_tile_workspace_bytes(int64_t capacity, int32_t num_tiles) {
+    if (capacity < 0 || num_tiles <= 0) return -1;
+    return (int64_t)make_tile_layout(capacity, num_tiles).total;
+}
+
+int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles) {
+    if (n < 0 || capacity < 0 || num_tiles <= 0) return -1;
+    return (int64_t)(make_depth_layout(n).total + make_tile_layout(capacity, num_tiles).total);
+}
+
+int gsx_bin_count_async(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
+                        int32_t width, int32_t height, void* depth_ws, int64_t depth_ws_bytes,
+                        int32_t* tile_ranges, uint32_t* bin_status, void* stream) {
+    return count_phase(n, tile_counts, depth_keys, width, height, depth_ws, depth_ws_bytes,
+                       tile_ranges, bin_status, false, (hipStream_t)stream);
+}
+
+int gsx_bin_depth_async(int64_t n, const uint32_t* depth_keys, void* depth_ws,
+                        int64_t depth_ws_bytes, uint32_t* bin_status, void* stream) {
+    if (n < 0 || n > (int64_t)kCountMask) return n < 0 ? GSX_ERR_INVALID : GSX_ERR_TOO_LARGE;
+    if (!bin_status) return GSX_ERR_INVALID;
+    if (n == 0) return GSX_OK;
+    if (!depth_keys || !depth_ws) return GSX_ERR_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    const DepthLayout L = make_depth_layout(n);
+    if (depth_ws_bytes < (int64_t)L.total) return GSX_ERR_WORKSPACE;
+    uint32_t* status = at<uint32_t>(depth_ws, L.status);
+    uint32_t* misc = at<uint32_t>(depth_ws, L.misc);
+    uint32_t* depth_hist = misc + kMiscCounters;
+    // stable sort of the Gaussians by depth key (index order breaks ties)
+    const uint32_t* kin = depth_keys;
+    const uint32_t* vin = nullptr;
+    uint32_t* kbuf[2] = {at<uint32_t>(depth_ws, L.dk0), at<uint32_t>(depth_ws, L.dk1)};
+    uint32_t* vbuf[2] = {at<uint32_t>(depth_ws, L.dv0), at<uint32_t>(depth_ws, L.dv1)};
+    for (int p = 0; p < 4; ++p) {
+        hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems>), dim3((unsigned)L.depth_chunks),
+                           dim3(kDepthThreads), 0, st, kin, vin, n, (const uint32_t*)nullptr,
+                           p * kRadixBits, kRadixBits, depth_hist + p * kRadix,
+                           status + (size_t)p * L.depth_chunks * kRadix, misc + p, kbuf[p & 1],
+                           vbuf[p & 1], bin_status + 1);
+        kin = kbuf[p & 1];
+        vin = vbuf[p & 1];
+    }
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_bin_tiles_async(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rects,
+                        const float* means2d, const float* conics, int64_t conic_stride,
+                        int32_t width, int32_t height, void* depth_ws, int64_t depth_ws_bytes,
+                        void* tile_ws, int64_t tile_ws_bytes, int64_t capacity,
+                        int32_t* sorted_ids, int32_t* tile_ranges, uint32_t* bin_status,
+                        void* stream) {
     int rc = check_args(n, width, height, capacity);
     if (rc != GSX_OK) return rc;
     if (!tile_ranges || !bin_status) return GSX_ERR_INVALID;
-    if (n > 0 && (!tile_counts || !depth_keys || !tile_rects || !workspace)) return GSX_ERR_INVALID;
+    if (n == 0) return GSX_OK;  // the depth phase cleared the ranges and status
+    if (!tile_counts || !tile_rects || !depth_ws || !tile_ws) return GSX_ERR_INVALID;
     const bool refine = conics != nullptr;
     if (refine && (!means2d || ((uintptr_t)means2d & 7u) != 0u || conic_stride < 3))
         return GSX_ERR_INVALID;
@@ -717,60 +844,34 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
     const int64_t T = (int64_t)tiles_x * tiles_y;
-    const Layout L = make_layout(n, capacity, T);
-    if (n > 0 && workspace_bytes < (int64_t)L.total) return GSX_ERR_WORKSPACE;
-    uint32_t* status = n > 0 ? at<uint32_t>(workspace, L.status) : nullptr;
-    uint32_t* misc = n > 0 ? at<uint32_t>(workspace, L.misc) : nullptr;
-    // ranges, D + error flags, look-back status words, counters and
-    // histograms all start at zero
-    rc = zero(ZeroRanges{{(uint32_t*)tile_ranges, bin_status, status, misc},
-                         {2 * T, 4, L.status_words, kMiscWords}},
-              st);
-    if (rc != GSX_OK || n == 0) return rc;
-
-    void* ws = workspace;
+    const DepthLayout D = make_depth_layout(n);
+    const TileLayout L = make_tile_layout(capacity, T);
+    if (depth_ws_bytes < (int64_t)D.total || tile_ws_bytes < (int64_t)L.total)
+        return GSX_ERR_WORKSPACE;
+    uint32_t* misc = at<uint32_t>(depth_ws, D.misc);
     uint32_t* d_total = bin_status;
     uint32_t* err = bin_status + 1;
     uint32_t* dropped = bin_status + 2;
-    uint32_t* depth_hist = misc + kMiscCounters;
-    uint32_t* tile_hist = depth_hist + kHistCopies * kHistStride;
+    uint32_t* tile_hist = misc + kMiscCounters + kHistCopies * kHistStride;
+    const uint32_t* gids = at<uint32_t>(depth_ws, D.dv1);  // after the four depth passes
 
-    // 1. stable sort of the Gaussians by depth key (index order breaks ties)
-    hipLaunchKernelGGL(k_depth_hist, dim3((unsigned)L.hist_blocks), dim3(kHistThreads), 0, st,
-                       depth_keys, n, depth_hist);
-    GSX_LAUNCH_CHECK();
-    const uint32_t* kin = depth_keys;
-    const uint32_t* vin = nullptr;
-    uint32_t* kbuf[2] = {at<uint32_t>(ws, L.dk0), at<uint32_t>(ws, L.dk1)};
-    uint32_t* vbuf[2] = {at<uint32_t>(ws, L.dv0), at<uint32_t>(ws, L.dv1)};
-    for (int p = 0; p < 4; ++p) {
-        hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems>), dim3((unsigned)L.depth_chunks),
-                           dim3(kDepthThreads), 0, st, kin, vin, n, (const uint32_t*)nullptr,
-                           p * kRadixBits, kRadixBits, depth_hist + p * kRadix,
-                           status + (size_t)p * L.depth_chunks * kRadix, misc + p, kbuf[p & 1],
-                           vbuf[p & 1], err);
-        kin = kbuf[p & 1];
-        vin = vbuf[p & 1];
-    }
-    GSX_LAUNCH_CHECK();
-    const uint32_t* gids = vin;
-
-    // 2. scan of the counts in depth order; 3. emission (+ tile digit
-    //    histograms) into the buffers from which the tile passes end in
-    //    sorted_ids; 4. tile sort over the device-side D
+    // scan of the counts in depth order (it also clears the tile passes'
+    // status words); emission (+ tile digit histograms) into the buffers
+    // from which the tile passes end in sorted_ids; tile sort over the
+    // device-side D; ranges
     const int passes = refine ? L.tile_passes : passes_for(T);
     // significant bits of the tile ids (the refine_tiles sentinel T included)
     const int tile_bits = bits_for(std::max<int64_t>(refine ? T + 1 : T, 1));
-    uint32_t* tk[2] = {at<uint32_t>(ws, L.tk0), at<uint32_t>(ws, L.tk1)};
-    uint32_t* tv[2] = {(uint32_t*)sorted_ids, at<uint32_t>(ws, L.tv)};
+    uint32_t* tk[2] = {at<uint32_t>(tile_ws, L.tk0), at<uint32_t>(tile_ws, L.tk1)};
+    uint32_t* tv[2] = {(uint32_t*)sorted_ids, at<uint32_t>(tile_ws, L.tv)};
     int cur = passes & 1;
-    uint32_t* tstatus = status + (size_t)4 * L.depth_chunks * kRadix;
-    uint32_t* sstatus = tstatus + (size_t)L.tile_passes * L.tile_chunks * kRadix;
-    uint32_t* offs = at<uint32_t>(ws, L.offs);
-    uint32_t* owner = at<uint32_t>(ws, L.owner);
-    hipLaunchKernelGGL(k_count_scan, dim3((unsigned)L.scan_chunks), dim3(kScanThreads), 0, st, n,
+    uint32_t* tstatus = at<uint32_t>(tile_ws, L.status);
+    uint32_t* sstatus = at<uint32_t>(depth_ws, D.status) + (size_t)4 * D.depth_chunks * kRadix;
+    uint32_t* offs = at<uint32_t>(depth_ws, D.offs);
+    uint32_t* owner = at<uint32_t>(tile_ws, L.owner);
+    hipLaunchKernelGGL(k_count_scan, dim3((unsigned)D.scan_chunks), dim3(kScanThreads), 0, st, n,
                        tile_counts, gids, sstatus, misc + 8, offs, owner, L.emit_blocks, d_total,
-                       err);
+                       err, tstatus, L.status_words);
     GSX_LAUNCH_CHECK();
     if (capacity == 0) return GSX_OK;
     hipLaunchKernelGGL(k_emit, dim3((unsigned)L.emit_blocks), dim3(kEmitThreads), 0, st, n,
@@ -790,11 +891,33 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
         cur ^= 1;
     }
     GSX_LAUNCH_CHECK();
-    // 4. ranges
     hipLaunchKernelGGL(k_tile_ranges, dim3(grid_for(capacity, 1024)), dim3(256), 0, st, capacity,
                        (const uint32_t*)d_total, tk[cur], T, (int2*)tile_ranges);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
+}
+
+int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
+                       const uint32_t* tile_rects, const float* means2d, const float* conics,
+                       int64_t conic_stride, int32_t width, int32_t height, void* workspace,
+                       int64_t workspace_bytes, int64_t capacity, int32_t* sorted_ids,
+                       int32_t* tile_ranges, uint32_t* bin_status, void* stream) {
+    int rc = check_args(n, width, height, capacity);
+    if (rc != GSX_OK) return rc;
+    if (!tile_ranges || !bin_status) return GSX_ERR_INVALID;
+    if (n > 0 && (!tile_counts || !depth_keys || !tile_rects || !workspace)) return GSX_ERR_INVALID;
+    const int64_t T = (int64_t)((width + kTile - 1) / kTile) * ((height + kTile - 1) / kTile);
+    const int64_t dbytes = (int64_t)make_depth_layout(n).total;
+    const int64_t tbytes = (int64_t)make_tile_layout(capacity, T).total;
+    if (n > 0 && workspace_bytes < dbytes + tbytes) return GSX_ERR_WORKSPACE;
+    rc = count_phase(n, tile_counts, depth_keys, width, height, workspace, dbytes, tile_ranges,
+                     bin_status, true, (hipStream_t)stream);
+    if (rc != GSX_OK || n == 0) return rc;
+    rc = gsx_bin_depth_async(n, depth_keys, workspace, dbytes, bin_status, stream);
+    if (rc != GSX_OK) return rc;
+    return gsx_bin_tiles_async(n, tile_counts, tile_rects, means2d, conics, conic_stride, width,
+                               height, workspace, dbytes, static_cast<char*>(workspace) + dbytes,
+                               tbytes, capacity, sorted_ids, tile_ranges, bin_status, stream);
 }
 
 int gsx_bin_status_check(const uint32_t* host_status, int64_t capacity, int64_t* num_dups) {
@@ -827,11 +950,11 @@ int gsx_bin_sort(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_k
     if (!workspace) return GSX_ERR_INVALID;
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
-    const Layout L = make_layout(n, capacity, (int64_t)tiles_x * tiles_y);
-    if (workspace_bytes < (int64_t)L.total) return GSX_ERR_WORKSPACE;
+    const int64_t need = gsx_bin_workspace_bytes(n, capacity, tiles_x * tiles_y);
+    if (workspace_bytes < need) return GSX_ERR_WORKSPACE;
     // the status words sit in the workspace's counter block, past the counters
     // the pipeline uses (it clears the whole block before the first kernel)
-    uint32_t* bs = at<uint32_t>(workspace, L.misc) + kSyncStatusWord;
+    uint32_t* bs = at<uint32_t>(workspace, make_depth_layout(n).misc) + kSyncStatusWord;
     rc = gsx_bin_sort_async(n, tile_counts, depth_keys, tile_rects, means2d, conics,
                             conic_stride, width, height, workspace, workspace_bytes, capacity,
                             sorted_ids, tile_ranges, bs, stream);

@@ -463,7 +463,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     int C, int c0, int nc, const float* __restrict__ depths, const int* __restrict__ ids,
     const int2* __restrict__ ranges, int64_t n, int64_t n_ids, const float* __restrict__ bg,
     int W, int H, int tiles_x, float* __restrict__ out, float* __restrict__ final_T,
-    int* __restrict__ n_contrib, float* __restrict__ depth_out) {
+    int* __restrict__ n_contrib, float* __restrict__ depth_out, float* __restrict__ alpha_out) {
     constexpr int F4 = (CH + 3) / 4;
     // entry kThreads of the records is the walk lists' padding: a record no
     // pixel can take (alpha bound +inf)
@@ -559,6 +559,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
         if (c0 == 0) {
             final_T[pid] = T;
             n_contrib[pid] = last;
+            if (alpha_out) alpha_out[pid] = 1.0f - T;
             if (DEPTH) {
                 const float al = 1.0f - T;
                 depth_out[pid] = al > 1e-6f ? dacc / al : 0.0f;
@@ -1043,15 +1044,15 @@ template <int CH>
 void launch_fwd(dim3 grid, hipStream_t st, bool depth, const float2* xy, const float4* co,
                 const float* feat, int C, int c0, int nc, const float* depths, const int* ids,
                 const int2* ranges, int64_t n, int64_t n_ids, const float* bg, int W, int H,
-                int tiles_x, float* out, float* fT, int* ncon, float* dout) {
+                int tiles_x, float* out, float* fT, int* ncon, float* dout, float* aout) {
     if (depth)
         hipLaunchKernelGGL((k_raster_fwd<CH, true>), grid, dim3(kThreads), 0, st, xy, co, feat, C,
                            c0, nc, depths, ids, ranges, n, n_ids, bg, W, H, tiles_x, out, fT,
-                           ncon, dout);
+                           ncon, dout, aout);
     else
         hipLaunchKernelGGL((k_raster_fwd<CH, false>), grid, dim3(kThreads), 0, st, xy, co, feat, C,
                            c0, nc, depths, ids, ranges, n, n_ids, bg, W, H, tiles_x, out, fT,
-                           ncon, dout);
+                           ncon, dout, aout);
 }
 
 template <int CH>
@@ -1077,7 +1078,7 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d, const float* coni
                    int64_t num_ids, const int32_t* tile_ranges, const float* background,
                    int32_t width,
                    int32_t height, float* out, float* final_T, int32_t* n_contrib,
-                   float* depth_out, void* stream) {
+                   float* depth_out, float* alpha_out, void* stream) {
     if (n < 0 || num_ids < 0 || C <= 0 || width <= 0 || height <= 0) return GSX_ERR_INVALID;
     if (!tile_ranges || !out || !final_T || !n_contrib) return GSX_ERR_INVALID;
     if (n > 0 && (!means2d || !conic_opacity || !features)) return GSX_ERR_INVALID;
@@ -1099,7 +1100,7 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d, const float* coni
         launch_fwd<V>(grid, st, depth, (const float2*)means2d, (const float4*)conic_opacity,     \
                       features, C, c0, nc, depths, sorted_ids, (const int2*)tile_ranges, n,      \
                       num_ids, background, width, height, tiles_x, out, final_T, n_contrib,      \
-                      depth_out);                                                                \
+                      depth_out, alpha_out);                                                     \
         break;
             GSX_FWD_CASE(1)
             GSX_FWD_CASE(2)

@@ -26,11 +26,13 @@ def _empty(shape, dev, dtype=torch.float32):
 
 def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, background, width,
                    height, depths=None):
-    """gsx_raster_fwd on prepared float32 contiguous tensors (no autograd)."""
+    """gsx_raster_fwd on prepared float32 contiguous tensors (no autograd):
+    (out, final_T, n_contrib, depth_map or None, alpha = 1 - final_T)."""
     dev = means2d.device
     n, C = feats.shape
     out = _empty((height, width, C), dev)
     final_T = _empty((height, width), dev)
+    alpha = _empty((height, width), dev)
     n_contrib = _empty((height, width), dev, torch.int32)
     depth_map = _empty((height, width), dev) if depths is not None else None
     L = _lib.load()
@@ -39,8 +41,15 @@ def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, backgrou
                                 _lib.ptr(tile_ranges),
                                 _lib.ptr(background), width, height, _lib.ptr(out),
                                 _lib.ptr(final_T), _lib.ptr(n_contrib), _lib.ptr(depth_map),
-                                _lib.stream_handle(dev)), "gsx_raster_fwd")
-    return out, final_T, n_contrib, depth_map
+                                _lib.ptr(alpha), _lib.stream_handle(dev)), "gsx_raster_fwd")
+    return out, final_T, n_contrib, depth_map, alpha
+
+
+def t_cotangent(g_final_T, g_alpha):
+    """Cotangent of final_T when alpha = 1 - final_T is an output too."""
+    if g_alpha is None:
+        return g_final_T
+    return -g_alpha if g_final_T is None else g_final_T - g_alpha
 
 
 def raster_backward(means2d, conic_opac, feats, sorted_ids, tile_ranges, background, width,
@@ -83,21 +92,22 @@ class _Rasterize(torch.autograd.Function):
                 width, height):
         _lib.require_device(means2d, conics, feats, opacities, sorted_ids, tile_ranges, background)
         co = pack_conic_opacity(conics, opacities)
-        out, final_T, n_contrib, _ = raster_forward(means2d, co, feats, sorted_ids, tile_ranges,
-                                                    background, width, height)
+        out, final_T, n_contrib, _, alpha = raster_forward(means2d, co, feats, sorted_ids,
+                                                           tile_ranges, background, width, height)
         ctx.save_for_backward(means2d, co, feats, sorted_ids, tile_ranges, background, final_T,
                               n_contrib)
         ctx.size = (width, height)
         ctx.mark_non_differentiable(n_contrib)
         ctx.set_materialize_grads(False)  # unused outputs: no zero-filled cotangents
-        return out, final_T, n_contrib
+        return out, final_T, alpha, n_contrib
 
     @staticmethod
-    def backward(ctx, g_out, g_final_T, _g_nc):
+    def backward(ctx, g_out, g_final_T, g_alpha, _g_nc):
         means2d, co, feats, ids, ranges, bg, final_T, n_contrib = ctx.saved_tensors
         width, height = ctx.size
         g_m, g_c, g_f, g_o = raster_backward(means2d, co, feats, ids, ranges, bg, width, height,
-                                             final_T, n_contrib, g_out, g_final_T)
+                                             final_T, n_contrib, g_out,
+                                             t_cotangent(g_final_T, g_alpha))
         return g_m, g_c, g_f, g_o, None, None, None, None, None
 
 
@@ -119,13 +129,12 @@ def rasterize(means2d, conics, colors, opacities, sorted_ids, tile_ranges, width
     """
     _check_grid(width, height, tiles_x, tiles_y)
     dev = means2d.device
-    if background is None:
-        background = torch.zeros((colors.shape[1],), dtype=torch.float32, device=dev)
-    image, final_T, n_contrib = _Rasterize.apply(
+    # None reaches the kernels as NULL, a zero background
+    bg = None if background is None else _lib.f32c(torch.as_tensor(background, device=dev))
+    image, final_T, alpha, n_contrib = _Rasterize.apply(
         _lib.f32c(means2d), _lib.f32c(conics), _lib.f32c(colors), _lib.f32c(opacities),
-        _ids(sorted_ids), _ids(tile_ranges), _lib.f32c(torch.as_tensor(background, device=dev)),
-        int(width), int(height))
-    return {"image": image, "alpha": 1.0 - final_T, "final_T": final_T, "n_contrib": n_contrib}
+        _ids(sorted_ids), _ids(tile_ranges), bg, int(width), int(height))
+    return {"image": image, "alpha": alpha, "final_T": final_T, "n_contrib": n_contrib}
 
 
 def rasterize_features(means2d, conics, features, opacities, sorted_ids, tile_ranges,
@@ -146,17 +155,17 @@ def rasterize_features(means2d, conics, features, opacities, sorted_ids, tile_ra
     _check_grid(width, height, tiles_x, tiles_y)
     dev = means2d.device
     if background is None or normalize:
-        bg = torch.zeros((channels,), dtype=torch.float32, device=dev)
+        bg = None  # NULL: a zero background
     else:
         bg = torch.as_tensor(background, dtype=torch.float32, device=dev)
         if bg.ndim == 0:
             bg = bg.expand(channels)
         if bg.shape != (channels,):
             raise ValueError(f"background must have shape ({channels},).")
-    feat, final_T, n_contrib = _Rasterize.apply(
+        bg = _lib.f32c(bg)
+    feat, final_T, alpha, n_contrib = _Rasterize.apply(
         _lib.f32c(means2d), _lib.f32c(conics), _lib.f32c(features), _lib.f32c(opacities),
-        _ids(sorted_ids), _ids(tile_ranges), _lib.f32c(bg), int(width), int(height))
-    alpha = 1.0 - final_T
+        _ids(sorted_ids), _ids(tile_ranges), bg, int(width), int(height))
     if normalize:
         a = alpha[..., None]
         feat = torch.where(a > 1e-6, feat / torch.clamp(a, min=1e-6), torch.zeros_like(feat))
@@ -172,7 +181,8 @@ def rasterize_depth(means2d, conics, opacities, depths, sorted_ids, tile_ranges,
         _lib.require_device(means2d, conics, opacities, depths, sorted_ids, tile_ranges)
         d = _lib.f32c(depths)
         co = pack_conic_opacity(_lib.f32c(conics), _lib.f32c(opacities))
-        _, final_T, _, depth = raster_forward(_lib.f32c(means2d), co, d[:, None].contiguous(),
-                                              _ids(sorted_ids), _ids(tile_ranges), None, width,
-                                              height, depths=d)
-    return {"depth": depth, "alpha": 1.0 - final_T, "final_T": final_T}
+        _, final_T, _, depth, alpha = raster_forward(_lib.f32c(means2d), co,
+                                                     d[:, None].contiguous(), _ids(sorted_ids),
+                                                     _ids(tile_ranges), None, width, height,
+                                                     depths=d)
+    return {"depth": depth, "alpha": alpha, "final_T": final_T}

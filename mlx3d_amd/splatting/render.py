@@ -2,7 +2,8 @@
 
 The render functions run the fused pipeline
 
-    gsx_preprocess_fwd -> gsx_bin_sort_async -> gsx_raster_fwd -> (read D)
+    gsx_preprocess_fwd -> gsx_bin_count_async -> gsx_bin_depth_async
+        -> (read the duplicate count) -> gsx_bin_tiles_async -> gsx_raster_fwd
     gsx_raster_bwd -> gsx_preprocess_bwd            (backward)
 
 inside one ``torch.autograd.Function``: activations, projection, opacity
@@ -20,7 +21,7 @@ import torch
 from .. import _lib
 from ..cameras import Camera
 from ..profiling import count, stage
-from .rasterize import raster_backward, raster_forward
+from .rasterize import raster_backward, raster_forward, t_cotangent
 from .sh import num_sh_bases
 from .tiles import BinJob
 
@@ -84,20 +85,15 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
             return raster_forward(means2d, co, feats, ids, job.ranges, background, cfg.width,
                                   cfg.height, depths=depths if cfg.return_depth else None)
 
-    # The rasterizer runs on the full-capacity id buffer (its ranges never
-    # reach past D), so D is read back only after it has been enqueued.
-    image, final_T, n_contrib, depth_map = raster(job.ids)
-    if not job.finish():
-        with stage("binning"):
-            job.retry()
-        image, final_T, n_contrib, depth_map = raster(job.ids)
-        if not job.finish():
-            raise _lib.GsxError("gsx_bin_sort_async: capacity retry failed")
+    # The rasterizer runs on the id buffer (its ranges never reach past D);
+    # only refine_tiles needs the final status for D, read after it has been
+    # enqueued.
+    image, final_T, n_contrib, depth_map, alpha = raster(job.ids)
     ids, ranges = job.result()
     count("duplicates", ids.shape[0])
     return dict(means2d=means2d, depths=depths, radii=radii, compensation=comp, conic_opac=co,
                 feats=feats, sorted_ids=ids, tile_ranges=ranges, image=image, final_T=final_T,
-                n_contrib=n_contrib, depth=depth_map)
+                alpha=alpha, n_contrib=n_contrib, depth=depth_map)
 
 
 class _RenderFn(torch.autograd.Function):
@@ -112,12 +108,12 @@ class _RenderFn(torch.autograd.Function):
         ctx.mark_non_differentiable(r["radii"], r["n_contrib"], depth, r["sorted_ids"],
                                     r["tile_ranges"])
         ctx.set_materialize_grads(False)  # unused outputs: no zero-filled cotangents
-        return (r["image"], r["final_T"], r["n_contrib"], r["means2d"], r["depths"], r["radii"],
-                r["compensation"], depth, r["sorted_ids"], r["tile_ranges"])
+        return (r["image"], r["final_T"], r["alpha"], r["n_contrib"], r["means2d"], r["depths"],
+                r["radii"], r["compensation"], depth, r["sorted_ids"], r["tile_ranges"])
 
     @staticmethod
-    def backward(ctx, g_image, g_final_T, _g_nc, g_means2d, g_depths, _g_radii, g_comp, _g_depth,
-                 _g_ids, _g_ranges):
+    def backward(ctx, g_image, g_final_T, g_alpha, _g_nc, g_means2d, g_depths, _g_radii, g_comp,
+                 _g_depth, _g_ids, _g_ranges):
         (means, quats, scales, opacities, sh_a, sh_b, feats, means2d, co, ids, ranges, final_T,
          n_contrib, background, radii) = ctx.saved_tensors
         cfg = ctx.cfg
@@ -126,7 +122,8 @@ class _RenderFn(torch.autograd.Function):
         with stage("raster_bwd"):
             g_m2, g_con, g_feat, g_op = raster_backward(means2d, co, feats, ids, ranges,
                                                         background, cfg.width, cfg.height,
-                                                        final_T, n_contrib, g_image, g_final_T)
+                                                        final_T, n_contrib, g_image,
+                                                        t_cotangent(g_final_T, g_alpha))
         if cfg.screen_stats is not None:
             acc, cnt = cfg.screen_stats
             _lib.check(_lib.load().gsx_accum_screen_grads(
@@ -163,7 +160,8 @@ def _check_common(projection: str) -> int:
 
 def _background(background, channels, dev):
     if background is None:
-        return torch.zeros((channels,), dtype=torch.float32, device=dev)
+        return None  # the kernels read NULL as a zero background
+
     bg = torch.as_tensor(background, dtype=torch.float32, device=dev)
     if bg.ndim == 0:
         bg = bg.expand(channels)
@@ -200,13 +198,13 @@ def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=Non
                return_depth=bool(return_depth), refine=bool(refine_tiles),
                screen_stats=_stats(screen_stats, n, dev))
     c = _lib.f32c
-    (image, final_T, n_contrib, means2d, depths, radii, comp, depth, ids,
+    (image, final_T, alpha, n_contrib, means2d, depths, radii, comp, depth, ids,
      ranges) = _RenderFn.apply(c(means), c(quats), c(scales), c(opacities),
                                None if sh_a is None else c(sh_a),
                                None if sh_b is None else c(sh_b),
                                None if colors is None else c(colors),
                                _background(background, channels, dev), cfg)
-    out = {"image": image, "alpha": 1.0 - final_T, "final_T": final_T, "n_contrib": n_contrib,
+    out = {"image": image, "alpha": alpha, "final_T": final_T, "n_contrib": n_contrib,
            "means2d": means2d, "depths": depths, "radii": radii, "compensation": comp,
            "sorted_ids": ids, "tile_ranges": ranges}
     if return_depth:

@@ -3,9 +3,10 @@
 ``bin_gaussians`` keeps the reference's signature and outputs: ``sorted_ids``
 (D,) int32 in (tile, depth, index) order and ``tile_ranges`` (tiles, 2)
 int32 with (0, 0) for empty tiles.  The work runs in ``gsx_bin_prepare`` and
-``gsx_bin_sort_async`` (device radix sorts); the only host sync is the
-8-byte readback of D that the reference also does (tiles.py:68), and the
-renderer places it after the rasterizer has been enqueued.
+``gsx_bin_count_async`` / ``gsx_bin_depth_async`` / ``gsx_bin_tiles_async``
+(device radix sorts).  The host reads the duplicate count (the sum of the tile
+counts, which the reference reads at tiles.py:68) while the depth sort still
+runs, and sizes the tile phase's buffers exactly from it.
 """
 
 from __future__ import annotations
@@ -19,24 +20,42 @@ import torch
 from .. import _lib
 
 TILE_SIZE = 16
+_BIN_ERR_OVERFLOW = 2  # gsx_bin_error
+_ERR_TOO_LARGE = -4    # gsx_status
+_ERR_DEVICE = -5
 
 __all__ = ["TILE_SIZE", "bin_gaussians"]
 
 
 class _Workspace:
-    """Grow-only scratch buffer for gsx_bin_sort_async, one per (device, stream)."""
+    """Grow-only scratch buffers of the binning phases and the persistent
+    bin_status words, one set per (device, stream)."""
 
-    def __init__(self):
-        self.buf = None
-        self.last_dups = 0
+    def __init__(self, dev):
+        self.depth = None
+        self.tiles = None
+        # device error bits accumulate here across jobs (gsx_bin_count_async
+        # leaves word 1 alone), so each job's count readback also reports
+        # the checks of the jobs before it
+        self.status = torch.zeros((4,), dtype=torch.int32, device=dev)
 
-    def get(self, dev, n: int, cap: int, num_tiles: int) -> torch.Tensor:
-        need = int(_lib.load().gsx_bin_workspace_bytes(n, cap, num_tiles))
+    @staticmethod
+    def _grow(buf, dev, need: int, what: str) -> torch.Tensor:
         if need < 0:
-            raise ValueError(f"bad binning sizes: n={n}, capacity={cap}")
-        if self.buf is None or self.buf.numel() < need:
-            self.buf = torch.empty(int(need * 1.1) + 4096, dtype=torch.uint8, device=dev)
-        return self.buf
+            raise ValueError(f"bad binning sizes for the {what} workspace")
+        if buf is None or buf.numel() < need:
+            buf = torch.empty(int(need * 1.1) + 4096, dtype=torch.uint8, device=dev)
+        return buf
+
+    def get_depth(self, dev, n: int) -> torch.Tensor:
+        self.depth = self._grow(self.depth, dev, int(_lib.load().gsx_bin_depth_workspace_bytes(n)),
+                                "depth")
+        return self.depth
+
+    def get_tiles(self, dev, cap: int, num_tiles: int) -> torch.Tensor:
+        need = int(_lib.load().gsx_bin_tile_workspace_bytes(cap, num_tiles))
+        self.tiles = self._grow(self.tiles, dev, need, "tile")
+        return self.tiles
 
 
 _workspaces: dict = {}
@@ -48,86 +67,117 @@ def _workspace_for(dev, stream) -> _Workspace:
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None:
-            ws = _workspaces[key] = _Workspace()
+            ws = _workspaces[key] = _Workspace(dev)
     return ws
 
 
-class BinJob:
-    """One binning on the device with the duplicate count D left there.
+def _pinned_status(status: torch.Tensor):
+    """Copy of the 4 status words into pinned host memory behind the work
+    enqueued so far, and the event that marks it."""
+    host = torch.empty((4,), dtype=torch.int32, pin_memory=True)
+    host.copy_(status, non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    return host, ev
 
-    ``ids`` (capacity,) and ``ranges`` are usable by kernels enqueued behind
-    the job right away.  The two status words (D, error bits) are copied to
-    pinned host memory right behind the binning kernels, so ``finish()``
-    (the one host sync, as tiles.py:68 does) waits for the binning only,
-    not for work the caller enqueued after it.  It reports whether the
-    capacity sufficed; when it did not, ``retry()`` re-enqueues the binning
-    with room for D and the caller re-enqueues what it ran on the
-    incomplete result.
+
+def _raise_on_errors(ws: _Workspace, err: int, what: str) -> None:
+    if err == 0:
+        return
+    ws.status[1:2].zero_()  # report once
+    if err & _BIN_ERR_OVERFLOW:
+        _lib.check(_ERR_TOO_LARGE, f"{what} (more than 2^30 - 1 duplicates)")
+    _lib.check(_ERR_DEVICE, f"{what} (a device-side check of this or an earlier binning "
+                            "on this stream)")
+
+
+class BinJob:
+    """One binning on the device, sized exactly.
+
+    gsx_bin_count_async sums the tile counts, the number of duplicates
+    emission writes; the job copies the status words to pinned memory,
+    enqueues the depth sort (gsx_bin_depth_async, which keeps the device
+    busy meanwhile) and waits for that copy only, allocates ``ids`` with
+    exactly that capacity and enqueues the rest (gsx_bin_tiles_async).
+    ``ids`` and ``ranges`` are usable by kernels enqueued behind the job
+    right away.  Without refine_tiles D is that count and no second host
+    sync is needed; the device-side error bits of the tile phase are then
+    reported by the next job's count readback on the same stream.  With
+    refine_tiles, or ``final=True``, the final status is copied behind the
+    job and ``check()`` (called by ``result()`` when D is unknown) waits for
+    it.
     """
 
-    def __init__(self, counts, dkeys, rects, width: int, height: int, refine=None):
+    def __init__(self, counts, dkeys, rects, width: int, height: int, refine=None,
+                 final: bool = False):
         """``refine`` = (means2d (N,2), conics (N,k>=3)) enables refine_tiles."""
         self.dev = counts.device
-        self.args = (counts, dkeys, rects)
-        self.refine = refine
-        self.n = counts.shape[0]
+        self.n = n = counts.shape[0]
         self.width, self.height = int(width), int(height)
         self.tiles_x = (self.width + TILE_SIZE - 1) // TILE_SIZE
         self.tiles_y = (self.height + TILE_SIZE - 1) // TILE_SIZE
-        self.stream = _lib.stream_handle(self.dev)
-        self.ws = _workspace_for(self.dev, self.stream)
-        self.ranges = torch.empty((self.tiles_x * self.tiles_y, 2), dtype=torch.int32,
-                                  device=self.dev)
-        self.status = torch.empty((4,), dtype=torch.int32, device=self.dev)
-        self.num_dups = None
-        self._enqueue(max(1024, int(self.ws.last_dups * 1.25), 4 * self.n))
-
-    def _enqueue(self, cap: int):
-        counts, dkeys, rects = self.args
-        self.cap = int(cap)
-        buf = self.ws.get(self.dev, self.n, self.cap, self.tiles_x * self.tiles_y)
+        num_tiles = self.tiles_x * self.tiles_y
+        stream = _lib.stream_handle(self.dev)
+        ws = self.ws = _workspace_for(self.dev, stream)
+        status = ws.status
+        self.ranges = torch.empty((num_tiles, 2), dtype=torch.int32, device=self.dev)
+        L = _lib.load()
+        dws = ws.get_depth(self.dev, n)
+        _lib.check(L.gsx_bin_count_async(
+            n, _lib.ptr(counts), _lib.ptr(dkeys), self.width, self.height, _lib.ptr(dws),
+            dws.numel(), _lib.ptr(self.ranges), _lib.ptr(status), stream),
+            "gsx_bin_count_async")
+        host, ev = _pinned_status(status)
+        _lib.check(L.gsx_bin_depth_async(n, _lib.ptr(dkeys), _lib.ptr(dws), dws.numel(),
+                                         _lib.ptr(status), stream), "gsx_bin_depth_async")
+        ev.synchronize()
+        words = host.numpy().view(np.uint32)
+        _raise_on_errors(ws, int(words[1]), "gsx_bin_count_async")
+        self.cap = int(words[3])
+        tws = ws.get_tiles(self.dev, self.cap, num_tiles)
         self.ids = torch.empty((self.cap,), dtype=torch.int32, device=self.dev)
-        m2, co = self.refine if self.refine is not None else (None, None)
-        _lib.check(_lib.load().gsx_bin_sort_async(
-            self.n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), _lib.ptr(m2),
-            _lib.ptr(co), 0 if co is None else co.shape[1], self.width, self.height,
-            _lib.ptr(buf), buf.numel(), self.cap, _lib.ptr(self.ids), _lib.ptr(self.ranges),
-            _lib.ptr(self.status), self.stream), "gsx_bin_sort_async")
-        self.host = torch.empty((4,), dtype=torch.int32, pin_memory=True)
-        self.host.copy_(self.status, non_blocking=True)
-        self.ready = torch.cuda.Event()
-        self.ready.record()
+        m2, co = refine if refine is not None else (None, None)
+        _lib.check(L.gsx_bin_tiles_async(
+            n, _lib.ptr(counts), _lib.ptr(rects), _lib.ptr(m2), _lib.ptr(co),
+            0 if co is None else co.shape[1], self.width, self.height, _lib.ptr(dws),
+            dws.numel(), _lib.ptr(tws), tws.numel(), self.cap, _lib.ptr(self.ids),
+            _lib.ptr(self.ranges), _lib.ptr(status), stream), "gsx_bin_tiles_async")
+        self.host = self.ready = None
+        self.num_dups = self.cap
+        if refine is not None or final:
+            self.host, self.ready = _pinned_status(status)
+            self.num_dups = None
 
-    def finish(self) -> bool:
-        """Read D back; True if the binning is complete (num_dups = duplicates
-        kept), False if retry() is due (num_dups = capacity needed)."""
+    def check(self) -> None:
+        """With a final status copy: wait for the binning, raise GsxError if
+        a device-side check failed and set num_dups (duplicates kept)."""
+        if self.ready is None:
+            return
         self.ready.synchronize()
-        host = np.ascontiguousarray(self.host.numpy().view(np.uint32))
+        self.ready = None
+        words = np.ascontiguousarray(self.host.numpy().view(np.uint32))
+        _raise_on_errors(self.ws, int(words[1]), "gsx_bin_tiles_async")
         nd = ctypes.c_int64(0)
         rc = _lib.check(_lib.load().gsx_bin_status_check(
-            host.ctypes.data_as(ctypes.c_void_p), self.cap, ctypes.byref(nd)),
-            "gsx_bin_sort_async")
+            words.ctypes.data_as(ctypes.c_void_p), self.cap, ctypes.byref(nd)),
+            "gsx_bin_tiles_async")
+        if rc != _lib.GSX_OK:  # not reached: the capacity is the emitted count
+            raise _lib.GsxError("gsx_bin_tiles_async: duplicates exceed the exact capacity")
         self.num_dups = int(nd.value)
-        self.ws.last_dups = self.num_dups
-        return rc == _lib.GSX_OK
-
-    def retry(self):
-        self._enqueue(self.num_dups + self.num_dups // 8 + 1024)
-        self.num_dups = None
 
     def result(self):
-        """(sorted_ids (D,), tile_ranges) once finish() returned True."""
+        """(sorted_ids (D,), tile_ranges); waits for the binning only when D
+        is not yet known (refine_tiles)."""
+        if self.num_dups is None:
+            self.check()
         return self.ids[:self.num_dups], self.ranges
 
 
 def _bin_sort(counts, dkeys, rects, width: int, height: int, refine=None):
-    """Binning with the capacity guessed from the previous call; one retry
-    with room for the exact duplicate count when the guess was short."""
-    job = BinJob(counts, dkeys, rects, width, height, refine)
-    if not job.finish():
-        job.retry()
-        if not job.finish():
-            raise _lib.GsxError("gsx_bin_sort_async: capacity retry failed")
+    """Binning with the exact capacity, reading the final status (the
+    reference also syncs here, tiles.py:68)."""
+    job = BinJob(counts, dkeys, rects, width, height, refine, final=True)
+    job.check()
     return job.result()
 
 

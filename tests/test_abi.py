@@ -32,7 +32,7 @@ def test_python_binding_covers_header():
 
 def test_status_strings_and_version():
     L = _lib.load()
-    assert L.gsx_abi_version() == 2
+    assert L.gsx_abi_version() == 3
     assert _lib.strerror(0) == "ok"
     assert "invalid" in _lib.strerror(-1)
     assert "capacity" in _lib.strerror(1)
@@ -53,6 +53,14 @@ def test_workspace_query_is_host_only():
     b = L.gsx_bin_workspace_bytes(1000, 50000, 100)
     assert 0 < a < b
     assert L.gsx_bin_workspace_bytes(-1, 0, 1) < 0
+    # the one-call workspace is the depth phase's followed by the tile phase's
+    dn = L.gsx_bin_depth_workspace_bytes(1000)
+    assert dn > 0 and dn % 256 == 0
+    assert a == dn + L.gsx_bin_tile_workspace_bytes(5000, 100)
+    assert b == dn + L.gsx_bin_tile_workspace_bytes(50000, 100)
+    assert L.gsx_bin_depth_workspace_bytes(-1) < 0
+    assert L.gsx_bin_tile_workspace_bytes(-1, 100) < 0
+    assert L.gsx_bin_tile_workspace_bytes(10, 0) < 0
 
 
 def test_invalid_arguments_rejected_before_launch():
@@ -90,3 +98,18 @@ def test_bin_status_check_is_host_only():
                           None, ctypes.byref(nd), None) == -4
     assert L.gsx_bin_sort_async(10, None, None, None, None, None, 0, 64, 64, None, 0, 100, None,
                                 None, None, None) == -1
+    # the two phases: null outputs / inputs, negative sizes, a short workspace
+    assert L.gsx_bin_count_async(10, None, None, 64, 64, None, 0, None, None, None) == -1
+    assert L.gsx_bin_count_async(-1, None, None, 64, 64, None, 0, None, None, None) == -1
+    assert L.gsx_bin_depth_async(-1, None, None, 0, None, None) == -1
+    assert L.gsx_bin_depth_async(10, None, None, 0, None, None) == -1
+    assert L.gsx_bin_depth_async(1 << 30, None, None, 0, None, None) == -4
+    st = np.zeros(4, np.uint32)
+    rg = np.zeros(32, np.int32)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731  (never dereferenced)
+    assert L.gsx_bin_tiles_async(10, p(st), p(st), None, None, 0, 64, 64, p(st), 16, p(st), 16,
+                                 100, p(rg), p(rg), p(st), None) == -3
+    assert L.gsx_bin_tiles_async(10, None, None, None, None, 0, 64, 64, None, 0, None, 0, 100,
+                                 None, p(rg), p(st), None) == -1
+    assert L.gsx_bin_tiles_async(10, None, None, None, None, 0, 64, 64, None, 0, None, 0,
+                                 1 << 30, None, p(rg), p(st), None) == -4

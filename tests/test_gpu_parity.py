@@ -165,6 +165,101 @@ def test_bin_sort_sync_abi_and_capacity():
             np.testing.assert_array_equal(host(ranges), rranges)
 
 
+def test_bin_two_phase_abi_exact_capacity():
+    """gsx_bin_count_async reports the emitted duplicate count in
+    bin_status[3] before the sorts run; gsx_bin_depth_async and
+    gsx_bin_tiles_async with that capacity match the oracle bit for bit,
+    plain and with refine_tiles."""
+    m, r, d, co = _elongated(9, n=4000)
+    n = m.shape[0]
+    L = _lib.load()
+    dev = torch.device("cuda")
+    st = _lib.stream_handle(dev)
+    m2, rad, dep, con = cu(m), cu(r), cu(d), cu(co)  # alive past the launches
+    counts = torch.empty(n, dtype=torch.int32, device=dev)
+    dkeys = torch.empty(n, dtype=torch.int32, device=dev)
+    rects = torch.empty((n, 2), dtype=torch.int32, device=dev)
+    _lib.check(L.gsx_bin_prepare(n, _lib.ptr(m2), _lib.ptr(rad), _lib.ptr(dep), 640, 360,
+                                 _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), st),
+               "prepare")
+    full, _, tx, ty = O.bin_gaussians(m, r, d, 640, 360, threads=8)
+    for refine in (False, True):
+        rids, rranges, _, _ = O.bin_gaussians(m, r, d, 640, 360, threads=8,
+                                              conics=co if refine else None)
+        say(f"two-phase binning refine={refine}: emitted {full.shape[0]}, kept {rids.shape[0]}")
+        dws = torch.empty(L.gsx_bin_depth_workspace_bytes(n), dtype=torch.uint8, device=dev)
+        ranges = torch.empty((tx * ty, 2), dtype=torch.int32, device=dev)
+        # words 0, 2, 3 are cleared by the count call, the error word is not
+        status = torch.tensor([-1, 0, -1, -1], dtype=torch.int32, device=dev)
+        _lib.check(L.gsx_bin_count_async(n, _lib.ptr(counts), _lib.ptr(dkeys), 640, 360,
+                                         _lib.ptr(dws), dws.numel(), _lib.ptr(ranges),
+                                         _lib.ptr(status), st), "count")
+        words = host(status).view(np.uint32)
+        assert words[0] == words[1] == words[2] == 0
+        assert words[3] == full.shape[0] == int(host(counts).sum())
+        _lib.check(L.gsx_bin_depth_async(n, _lib.ptr(dkeys), _lib.ptr(dws), dws.numel(),
+                                         _lib.ptr(status), st), "depth sort")
+        cap = int(words[3])
+        tws = torch.empty(L.gsx_bin_tile_workspace_bytes(cap, tx * ty), dtype=torch.uint8,
+                          device=dev)
+        ids = torch.full((cap,), -1, dtype=torch.int32, device=dev)
+        _lib.check(L.gsx_bin_tiles_async(
+            n, _lib.ptr(counts), _lib.ptr(rects), _lib.ptr(m2) if refine else None,
+            _lib.ptr(con) if refine else None, 3 if refine else 0, 640, 360, _lib.ptr(dws),
+            dws.numel(), _lib.ptr(tws), tws.numel(), cap, _lib.ptr(ids), _lib.ptr(ranges),
+            _lib.ptr(status), st), "tile phase")
+        words = host(status).view(np.uint32)
+        nd = ctypes.c_int64(0)
+        hw = np.ascontiguousarray(words)
+        assert L.gsx_bin_status_check(hw.ctypes.data_as(ctypes.c_void_p), cap,
+                                      ctypes.byref(nd)) == 0
+        assert words[0] == cap and nd.value == rids.shape[0]
+        np.testing.assert_array_equal(host(ids[:nd.value]), rids)
+        np.testing.assert_array_equal(host(ranges), rranges)
+
+
+def test_binning_error_bits_reported_once():
+    """The renderer's binning reads the sticky error word with its count
+    readback: an error bit set (here from the host, as a tile phase's
+    bounded wait would set it) makes the next render raise, once."""
+    from mlx3d_amd.splatting import tiles
+
+    cam, means, quats, scales, opac, colors = random_scene(11, n=3000, width=320, height=240)
+    t = [cu(a) for a in (means, quats, scales, opac, colors)]
+    a = render_gaussians(cam, *t[:4], colors=t[4])
+    dev = t[0].device
+    ws = tiles._workspace_for(dev, _lib.stream_handle(dev))
+    ws.status[1] = 1  # GSX_BIN_ERR_LOOKBACK
+    with pytest.raises(_lib.GsxError, match="device-side check"):
+        render_gaussians(cam, *t[:4], colors=t[4])
+    b = render_gaussians(cam, *t[:4], colors=t[4])
+    assert_bits(host(b["image"]), host(a["image"]), "image after the reported error")
+
+
+def test_render_alpha_output_and_gradient():
+    """alpha comes from the forward kernel (bit-identical to 1 - final_T) and
+    its cotangent reaches the rasterizer as -grad_alpha: a loss on alpha
+    and final_T gives the gradients of the same loss written on final_T."""
+    cam, means, quats, scales, opac, colors = random_scene(12, n=3000, width=320, height=240)
+    rng = np.random.default_rng(12)
+    w1, w2 = (cu(rng.normal(size=(240, 320)).astype(np.float32)) for _ in range(2))
+    grads = []
+    for via_alpha in (True, False):
+        t = [cu(a).requires_grad_(True) for a in (means, quats, scales, opac, colors)]
+        out = render_gaussians(cam, *t[:4], colors=t[4], antialias=True)
+        if via_alpha:
+            assert_bits(host(out["alpha"]), host(1.0 - out["final_T"]), "alpha")
+            a = out["alpha"]
+        else:
+            a = 1.0 - out["final_T"]
+        loss = (a * w1).sum() + (out["final_T"] * w2).sum() + out["image"].sum()
+        grads.append(torch.autograd.grad(loss, t))
+    for name, ga, gb in zip(("means", "quats", "scales", "opacities", "colors"), *grads):
+        err = rel_err(host(ga), host(gb))
+        say(f"alpha path {name}: rel err {err:.2e}")
+        assert err < 1e-5, name
+
+
 def _elongated(seed, n=3000, width=640, height=360):
     rng = np.random.default_rng(seed)
     means2d = rng.uniform(-20, [width + 20, height + 20], (n, 2)).astype(np.float32)
