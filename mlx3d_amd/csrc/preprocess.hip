@@ -39,10 +39,11 @@ __device__ __forceinline__ void row_col(int j, int cols, float inv, int& r, int&
 
 // Rows [g0, g0 + rows) of `cols` floats (row r at base + (g0 + r) * stride)
 // into LDS rows of `pad` floats.  Loads go out kBatch at a time so their
-// latencies overlap.
+// latencies overlap; 48 covers a whole workgroup's rows (<= 48 columns) in
+// one batch.
 __device__ __forceinline__ void rows_to_lds(float* s, int pad, const float* __restrict__ base,
                                             int64_t stride, int64_t g0, int rows, int cols) {
-    constexpr int kBatch = 16;
+    constexpr int kBatch = 48;
     const int total = rows * cols;
     const float inv = 1.0f / (float)cols;
     for (int j0 = threadIdx.x; j0 < total; j0 += kBatch * kThreads) {
@@ -246,6 +247,14 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     const int64_t g0 = (int64_t)blockIdx.x * kThreads;
     const int64_t i = g0 + threadIdx.x;
     const int pad = sh_cols | 1;
+    // the Gaussian's own inputs are requested before the SH rows, so both
+    // loads are in flight together (lanes past n re-read row n - 1; the host
+    // launches nothing for n == 0)
+    const int64_t il = i < n ? i : n - 1;
+    const float m0 = means[3 * il], m1 = means[3 * il + 1], m2 = means[3 * il + 2];
+    const float4 q = quats[il];
+    const float r0 = scales[3 * il], r1 = scales[3 * il + 1], r2 = scales[3 * il + 2];
+    const float ro = opacities[il];
     if (sh_mode != kShDirect) {
         const int rows = (int)min<int64_t>(kThreads, n - g0);
         rows_to_lds(s_sh, pad, sh_mode == kShPacked ? sh0 : shr, sh_mode == kShPacked ? s0 : sr,
@@ -253,12 +262,10 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
         __syncthreads();
     }
     if (i >= n) return;
-    const float m0 = means[3 * i], m1 = means[3 * i + 1], m2 = means[3 * i + 2];
-    const float4 q = quats[i];
-    const float sx = act_scale(scales[3 * i], flags);
-    const float sy = act_scale(scales[3 * i + 1], flags);
-    const float sz = act_scale(scales[3 * i + 2], flags);
-    const float o = act_opacity(opacities[i], flags);
+    const float sx = act_scale(r0, flags);
+    const float sy = act_scale(r1, flags);
+    const float sz = act_scale(r2, flags);
+    const float o = act_opacity(ro, flags);
     typename ProjOf<UT>::T p;
     project_any<UT>(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
     means2d[i] = make_float2(p.u, p.v);
