@@ -71,7 +71,7 @@ def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
     """Compulsory HBM bytes per stage (each tensor read or written once)."""
     Cw = C if sh_path else 0
     dz = 4 if depth else 0
-    raster_fwd = D * (28 + 4 * C + dz) + P * (4 * C + 8 + dz)
+    raster_fwd = D * (28 + 4 * C + dz) + P * (4 * C + 12 + dz)  # out, final_T, alpha, n_contrib
     raster_bwd = D * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C)
     pre_fwd = N * (44 + 12 * Ka) + N * (36 + 4 * Cw)
     binning = 28 * N + 44 * D
