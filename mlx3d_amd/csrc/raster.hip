@@ -821,10 +821,10 @@ __device__ __forceinline__ void bwd_walk(const uint16_t* list, int cnt, int lim,
 }
 
 // Waves per SIMD the backward asks for (more waves hide LDS and ballot
-// latencies): five up to four channels (<= 96 VGPRs; the 31.6 KB of LDS of
-// the 128-Gaussian batches also caps them at five blocks per CU), four up
-// to 16 channels, three at 32, all without spills.
-constexpr int bwd_min_waves(int ch) { return ch <= 4 ? 5 : (ch <= 16 ? 4 : 3); }
+// latencies): six up to four channels (<= 80 VGPRs, 12-16 KB of LDS), except
+// five at two channels (which would spill at 80), four up to 16 channels,
+// three at 32, all without spills.
+constexpr int bwd_min_waves(int ch) { return ch == 2 ? 5 : (ch <= 4 ? 6 : (ch <= 16 ? 4 : 3)); }
 
 template <int CH>
 __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
@@ -838,7 +838,9 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     constexpr int F4 = (CH + 3) / 4;
     constexpr int NV = CH + 6;             // u, w, u dx, u dy, w dy, opacity term, channels
     constexpr int NV4 = (NV + 3) / 4;
-    constexpr int BB = (CH <= 4) ? 128 : 64;  // Gaussians per batch (bounded by slot LDS)
+    // Gaussians per batch: 64 keeps the slot LDS at 16 KB up to four
+    // channels (more workgroups per CU; measured faster than 128)
+    constexpr int BB = 64;
     constexpr int NLW = BB / kWave;  // mask words per quadrant
     // entry BB of the records and slots is the walk lists' padding: a record
     // no pixel can take (alpha bound +inf) whose slot the flush never reads
