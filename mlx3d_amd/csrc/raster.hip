@@ -139,14 +139,18 @@ __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, in
     };
     const bool inl = xl0 <= 0.0f && xl1 >= 0.0f, inr = xr0 <= 0.0f && xr1 >= 0.0f;
     const bool intp = yt0 <= 0.0f && yt1 >= 0.0f, inb = yb0 <= 0.0f && yb1 >= 0.0f;
-    const float q0 = fminf(fminf(row(yt0, xl0, xl1), row(yt1, xl0, xl1)),
-                           fminf(col(xl0, yt0, yt1), col(xl1, yt0, yt1)));
-    const float q1 = fminf(fminf(row(yt0, xr0, xr1), row(yt1, xr0, xr1)),
-                           fminf(col(xr0, yt0, yt1), col(xr1, yt0, yt1)));
-    const float q2 = fminf(fminf(row(yb0, xl0, xl1), row(yb1, xl0, xl1)),
-                           fminf(col(xl0, yb0, yb1), col(xl1, yb0, yb1)));
-    const float q3 = fminf(fminf(row(yb0, xr0, xr1), row(yb1, xr0, xr1)),
-                           fminf(col(xr0, yb0, yb1), col(xr1, yb0, yb1)));
+    // With the mean outside a rectangle, q's minimum over it lies on an edge
+    // whose outer side holds the mean (at a minimiser inside an edge the
+    // gradient 2M(p - mean) points into the rectangle, so the mean lies
+    // beyond that edge): of each quadrant's two rows and two columns only
+    // the one nearer the mean can hold it, and the other edge of the pair
+    // is an upper bound, so min(row edge, column edge) is the minimum.
+    const float kt = yt1 < 0.0f ? yt1 : yt0, kb = yb1 < 0.0f ? yb1 : yb0;
+    const float kl = xl1 < 0.0f ? xl1 : xl0, kr = xr1 < 0.0f ? xr1 : xr0;
+    const float q0 = fminf(row(kt, xl0, xl1), col(kl, yt0, yt1));
+    const float q1 = fminf(row(kt, xr0, xr1), col(kr, yt0, yt1));
+    const float q2 = fminf(row(kb, xl0, xl1), col(kl, yb0, yb1));
+    const float q3 = fminf(row(kb, xr0, xr1), col(kr, yb0, yb1));
     return ((inl && intp) || q0 <= t2 ? 1u : 0u) | ((inr && intp) || q1 <= t2 ? 2u : 0u) |
            ((inl && inb) || q2 <= t2 ? 4u : 0u) | ((inr && inb) || q3 <= t2 ? 8u : 0u);
 }
