@@ -98,6 +98,25 @@ def _traffic(kernel: str, workload: str):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+VALU_PEAK_G = 732.3  # measured wave-level VALU issue rate of the rasterizers' mix
+
+
+def _issue(kernel: str, workload: str, mean_ms: float):
+    """VALU issue rate of the kernel: wave-level VALU instructions per launch
+    (rocprofv3 SQ_INSTS_VALU, recorded under profiles/) over its mean
+    duration, against the measured issue ceiling, if recorded."""
+    path = os.path.join(_profiles_dir(), f"valu_{kernel}_{workload}.json")
+    if not os.path.exists(path) or not mean_ms or mean_ms != mean_ms:
+        return None
+    with open(path) as f:
+        n = json.load(f).get("valu_instructions_per_launch")
+    if not n:
+        return None
+    g = n / (mean_ms * 1e-3) / 1e9
+    return {"bound": "valu", "valu_instructions": int(n), "achieved": round(g, 1),
+            "peak": VALU_PEAK_G, "unit": "G wave-instr/s", "frac": round(g / VALU_PEAK_G, 4)}
+
+
 def _read_csv(path):
     import csv
 
@@ -471,7 +490,8 @@ def main():
                      "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": _traffic(dom, workload),
-                     "algorithmic_bytes": int(B[dom]), "mean_ms": stages[dom]["ms"]},
+                     "algorithmic_bytes": int(B[dom]), "mean_ms": stages[dom]["ms"],
+                     "issue": _issue(dom, workload, stages[dom]["ms"])},
         "stages": stages,
     }
     if args.train_steps > 0 and scene.backward and not feat_mode:
