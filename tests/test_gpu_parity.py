@@ -414,7 +414,7 @@ def test_model_render_sh_raw_params(degree):
         assert e < 1e-3
 
 
-@pytest.mark.parametrize("channels", [1, 5, 32, 37])
+@pytest.mark.parametrize("channels", [1, 2, 4, 5, 12, 32, 37])
 def test_features(channels):
     cam, means, quats, scales, opac, _ = random_scene(6, n=3000, width=128, height=96)
     opac = np.minimum(opac, 0.95).astype(np.float32)
