@@ -382,25 +382,30 @@ __device__ __forceinline__ float comp4(const float4& v, int e) {
 // One (pixel, Gaussian) step of the front-to-back loop (rasterize.py:74-87),
 // straight-line: lanes that do not composite keep their state through
 // selects.  PLAIN: the Gaussian passed plain_gaussian(), so exp needs no
-// range handling and a non-compositing lane can add a zero weight.
+// range handling and a non-compositing lane can add a zero weight.  The
+// per-lane decisions are kept as wave masks (alive: the pixel has not
+// stopped): a ballot of one comparison is that comparison's lane mask, the
+// masks combine in scalar registers, and inverse_ballot hands one back to
+// the lanes as a select condition, so none of it costs vector ALU work.
 template <int CH, bool DEPTH, bool PLAIN>
 __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
                                          const float4* __restrict__ fsrc, int off, float pxf,
                                          float pyf, float& T, float* acc, float& dacc,
-                                         int& last_off, bool& done) {
+                                         int& last_off, uint64_t& alive) {
     constexpr int F4 = (CH + 3) / 4;
     float4 fv[F4];
 #pragma unroll
     for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
     const float dx = r0.x - pxf, dy = r0.y - pyf;
     const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
-    const bool live = !done && !(power > 0.0f) && !(power < r0.z);
+    const uint64_t live = alive & __ballot(!(power > 0.0f)) & __ballot(!(power < r0.z));
     const float e = PLAIN ? splat_exp_core(power) : splat_exp_sel(power);
     const float alpha = fminf(0.99f, r0.w * e);
-    const bool pass = live && !(alpha < 1.0f / 255.0f);
+    const uint64_t pass = live & __ballot(!(alpha < 1.0f / 255.0f));
     const float next_T = T * (1.0f - alpha);
-    const bool stop = pass && next_T < 1e-4f;
-    const bool add = pass && !stop;
+    const uint64_t lt = __ballot(next_T < 1e-4f);
+    alive &= ~(pass & lt);  // the reference's early stop
+    const bool add = __builtin_amdgcn_inverse_ballot_w64(pass & ~lt);
     // acc += rgb * (alpha * T) (rasterize.py:84) as one fused multiply-add,
     // the contraction Metal's default fast-math applies to the reference
     const float w = alpha * T;
@@ -422,7 +427,6 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
     }
     T = add ? next_T : T;
     last_off = add ? off : last_off;
-    done = done || stop;
 }
 
 // Front-to-back walk of one quadrant wave over its list, two Gaussians per
@@ -437,7 +441,7 @@ template <int CH, bool DEPTH, bool PLAIN>
 __device__ __forceinline__ void fwd_walk(const uint16_t* list, int cnt, const float4* s_r0,
                                          const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
                                          float pxf, float pyf, float& T, float* acc, float& dacc,
-                                         int& last_off, bool& done) {
+                                         int& last_off, uint64_t& alive) {
     constexpr int F4 = (CH + 3) / 4;
     const float4* sf = &s_f[0][0];
     int oa = list[0], ob = list[1];
@@ -446,12 +450,12 @@ __device__ __forceinline__ void fwd_walk(const uint16_t* list, int cnt, const fl
         const int na = list[i + 2], nb = list[i + 3];
         const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
         fwd_pair<CH, DEPTH, PLAIN>(a0, a1, &rec_at(sf, oa * F4), oa, pxf, pyf, T, acc, dacc,
-                                   last_off, done);
+                                   last_off, alive);
         a0 = rec_at(s_r0, na);
         a1 = rec_at(s_r1, na);
         fwd_pair<CH, DEPTH, PLAIN>(b0, b1, &rec_at(sf, ob * F4), ob, pxf, pyf, T, acc, dacc,
-                                   last_off, done);
-        if (__ballot(!done) == 0ull) return;
+                                   last_off, alive);
+        if (alive == 0ull) return;
         oa = na;
         ob = nb;
     }
@@ -500,7 +504,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
 #pragma unroll
     for (int k = 0; k < CH; ++k) acc[k] = 0.0f;
     int last = 0;
-    bool done = !inside;
+    uint64_t alive = __ballot(inside);  // the wave's pixels still compositing
     // the padding record (written before the first barrier)
     if (tid == 0) {
         s_r0[kThreads] = make_float4(0.0f, 0.0f, __builtin_huge_valf(), 0.0f);
@@ -510,7 +514,6 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     }
 
     for (int base = 0; base < num; base += kThreads) {
-        const uint64_t alive = __ballot(!done);
         if (lane == 0) s_alive[wave] = alive != 0ull;
         __syncthreads();
         const uint4 al = *reinterpret_cast<const uint4*>(s_alive);
@@ -548,10 +551,10 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
         int last_off = -1;
         if (batch_plain)
             fwd_walk<CH, DEPTH, true>(s_list[wave], cnt, s_r0, s_r1, s_f, pxf, pyf, T, acc, dacc,
-                                      last_off, done);
+                                      last_off, alive);
         else
             fwd_walk<CH, DEPTH, false>(s_list[wave], cnt, s_r0, s_r1, s_f, pxf, pyf, T, acc,
-                                       dacc, last_off, done);
+                                       dacc, last_off, alive);
         if (last_off >= 0) last = base + (last_off >> 4) + 1;
     }
     if (inside) {
