@@ -341,8 +341,10 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: only --gpus 1 is supported (got --gpus {args.gpus}, WORLD_SIZE "
-              f"{world}). This build measures the rasterizer on one MI355X; DESIGN.md describes "
-              "how the path would shard across GPUs.", file=sys.stderr)
+              f"{world}). This build measures the rasterizer on one MI355X; across GPUs the "
+              "path would shard by view for multi-view training (by bands of tile rows for a "
+              "single view), with the per-Gaussian gradients all-reduced once per step.",
+              file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
