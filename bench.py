@@ -67,12 +67,18 @@ KERNEL_SYMBOL = {"raster_fwd": "k_raster_fwd", "raster_bwd": "k_raster_bwd",
 COPY_PROBE_KERNEL = "k_debug_expf"
 
 
-def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
-    """Compulsory HBM bytes per stage (each tensor read or written once)."""
+def algorithmic_bytes(N, D, Dn, P, C, Ka, sh_path, depth):
+    """Compulsory HBM bytes per stage (each tensor read or written once).
+
+    D is the number of (tile, Gaussian) duplicates binning writes; Dn the
+    list entries the rasterizers must read: per tile, up to the last
+    Gaussian any of its pixels composited (sum over tiles of the largest
+    n_contrib).  The backward replays exactly those entries; the forward
+    may read further (up to each pixel's stop), so Dn is its lower bound."""
     Cw = C if sh_path else 0
     dz = 4 if depth else 0
-    raster_fwd = D * (28 + 4 * C + dz) + P * (4 * C + 12 + dz)  # out, final_T, alpha, n_contrib
-    raster_bwd = D * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C)
+    raster_fwd = Dn * (28 + 4 * C + dz) + P * (4 * C + 12 + dz)  # out, final_T, alpha, n_contrib
+    raster_bwd = Dn * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C)
     pre_fwd = N * (44 + 12 * Ka) + N * (36 + 4 * Cw)
     binning = 28 * N + 44 * D
     pre_bwd = N * (44 + 12 * Ka + 24 + 4 * Cw) + N * (44 + 12 * Ka)
@@ -82,6 +88,18 @@ def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
     return dict(raster_fwd=raster_fwd, raster_bwd=raster_bwd, preprocess_fwd=pre_fwd,
                 binning=binning, preprocess_bwd=pre_bwd, fwd=fwd, bwd=bwd, loss=loss,
                 iter=fwd + bwd + loss)
+
+
+def needed_entries(n_contrib, tile: int = 16) -> int:
+    """Sum over 16x16 tiles of the largest n_contrib (the 1-based list
+    position of a pixel's last composited Gaussian) in the tile."""
+    import torch
+
+    H, W = n_contrib.shape
+    ty, tx = -(-H // tile), -(-W // tile)
+    pad = torch.zeros((ty * tile, tx * tile), dtype=torch.int64, device=n_contrib.device)
+    pad[:H, :W] = n_contrib
+    return int(pad.view(ty, tile, tx, tile).amax(dim=(1, 3)).sum())
 
 
 def _profiles_dir():
@@ -384,15 +402,16 @@ def main():
     targets = [cu(scene.target(c)) for c in cams]
     torch.cuda.synchronize()
 
-    def render(i):
+    def render_all(i):
         cam = cams[i % nviews]
         if feat_mode:
-            out = render_gaussian_features(cam, leaf["means"], leaf["quats"], leaf["scales"],
-                                           leaf["opacities"], leaf["features"],
-                                           antialias=scene.antialias, return_depth=scene.depth)
-            return out["features"]
-        out = model.render(cam, antialias=scene.antialias, return_depth=scene.depth)
-        return out["image"]
+            return render_gaussian_features(cam, leaf["means"], leaf["quats"], leaf["scales"],
+                                            leaf["opacities"], leaf["features"],
+                                            antialias=scene.antialias, return_depth=scene.depth)
+        return model.render(cam, antialias=scene.antialias, return_depth=scene.depth)
+
+    def render(i):
+        return render_all(i)["features" if feat_mode else "image"]
 
     def step(i):
         for p in leaf.values():
@@ -451,7 +470,10 @@ def main():
     C = scene.channels
     Ka = 0 if feat_mode else (scene.sh_degree + 1) ** 2
     D = float(np.mean(timer.counters["duplicates"]))
-    B = algorithmic_bytes(N, D, P, C, Ka, not feat_mode, scene.depth)
+    with torch.no_grad():  # outside the timed regions, over the views the steps used
+        Dn = float(np.mean([needed_entries(render_all(i)["n_contrib"])
+                            for i in range(min(args.steps, nviews))]))
+    B = algorithmic_bytes(N, D, Dn, P, C, Ka, not feat_mode, scene.depth)
     stages = {}
     for name in ("preprocess_fwd", "binning", "raster_fwd", "raster_bwd", "preprocess_bwd"):
         ms = timer.mean_ms(name)
@@ -483,7 +505,7 @@ def main():
         "config": {"workload": workload, "gaussians": N, "width": cams[0].width,
                    "height": cams[0].height, "views": nviews, "sh_degree": scene.sh_degree,
                    "channels": C, "antialias": scene.antialias, "depth": scene.depth,
-                   "duplicates_mean": int(D)},
+                   "duplicates_mean": int(D), "needed_entries_mean": int(Dn)},
         "fwd_fps": round(1e3 / ms_fwd, 2),
         "fwd_ms": round(ms_fwd, 4),
         "fwd_hbm_roofline_frac": round(fwd_gbs / HBM_PEAK_GBS, 4),
