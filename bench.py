@@ -67,18 +67,22 @@ KERNEL_SYMBOL = {"raster_fwd": "k_raster_fwd", "raster_bwd": "k_raster_bwd",
 COPY_PROBE_KERNEL = "k_debug_expf"
 
 
-def algorithmic_bytes(N, D, Dn, P, C, Ka, sh_path, depth):
-    """Compulsory HBM bytes per stage (each tensor read or written once).
+def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
+    """Compulsory HBM bytes per stage, SURVEY 8(d)'s formulas: each tensor
+    read or written once.  D is the number of (tile, Gaussian) duplicates
+    binning writes; the rasterizers are charged one gather per duplicate.
 
-    D is the number of (tile, Gaussian) duplicates binning writes; Dn the
-    list entries the rasterizers must read: per tile, up to the last
-    Gaussian any of its pixels composited (sum over tiles of the largest
-    n_contrib).  The backward replays exactly those entries; the forward
-    may read further (up to each pixel's stop), so Dn is its lower bound."""
+        raster fwd   D (28 + 4C [+4 depth]) + P (4C + 8 [+4 depth])
+        raster bwd   D (28 + 4C) + P (4C + 8) + N (24 + 4C)
+        preprocess   N (44 + 12 Ka) + N (36 + 4 Cw)      Cw = C on the SH path
+        binning      28 N + 44 D
+        pre bwd      N (44 + 12 Ka + 24 + 4 Cw) + N (44 + 12 Ka)
+        loss (L1)    12 C P
+    """
     Cw = C if sh_path else 0
     dz = 4 if depth else 0
-    raster_fwd = Dn * (28 + 4 * C + dz) + P * (4 * C + 12 + dz)  # out, final_T, alpha, n_contrib
-    raster_bwd = Dn * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C)
+    raster_fwd = D * (28 + 4 * C + dz) + P * (4 * C + 8 + dz)
+    raster_bwd = D * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C)
     pre_fwd = N * (44 + 12 * Ka) + N * (36 + 4 * Cw)
     binning = 28 * N + 44 * D
     pre_bwd = N * (44 + 12 * Ka + 24 + 4 * Cw) + N * (44 + 12 * Ka)
@@ -88,6 +92,16 @@ def algorithmic_bytes(N, D, Dn, P, C, Ka, sh_path, depth):
     return dict(raster_fwd=raster_fwd, raster_bwd=raster_bwd, preprocess_fwd=pre_fwd,
                 binning=binning, preprocess_bwd=pre_bwd, fwd=fwd, bwd=bwd, loss=loss,
                 iter=fwd + bwd + loss)
+
+
+def needed_bytes(Dn, N, P, C, depth):
+    """The rasterizers' bytes when only the list entries a pixel can reach are
+    charged: Dn = sum over tiles of the largest n_contrib (the backward
+    replays exactly those; the forward reads at least those).  A secondary
+    figure beside SURVEY 8(d)'s, which charges every duplicate."""
+    dz = 4 if depth else 0
+    return dict(raster_fwd=Dn * (28 + 4 * C + dz) + P * (4 * C + 12 + dz),
+                raster_bwd=Dn * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C))
 
 
 def needed_entries(n_contrib, tile: int = 16) -> int:
@@ -116,13 +130,19 @@ def _traffic(kernel: str, workload: str):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-VALU_PEAK_G = 732.3  # measured wave-level VALU issue rate of the rasterizers' mix
+# Nominal wave-level VALU issue rate: one wave64 instruction per SIMD every
+# 4 cycles, 4 SIMDs x 256 CUs at 2.4 GHz.
+VALU_PEAK_G = 256 * 4 * 2.4e9 / 4 / 1e9
+# Rate a standalone probe measured on the box for the rasterizers' mix of
+# fma / compare / multiply / select (dual-issue of independent VALU ops).
+VALU_MEASURED_G = 732.3
 
 
 def _issue(kernel: str, workload: str, mean_ms: float):
     """VALU issue rate of the kernel: wave-level VALU instructions per launch
     (rocprofv3 SQ_INSTS_VALU, recorded under profiles/) over its mean
-    duration, against the measured issue ceiling, if recorded."""
+    duration, against the nominal issue peak (and the measured mix rate),
+    if recorded."""
     path = os.path.join(_profiles_dir(), f"valu_{kernel}_{workload}.json")
     if not os.path.exists(path) or not mean_ms or mean_ms != mean_ms:
         return None
@@ -132,7 +152,10 @@ def _issue(kernel: str, workload: str, mean_ms: float):
         return None
     g = n / (mean_ms * 1e-3) / 1e9
     return {"bound": "valu", "valu_instructions": int(n), "achieved": round(g, 1),
-            "peak": VALU_PEAK_G, "unit": "G wave-instr/s", "frac": round(g / VALU_PEAK_G, 4)}
+            "peak": round(VALU_PEAK_G, 1), "unit": "G wave-instr/s",
+            "frac": round(g / VALU_PEAK_G, 4),
+            "measured_mix_peak": VALU_MEASURED_G,
+            "frac_of_measured_mix": round(g / VALU_MEASURED_G, 4)}
 
 
 def _read_csv(path):
@@ -439,9 +462,13 @@ def main():
         t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
 
+    # The stage pass covers every view equally often (a whole number of
+    # passes over the views, at least K steps), so per-stage means and
+    # medians weigh the views alike even when K is not a multiple of them.
+    stage_steps = -(-args.steps // nviews) * nviews
     timer = StageTimer()
     with timer, _no_gc():
-        for i in range(args.steps):
+        for i in range(stage_steps):
             step(i)
         torch.cuda.synchronize()
 
@@ -470,17 +497,23 @@ def main():
     C = scene.channels
     Ka = 0 if feat_mode else (scene.sh_degree + 1) ** 2
     D = float(np.mean(timer.counters["duplicates"]))
-    with torch.no_grad():  # outside the timed regions, over the views the steps used
+    with torch.no_grad():  # outside the timed regions, one render per view
         Dn = float(np.mean([needed_entries(render_all(i)["n_contrib"])
-                            for i in range(min(args.steps, nviews))]))
-    B = algorithmic_bytes(N, D, Dn, P, C, Ka, not feat_mode, scene.depth)
+                            for i in range(nviews)]))
+    B = algorithmic_bytes(N, D, P, C, Ka, not feat_mode, scene.depth)
+    Bn = needed_bytes(Dn, N, P, C, scene.depth)
     stages = {}
     for name in ("preprocess_fwd", "binning", "raster_fwd", "raster_bwd", "preprocess_bwd"):
         ms = timer.mean_ms(name)
         if not math.isnan(ms):
+            med = timer.median_ms(name)
             gbs = B[name] / (ms * 1e-3) / 1e9
-            stages[name] = {"ms": round(ms, 4), "GB/s": round(gbs, 1),
-                            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            stages[name] = {"ms": round(ms, 4), "median_ms": round(med, 4),
+                            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                            "frac_median": round(B[name] / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            if name in Bn:
+                stages[name]["frac_needed_entries"] = round(
+                    Bn[name] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     kernels = [k for k in ("raster_fwd", "raster_bwd", "preprocess_fwd", "preprocess_bwd")
                if k in stages]
     dom = max(kernels, key=lambda k: stages[k]["ms"])
@@ -515,6 +548,10 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": _traffic(dom, workload),
                      "algorithmic_bytes": int(B[dom]), "mean_ms": stages[dom]["ms"],
+                     "median_ms": stages[dom]["median_ms"],
+                     "frac_median": stages[dom]["frac_median"],
+                     "bytes_formula": "SURVEY 8(d), every duplicate charged",
+                     "frac_needed_entries": stages[dom].get("frac_needed_entries"),
                      "issue": _issue(dom, workload, stages[dom]["ms"])},
         "stages": stages,
     }

@@ -7,12 +7,17 @@ the source tree).  Flags:
                              radii, tile rectangles, contributor counts)
   -munsafe-fp-atomics        hardware global_atomic_add_f32 in the backward
   -packed-fp32-ops disabled  no v_pk_*_f32 generated
+The compiler's per-kernel resource usage (VGPRs, scratch, occupancy) is
+written to _build/resource_usage.json, and the build fails if any kernel
+spills registers to scratch memory.
 """
 
 from __future__ import annotations
 
 import concurrent.futures
+import json
 import os
+import re
 import subprocess
 import sys
 
@@ -34,15 +39,43 @@ FLAGS = [
 ]
 
 
-def _compile(src: str, obj: str) -> None:
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+_REMARK = "-Rpass-analysis=kernel-resource-usage"
+
+
+def _resources(stderr: str) -> dict:
+    """{kernel: {VGPRs, AGPRs, ScratchSize, Occupancy, LDS}} from the
+    compiler's kernel-resource-usage remarks."""
+    out: dict = {}
+    cur = None
+    for ln in stderr.splitlines():
+        if _REMARK not in ln or "remark:" not in ln:
+            continue
+        body = ln.split("remark:", 1)[1].replace(f"[{_REMARK}]", "").strip()
+        key, _, val = body.partition(":")
+        if key == "Function Name":
+            cur = out.setdefault(val.strip(), {})
+        elif cur is not None:
+            name = key.split("[")[0].strip()
+            try:
+                cur[name] = int(val.strip())
+            except ValueError:
+                pass
+    return out
+
+
+def _compile(src: str, obj: str) -> dict:
+    cmd = [HIPCC, *FLAGS, _REMARK, "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
-    # The host pass warns that it does not know the packed-fp32 feature.
-    noise = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+    # The host pass warns that it does not know the packed-fp32 feature;
+    # resource-usage remarks are collected, not echoed.
+    noise = [ln for ln in r.stderr.splitlines()
+             if "packed-fp32-ops" not in ln and _REMARK not in ln and ln.strip()
+             and not re.match(r"^\s*\d*\s*\|", ln)]  # the remarks' source excerpts
     if noise:
         sys.stderr.write("\n".join(noise) + "\n")
+    return _resources(r.stderr)
 
 
 def build(verbose: bool = False) -> str:
@@ -50,7 +83,14 @@ def build(verbose: bool = False) -> str:
     os.makedirs(objdir, exist_ok=True)
     objs = [os.path.join(objdir, s.replace(".hip", ".o")) for s in SOURCES]
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
-        list(ex.map(lambda a: _compile(*a), zip(SOURCES, objs)))
+        usage = list(ex.map(lambda a: _compile(*a), zip(SOURCES, objs)))
+    kernels = {k: v for u in usage for k, v in u.items()}
+    with open(os.path.join(objdir, "resource_usage.json"), "w") as f:
+        json.dump(kernels, f, indent=1, sort_keys=True)
+    spills = sorted(k for k, v in kernels.items() if v.get("ScratchSize", 0) > 0)
+    if spills:
+        raise RuntimeError("kernels spill registers to scratch (ScratchSize > 0): "
+                           + ", ".join(spills))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -828,10 +828,13 @@ __device__ __forceinline__ void bwd_walk(const uint16_t* list, int cnt, int lim,
 }
 
 // Waves per SIMD the backward asks for (more waves hide LDS and ballot
-// latencies): six up to four channels (<= 80 VGPRs, 12-16 KB of LDS), except
-// five at two channels (which would spill at 80), four up to 16 channels,
-// three at 32, all without spills.
-constexpr int bwd_min_waves(int ch) { return ch == 2 ? 5 : (ch <= 4 ? 6 : (ch <= 16 ? 4 : 3)); }
+// latencies): six at one and three channels (<= 80 VGPRs, 12-16 KB of LDS),
+// five at two and four channels (which would spill at 80), four up to 16
+// channels, three at 32; no instantiation spills (checked with
+// -Rpass-analysis=kernel-resource-usage: ScratchSize 0 for every one).
+constexpr int bwd_min_waves(int ch) {
+    return (ch == 2 || ch == 4) ? 5 : (ch <= 4 ? 6 : (ch <= 16 ? 4 : 3));
+}
 
 template <int CH>
 __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(

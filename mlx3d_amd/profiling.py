@@ -47,6 +47,13 @@ class StageTimer:
         s = self.samples.get(name, [])
         return sum(s) / len(s) if s else float("nan")
 
+    def median_ms(self, name: str) -> float:
+        s = sorted(self.samples.get(name, []))
+        if not s:
+            return float("nan")
+        m = len(s) // 2
+        return s[m] if len(s) % 2 else 0.5 * (s[m - 1] + s[m])
+
     def count(self, name: str, value: float):
         self.counters[name].append(float(value))
 

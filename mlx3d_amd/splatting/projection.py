@@ -14,7 +14,20 @@ import torch
 from .. import _lib
 from ..cameras import Camera
 
-__all__ = ["project_gaussians", "project_gaussians_ut"]
+__all__ = ["quat_scale_to_cov3d", "project_gaussians", "project_gaussians_ut"]
+
+
+def quat_scale_to_cov3d(quats: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """3D covariances R diag(s)^2 R^T, (N, 3, 3), from (N, 4) wxyz quaternions
+    (normalised here) and (N, 3) standard deviations (projection.py:17-21).
+    Differentiable torch ops on the tensors' device; the render path never
+    calls it (its kernels form the same covariance per Gaussian)."""
+    from ..transforms import quaternion_to_matrix
+
+    if quats.ndim != 2 or quats.shape[1] != 4 or scales.shape != (quats.shape[0], 3):
+        raise ValueError("quats must be (N, 4) and scales (N, 3).")
+    rs = quaternion_to_matrix(quats) * scales[:, None, :]  # columns scaled: R diag(s)
+    return rs @ rs.transpose(1, 2).contiguous()
 
 
 class _Project(torch.autograd.Function):

@@ -120,6 +120,21 @@ def _ids(t):
     return t.to(torch.int32).contiguous()
 
 
+def background_tensor(background, channels: int, dev):
+    """None (a zero background: the kernels read NULL) or a contiguous float32
+    (channels,) tensor; a scalar is broadcast to every channel.  The kernels
+    read one background value per channel, so any other shape is refused
+    (rasterize.py:428-429, 493-500)."""
+    if background is None:
+        return None
+    bg = torch.as_tensor(background, dtype=torch.float32, device=dev)
+    if bg.ndim == 0:
+        bg = bg.expand(channels)
+    if bg.shape != (channels,):
+        raise ValueError(f"background must have shape ({channels},).")
+    return bg.contiguous()
+
+
 def rasterize(means2d, conics, colors, opacities, sorted_ids, tile_ranges, width: int,
               height: int, tiles_x: int, tiles_y: int, background=None) -> dict:
     """Alpha-composite binned 2D Gaussians into an image (rasterize.py:406-446).
@@ -129,8 +144,9 @@ def rasterize(means2d, conics, colors, opacities, sorted_ids, tile_ranges, width
     """
     _check_grid(width, height, tiles_x, tiles_y)
     dev = means2d.device
-    # None reaches the kernels as NULL, a zero background
-    bg = None if background is None else _lib.f32c(torch.as_tensor(background, device=dev))
+    if colors.ndim != 2:
+        raise ValueError("colors must have shape (N, C).")
+    bg = background_tensor(background, int(colors.shape[1]), dev)
     image, final_T, alpha, n_contrib = _Rasterize.apply(
         _lib.f32c(means2d), _lib.f32c(conics), _lib.f32c(colors), _lib.f32c(opacities),
         _ids(sorted_ids), _ids(tile_ranges), bg, int(width), int(height))
@@ -154,15 +170,7 @@ def rasterize_features(means2d, conics, features, opacities, sorted_ids, tile_ra
         raise ValueError("features must contain at least one channel.")
     _check_grid(width, height, tiles_x, tiles_y)
     dev = means2d.device
-    if background is None or normalize:
-        bg = None  # NULL: a zero background
-    else:
-        bg = torch.as_tensor(background, dtype=torch.float32, device=dev)
-        if bg.ndim == 0:
-            bg = bg.expand(channels)
-        if bg.shape != (channels,):
-            raise ValueError(f"background must have shape ({channels},).")
-        bg = _lib.f32c(bg)
+    bg = None if normalize else background_tensor(background, channels, dev)
     feat, final_T, alpha, n_contrib = _Rasterize.apply(
         _lib.f32c(means2d), _lib.f32c(conics), _lib.f32c(features), _lib.f32c(opacities),
         _ids(sorted_ids), _ids(tile_ranges), bg, int(width), int(height))

@@ -21,7 +21,7 @@ import torch
 from .. import _lib
 from ..cameras import Camera
 from ..profiling import count, stage
-from .rasterize import raster_backward, raster_forward, t_cotangent
+from .rasterize import background_tensor, raster_backward, raster_forward, t_cotangent
 from .sh import num_sh_bases
 from .tiles import BinJob
 
@@ -93,7 +93,7 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
     count("duplicates", ids.shape[0])
     return dict(means2d=means2d, depths=depths, radii=radii, compensation=comp, conic_opac=co,
                 feats=feats, sorted_ids=ids, tile_ranges=ranges, image=image, final_T=final_T,
-                alpha=alpha, n_contrib=n_contrib, depth=depth_map)
+                alpha=alpha, n_contrib=n_contrib, depth=depth_map, job=job)
 
 
 class _RenderFn(torch.autograd.Function):
@@ -101,6 +101,7 @@ class _RenderFn(torch.autograd.Function):
     def forward(ctx, means, quats, scales, opacities, sh_a, sh_b, colors, background, cfg):
         r = _forward(cfg, means, quats, scales, opacities, sh_a, sh_b, colors, background)
         ctx.cfg = cfg
+        ctx.bin_job = r["job"]
         ctx.save_for_backward(means, quats, scales, opacities, sh_a, sh_b, r["feats"],
                               r["means2d"], r["conic_opac"], r["sorted_ids"], r["tile_ranges"],
                               r["final_T"], r["n_contrib"], background, r["radii"])
@@ -137,16 +138,24 @@ class _RenderFn(torch.autograd.Function):
             g_sh_b = torch.empty_like(sh_b) if cfg.sh_mode == "split" else None
         gs0, s0, gshr, sr = _sh_views(cfg, g_sh_a, g_sh_b)
         c = lambda t: None if t is None else _lib.f32c(t)  # noqa: E731
+        # The contiguous copies of the output cotangents (a stride-0 expand
+        # from .sum() is copied) must outlive the enqueued kernel: only their
+        # addresses cross the ABI, so they are bound to locals here.
+        gm2_in, gdep_in, gcomp_in = c(g_means2d), c(g_depths), c(g_comp)
         L = _lib.load()
         with stage("preprocess_bwd"):
             _lib.check(L.gsx_preprocess_bwd(
                 cfg.cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
                 _lib.ptr(opacities), _lib.ptr(feats if cfg.sh_mode else None), cfg.K, cfg.degree,
                 cfg.flags, cfg.blur, _lib.ptr(g_m2), _lib.ptr(g_con), _lib.ptr(g_op),
-                _lib.ptr(g_feat if cfg.sh_mode else None), _lib.ptr(c(g_means2d)),
-                _lib.ptr(c(g_depths)), _lib.ptr(c(g_comp)), _lib.ptr(g_means),
+                _lib.ptr(g_feat if cfg.sh_mode else None), _lib.ptr(gm2_in),
+                _lib.ptr(gdep_in), _lib.ptr(gcomp_in), _lib.ptr(g_means),
                 _lib.ptr(g_quats), _lib.ptr(g_scales), _lib.ptr(g_opac), _lib.ptr(gs0), s0, gshr,
                 sr, _lib.stream_handle(dev)), "gsx_preprocess_bwd")
+        # The binning's final device status was copied behind it in the
+        # forward; a failed device-side check raises here, before any
+        # optimizer sees these gradients.
+        ctx.bin_job.check()
         g_colors = None if cfg.sh_mode else g_feat
         return g_means, g_quats, g_scales, g_opac, g_sh_a, g_sh_b, g_colors, None, None
 
@@ -156,18 +165,6 @@ def _check_common(projection: str) -> int:
     if projection not in ("ewa", "ut"):
         raise ValueError("projection must be 'ewa' or 'ut'.")
     return _lib.PROJECT_UT if projection == "ut" else 0
-
-
-def _background(background, channels, dev):
-    if background is None:
-        return None  # the kernels read NULL as a zero background
-
-    bg = torch.as_tensor(background, dtype=torch.float32, device=dev)
-    if bg.ndim == 0:
-        bg = bg.expand(channels)
-    if bg.shape != (channels,):
-        raise ValueError(f"background must have shape ({channels},).")
-    return bg.contiguous()
 
 
 def _stats(screen_stats, n, dev):
@@ -203,7 +200,7 @@ def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=Non
                                None if sh_a is None else c(sh_a),
                                None if sh_b is None else c(sh_b),
                                None if colors is None else c(colors),
-                               _background(background, channels, dev), cfg)
+                               background_tensor(background, channels, dev), cfg)
     out = {"image": image, "alpha": alpha, "final_T": final_T, "n_contrib": n_contrib,
            "means2d": means2d, "depths": depths, "radii": radii, "compensation": comp,
            "sorted_ids": ids, "tile_ranges": ranges}

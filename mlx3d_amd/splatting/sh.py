@@ -51,9 +51,10 @@ class _EvalSH(torch.autograd.Function):
         dev = sh.device
         g_sh = torch.empty_like(sh)
         g_dirs = torch.empty((n, 3), dtype=torch.float32, device=dev) if ctx.needs_input_grad[1] else None
+        g_in = _lib.f32c(g_out)  # kept alive until the kernel has been enqueued
         L = _lib.load()
         _lib.check(L.gsx_eval_sh_bwd(n, K, C, ctx.degree, _lib.ptr(sh), _lib.ptr(dirs),
-                                     _lib.ptr(g_out.contiguous()), _lib.ptr(g_sh), _lib.ptr(g_dirs),
+                                     _lib.ptr(g_in), _lib.ptr(g_sh), _lib.ptr(g_dirs),
                                      _lib.stream_handle(dev)), "gsx_eval_sh_bwd")
         return (g_sh if ctx.needs_input_grad[0] else None), g_dirs, None
 

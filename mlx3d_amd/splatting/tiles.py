@@ -101,11 +101,13 @@ class BinJob:
     exactly that capacity and enqueues the rest (gsx_bin_tiles_async).
     ``ids`` and ``ranges`` are usable by kernels enqueued behind the job
     right away.  Without refine_tiles D is that count and no second host
-    sync is needed; the device-side error bits of the tile phase are then
-    reported by the next job's count readback on the same stream.  With
-    refine_tiles, or ``final=True``, the final status is copied behind the
-    job and ``check()`` (called by ``result()`` when D is unknown) waits for
-    it.
+    sync is needed.  Every job copies its final status words to pinned
+    memory behind the tile phase (no wait); ``check()`` waits for that copy
+    and raises on a device-side error bit of the tile phase.  ``result()``
+    calls it when D is unknown (refine_tiles); the render backward calls it
+    after enqueuing its kernels, so a failed binning raises before the
+    gradients reach an optimizer.  A job nobody checks has its error bits
+    reported by the next job's count readback on the same stream.
     """
 
     def __init__(self, counts, dkeys, rects, width: int, height: int, refine=None,
@@ -142,11 +144,8 @@ class BinJob:
             0 if co is None else co.shape[1], self.width, self.height, _lib.ptr(dws),
             dws.numel(), _lib.ptr(tws), tws.numel(), self.cap, _lib.ptr(self.ids),
             _lib.ptr(self.ranges), _lib.ptr(status), stream), "gsx_bin_tiles_async")
-        self.host = self.ready = None
-        self.num_dups = self.cap
-        if refine is not None or final:
-            self.host, self.ready = _pinned_status(status)
-            self.num_dups = None
+        self.host, self.ready = _pinned_status(status)
+        self.num_dups = None if (refine is not None or final) else self.cap
 
     def check(self) -> None:
         """With a final status copy: wait for the binning, raise GsxError if
@@ -163,7 +162,8 @@ class BinJob:
             "gsx_bin_tiles_async")
         if rc != _lib.GSX_OK:  # not reached: the capacity is the emitted count
             raise _lib.GsxError("gsx_bin_tiles_async: duplicates exceed the exact capacity")
-        self.num_dups = int(nd.value)
+        if self.num_dups is None:
+            self.num_dups = int(nd.value)
 
     def result(self):
         """(sorted_ids (D,), tile_ranges); waits for the binning only when D

@@ -288,7 +288,7 @@ def tile_mask(means2d, radii, width, height):
 
 # ------------------------------------------------------------ compositing
 def dense_composite_f64(means2d, conics, opac, feats, order, width, height, bg=None,
-                        mask=None, kernel_stop=True):
+                        mask=None, kernel_stop=True, straight_through=False):
     """Dense float64 compositing of reference.py:47-74.
 
     ``order`` is the global front-to-back order.  With ``mask`` (N, H, W)
@@ -296,7 +296,11 @@ def dense_composite_f64(means2d, conics, opac, feats, order, width, height, bg=N
     binned to).  ``kernel_stop`` applies the kernel's termination: the splat
     that would take T below 1e-4 is not composited and nothing after it is
     (rasterize.py:82-83); otherwise the reference.py rule (keep while the
-    transmittance in front is > 1e-4).
+    transmittance in front is > 1e-4).  ``straight_through`` gives the 0.99
+    alpha clamp the gradient rule of the reference's backward kernel
+    (rasterize.py:193: dL/dG = o dL/dalpha whether or not the clamp is
+    active); without it autograd gives the clamp zero gradient when active,
+    the rule of the reference's dense oracle.
     """
     xs = torch.arange(width, dtype=torch.float64) + 0.5
     ys = torch.arange(height, dtype=torch.float64) + 0.5
@@ -308,7 +312,12 @@ def dense_composite_f64(means2d, conics, opac, feats, order, width, height, bg=N
     dy = m[:, 1, None, None] - ys[None, :, None]
     a, b, c = co[:, 0, None, None], co[:, 1, None, None], co[:, 2, None, None]
     power = -0.5 * (a * dx * dx + c * dy * dy) - b * dx * dy
-    alpha = torch.clamp(o[:, None, None] * torch.exp(power), max=0.99)
+    raw = o[:, None, None] * torch.exp(power)
+    if straight_through:
+        # value min(raw, 0.99), derivative d raw everywhere
+        alpha = raw - torch.clamp(raw - 0.99, min=0.0).detach()
+    else:
+        alpha = torch.clamp(raw, max=0.99)
     alpha = torch.where(power > 0, torch.zeros_like(alpha), alpha)
     alpha = torch.where(alpha < 1.0 / 255.0, torch.zeros_like(alpha), alpha)
     if mask is not None:
@@ -360,7 +369,8 @@ def eval_sh_f64(degree: int, sh: torch.Tensor, dirs: torch.Tensor) -> torch.Tens
 
 
 def render_f64(cam: Camera, means, quats, scales, opac, colors=None, sh=None, degree=0,
-               bg=None, antialias=False, mask=None, order=None, kernel_stop=True):
+               bg=None, antialias=False, mask=None, order=None, kernel_stop=True,
+               straight_through=False):
     """Differentiable float64 render: matrix-form projection, SH colour with
     stop-gradient directions (render.py:73-80), dense restricted compositing."""
     p = project_matrix_f64(cam, means, quats, scales, antialias=antialias)
@@ -371,7 +381,8 @@ def render_f64(cam: Camera, means, quats, scales, opac, colors=None, sh=None, de
         d = d / torch.clamp(torch.linalg.norm(d, dim=-1, keepdim=True), min=1e-8)
         colors = torch.clamp(eval_sh_f64(degree, sh, d), min=0.0)
     img, T, _ = dense_composite_f64(p["means2d"], p["conics"], oe, colors, order, cam.width,
-                                    cam.height, bg=bg, mask=mask, kernel_stop=kernel_stop)
+                                    cam.height, bg=bg, mask=mask, kernel_stop=kernel_stop,
+                                    straight_through=straight_through)
     return img, T, p
 
 

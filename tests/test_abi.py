@@ -6,6 +6,7 @@ import os
 import re
 
 import numpy as np
+import pytest
 
 from mlx3d_amd import _lib
 
@@ -113,3 +114,19 @@ def test_bin_status_check_is_host_only():
                                  None, p(rg), p(st), None) == -1
     assert L.gsx_bin_tiles_async(10, None, None, None, None, 0, 64, 64, None, 0, None, 0,
                                  1 << 30, None, p(rg), p(st), None) == -4
+
+
+def test_no_kernel_spills_registers():
+    """build() records the compiler's per-kernel resource usage; no kernel
+    may use scratch memory (register spills)."""
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                        "mlx3d_amd", "_build", "resource_usage.json")
+    if not os.path.exists(path):
+        pytest.skip("libgsx.so was not built in this tree")
+    usage = json.load(open(path))
+    assert len(usage) > 50
+    spills = {k: v["ScratchSize"] for k, v in usage.items() if v.get("ScratchSize", 0)}
+    assert not spills, spills

@@ -464,3 +464,96 @@ def test_empty_and_culled_render():
     out = render_gaussians(cam, cu(z), cu(np.zeros((0, 4), np.float32)), cu(z),
                            cu(np.zeros(0, np.float32)), colors=cu(z))
     assert (host(out["alpha"]) == 0).all()
+
+
+@pytest.mark.parametrize("offset", [0.0, 0.3])
+def test_raster_active_clamp_closed_form(offset):
+    """One splat with o G > 0.99 at the centre pixel (the 0.99 clamp is
+    active there), loss = image[8, 8, 0]: the reference's backward passes the
+    gradient through the clamp (rasterize.py:193), so dL/dopacity = G c0,
+    dL/dc0 = 0.99 and dL/dmean_x = o c0 G (-a dx) in closed form."""
+    W = H = 16
+    sigma = 3.0
+    m2 = np.array([[8.5 + offset, 8.5]], np.float32)
+    con = np.array([[1.0 / sigma ** 2, 0.0, 1.0 / sigma ** 2]], np.float32)
+    op = np.array([1.0], np.float32)
+    col = np.array([[0.7, 0.2, 0.4]], np.float32)
+    ids = np.zeros(1, np.int32)
+    ranges = np.array([[0, 1]], np.int32)
+    t = [cu(a).requires_grad_(True) for a in (m2, con, col, op)]
+    out = rasterize(*t, cu(ids), cu(ranges), W, H, 1, 1)
+    out["image"][8, 8, 0].backward()
+    a = np.float64(con[0, 0])
+    dx = np.float64(m2[0, 0]) - 8.5
+    G = np.exp(-0.5 * a * dx * dx)
+    c0 = np.float64(col[0, 0])
+    assert op[0] * G > 0.99
+    say(f"clamp closed form offset={offset}: g_opac {float(t[3].grad[0]):.7f} vs {G * c0:.7f}")
+    np.testing.assert_allclose(host(out["image"])[8, 8, 0], 0.99 * c0, rtol=1e-6)
+    np.testing.assert_allclose(host(t[3].grad)[0], G * c0, rtol=1e-5)
+    np.testing.assert_allclose(host(t[2].grad)[0], [0.99, 0.0, 0.0], rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(host(t[0].grad)[0, 0], op[0] * c0 * G * (-a * dx), rtol=1e-4,
+                               atol=1e-7)
+    np.testing.assert_allclose(host(t[1].grad)[0], [-0.5 * G * dx * dx * op[0] * c0, 0, 0],
+                               rtol=1e-4, atol=1e-7)
+
+
+@pytest.mark.parametrize("antialias", [False, True])
+def test_render_active_clamp_gradients(antialias):
+    """Opacities up to 1 (the clamp active at many pixels): the full render
+    backward against the oracle, whose clamp branch the CPU suite pins by a
+    closed form and a straight-through float64 autograd check."""
+    cam, means, quats, scales, opac, colors = random_scene(9, n=4000, width=160, height=96)
+    rng = np.random.default_rng(90)
+    opac = rng.uniform(0.6, 1.0, opac.shape).astype(np.float32)
+    opac[::2] = 1.0
+    scales = (scales * 3.0).astype(np.float32)
+    flags = O.ANTIALIAS if antialias else 0
+    t = [cu(a).requires_grad_(True) for a in (means, quats, scales, opac, colors)]
+    out = render_gaussians(cam, t[0], t[1], t[2], t[3], colors=t[4], antialias=antialias)
+    pre, feats, ids, ranges, r = oracle_forward(cam, means, quats, scales, opac, colors=colors,
+                                                flags=flags)
+    np.testing.assert_array_equal(host(out["n_contrib"]), r["n_contrib"])
+    assert_bits(host(out["image"]), r["image"], "image")
+    g_img = rng.standard_normal(r["image"].shape).astype(np.float32)
+    g_a = rng.standard_normal(r["final_T"].shape).astype(np.float32)
+    ((out["image"] * cu(g_img)).sum() + (out["alpha"] * cu(g_a)).sum()).backward()
+    g = oracle_backward(cam, means, quats, scales, opac, pre, feats, ids, ranges, r, g_img, g_a,
+                        flags=flags)
+    for name, a, key in [("means", t[0], "means"), ("quats", t[1], "quats"),
+                         ("scales", t[2], "scales"), ("opacities", t[3], "opacities"),
+                         ("colors", t[4], "features")]:
+        e = rel_err(host(a.grad), g[key])
+        say(f"render clamp aa={antialias} grad {name}: rel {e:.2e}")
+        assert e < 1e-3
+
+
+def test_render_direct_output_cotangents():
+    """Cotangents on means2d, depths and compensation arrive as stride-0
+    expands (from .sum()), which the backward copies before the preprocess
+    VJP reads them; they must reach the kernel intact."""
+    cam, means, quats, scales, opac, colors = random_scene(11, n=3000, width=128, height=96)
+    opac = np.minimum(opac, 0.95).astype(np.float32)
+    flags = O.ANTIALIAS
+    t = [cu(a).requires_grad_(True) for a in (means, quats, scales, opac, colors)]
+    out = render_gaussians(cam, t[0], t[1], t[2], t[3], colors=t[4], antialias=True)
+    pre, feats, ids, ranges, r = oracle_forward(cam, means, quats, scales, opac, colors=colors,
+                                                flags=flags)
+    rng = np.random.default_rng(11)
+    g_img = rng.standard_normal(r["image"].shape).astype(np.float32)
+    loss = ((out["image"] * cu(g_img)).sum() + out["means2d"].sum() + 2.0 * out["depths"].sum()
+            + 3.0 * out["compensation"].sum())
+    loss.backward()
+    oc = oracle_camera(cam)
+    gr = O.raster_bwd(pre["means2d"], pre["conics"], pre["opac_eff"], feats, ids, ranges,
+                      cam.width, cam.height, r["final_T"], r["n_contrib"], g_img)
+    n = means.shape[0]
+    g = O.preprocess_bwd(oc, means, quats, scales, opac, None, 0, 0, flags,
+                         gr["means2d"] + np.ones((n, 2), np.float32), gr["conics"],
+                         gr["opacities"], None, g_depths=np.full(n, 2.0, np.float32),
+                         g_comp=np.full(n, 3.0, np.float32))
+    for name, a, key in [("means", t[0], "means"), ("quats", t[1], "quats"),
+                         ("scales", t[2], "scales"), ("opacities", t[3], "opacities")]:
+        e = rel_err(host(a.grad), g[key])
+        say(f"direct cotangents grad {name}: rel {e:.2e}")
+        assert e < 1e-3

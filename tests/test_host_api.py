@@ -80,3 +80,39 @@ def test_model_from_points_scales_and_layout():
 
 def test_render_function_is_a_renderer():
     assert isinstance(render_gaussians, Renderer)
+
+
+# The public names of the reference's mlx3d.splatting (splatting/__init__.py:10-30).
+_REFERENCE_SPLATTING_ALL = {
+    "GaussianModel", "GaussianTrainer", "TILE_SIZE", "TrainerConfig", "bin_gaussians",
+    "eval_sh", "num_sh_bases", "project_gaussians", "project_gaussians_ut",
+    "quat_scale_to_cov3d", "rasterize", "rasterize_depth", "rasterize_features",
+    "render_gaussian_depth", "render_gaussian_features", "render_gaussians",
+    "render_gaussians_reference", "rgb_to_sh", "sh_to_rgb",
+}
+
+
+def test_splatting_exports_cover_the_reference():
+    import mlx3d_amd.splatting as S
+
+    assert _REFERENCE_SPLATTING_ALL <= set(S.__all__)
+    for name in _REFERENCE_SPLATTING_ALL:
+        assert getattr(S, name) is not None
+
+
+def test_quat_scale_to_cov3d_closed_form():
+    from mlx3d_amd.splatting import quat_scale_to_cov3d
+
+    # 90 degrees about z (unnormalised quaternion): diag(1, 4, 9) -> diag(4, 1, 9)
+    q = torch.tensor([[2.0, 0.0, 0.0, 2.0]])
+    s = torch.tensor([[1.0, 2.0, 3.0]])
+    cov = quat_scale_to_cov3d(q, s)
+    np.testing.assert_allclose(cov[0].numpy(), np.diag([4.0, 1.0, 9.0]), atol=1e-5)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(64, 4, generator=g)
+    s = torch.rand(64, 3, generator=g) + 0.1
+    cov = quat_scale_to_cov3d(q, s).double()
+    # symmetric positive definite with determinant prod(s^2)
+    np.testing.assert_allclose(cov.numpy(), cov.transpose(1, 2).numpy(), atol=1e-6)
+    np.testing.assert_allclose(torch.linalg.det(cov).numpy(),
+                               (s.double() ** 2).prod(1).numpy(), rtol=1e-4)
