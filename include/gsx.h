@@ -12,7 +12,8 @@
  *  - Every pointer is device memory (hipMalloc/torch CUDA tensors) unless
  *    documented otherwise, contiguous, float32 or int32/uint32 as named.
  *  - The caller owns all buffers; no entry point allocates device memory.
- *    Scratch space comes in through an explicit workspace argument.
+ *    Scratch space comes in through an explicit workspace argument (the one
+ *    exception, gsx_l1_fwd_noalloc, uses a fixed file-scope device array).
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
  *    Only gsx_bin_sort synchronises the stream (one 8-byte readback of the
  *    duplicate count, as the reference does at tiles.py:68);
@@ -380,6 +381,21 @@ int64_t gsx_l1_workspace_bytes(int64_t n);
 int gsx_l1_fwd(int64_t n, const float* pred, const float* target,
                void* workspace, int64_t workspace_bytes, float* out,
                void* stream);
+
+/* gsx_l1_fwd without a workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The partial sums go
+ * to a file-scope device array (512 KiB per GPU, held until the process
+ * ends), so n is at most gsx_l1_noalloc_max_elements() (2^28); larger n
+ * returns GSX_ERR_TOO_LARGE.  The call allocates nothing: the array's
+ * address is looked up once per device (GSX_ERR_HIP if that fails).  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, different host threads) race and must be ordered by
+ * the caller.  Same kernels and summation order as gsx_l1_fwd, so the
+ * results are bit-identical. */
+int64_t gsx_l1_noalloc_max_elements(void);
+int gsx_l1_fwd_noalloc(int64_t n, const float* pred, const float* target, float* out,
+                       void* stream);
 
 /* Its gradient: grad_pred = sign(pred - target) grad_out[0] / n (sign(0) =
  * 0), grad_out (1 float) on the device. */

@@ -117,6 +117,8 @@ SIGNATURES = {
                                            _P]),
     "gsx_l1_workspace_bytes": (_I64, [_I64]),
     "gsx_l1_fwd": (ctypes.c_int, [_I64, _P, _P, _P, _I64, _P, _P]),
+    "gsx_l1_noalloc_max_elements": (_I64, []),
+    "gsx_l1_fwd_noalloc": (ctypes.c_int, [_I64, _P, _P, _P, _P]),
     "gsx_l1_bwd": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P]),
     "gsx_adam_step": (ctypes.c_int, [_I32, ctypes.c_void_p, _F, _F, _F, _P]),
     "gsx_accum_screen_grads": (ctypes.c_int, [_I64, _P, _P, _I32, _I32, _P, _P, _P]),

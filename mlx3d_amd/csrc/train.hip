@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "gsx.h"
 #include "gsx_device.h"
@@ -448,6 +449,55 @@ __global__ __launch_bounds__(kL1Threads) void k_l1_bwd(int64_t n, const float* _
 
 inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
+// Scratch of gsx_l1_fwd_noalloc: the per-workgroup partial sums of at most
+// kL1NoAllocMaxN elements, in a file-scope device array instead of a
+// caller workspace (512 KiB, held on every GPU the library runs on until the
+// process ends).  Host code never hands the array's name to a kernel: the
+// name is a host-side stand-in, so the kernels get the address that
+// hipGetSymbolAddress reports for the current device.
+constexpr int64_t kL1NoAllocMaxN = int64_t(1) << 28;
+constexpr int64_t kL1NoAllocMaxBlocks = kL1NoAllocMaxN / kL1Block;
+static __device__ __align__(256) float scratch[2 * kL1NoAllocMaxBlocks];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices];  // per device; filled once, under the mutex
+
+// Address of `scratch` on `dev`, looked up once per device with that device
+// current; nullptr if the lookup fails.
+float* scratch_on(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+    return g_scratch_ptr[dev];
+}
+
+// The L1 forward on given partials storage (the workspace or the scratch).
+int l1_fwd_into(int64_t n, const float* pred, const float* target, float* partials, float* out,
+                hipStream_t st) {
+    const int64_t nblk = (n + kL1Block - 1) / kL1Block;
+    const bool vec = (((uintptr_t)pred | (uintptr_t)target) & 15u) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_l1_partial<true>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
+                           pred, target, partials);
+    else
+        hipLaunchKernelGGL(k_l1_partial<false>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
+                           pred, target, partials);
+    GSX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, (const float*)partials, nblk,
+                       1.0 / (double)n, out);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -568,20 +618,29 @@ int gsx_l1_fwd(int64_t n, const float* pred, const float* target, void* workspac
     if (workspace_bytes < gsx_l1_workspace_bytes(n)) return GSX_ERR_WORKSPACE;
     const int64_t nblk = (n + kL1Block - 1) / kL1Block;
     if (nblk > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
+    return l1_fwd_into(n, pred, target, (float*)workspace, out, (hipStream_t)stream);
+}
+
+int64_t gsx_l1_noalloc_max_elements(void) { return kL1NoAllocMaxN; }
+
+int gsx_l1_fwd_noalloc(int64_t n, const float* pred, const float* target, float* out,
+                       void* stream) {
+    if (n <= 0 || !pred || !target || !out) return GSX_ERR_INVALID;
+    if (n > kL1NoAllocMaxN) return GSX_ERR_TOO_LARGE;
     hipStream_t st = (hipStream_t)stream;
-    float* partials = (float*)workspace;
-    const bool vec = (((uintptr_t)pred | (uintptr_t)target) & 15u) == 0;
-    if (vec)
-        hipLaunchKernelGGL(k_l1_partial<true>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
-                           pred, target, partials);
-    else
-        hipLaunchKernelGGL(k_l1_partial<false>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
-                           pred, target, partials);
-    GSX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, (const float*)partials, nblk,
-                       1.0 / (double)n, out);
-    GSX_LAUNCH_CHECK();
-    return GSX_OK;
+    int dev = -1;
+    if (st) {
+        hipDevice_t d;
+        if (hipStreamGetDevice(st, &d) != hipSuccess) return GSX_ERR_HIP;
+        dev = (int)d;
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return GSX_ERR_HIP;
+    }
+    float* partials = scratch_on(dev);
+    if (!partials) return GSX_ERR_HIP;
+    // every workgroup writes both of its partial words, and the reduction
+    // reads only this call's nblk of them: nothing needs clearing first
+    return l1_fwd_into(n, pred, target, partials, out, st);
 }
 
 int gsx_l1_bwd(int64_t n, const float* pred, const float* target, const float* grad_out,

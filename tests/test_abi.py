@@ -71,6 +71,15 @@ def test_invalid_arguments_rejected_before_launch():
                              None) == -1
     assert L.gsx_eval_sh_fwd(-1, 16, 3, 3, None, None, None, None) == -1
     assert L.gsx_eval_sh_fwd(10, 4, 3, 3, None, None, None, None) == -1  # K < (deg+1)^2
+    # the no-allocation L1 refuses sizes beyond its fixed scratch on the host
+    # (the pointers are never dereferenced)
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    limit = L.gsx_l1_noalloc_max_elements()
+    assert limit == 1 << 28
+    assert L.gsx_l1_fwd_noalloc(limit + 1, p, p, p, None) == -4
+    assert L.gsx_l1_fwd_noalloc(0, p, p, p, None) == -1
+    assert L.gsx_l1_fwd_noalloc(10, None, p, p, None) == -1
 
 
 def test_bin_status_check_is_host_only():
