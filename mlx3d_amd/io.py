@@ -1,13 +1,22 @@
-"""PLY reading and writing (``src/mlx3d/io/ply_io.py``) for Gaussian
-checkpoints and point clouds.
+"""PLY files: Gaussian checkpoints, point clouds and triangle meshes.
 
-``load_ply`` accepts ``ascii`` and ``binary_little_endian`` files with
-scalar vertex properties of any PLY type and one list property per face
-element (polygons are fan-triangulated); ``save_ply`` writes float32
-positions / normals / extra properties, uchar colours and int32 triangle
-lists, binary or ascii.  Values come back as CPU torch tensors; Gaussian
-checkpoints go to the GPU through ``GaussianModel.load_ply``, which moves the
-whole vertex table in one host-to-device copy.
+The interface is the reference's (``src/mlx3d/io/ply_io.py:37-271``):
+``load_ply(path) -> PlyData`` and ``save_ply(path, verts, faces=None,
+normals=None, colors=None, extra=None, binary=True)``, with the same
+observable conventions -- uchar colours scaled to [0, 1] on load (values
+above 1 mean a 0-255 range), an ``alpha`` property consumed with the colours,
+every other vertex property returned in ``extra``, polygons fan-triangulated.
+
+The implementation is a small schema model of the PLY header: each element
+becomes a numpy record type, so a binary element without list properties is
+one zero-copy ``frombuffer`` view, a triangle-only face list is a second
+record view (count + three indices), and only polygons of mixed size take a
+per-polygon walk.  ASCII bodies are read as one token stream.  Writing goes
+the other way: the columns are gathered into one record array and written
+with a single ``tobytes``; ASCII floats use 9 significant digits, enough to
+round-trip every float32 exactly.  Values come back as CPU torch tensors;
+``GaussianModel.load_ply`` moves a checkpoint's whole vertex table to the GPU
+in one copy via :func:`read_ply_vertices`.
 """
 
 from __future__ import annotations
@@ -20,19 +29,23 @@ import torch
 
 __all__ = ["PlyData", "load_ply", "read_ply_vertices", "save_ply"]
 
-# ply_io.py:17-34
-_PLY_TO_NP = {
-    "char": "i1", "int8": "i1", "uchar": "u1", "uint8": "u1",
-    "short": "i2", "int16": "i2", "ushort": "u2", "uint16": "u2",
-    "int": "i4", "int32": "i4", "uint": "u4", "uint32": "u4",
-    "float": "f4", "float32": "f4", "double": "f8", "float64": "f8",
-}
+# PLY scalar type names (both spellings of the format) -> numpy type codes
+_TYPES = {}
+for _codes, _names in (("i1", ("char", "int8")), ("u1", ("uchar", "uint8")),
+                       ("i2", ("short", "int16")), ("u2", ("ushort", "uint16")),
+                       ("i4", ("int", "int32")), ("u4", ("uint", "uint32")),
+                       ("f4", ("float", "float32")), ("f8", ("double", "float64"))):
+    for _n in _names:
+        _TYPES[_n] = np.dtype("<" + _codes)
+
+_HEADER_END = b"end_header"
+_ENCODINGS = ("ascii", "binary_little_endian")
 
 
 @dataclass
 class PlyData:
-    """Result of :func:`load_ply` (ply_io.py:37-52): ``verts`` (V, 3),
-    ``faces`` (F, 3) or None, ``normals`` / ``colors`` (V, 3) or None
+    """What :func:`load_ply` returns (ply_io.py:37-52): ``verts`` (V, 3),
+    ``faces`` (F, 3) int32 or None, ``normals`` / ``colors`` (V, 3) or None
     (colours in [0, 1]), ``extra``: every other vertex property, (V,) each."""
 
     verts: torch.Tensor
@@ -42,203 +55,249 @@ class PlyData:
     extra: dict[str, torch.Tensor] = field(default_factory=dict)
 
 
-def _parse_header(data: bytes, path: str):
-    end = data.find(b"end_header\n")
-    if end < 0:
-        raise ValueError(f"{path!r} is not a valid PLY file (no end_header).")
-    lines = data[:end].decode("ascii", errors="replace").splitlines()
+@dataclass(frozen=True)
+class _Prop:
+    name: str
+    dtype: np.dtype
+    length_dtype: np.dtype | None = None  # set for list properties
+
+
+@dataclass
+class _Element:
+    name: str
+    size: int
+    props: list[_Prop] = field(default_factory=list)
+
+    @property
+    def fixed(self) -> bool:
+        return all(p.length_dtype is None for p in self.props)
+
+    def record(self) -> np.dtype:
+        return np.dtype([(p.name, p.dtype) for p in self.props])
+
+
+def _schema(buf, path: str):
+    """(encoding, elements, body offset) of a PLY header."""
+    stop = buf.find(_HEADER_END)
+    if stop < 0:
+        raise ValueError(f"{path!r}: no 'end_header' line, so not a readable PLY file.")
+    body = buf.find(b"\n", stop)
+    body = len(buf) if body < 0 else body + 1
+    lines = bytes(buf[:stop]).decode("ascii", errors="replace").splitlines()
     if not lines or lines[0].strip() != "ply":
-        raise ValueError(f"{path!r} is not a PLY file.")
-    fmt = None
-    elements: list[tuple[str, int, list]] = []
-    for line in lines[1:]:
-        parts = line.strip().split()
-        if not parts or parts[0] in ("comment", "obj_info"):
+        raise ValueError(f"{path!r} is not a PLY file (missing the 'ply' magic line).")
+    encoding = None
+    elements: list[_Element] = []
+    for raw in lines[1:]:
+        tok = raw.split()
+        if not tok or tok[0] in ("comment", "obj_info"):
             continue
-        if parts[0] == "format":
-            fmt = parts[1]
-        elif parts[0] == "element":
-            elements.append((parts[1], int(parts[2]), []))
-        elif parts[0] == "property":
+        kind = tok[0]
+        if kind == "format":
+            encoding = tok[1] if len(tok) > 1 else None
+        elif kind == "element":
+            elements.append(_Element(tok[1], int(tok[2])))
+        elif kind == "property":
             if not elements:
-                raise ValueError("property before element in PLY header.")
-            if parts[1] == "list":
-                elements[-1][2].append(("__list__", parts[4], _PLY_TO_NP[parts[2]],
-                                        _PLY_TO_NP[parts[3]]))
-            else:
-                elements[-1][2].append((parts[2], _PLY_TO_NP[parts[1]]))
-    if fmt not in ("ascii", "binary_little_endian"):
-        raise ValueError(f"Unsupported PLY format {fmt!r}.")
-    return fmt, elements, end + len(b"end_header\n")
+                raise ValueError(f"{path!r}: a property line comes before any element line.")
+            try:
+                if tok[1] == "list":
+                    prop = _Prop(tok[4], _TYPES[tok[3]], _TYPES[tok[2]])
+                else:
+                    prop = _Prop(tok[2], _TYPES[tok[1]])
+            except (KeyError, IndexError) as e:
+                raise ValueError(f"{path!r}: cannot read the property line {raw!r}.") from e
+            elements[-1].props.append(prop)
+    if encoding not in _ENCODINGS:
+        raise ValueError(f"Unsupported PLY format {encoding!r} in {path!r} "
+                         f"(supported: {', '.join(_ENCODINGS)}).")
+    return encoding, elements, body
 
 
-def _read_elements(data: bytes, fmt: str, elements, body_off: int):
-    """{element: {property: array}}; list elements give {'__faces__': (F, 3)}."""
-    parsed: dict[str, dict[str, np.ndarray]] = {}
-    off = body_off
-    rows = data[body_off:].decode("ascii", errors="replace").splitlines() \
-        if fmt == "ascii" else None
-    row = 0
-    for name, count, props in elements:
-        lists = [p for p in props if p[0] == "__list__"]
-        if not lists:
-            dt = np.dtype([(p[0], "<" + p[1]) for p in props])
-            if fmt == "ascii":
-                vals = np.array([[float(x) for x in rows[row + i].split()[:len(props)]]
-                                 for i in range(count)], dtype=np.float64)
-                row += count
-                arr = np.empty(count, dt)
-                for j, p in enumerate(props):
-                    arr[p[0]] = vals[:, j] if count else vals.reshape(0)
+def _fan(polygons) -> np.ndarray:
+    """Fan triangulation (p0, p_k, p_k+1), polygon by polygon, as int32 (T, 3)."""
+    tris = [(p[0], p[k], p[k + 1]) for p in polygons for k in range(1, len(p) - 1)]
+    return np.asarray(tris, dtype=np.int32).reshape(-1, 3)
+
+
+def _binary_list_element(buf, off: int, el: _Element):
+    """(triangles, end offset) of a binary element with one list property."""
+    if len(el.props) != 1:
+        raise ValueError(f"element {el.name!r}: only a single list property is supported")
+    prop = el.props[0]
+    if el.size == 0:
+        return np.zeros((0, 3), np.int32), off
+    first = int(np.frombuffer(buf, prop.length_dtype, 1, off)[0])
+    rec = np.dtype([("n", prop.length_dtype), ("i", prop.dtype, (first,))])
+    if off + rec.itemsize * el.size <= len(buf):
+        view = np.frombuffer(buf, rec, el.size, off)
+        if (view["n"] == first).all():  # every polygon has the first one's size
+            idx = view["i"].reshape(el.size, first).astype(np.int64)
+            if first == 3:
+                return idx.astype(np.int32), off + rec.itemsize * el.size
+            return _fan(idx.tolist()), off + rec.itemsize * el.size
+    polys = []
+    for _ in range(el.size):  # mixed polygon sizes: walk record by record
+        k = int(np.frombuffer(buf, prop.length_dtype, 1, off)[0])
+        off += prop.length_dtype.itemsize
+        polys.append(np.frombuffer(buf, prop.dtype, k, off).tolist())
+        off += prop.dtype.itemsize * k
+    return _fan(polys), off
+
+
+def _parse_body(buf, encoding: str, elements, off: int) -> dict:
+    """{element name: {property: (count,) array}}; an element with a list
+    property gives {"faces": (T, 3) int32} instead."""
+    out: dict = {}
+    tokens = bytes(buf[off:]).split() if encoding == "ascii" else None
+    pos = 0
+    for el in elements:
+        if el.fixed:
+            if tokens is not None:
+                width = len(el.props)
+                flat = np.asarray(tokens[pos:pos + width * el.size], dtype=np.float64)
+                pos += width * el.size
+                table = flat.reshape(el.size, width)
+                out[el.name] = {p.name: table[:, j].astype(p.dtype) for j, p in enumerate(el.props)}
             else:
-                arr = np.frombuffer(data, dtype=dt, count=count, offset=off)
-                off += dt.itemsize * count
-            parsed[name] = {p[0]: arr[p[0]] for p in props}
+                rec = el.record()
+                arr = np.frombuffer(buf, rec, el.size, off)
+                off += rec.itemsize * el.size
+                out[el.name] = {p.name: arr[p.name] for p in el.props}
             continue
-        # one list property (vertex_indices): fan-triangulate polygons
-        polys = []
-        if fmt == "ascii":
-            for i in range(count):
-                vals = rows[row + i].split()
-                n = int(vals[0])
-                polys.append([int(x) for x in vals[1:1 + n]])
-            row += count
+        if tokens is not None:
+            polys = []
+            for _ in range(el.size):
+                k = int(tokens[pos])
+                polys.append([int(t) for t in tokens[pos + 1:pos + 1 + k]])
+                pos += 1 + k
+            tris = _fan(polys)
         else:
-            lp = lists[0]
-            cdt, idt = np.dtype("<" + lp[2]), np.dtype("<" + lp[3])
-            for _ in range(count):
-                n = int(np.frombuffer(data, dtype=cdt, count=1, offset=off)[0])
-                off += cdt.itemsize
-                polys.append(np.frombuffer(data, dtype=idt, count=n, offset=off).tolist())
-                off += idt.itemsize * n
-        tris = [[p[0], p[i], p[i + 1]] for p in polys for i in range(1, len(p) - 1)]
-        parsed[name] = {"__faces__": np.asarray(tris, dtype=np.int32).reshape(-1, 3)}
-    return parsed
+            tris, off = _binary_list_element(buf, off, el)
+        out[el.name] = {"faces": tris}
+    return out
 
 
-def _read(path: str):
-    # a writable buffer: arrays viewing it can back torch tensors directly
-    data = bytearray(os.path.getsize(path))
+def _slurp(path: str):
+    """The file's bytes in a writable buffer (arrays viewing it can back
+    torch tensors without a copy)."""
+    buf = bytearray(os.path.getsize(path))
     with open(path, "rb") as f:
-        f.readinto(data)
-    fmt, elements, body = _parse_header(data, path)
-    return data, fmt, elements, body
+        f.readinto(buf)
+    return buf
 
 
 def load_ply(path: str) -> PlyData:
-    """Load a PLY file (ply_io.py:56-182)."""
-    data, fmt, elements, body = _read(path)
-    parsed = _read_elements(data, fmt, elements, body)
-    if "vertex" not in parsed:
-        raise ValueError(f"No vertex element in {path!r}.")
-    vp = parsed["vertex"]
-    for axis in ("x", "y", "z"):
-        if axis not in vp:
-            raise ValueError(f"Vertex element missing {axis!r} property.")
-    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))  # noqa: E731
-    verts = np.stack([vp["x"], vp["y"], vp["z"]], axis=-1)
-    used = {"x", "y", "z"}
-    normals = None
-    if all(k in vp for k in ("nx", "ny", "nz")):
-        normals = t(np.stack([vp["nx"], vp["ny"], vp["nz"]], axis=-1))
-        used |= {"nx", "ny", "nz"}
-    colors = None
-    if all(k in vp for k in ("red", "green", "blue")):
-        rgb = np.stack([vp["red"], vp["green"], vp["blue"]], axis=-1).astype(np.float32)
-        if rgb.size and rgb.max() > 1.0:
-            rgb = rgb / 255.0
-        colors = t(rgb)
-        used |= {"red", "green", "blue", "alpha"}
-    extra = {k: t(v) for k, v in vp.items() if k not in used}
+    """Read an ascii or binary_little_endian PLY file (ply_io.py:56-182)."""
+    buf = _slurp(path)
+    encoding, elements, body = _schema(buf, path)
+    parsed = _parse_body(buf, encoding, elements, body)
+    vertex = parsed.get("vertex")
+    if vertex is None:
+        raise ValueError(f"{path!r} has no vertex element.")
+    missing = [a for a in "xyz" if a not in vertex]
+    if missing:
+        raise ValueError(f"{path!r}: the vertex element lacks the {', '.join(missing)} "
+                         "coordinate(s).")
+
+    def f32(cols):
+        return torch.from_numpy(np.stack([np.asarray(vertex[c], np.float32) for c in cols], -1))
+
+    taken = {"x", "y", "z"}
+    normals = colors = None
+    if {"nx", "ny", "nz"} <= vertex.keys():
+        normals = f32(("nx", "ny", "nz"))
+        taken |= {"nx", "ny", "nz"}
+    if {"red", "green", "blue"} <= vertex.keys():
+        colors = f32(("red", "green", "blue"))
+        if colors.numel() and float(colors.max()) > 1.0:  # stored as 0..255
+            colors = colors / 255.0
+        taken |= {"red", "green", "blue", "alpha"}
+    extra = {k: torch.from_numpy(np.ascontiguousarray(v, np.float32))
+             for k, v in vertex.items() if k not in taken}
     faces = None
-    if "face" in parsed and parsed["face"]["__faces__"].size > 0:
-        faces = torch.from_numpy(parsed["face"]["__faces__"])
-    return PlyData(verts=t(verts), faces=faces, normals=normals, colors=colors, extra=extra)
+    face = parsed.get("face")
+    if face is not None and face["faces"].size:
+        faces = torch.from_numpy(face["faces"])
+    return PlyData(verts=f32(("x", "y", "z")), faces=faces, normals=normals, colors=colors,
+                   extra=extra)
 
 
 def read_ply_vertices(path: str) -> tuple[list[str], np.ndarray]:
-    """(property names, (V, P) float32 table) for a binary little-endian
-    file whose vertex properties are all float32 (the 3DGS checkpoint case):
-    a zero-copy view of the file's bytes, in file order."""
-    data, fmt, elements, body = _read(path)
-    off = body
-    for name, count, props in elements:
-        if name == "vertex":
-            if fmt != "binary_little_endian" or any(p[0] == "__list__" or p[1] != "f4"
-                                                    for p in props):
-                raise ValueError("not an all-float32 binary vertex table")
-            arr = np.frombuffer(data, dtype="<f4", count=count * len(props), offset=off)
-            return [p[0] for p in props], arr.reshape(count, len(props))
-        if any(p[0] == "__list__" for p in props):
-            raise ValueError("list element before the vertex element")
-        off += np.dtype([(p[0], "<" + p[1]) for p in props]).itemsize * count
-    raise ValueError(f"No vertex element in {path!r}.")
+    """(property names, (V, P) float32 table) of a binary little-endian file
+    whose vertex properties are all float32 (a 3DGS checkpoint): a zero-copy
+    view of the file's bytes, columns in file order.  Raises ValueError for
+    any other file (``GaussianModel.load_ply`` then reads it generically)."""
+    buf = _slurp(path)
+    encoding, elements, off = _schema(buf, path)
+    for el in elements:
+        if el.name == "vertex":
+            if encoding != "binary_little_endian" or not el.fixed or any(
+                    p.dtype != np.dtype("<f4") for p in el.props):
+                raise ValueError("the vertex element is not an all-float32 binary table")
+            table = np.frombuffer(buf, np.dtype("<f4"), el.size * len(el.props), off)
+            return [p.name for p in el.props], table.reshape(el.size, len(el.props))
+        if not el.fixed:
+            raise ValueError("a list element precedes the vertex element")
+        off += el.record().itemsize * el.size
+    raise ValueError(f"{path!r} has no vertex element.")
 
 
-def _np32(a, shape=None):
-    a = a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
-    a = np.ascontiguousarray(a, dtype=np.float32)
+def _host(a, dtype, shape=None) -> np.ndarray:
+    if isinstance(a, torch.Tensor):
+        a = a.detach().cpu().numpy()
+    a = np.ascontiguousarray(a, dtype=dtype)
     return a.reshape(shape) if shape is not None else a
 
 
 def save_ply(path: str, verts, faces=None, normals=None, colors=None, extra=None,
              binary: bool = True) -> None:
-    """Save points / a triangle mesh (ply_io.py:185-271).  ``colors`` in
-    [0, 1] are stored as uchar; ``extra`` properties as float32 in
-    insertion order."""
-    v = _np32(verts)
-    n = _np32(normals) if normals is not None else None
-    c = (np.clip(_np32(colors) * 255.0, 0, 255).astype(np.uint8)
-         if colors is not None else None)
-    ex = {k: _np32(a, (len(v),)) for k, a in (extra or {}).items()}
+    """Write points or a triangle mesh (ply_io.py:185-271): float32 x y z,
+    optional float32 normals, colours in [0, 1] stored as uchar red green
+    blue, ``extra`` properties as float32 in insertion order, faces as
+    ``list uchar int vertex_indices`` triangles."""
+    v = _host(verts, np.float32, (-1, 3))
+    count = v.shape[0]
+    columns: list[tuple[str, np.dtype, np.ndarray]] = [
+        (a, np.dtype("<f4"), v[:, j]) for j, a in enumerate("xyz")]
+    if normals is not None:
+        nrm = _host(normals, np.float32, (count, 3))
+        columns += [(a, np.dtype("<f4"), nrm[:, j]) for j, a in enumerate(("nx", "ny", "nz"))]
+    if colors is not None:
+        rgb = np.clip(_host(colors, np.float32, (count, 3)) * 255.0, 0, 255).astype(np.uint8)
+        columns += [(a, np.dtype("u1"), rgb[:, j]) for j, a in enumerate(("red", "green", "blue"))]
+    for name, vals in (extra or {}).items():
+        columns.append((name, np.dtype("<f4"), _host(vals, np.float32, (count,))))
+    tris = None if faces is None else _host(faces, np.int64, (-1, 3))
+
+    type_name = {np.dtype("<f4"): "float", np.dtype("u1"): "uchar"}
+    lines = ["ply", f"format {'binary_little_endian' if binary else 'ascii'} 1.0",
+             f"element vertex {count}"]
+    lines += [f"property {type_name[dt]} {name}" for name, dt, _ in columns]
+    if tris is not None:
+        lines += [f"element face {tris.shape[0]}", "property list uchar int vertex_indices"]
+    lines.append("end_header")
     os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
-    fmt = "binary_little_endian" if binary else "ascii"
-    header = ["ply", f"format {fmt} 1.0", f"element vertex {len(v)}"]
-    header += [f"property float {a}" for a in ("x", "y", "z")]
-    if n is not None:
-        header += [f"property float n{a}" for a in ("x", "y", "z")]
-    if c is not None:
-        header += [f"property uchar {a}" for a in ("red", "green", "blue")]
-    header += [f"property float {k}" for k in ex]
-    if faces is not None:
-        header += [f"element face {len(faces)}", "property list uchar int vertex_indices"]
-    header.append("end_header")
     with open(path, "wb") as out:
-        out.write(("\n".join(header) + "\n").encode("ascii"))
+        out.write(("\n".join(lines) + "\n").encode("ascii"))
         if binary:
-            fields = [("xyz", "<f4", (3,))]
-            if n is not None:
-                fields.append(("n", "<f4", (3,)))
-            if c is not None:
-                fields.append(("rgb", "u1", (3,)))
-            fields += [(k, "<f4") for k in ex]
-            rec = np.empty(len(v), dtype=np.dtype(fields))
-            rec["xyz"] = v
-            if n is not None:
-                rec["n"] = n
-            if c is not None:
-                rec["rgb"] = c
-            for k, a in ex.items():
-                rec[k] = a
-            out.write(rec.tobytes())
-            if faces is not None:
-                f = np.asarray(faces.cpu() if isinstance(faces, torch.Tensor) else faces,
-                               dtype=np.int32).reshape(-1, 3)
-                frec = np.empty(len(f), dtype=np.dtype([("n", "u1"), ("idx", "<i4", (3,))]))
+            table = np.empty(count, dtype=[(name, dt) for name, dt, _ in columns])
+            for name, _, vals in columns:
+                table[name] = vals
+            out.write(table.tobytes())
+            if tris is not None:
+                frec = np.empty(tris.shape[0], dtype=[("n", "u1"), ("i", "<i4", (3,))])
                 frec["n"] = 3
-                frec["idx"] = f
+                frec["i"] = tris
                 out.write(frec.tobytes())
-        else:
-            for i in range(len(v)):
-                row = [f"{x:.8f}" for x in v[i]]
-                if n is not None:
-                    row += [f"{x:.8f}" for x in n[i]]
-                if c is not None:
-                    row += [str(int(x)) for x in c[i]]
-                row += [f"{ex[k][i]:.8f}" for k in ex]
-                out.write((" ".join(row) + "\n").encode("ascii"))
-            if faces is not None:
-                f = np.asarray(faces.cpu() if isinstance(faces, torch.Tensor) else faces,
-                               dtype=np.int64).reshape(-1, 3)
-                for tri in f:
-                    out.write(f"3 {tri[0]} {tri[1]} {tri[2]}\n".encode("ascii"))
+            return
+        # ascii: one formatted line per record (floats with 9 significant
+        # digits, which round-trips float32)
+        fmts = ["%d" if dt.kind == "u" else "%.9g" for _, dt, _ in columns]
+        line_fmt = " ".join(fmts) + "\n"
+        cols = [vals.astype(np.float64) if dt.kind == "f" else vals.astype(np.int64)
+                for _, dt, vals in columns]
+        out.write("".join(line_fmt % tuple(c[i] for c in cols) for i in range(count))
+                  .encode("ascii"))
+        if tris is not None:
+            out.write("".join(f"3 {a} {b} {c}\n" for a, b, c in tris.tolist()).encode("ascii"))

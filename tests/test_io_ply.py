@@ -161,3 +161,42 @@ def test_model_ply_degree_inference_and_generic_path(tmp_path):
     assert la.sh_degree == 1
     for k in P:
         torch.testing.assert_close(la.params[k], P[k], atol=1e-7, rtol=1e-7)
+
+
+def test_ply_binary_polygons_and_alpha(tmp_path):
+    """Binary faces: uniform quads (one record view) and mixed sizes (the
+    per-polygon walk) triangulate as fans; an alpha property is consumed with
+    the colours; ushort/double properties load as float32 extras."""
+    head = ("ply\nformat binary_little_endian 1.0\nelement vertex 4\n"
+            "property double x\nproperty double y\nproperty double z\n"
+            "property uchar red\nproperty uchar green\nproperty uchar blue\nproperty uchar alpha\n"
+            "property ushort label\nelement face {nf}\nproperty list uchar uint vertex_indices\n"
+            "end_header\n")
+    verts = b"".join(struct.pack("<3d4BH", x, y, 0.0, 255, 128, 0, 255, i)
+                     for i, (x, y) in enumerate([(0, 0), (1, 0), (1, 1), (0, 1)]))
+    quads = struct.pack("<B4I", 4, 0, 1, 2, 3) + struct.pack("<B4I", 4, 3, 2, 1, 0)
+    mixed = struct.pack("<B3I", 3, 0, 1, 2) + struct.pack("<B4I", 4, 0, 1, 2, 3)
+    for name, faces, nf, want in [
+            ("quads", quads, 2, [[0, 1, 2], [0, 2, 3], [3, 2, 1], [3, 1, 0]]),
+            ("mixed", mixed, 2, [[0, 1, 2], [0, 1, 2], [0, 2, 3]])]:
+        p = tmp_path / f"{name}.ply"
+        p.write_bytes(head.format(nf=nf).encode() + verts + faces)
+        d = load_ply(str(p))
+        assert d.faces.tolist() == want, name
+        assert d.faces.dtype == torch.int32
+        torch.testing.assert_close(d.colors[0], torch.tensor([1.0, 128 / 255, 0.0]))
+        assert set(d.extra) == {"label"}
+        assert d.extra["label"].tolist() == [0.0, 1.0, 2.0, 3.0]
+        assert d.verts.dtype == torch.float32 and d.verts[2].tolist() == [1.0, 1.0, 0.0]
+
+
+def test_ply_ascii_floats_round_trip_exactly(tmp_path):
+    """The ascii writer's 9 significant digits round-trip every float32,
+    tiny and huge magnitudes included."""
+    vals = np.array([1e-30, -3.4e38, 0.1, 1 / 3, 2.0 ** -126, 123456.789], np.float32)
+    pts = torch.from_numpy(np.stack([vals, vals[::-1].copy(), -vals], 1))
+    p = str(tmp_path / "exact.ply")
+    save_ply(p, pts, extra={"v": torch.from_numpy(vals)}, binary=False)
+    d = load_ply(p)
+    assert torch.equal(d.verts, pts)
+    assert torch.equal(d.extra["v"], torch.from_numpy(vals))
