@@ -429,6 +429,115 @@ int gsx_accum_screen_grads(int64_t n, const float* g_means2d,
                            const float* radii, int32_t width, int32_t height,
                            float* grad_accum, float* grad_count, void* stream);
 
+/* ------------------------------------------------------ table edits --
+ * A Gaussian table: up to GSX_TABLE_MAX float32 tensors of N rows, tensor k
+ * holding width[k] contiguous floats per row (the parameter groups, and in
+ * training their Adam moments).  src and dst are the tensors before and
+ * after the edit (the same pointers for in-place edits).  Host struct. */
+#define GSX_TABLE_MAX 20
+enum gsx_row_role {
+    GSX_ROW_PARAM = 1,   /* a parameter tensor: rows are copied or edited     */
+    GSX_ROW_MOMENT = 2   /* an optimizer moment: new or moved rows are zero    */
+};
+typedef struct gsx_row_table {
+    int32_t count;
+    int32_t width[GSX_TABLE_MAX];
+    int32_t role[GSX_TABLE_MAX];
+    const float* src[GSX_TABLE_MAX];
+    float* dst[GSX_TABLE_MAX];
+} gsx_row_table;
+
+/* Replaces the nearest-neighbour scale of GaussianModel.from_points
+ * (splatting/model.py:72-92 with ops/knn.py:121-177): for each of n_query
+ * points the k nearest of n_ref reference points (squared distance = sum of
+ * the squared coordinate differences, ties to the lower index), the mean of
+ * the k - 1 nearest skipping a self hit (first distance <= 1e-12), clamped
+ * at 1e-8, written as log(sqrt(mean)) capped at log_cap.  2 <= k <= 8,
+ * k <= n_ref. */
+int gsx_knn_log_scale(int64_t n_query, const float* query, int64_t n_ref,
+                      const float* ref, int32_t k, float log_cap, float* log_scale,
+                      void* stream);
+
+/* Replaces densify_and_prune (splatting/model.py:406-480), in two calls.
+ * gsx_density_classify: per row, avg = grad_accum / max(grad_count, 1),
+ * s = max of exp(log_scales); clone if avg > grad_threshold and s <=
+ * dense_scale, split if avg > grad_threshold and s > dense_scale; pruned
+ * (not kept) if sigmoid(clip(logit, -50, 50)) < min_opacity, split, or s >
+ * prune_scale.  totals (3 uint32, device) = (kept, cloned, split).  The
+ * workspace (gsx_density_workspace_bytes) carries the classes to the second
+ * call.  gsx_density_emit: with the new tensors sized kept + cloned +
+ * 2 split rows, writes rows [kept originals, clones, split pairs], each part
+ * in source order; a split pair's means move by R(q) (s * xi) with xi from
+ * split_samples ((2 split, 3) float64 standard normals, pair-major, as the
+ * reference draws them) and R from the normalised quaternion, log-scales drop
+ * by log_shrink; GSX_ROW_MOMENT tensors keep kept rows' values and are zero in
+ * new rows. */
+int64_t gsx_density_workspace_bytes(int64_t n);
+int gsx_density_classify(int64_t n, const float* log_scales, const float* logit_opacities,
+                         const float* grad_accum, const float* grad_count,
+                         float grad_threshold, float dense_scale, float prune_scale,
+                         float min_opacity, void* workspace, int64_t workspace_bytes,
+                         uint32_t* totals, void* stream);
+int gsx_density_emit(int64_t n, const void* workspace, int64_t workspace_bytes,
+                     const uint32_t* totals, const gsx_row_table* table, int32_t means_col,
+                     int32_t scales_col, int32_t quats_col, const double* split_samples,
+                     float log_shrink, void* stream);
+
+/* Replaces the scores relocate_mcmc selects by (splatting/model.py:497-512):
+ * target_score = 2 - sigmoid(o) where the row is underused (sigmoid(o) <
+ * min_opacity or grad_count <= 0), else -sigmoid(o); source_score =
+ * grad_accum / max(grad_count, 1); *under_count (device, caller-zeroed) +=
+ * the number of underused rows.  The caller picks the k largest of each
+ * (sources among rows that are not destinations). */
+int gsx_relocate_scores(int64_t n, const float* grad_accum, const float* grad_count,
+                        const float* logit_opacities, float min_opacity, float* target_score,
+                        float* source_score, uint32_t* under_count, void* stream);
+
+/* Replaces the row rewrite of relocate_mcmc (splatting/model.py:517-529), in
+ * place: row dst_rows[j] takes source row src_rows[j] (k pairs, int64,
+ * device) with means + noise[j] * exp(log-scale) * jitter, the opacity
+ * logit reset_logit and log-scales - log_shrink, written as old + (new -
+ * old) (the reference's scatter-add); moments of the destination rows
+ * become zero.  staging: k times the sum of the parameter widths floats. */
+int gsx_density_relocate(int64_t k, const int64_t* src_rows, const int64_t* dst_rows,
+                         const gsx_row_table* table, int32_t means_col, int32_t scales_col,
+                         int32_t opac_col, const float* noise, float jitter,
+                         float reset_logit, float log_shrink, float* staging,
+                         int64_t staging_floats, void* stream);
+
+/* ---------------------------------------------------- 2DGS geometry --
+ * Replaces the 2DGS regularisers of GaussianTrainer._geometry_loss_2dgs
+ * (splatting/trainer.py:187-259).
+ * gsx_geom_features: features (N,5) = (z, z^2, n), n the normalised third
+ * column of the rotation of the normalised quaternion, negated when
+ * n . (center - mean) < 0; center = the camera centre (3 floats, host).
+ * gsx_geom_features_bwd: the VJP into depths (N) and quaternions (N,4).
+ * gsx_geom_loss_fwd: on the alpha-normalised render F (H,W,5) of those
+ * features and alpha (H,W), with unprojection maps P = base + z dir
+ * ((H,W,3) each, the world point of a pixel centre at z-depth z):
+ *   depth variance = sum over alpha > min_alpha of max(F1 - F0^2, 0) / max(count, 1)
+ *   normal term    = sum over 2x2 quads whose 4 pixels pass of
+ *                    1 - |unit(F[2:5]) . unit((P01 - P00) x (P10 - P00))| / max(count, 1)
+ * out (5 floats, device) = [lam_dv dv + lam_nc nc, dv, nc, dv divisor, nc
+ * divisor]; a term with lambda <= 0 is off (and the normal term needs W, H
+ * > 1).  gsx_geom_loss_bwd: dL/dF (H,W,5) from fwd_out and the loss
+ * cotangent grad_loss (1 float, device); alpha gets no gradient (its test
+ * is a step). */
+int gsx_geom_features(int64_t n, const float* means, const float* quats, const float* depths,
+                      const float* center, float* features, void* stream);
+int gsx_geom_features_bwd(int64_t n, const float* means, const float* quats,
+                          const float* depths, const float* center, const float* g_features,
+                          float* g_depths, float* g_quats, void* stream);
+int64_t gsx_geom_loss_workspace_bytes(int32_t width, int32_t height);
+int gsx_geom_loss_fwd(int32_t width, int32_t height, const float* features, const float* alpha,
+                      const float* base, const float* dir, float min_alpha, float lam_dv,
+                      float lam_nc, void* workspace, int64_t workspace_bytes, float* out,
+                      void* stream);
+int gsx_geom_loss_bwd(int32_t width, int32_t height, const float* features, const float* alpha,
+                      const float* base, const float* dir, float min_alpha, float lam_dv,
+                      float lam_nc, const float* fwd_out, const float* grad_loss,
+                      float* g_features, void* stream);
+
 /* --------------------------------------------------------- mesh raster --
  * Replaces the hard z-buffer kernel of rasterize_meshes
  * (renderer/rasterizer.py:29-87), the mesh consumer of bin_gaussians: the

@@ -65,6 +65,41 @@ class GsxAdamGroup(ctypes.Structure):
     ]
 
 
+TABLE_MAX = 20  # GSX_TABLE_MAX
+ROW_PARAM = 1
+ROW_MOMENT = 2
+
+
+class GsxRowTable(ctypes.Structure):
+    """gsx_row_table of include/gsx.h."""
+
+    _fields_ = [
+        ("count", ctypes.c_int32),
+        ("width", ctypes.c_int32 * TABLE_MAX),
+        ("role", ctypes.c_int32 * TABLE_MAX),
+        ("src", ctypes.c_void_p * TABLE_MAX),
+        ("dst", ctypes.c_void_p * TABLE_MAX),
+    ]
+
+
+def row_table(columns) -> GsxRowTable:
+    """GsxRowTable of ``[(src, dst, role), ...]``: (N, ...) float32
+    contiguous tensors, width = elements per row."""
+    if not 0 < len(columns) <= TABLE_MAX:
+        raise ValueError(f"a row table holds 1..{TABLE_MAX} tensors")
+    t = GsxRowTable()
+    t.count = len(columns)
+    for k, (src, dst, role) in enumerate(columns):
+        for x in (src, dst):
+            if x.dtype != torch.float32 or not x.is_contiguous():
+                raise ValueError("row-table tensors must be contiguous float32")
+        t.width[k] = int(src[0].numel()) if src.shape[0] else int(dst[0].numel())
+        t.role[k] = role
+        t.src[k] = src.data_ptr()
+        t.dst[k] = dst.data_ptr()
+    return t
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -122,6 +157,22 @@ SIGNATURES = {
     "gsx_l1_bwd": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P]),
     "gsx_adam_step": (ctypes.c_int, [_I32, ctypes.c_void_p, _F, _F, _F, _P]),
     "gsx_accum_screen_grads": (ctypes.c_int, [_I64, _P, _P, _I32, _I32, _P, _P, _P]),
+    "gsx_knn_log_scale": (ctypes.c_int, [_I64, _P, _I64, _P, _I32, _F, _P, _P]),
+    "gsx_density_workspace_bytes": (_I64, [_I64]),
+    "gsx_density_classify": (ctypes.c_int, [_I64, _P, _P, _P, _P, _F, _F, _F, _F, _P, _I64,
+                                            _P, _P]),
+    "gsx_density_emit": (ctypes.c_int, [_I64, _P, _I64, _P, ctypes.POINTER(GsxRowTable), _I32,
+                                        _I32, _I32, _P, _F, _P]),
+    "gsx_relocate_scores": (ctypes.c_int, [_I64, _P, _P, _P, _F, _P, _P, _P, _P]),
+    "gsx_density_relocate": (ctypes.c_int, [_I64, _P, _P, ctypes.POINTER(GsxRowTable), _I32,
+                                            _I32, _I32, _P, _F, _F, _F, _P, _I64, _P]),
+    "gsx_geom_features": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P, _P]),
+    "gsx_geom_features_bwd": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "gsx_geom_loss_workspace_bytes": (_I64, [_I32, _I32]),
+    "gsx_geom_loss_fwd": (ctypes.c_int, [_I32, _I32, _P, _P, _P, _P, _F, _F, _F, _P, _I64, _P,
+                                         _P]),
+    "gsx_geom_loss_bwd": (ctypes.c_int, [_I32, _I32, _P, _P, _P, _P, _F, _F, _F, _P, _P, _P,
+                                         _P]),
     "gsx_mesh_raster": (ctypes.c_int, [_I64, _P, _P, _P, _I64, _P, _I32, _I32, _F, _P, _P, _P]),
     "gsx_debug_expf": (ctypes.c_int, [_I64, _P, _P, _P]),
     "gsx_debug_atanf": (ctypes.c_int, [_I64, _P, _P, _P]),

@@ -24,7 +24,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "raster.hip", "train.hip", "mesh.hip"]
+SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "raster.hip", "train.hip", "mesh.hip",
+           "density.hip", "geometry.hip"]
 LIB = os.path.join(PKG, "libgsx.so")
 ARCH = os.environ.get("GSX_OFFLOAD_ARCH", "gfx950")
 

@@ -24,22 +24,6 @@ from .sh import num_sh_bases, rgb_to_sh
 __all__ = ["GaussianModel"]
 
 
-def _knn_mean_sq(points: torch.Tensor, ref: torch.Tensor, k: int, chunk: int) -> torch.Tensor:
-    """Mean squared distance to the k-1 nearest neighbours (skipping a
-    zero-distance self hit), as model.py:81-88 derives it from knn_points."""
-    out = []
-    r2 = (ref * ref).sum(-1)
-    for s in range(0, points.shape[0], chunk):
-        p = points[s:s + chunk]
-        d = (p * p).sum(-1, keepdim=True) - 2.0 * p @ ref.T + r2[None]
-        d = torch.clamp(d, min=0.0)
-        vals, _ = torch.topk(d, k, dim=1, largest=False, sorted=True)
-        self_hit = vals[:, 0] <= 1e-12
-        nearest = torch.where(self_hit[:, None], vals[:, 1:k], vals[:, :k - 1])
-        out.append(torch.clamp(nearest.mean(-1), min=1e-8))
-    return torch.cat(out)
-
-
 class GaussianModel:
     """A scene of 3D Gaussians with the standard 3DGS parameterisation."""
 
@@ -53,40 +37,52 @@ class GaussianModel:
     def from_points(cls, points, colors=None, sh_degree: int = 3, initial_opacity: float = 0.1,
                     scale_init_max_ref: int = 10_000, scale_init_chunk_size: int = 1024,
                     scale_init_max_scale: float | None = None,
-                    generator: torch.Generator | None = None) -> "GaussianModel":
-        """Initialise from a point cloud (model.py:37-106): isotropic scales
-        from the mean squared distance to the 3 nearest neighbours, identity
-        rotations, opacity ``initial_opacity``, DC colour from ``colors``."""
-        points = torch.as_tensor(points, dtype=torch.float32)
-        N = points.shape[0]
-        dev = points.device
-        if colors is None:
-            colors = torch.full((N, 3), 0.5, device=dev)
-        colors = torch.as_tensor(colors, dtype=torch.float32, device=dev)
-        ref_count = min(N, max(1, int(scale_init_max_ref)))
-        if N > ref_count:
-            perm = torch.randperm(N, generator=generator)[:ref_count].to(dev)
-            ref = points[perm]
+                    generator: torch.Generator | None = None,
+                    device=None) -> "GaussianModel":
+        """A table initialised from a point cloud (model.py:37-106).
+
+        Isotropic log-scales come from ``gsx_knn_log_scale`` on the GPU: the
+        mean squared distance to the 3 nearest of at most
+        ``scale_init_max_ref`` reference points (a random subset of a larger
+        cloud, drawn with ``generator``), a self hit skipped, optionally capped
+        at ``scale_init_max_scale``.  Rotations are the identity, opacity
+        logits ``logit(initial_opacity)``, the DC colour ``rgb_to_sh(colors)``
+        (grey without colours) and higher SH bands zero.  The table lives on
+        ``device`` (default: the GPU).  ``scale_init_chunk_size`` bounded the
+        reference's query chunks; the kernel streams the reference points, so
+        it is accepted and unused."""
+        from .density import knn_log_scales
+
+        dev = torch.device(device if device is not None else "cuda")
+        pts = torch.as_tensor(points, dtype=torch.float32).to(dev).contiguous()
+        if pts.ndim != 2 or pts.shape[1] != 3:
+            raise ValueError("points must have shape (N, 3).")
+        count = pts.shape[0]
+        rgb = (torch.full((count, 3), 0.5, device=dev) if colors is None
+               else torch.as_tensor(colors, dtype=torch.float32).to(dev))
+        n_ref = min(count, max(1, int(scale_init_max_ref)))
+        if n_ref < count:
+            pick = torch.randperm(count, generator=generator)[:n_ref].to(dev)
+            ref = pts[pick].contiguous()
         else:
-            ref = points
-        if ref_count <= 1:
-            mean_sq = torch.full((N,), 1e-8, device=dev)
+            ref = pts
+        if n_ref <= 1:  # no neighbour: the reference's floor of 1e-8
+            log_s = torch.full((count,), 0.5 * math.log(1e-8), device=dev)
+            if scale_init_max_scale is not None:
+                log_s = torch.clamp(log_s, max=math.log(max(scale_init_max_scale, 1e-8)))
         else:
-            mean_sq = _knn_mean_sq(points, ref, min(4, ref_count), scale_init_chunk_size)
-        scales = torch.log(torch.sqrt(mean_sq))[:, None] * torch.ones((1, 3), device=dev)
-        if scale_init_max_scale is not None:
-            scales = torch.clamp(scales, max=math.log(max(scale_init_max_scale, 1e-8)))
-        quats = torch.zeros((N, 4), device=dev)
-        quats[:, 0] = 1.0
+            log_s = knn_log_scales(pts, ref, min(4, n_ref), scale_init_max_scale)
         K = num_sh_bases(sh_degree)
+        quats = torch.zeros((count, 4), device=dev)
+        quats[:, 0] = 1.0
+        logit = math.log(initial_opacity / (1 - initial_opacity))
         params = {
-            "means": points.clone(),
-            "scales": scales,
+            "means": pts.clone(),
+            "scales": log_s[:, None].expand(count, 3).contiguous(),
             "quats": quats,
-            "opacities": torch.full((N,), math.log(initial_opacity / (1 - initial_opacity)),
-                                    device=dev),
-            "sh_dc": rgb_to_sh(colors)[:, None, :].contiguous(),
-            "sh_rest": torch.zeros((N, K - 1, 3), device=dev),
+            "opacities": torch.full((count,), logit, device=dev),
+            "sh_dc": rgb_to_sh(rgb)[:, None, :].contiguous(),
+            "sh_rest": torch.zeros((count, K - 1, 3), device=dev),
         }
         return cls(params, sh_degree=sh_degree)
 
@@ -330,102 +326,51 @@ class GaussianModel:
     def densify_and_prune(self, grad_accum: torch.Tensor, grad_count: torch.Tensor,
                           grad_threshold: float = 0.0002, scene_extent: float = 1.0,
                           percent_dense: float = 0.01, min_opacity: float = 0.005,
-                          return_optimizer_state: bool = False) -> dict:
-        """Adaptive density control of the 3DGS paper (model.py:406-480).
+                          return_optimizer_state: bool = False, moments: dict | None = None
+                          ) -> dict:
+        """Adaptive density control of the 3DGS paper (model.py:406-480), on
+        the device (``gsx_density_classify`` / ``gsx_density_emit``).
 
-        High average screen gradient: clone if max(scale) <= percent_dense
-        extent, else split into two samples N(0, diag(s^2)) rotated by the
-        Gaussian's rotation, log-scales reduced by log 1.6.  Prune split
-        sources, sigmoid(opacity) < min_opacity and max(scale) > 0.5 extent.
-        The split samples come from ``np.random.normal`` (the global NumPy
-        generator, as the reference draws them).  Rows end up ordered
-        [kept originals, clones, split pairs].
+        A row whose average screen gradient exceeds ``grad_threshold`` is
+        cloned when its largest scale is at most ``percent_dense *
+        scene_extent`` and split otherwise: two samples N(0, diag(s^2))
+        rotated by the Gaussian's rotation (drawn from ``np.random.normal``,
+        the reference's generator and order), log-scales reduced by log 1.6.
+        Split sources, rows with sigmoid(opacity) < ``min_opacity`` and rows
+        larger than half the extent are pruned.  New row order: kept rows,
+        clones, split pairs.  ``moments`` ({group: {"m", "v"}}) are edited
+        alongside (zero in new rows) and returned under ``"_moments"``.
         """
-        from ..transforms import quaternion_to_matrix
+        from .density import densify
 
-        with torch.no_grad():
-            p = {k: v.detach() for k, v in self.params.items()}
-            dev = p["means"].device
-            avg_grad = grad_accum / torch.clamp(grad_count, min=1.0)
-            scales = torch.exp(p["scales"])
-            max_scale = scales.max(dim=1).values
-            high_grad = avg_grad > grad_threshold
-            dense = percent_dense * scene_extent
-            clone_mask = high_grad & (max_scale <= dense)
-            split_mask = high_grad & (max_scale > dense)
-            clone_idx = torch.nonzero(clone_mask).flatten()
-            split_idx = torch.nonzero(split_mask).flatten()
-            opac = 1.0 / (1.0 + torch.exp(-torch.clamp(p["opacities"], -50.0, 50.0)))
-            prune_mask = (opac < min_opacity) | split_mask | (max_scale > 0.5 * scene_extent)
-            keep_idx = torch.nonzero(~prune_mask).flatten()
-            parts = {k: [v[keep_idx], v[clone_idx]] for k, v in p.items()}
-            n_split = int(split_idx.numel())
-            if n_split > 0:
-                q = p["quats"][split_idx]
-                R = quaternion_to_matrix(q / torch.linalg.norm(q, dim=1, keepdim=True))
-                s = scales[split_idx].cpu().numpy()
-                samples = np.random.normal(size=(2 * n_split, 3)) * np.repeat(s, 2, axis=0)
-                offsets = np.einsum("nij,nj->ni", np.repeat(R.cpu().numpy(), 2, axis=0), samples)
-                for k, v in p.items():
-                    rows = torch.repeat_interleave(v[split_idx], 2, dim=0)
-                    if k == "means":
-                        rows = rows + torch.from_numpy(offsets.astype(np.float32)).to(dev)
-                    elif k == "scales":
-                        rows = rows - float(np.log(1.6))
-                    parts[k].append(rows)
-            self._replace({k: torch.cat(v, dim=0) for k, v in parts.items()})
-        stats: dict = {"cloned": int(clone_idx.numel()), "split": n_split,
-                       "pruned": int(prune_mask.sum())}
+        new, new_moments, stats, keep_idx = densify(
+            self.params, grad_accum, grad_count, grad_threshold=grad_threshold,
+            scene_extent=scene_extent, percent_dense=percent_dense, min_opacity=min_opacity,
+            moments=moments)
+        self._replace(new)
+        if moments is not None:
+            stats["_moments"] = new_moments
         if return_optimizer_state:
             stats["_keep_idx"] = keep_idx.cpu().numpy().astype(np.int32)
-            stats["_new_count"] = int(clone_idx.numel() + 2 * n_split)
+            stats["_new_count"] = int(stats["cloned"] + 2 * stats["split"])
         return stats
 
     def relocate_mcmc(self, grad_accum: torch.Tensor, grad_count: torch.Tensor,
                       relocate_frac: float = 0.02, min_opacity: float = 0.01,
-                      jitter_scale: float = 0.25,
-                      generator: torch.Generator | None = None) -> dict:
-        """Fixed-budget relocation (model.py:482-531): the k best relocation
-        targets (never-seen or sigmoid(opacity) < min_opacity rows first, then
-        the least opaque) take jittered copies of the k rows with the highest
-        average screen gradient among the rest; opacity resets to 0.05 and
-        log-scales shrink by log 1.6.  Rows are rewritten as
-        ``a[dst] + (new - a[dst])``, the reference's scatter-add."""
-        n = self.num_gaussians
-        max_relocate = int(max(0, min(relocate_frac, 1.0)) * n)
-        if max_relocate <= 0 or n <= 1:
-            return {"relocated": 0}
+                      jitter_scale: float = 0.25, generator: torch.Generator | None = None,
+                      moments: dict | None = None) -> dict:
+        """Fixed-budget MCMC relocation (model.py:482-531), in place on the
+        device: up to ``relocate_frac`` N underused rows (sigmoid(opacity) <
+        ``min_opacity`` or never seen; otherwise the least opaque) take
+        jittered copies of the rows with the largest average screen gradient,
+        opacity reset to 0.05 and log-scales shrunk by log 1.6.  ``moments``
+        of the moved rows are cleared."""
+        from .density import relocate
+
         with torch.no_grad():
-            p = {k: v.detach() for k, v in self.params.items()}
-            avg_grad = grad_accum / torch.clamp(grad_count, min=1.0)
-            opac = torch.sigmoid(p["opacities"])
-            underused = (opac < min_opacity) | (grad_count <= 0)
-            underused_count = int(underused.sum())
-            k = max_relocate if underused_count == 0 else min(max_relocate, underused_count)
-            k = min(k, n - 1)
-            if k == 0:
-                return {"relocated": 0}
-            target_score = torch.where(underused, 2.0 - opac, -opac)
-            dst = torch.topk(target_score, k).indices
-            source_score = avg_grad.clone()
-            source_score[dst] = source_score[dst] + (-1e30 - avg_grad[dst])
-            src = torch.topk(source_score, k).indices
-            source_scales = torch.exp(p["scales"][src])
-            reset_opacity = float(np.log(0.05 / 0.95))
-            shrink = float(np.log(1.6))
-            out = {}
-            for name, arr in p.items():
-                values = arr[src]
-                if name == "means" and jitter_scale > 0:
-                    gdev = generator.device if generator is not None else values.device
-                    noise = torch.randn(values.shape, generator=generator, device=gdev)
-                    values = values + noise.to(values.device) * source_scales * float(jitter_scale)
-                elif name == "opacities":
-                    values = torch.full_like(values, reset_opacity)
-                elif name == "scales":
-                    values = values - shrink
-                arr = arr.clone()
-                arr[dst] = arr[dst] + (values - arr[dst])
-                out[name] = arr
-            self._replace(out)
+            k, dst = relocate(self.params, grad_accum, grad_count, relocate_frac=relocate_frac,
+                              min_opacity=min_opacity, jitter_scale=jitter_scale,
+                              generator=generator, moments=moments)
+        if k == 0:
+            return {"relocated": 0}
         return {"relocated": int(k), "_moved_idx": dst}

@@ -449,3 +449,48 @@ def mesh_zbuffer_f64(tri_xy, tri_z, width, height, znear=0.01):
     amb = (ok & (z > znear) & (np.abs(lmin + 1e-5) < 1e-4)).any(axis=-1)
     return (np.where(np.isfinite(bz), best, -1).astype(np.int32),
             np.where(np.isfinite(bz), bz, 0.0), margin, amb)
+
+
+# ------------------------------------------------------------ 2DGS geometry
+def surfel_features_f64(means, quats, depths, center):
+    """(N, 5) = (z, z^2, n) of trainer.py:200-206 in float64: n the third
+    column of the rotation of the normalised quaternion, normalised, flipped
+    to face the camera centre."""
+    q = quats / torch.linalg.norm(quats, dim=-1, keepdim=True)
+    w, x, y, z = q.unbind(-1)
+    col = torch.stack([2 * (x * z + w * y), 2 * (y * z - w * x), 1 - 2 * (x * x + y * y)], -1)
+    n = col / torch.clamp(torch.linalg.norm(col, dim=-1, keepdim=True), min=1e-8)
+    view = torch.as_tensor(center, dtype=means.dtype) - means
+    n = torch.where((n * view).sum(-1, keepdim=True) < 0, -n, n)
+    return torch.cat([depths[:, None], (depths * depths)[:, None], n], 1)
+
+
+def geometry_loss_f64(F, alpha, camera, min_alpha, lam_dv, lam_nc):
+    """The 2DGS losses of trainer.py:208-257 on an alpha-normalised (H, W, 5)
+    render, float64 (the camera's unprojection evaluated in float64)."""
+    H, W = alpha.shape
+    valid = (alpha > min_alpha).to(F.dtype)
+    ed, ed2 = F[..., 0], F[..., 1]
+    dv = (torch.clamp(ed2 - ed * ed, min=0.0) * valid).sum() / torch.clamp(valid.sum(), min=1.0)
+    u = torch.arange(W, dtype=F.dtype) + 0.5
+    v = torch.arange(H, dtype=F.dtype) + 0.5
+    # cameras.py:327-336 in float64: undistorted normalised coordinates,
+    # scaled by the depth, then (X_cam - t) R
+    xn = ((u[None, :] - camera.cx) / camera.fx).expand(H, W)
+    yn = ((v[:, None] - camera.cy) / camera.fy).expand(H, W)
+    R, t = camera.R.double(), camera.t.double()
+    if camera.orthographic:
+        pc = torch.stack([xn, yn, ed], -1)
+    else:
+        xu, yu = camera._undistort(xn, yn)
+        pc = torch.stack([xu * ed, yu * ed, ed], -1)
+    pts = (pc - t) @ R
+    tx = pts[:-1, 1:] - pts[:-1, :-1]
+    ty = pts[1:, :-1] - pts[:-1, :-1]
+    dn = torch.linalg.cross(tx, ty)
+    dn = dn / torch.clamp(torch.linalg.norm(dn, dim=-1, keepdim=True), min=1e-8)
+    rn = F[:-1, :-1, 2:5]
+    rn = rn / torch.clamp(torch.linalg.norm(rn, dim=-1, keepdim=True), min=1e-8)
+    v4 = valid[:-1, :-1] * valid[:-1, 1:] * valid[1:, :-1] * valid[1:, 1:]
+    nc = ((1.0 - (rn * dn).sum(-1).abs()) * v4).sum() / torch.clamp(v4.sum(), min=1.0)
+    return lam_dv * dv + lam_nc * nc, dv, nc

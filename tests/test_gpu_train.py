@@ -264,6 +264,94 @@ def test_relocate_mcmc_moves_rows():
         np.testing.assert_allclose(p["scales"][i], srcs[j], rtol=0, atol=1e-6)
 
 
+def test_densify_carries_moments():
+    """Moments passed to densify_and_prune follow their rows: a kept row's
+    moments move with it, clones and split rows start at zero."""
+    say("densify moments")
+    _, model, raw, _ = _model(33, 2500)
+    raw["opacities"][:40] = -7.0
+    model.params["opacities"][:40] = -7.0
+    rng = np.random.default_rng(4)
+    acc = (rng.random(2500) * 4e-3).astype(np.float32)
+    cnt = rng.integers(0, 10, 2500).astype(np.float32)
+    moments = {k: {"m": cu(rng.normal(size=raw[k].shape).astype(np.float32)),
+                   "v": cu(rng.random(raw[k].shape).astype(np.float32))}
+               for k in ("means", "sh_rest", "opacities")}
+    old = {k: {s: host(t) for s, t in v.items()} for k, v in moments.items()}
+    np.random.seed(5)
+    stats = model.densify_and_prune(cu(acc), cu(cnt), scene_extent=8.0, moments=moments,
+                                    return_optimizer_state=True)
+    new = stats["_moments"]
+    keep = stats["_keep_idx"]
+    nk = keep.shape[0]
+    assert nk == 2500 - stats["pruned"] and stats["cloned"] > 0 and stats["split"] > 0
+    for k, slots in new.items():
+        for s, t in slots.items():
+            a = host(t)
+            assert a.shape[0] == model.num_gaussians
+            np.testing.assert_array_equal(a[:nk], old[k][s][keep], err_msg=f"{k}.{s}")
+            assert not a[nk:].any(), f"{k}.{s}: new rows must start at zero"
+
+
+def test_relocate_clears_moved_moments():
+    say("relocate moments")
+    _, model, raw, _ = _model(34, 1500)
+    rng = np.random.default_rng(6)
+    acc = rng.random(1500).astype(np.float32)
+    cnt = rng.integers(0, 4, 1500).astype(np.float32)
+    m = cu(rng.normal(size=(1500, 3)).astype(np.float32))
+    v = cu(rng.random((1500, 3)).astype(np.float32))
+    before = host(m)
+    out = model.relocate_mcmc(cu(acc), cu(cnt), relocate_frac=0.05, min_opacity=0.1,
+                              jitter_scale=0.0, moments={"means": {"m": m, "v": v}})
+    moved = np.zeros(1500, bool)
+    moved[host(out["_moved_idx"])] = True
+    assert out["relocated"] == moved.sum() > 0
+    assert not host(m)[moved].any() and not host(v)[moved].any()
+    np.testing.assert_array_equal(host(m)[~moved], before[~moved])
+
+
+def _knn_reference(pts, ref, k):
+    """Brute force of the rule gsx_knn_log_scale restates: float32 squared
+    distances summed over x, y, z, stable order by (distance, index)."""
+    out = np.empty(len(pts), np.float32)
+    for i, q in enumerate(pts):
+        d = ((q[None, :] - ref) ** 2).astype(np.float32)
+        d = (d[:, 0] + d[:, 1]) + d[:, 2]
+        order = np.argsort(d, kind="stable")[:k]
+        dk = d[order]
+        near = dk[1:k] if dk[0] <= np.float32(1e-12) else dk[:k - 1]
+        s = np.float32(0.0)
+        for x in near:
+            s = np.float32(s + x)
+        mean = max(np.float32(s / np.float32(k - 1)), np.float32(1e-8))
+        out[i] = np.log(np.sqrt(mean, dtype=np.float32), dtype=np.float32)
+    return out
+
+
+def test_knn_log_scale_matches_bruteforce():
+    """from_points' nearest-neighbour scale (model.py:72-92): self hits
+    skipped, ties to the lower index, duplicates, a capped variant."""
+    say("knn log scale")
+    from mlx3d_amd.splatting.density import knn_log_scales
+
+    rng = np.random.default_rng(8)
+    pts = rng.normal(0, 1, (3000, 3)).astype(np.float32)
+    pts[100:110] = pts[99]  # exact duplicates: zero distances
+    pts[200:400] = np.round(pts[200:400] * 4) / 4  # a lattice: many equal distances
+    ref = pts[rng.permutation(3000)[:1200]]  # a subset: some queries have no self hit
+    for r, k in [(pts, 4), (ref, 4), (pts, 2), (ref, 8)]:
+        got = host(knn_log_scales(cu(pts), cu(r), k))
+        want = _knn_reference(pts, r, k)
+        e = np.abs(got - want).max()
+        say(f"  n_ref={len(r)} k={k}: max |d| {e:.2e}")
+        assert e <= 2e-6
+    capped = host(knn_log_scales(cu(pts), cu(pts), 4, max_scale=0.05))
+    assert capped.max() <= np.log(0.05) + 1e-6
+    np.testing.assert_array_equal(capped, np.minimum(host(knn_log_scales(cu(pts), cu(pts), 4)),
+                                                     np.float32(np.log(0.05))))
+
+
 @pytest.mark.parametrize("method", ["vanilla", "mcmc", "2dgs"])
 def test_trainer_loop(method):
     """Fits a random scene to the render of another for 40 steps: the loss

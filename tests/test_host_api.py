@@ -65,6 +65,7 @@ def test_cpu_tensors_are_refused():
         bin_gaussians(torch.zeros(4, 2), torch.ones(4), torch.ones(4), 32, 32)
 
 
+@pytest.mark.gpu
 def test_model_from_points_scales_and_layout():
     pts = torch.tensor([[0.0, 0, 0], [1.0, 0, 0], [0, 2.0, 0], [0, 0, 3.0], [1.0, 1.0, 0]])
     model = GaussianModel.from_points(pts, sh_degree=2)
