@@ -128,6 +128,38 @@ def test_binning_edge_cases():
               8, 8, "one tile")
 
 
+def test_binning_culled_owners_and_clusters():
+    """Long runs of zero-count (off-screen) Gaussians between owners in depth
+    order (emission's unstaged owner search), and splats clustered over a few
+    tiles (long per-tile runs)."""
+    rng = np.random.default_rng(21)
+    W, H = 640, 360
+    n = 120000
+    m = rng.uniform(0, [W, H], (n, 2)).astype(np.float32)
+    m[::2, 0] += 5000.0  # every other Gaussian off-screen: count 0, valid depth
+    r = rng.integers(1, 60, n).astype(np.float32)
+    d = rng.uniform(1, 10, n).astype(np.float32)
+    _bin_case(m, r, d, W, H, "culled owners")
+    # clustered: most splats over a few tiles (long per-tile runs in a sub-chunk)
+    m2 = (rng.normal(0, 6, (60000, 2)) + [320, 180]).astype(np.float32)
+    _bin_case(m2, rng.integers(1, 12, 60000).astype(np.float32),
+              rng.choice(np.linspace(1, 3, 50), 60000).astype(np.float32), W, H, "cluster")
+
+
+def test_binning_large_image():
+    """Images with more tiles than 14 bits of tile id (three radix passes
+    over the tile ids) and just below, against the oracle's order."""
+    rng = np.random.default_rng(22)
+    W, H = 2112, 2064  # 132 x 129 = 17028 tiles (15 significant bits)
+    n = 40000
+    m = rng.uniform(-50, [W + 50, H + 50], (n, 2)).astype(np.float32)
+    r = rng.integers(0, 80, n).astype(np.float32)
+    d = rng.uniform(0.5, 8, n).astype(np.float32)
+    _bin_case(m, r, d, W, H, "large image")
+    W2, H2 = 2032, 2048  # 127 x 128 = 16256 tiles
+    _bin_case(m, r, d, W2, H2, "16256 tiles")
+
+
 def test_bin_sort_sync_abi_and_capacity():
     """gsx_bin_sort (the synchronous entry point) at exact, short and zero
     capacity: short capacity returns 1 with the true D; exact matches the
