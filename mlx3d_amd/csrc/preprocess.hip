@@ -67,6 +67,26 @@ __device__ __forceinline__ void rows_to_lds(float* s, int pad, const float* __re
     }
 }
 
+// Contiguous rows (stride == cols, odd cols so that lane r walking its own
+// row of the unpadded copy hits distinct banks): `total` floats from src
+// (16-byte aligned) into LDS by direct-to-LDS loads (global_load_lds_dwordx4:
+// each lane's 16 bytes land at the wave's LDS base + 16 lane), no VGPR
+// round trip; the < 4 tail floats go through registers.  The caller waits
+// for the loads (vmcnt) before its barrier.
+__device__ __forceinline__ void rows_to_lds_direct(float* s, const float* __restrict__ src,
+                                                   int total) {
+    const int n4 = total >> 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int b4 = wave * kWave; b4 < n4; b4 += kThreads) {
+        if (b4 + lane < n4)
+            __builtin_amdgcn_global_load_lds(
+                src + 4 * (b4 + lane),
+                (__attribute__((address_space(3))) void*)(s + 4 * b4), 16, 0, 0);
+    }
+    const int t = 4 * n4 + (int)threadIdx.x;
+    if (t < total) s[t] = src[t];
+}
+
 // The reverse: LDS rows of `pad` floats out to rows of `cols` floats.
 __device__ __forceinline__ void lds_to_rows(const float* s, int pad, float* __restrict__ base,
                                             int64_t stride, int64_t g0, int rows, int cols) {
@@ -257,8 +277,15 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     const float ro = opacities[il];
     if (sh_mode != kShDirect) {
         const int rows = (int)min<int64_t>(kThreads, n - g0);
-        rows_to_lds(s_sh, pad, sh_mode == kShPacked ? sh0 : shr, sh_mode == kShPacked ? s0 : sr,
-                    g0, rows, sh_cols);
+        const float* base = sh_mode == kShPacked ? sh0 : shr;
+        const int64_t stride = sh_mode == kShPacked ? s0 : sr;
+        if (stride == sh_cols && pad == sh_cols &&
+            ((uintptr_t)(base + g0 * stride) & 15u) == 0u) {
+            rows_to_lds_direct(s_sh, base + g0 * stride, rows * sh_cols);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            rows_to_lds(s_sh, pad, base, stride, g0, rows, sh_cols);
+        }
         __syncthreads();
     }
     if (i >= n) return;
