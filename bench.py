@@ -305,6 +305,70 @@ def cpu_baseline(scene, views, cfg_name: str):
             "cpu_model": cpu}
 
 
+def dense_reference_cpu(scene, view: int, gpu_image):
+    """C1's "reference compositing path": reference.py:16-74 restated as
+    torch-CPU float32, every Gaussian at every pixel in one global depth
+    order, chunked over Gaussians (the transmittance in front of a chunk
+    carries over; a splat is kept while the product of the earlier
+    1 - alpha factors exceeds 1e-4, as reference.py:64-69).  Projection and
+    colours come from the CPU oracle.  Timed end to end (projection, sort,
+    compositing) on the host's torch threads, and compared with the GPU image
+    of the same view."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    cam = scene.cameras[view]
+    f = cam.gsx_fields()
+    oc = O.make_camera(f["R"], f["t"], f["center"], f["fx"], f["fy"], f["cx"], f["cy"],
+                       f["lim_x"], f["lim_y"], f["znear"], f["width"], f["height"])
+    flags = O.LOG_SCALES | O.LOGIT_OPACITY | (O.ANTIALIAS if scene.antialias else 0)
+    sh = np.concatenate([scene.sh_dc, scene.sh_rest], 1)
+    H, W = cam.height, cam.width
+    chunk = 256
+    threads = torch.get_num_threads()
+    t0 = time.perf_counter()
+    pre = O.preprocess_fwd(oc, scene.means, scene.quats, scene.log_scales,
+                           scene.logit_opacities, sh=sh, degree=scene.sh_degree, flags=flags,
+                           threads=O.default_threads())
+    order = np.argsort(pre["depths"], kind="stable")
+    live = pre["radii"][order] > 0
+    order = order[live]  # culled Gaussians have alpha 0 everywhere (reference.py:62)
+    m2 = torch.from_numpy(pre["means2d"][order])
+    con = torch.from_numpy(pre["conics"][order])
+    op = torch.from_numpy(pre["opac_eff"][order])
+    col = torch.from_numpy(pre["colors"][order])
+    xs = (torch.arange(W, dtype=torch.float32) + 0.5).repeat(H)
+    ys = (torch.arange(H, dtype=torch.float32) + 0.5).repeat_interleave(W)
+    T = torch.ones(H * W)
+    acc = torch.zeros(H * W, col.shape[1])
+    with torch.no_grad():
+        for s in range(0, m2.shape[0], chunk):
+            e = min(s + chunk, m2.shape[0])
+            dx = m2[s:e, 0:1] - xs[None]
+            dy = m2[s:e, 1:2] - ys[None]
+            power = -0.5 * (con[s:e, 0:1] * dx * dx + con[s:e, 2:3] * dy * dy) \
+                - con[s:e, 1:2] * dx * dy
+            a = torch.clamp_max(op[s:e, None] * torch.exp(power), 0.99)
+            a = torch.where((power > 0) | (a < 1.0 / 255.0), torch.zeros_like(a), a)
+            om = 1.0 - a
+            front = T[None] * torch.cat([torch.ones_like(om[:1]), torch.cumprod(om, 0)[:-1]], 0)
+            keep = front > 1e-4
+            acc += (a * front * keep).transpose(0, 1) @ col[s:e]
+            T = T * torch.where(keep, om, torch.ones_like(om)).prod(0)
+    image = acc.reshape(H, W, -1).numpy()  # background 0, as the GPU render
+    sec = time.perf_counter() - t0
+    diff = np.abs(image - gpu_image)
+    return {"value": round(1.0 / sec, 4), "unit": "frames/s", "cores": threads,
+            "kind": "port",
+            "sample": f"1 forward of view {view} of {scene.name}: reference.py:16-74 as dense "
+                      f"torch-CPU fp32 over {m2.shape[0]} live Gaussians x {H * W} pixels, "
+                      f"chunks of {chunk} Gaussians; projection/SH by the C oracle",
+            "max_abs_vs_gpu": float(diff.max()),
+            "pixels_over_1e-3": int((diff.max(-1) > 1e-3).sum())}
+
+
 @contextlib.contextmanager
 def _no_gc():
     """Python's cyclic garbage collector off inside a timed region (as timeit
@@ -563,6 +627,12 @@ def main():
         out["cpu_baseline"] = cpu_baseline(scene, list(range(nviews)), workload)
     else:
         out["cpu_baseline"] = None
+    if args.config == 1 and not args.no_cpu_baseline:
+        print("bench: timing the dense reference path on the CPU ...", file=sys.stderr,
+              flush=True)
+        with torch.no_grad():
+            gpu_img = render(0).cpu().numpy()
+        out["reference_path_cpu"] = dense_reference_cpu(scene, 0, gpu_img)
     if args.profile_stages:
         print(json.dumps(stages, indent=1), file=sys.stderr)
     print(json.dumps(out), flush=True)

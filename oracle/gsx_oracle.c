@@ -764,13 +764,35 @@ int64_t orc_bin(int64_t n, const float* means2d, const float* radii,
 }
 
 /* ---------------------------------------------------------- rasterizer -- */
+/* The shipped arithmetic (arith = 0) and, for measuring how far it lies
+ * from the reference's literal expressions, three alternatives that can be
+ * combined (ORC_ARITH_* bits):
+ *  - LITERAL_POWER: rasterize.py:75-76 as written,
+ *    -0.5f * (a dx dx + c dy dy) - b dx dy, every product and sum rounded
+ *    separately in source order (the library builds with -ffp-contract=off);
+ *  - SEPARATE_ACC: rasterize.py:84 `acc += rgb * (alpha * T)` as a rounded
+ *    product then a rounded sum instead of one multiply-add;
+ *  - ROUNDED_EXP: metal::exp replaced by the float32 rounding of the
+ *    double-precision exp (the result a correctly rounded exp gives except in
+ *    rare double-rounding ties) instead of orc_splat_expf. */
+static inline float literal_power(float a, float b, float c, float dx, float dy) {
+    const float ax = a * dx, axx = ax * dx;
+    const float cy = c * dy, cyy = cy * dy;
+    const float bx = b * dx, bxy = bx * dy;
+    return -0.5f * (axx + cyy) - bxy;
+}
+
+float orc_literal_power(float a, float b, float c, float dx, float dy) {
+    return literal_power(a, b, c, dx, dy);
+}
+
 static void raster_tile_fwd(int64_t tile, int C, const float* means2d,
                             const float* conics, const float* opacities,
                             const float* feats, const float* depths,
                             const int32_t* ids, const int32_t* ranges,
                             const float* bg, int width, int height,
                             int tiles_x, float* out, float* final_T,
-                            int32_t* n_contrib, float* depth_out) {
+                            int32_t* n_contrib, float* depth_out, int arith) {
     const int tx = (int)(tile % tiles_x), ty = (int)(tile / tiles_x);
     const int start = ranges[2 * tile], num = ranges[2 * tile + 1] - ranges[2 * tile];
     float acc[64];
@@ -788,19 +810,36 @@ static void raster_tile_fwd(int64_t tile, int C, const float* means2d,
                 for (int j = 0; j < num; ++j) {
                     const int g = ids[start + j];
                     const float dx = means2d[2 * g] - pxf, dy = means2d[2 * g + 1] - pyf;
-                    const float power = orc_splat_power(conics[3 * g], conics[3 * g + 1],
-                                                        conics[3 * g + 2], dx, dy);
+                    const float* cg = conics + 3 * g;
+                    const float power =
+                        (arith & ORC_ARITH_LITERAL_POWER)
+                            ? literal_power(cg[0], cg[1], cg[2], dx, dy)
+                            : orc_splat_power(cg[0], cg[1], cg[2], dx, dy);
                     if (power > 0.0f) continue;
-                    const float alpha = fminf(0.99f, opacities[g] * orc_splat_expf(power));
+                    const float e = (arith & ORC_ARITH_ROUNDED_EXP)
+                                        ? (float)exp((double)power)
+                                        : orc_splat_expf(power);
+                    const float alpha = fminf(0.99f, opacities[g] * e);
                     if (alpha < 1.0f / 255.0f) continue;
                     const float next_T = T * (1.0f - alpha);
                     if (next_T < 1e-4f) break;
                     /* rasterize.py:84 `acc += rgb * (alpha * T)`, fused as Metal's
                      * default fast-math contraction compiles it */
                     const float w = alpha * T;
-                    for (int k = 0; k < nc; ++k)
-                        acc[k] = fmaf(feats[(int64_t)g * C + c0 + k], w, acc[k]);
-                    if (depths) dacc = fmaf(depths[g], w, dacc); /* rasterize.py:276-279 */
+                    if (arith & ORC_ARITH_SEPARATE_ACC) {
+                        for (int k = 0; k < nc; ++k) {
+                            const float t = feats[(int64_t)g * C + c0 + k] * w;
+                            acc[k] = acc[k] + t;
+                        }
+                        if (depths) {
+                            const float t = depths[g] * w;
+                            dacc = dacc + t;
+                        }
+                    } else {
+                        for (int k = 0; k < nc; ++k)
+                            acc[k] = fmaf(feats[(int64_t)g * C + c0 + k], w, acc[k]);
+                        if (depths) dacc = fmaf(depths[g], w, dacc); /* rasterize.py:276-279 */
+                    }
                     T = next_T;
                     last = j + 1;
                 }
@@ -824,6 +863,18 @@ void orc_raster_fwd(int64_t n, int C, const float* means2d,
                     const float* bg, int width, int height, float* out,
                     float* final_T, int32_t* n_contrib, float* depth_out,
                     const int32_t* tiles, int64_t n_tiles, int nthreads) {
+    orc_raster_fwd_arith(n, C, means2d, conics, opacities, feats, depths, sorted_ids,
+                         tile_ranges, bg, width, height, out, final_T, n_contrib, depth_out,
+                         tiles, n_tiles, nthreads, 0);
+}
+
+void orc_raster_fwd_arith(int64_t n, int C, const float* means2d,
+                          const float* conics, const float* opacities,
+                          const float* feats, const float* depths,
+                          const int32_t* sorted_ids, const int32_t* tile_ranges,
+                          const float* bg, int width, int height, float* out,
+                          float* final_T, int32_t* n_contrib, float* depth_out,
+                          const int32_t* tiles, int64_t n_tiles, int nthreads, int arith) {
     (void)n;
     const int tiles_x = (width + TILE - 1) / TILE;
     const int tiles_y = (height + TILE - 1) / TILE;
@@ -833,7 +884,7 @@ void orc_raster_fwd(int64_t n, int C, const float* means2d,
         const int64_t tile = tiles ? tiles[i] : i;
         raster_tile_fwd(tile, C, means2d, conics, opacities, feats, depths, sorted_ids,
                         tile_ranges, bg, width, height, tiles_x, out, final_T, n_contrib,
-                        depth_out);
+                        depth_out, arith);
     }
 }
 

@@ -124,6 +124,21 @@ void orc_raster_fwd(int64_t n, int C, const float* means2d,
                     float* final_T, int32_t* n_contrib, float* depth_out,
                     const int32_t* tiles, int64_t n_tiles, int nthreads);
 
+/* orc_raster_fwd with the arithmetic chosen by `arith` (0: as orc_raster_fwd;
+ * bits below: the reference's literal expressions, for measuring how many
+ * decisions the shipped arithmetic changes).  Not a parity target. */
+#define ORC_ARITH_LITERAL_POWER 1 /* rasterize.py:75-76 unfactored, op by op */
+#define ORC_ARITH_SEPARATE_ACC 2  /* rasterize.py:84 multiply then add */
+#define ORC_ARITH_ROUNDED_EXP 4   /* float32 rounding of the double exp */
+float orc_literal_power(float a, float b, float c, float dx, float dy);
+void orc_raster_fwd_arith(int64_t n, int C, const float* means2d,
+                          const float* conics, const float* opacities,
+                          const float* feats, const float* depths,
+                          const int32_t* sorted_ids, const int32_t* tile_ranges,
+                          const float* bg, int width, int height, float* out,
+                          float* final_T, int32_t* n_contrib, float* depth_out,
+                          const int32_t* tiles, int64_t n_tiles, int nthreads, int arith);
+
 void orc_raster_bwd(int64_t n, int C, const float* means2d,
                     const float* conics, const float* opacities,
                     const float* feats, const int32_t* sorted_ids,

@@ -90,6 +90,9 @@ def _declare(L):
     L.orc_bin.restype = _I64
     L.orc_raster_fwd.argtypes = [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
                                  _P, _P, _P, _P, _P, _I64, _I]
+    L.orc_raster_fwd_arith.argtypes = L.orc_raster_fwd.argtypes + [_I]
+    L.orc_literal_power.argtypes = [_F, _F, _F, _F, _F]
+    L.orc_literal_power.restype = _F
     L.orc_raster_bwd.argtypes = [_I64, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P,
                                  _P, _P, _P, _P, _P, _P, _I]
     L.orc_atanf.argtypes = [_F]
@@ -292,8 +295,18 @@ def bin_gaussians(means2d, radii, depths, width, height, threads=1, conics=None)
     return ids, ranges, tx, ty
 
 
+# arithmetic variants of raster_fwd (gsx_oracle.h ORC_ARITH_*): the
+# reference's literal expressions, for measurement only
+ARITH_LITERAL_POWER, ARITH_SEPARATE_ACC, ARITH_ROUNDED_EXP = 1, 2, 4
+
+
+def literal_power(a, b, c, dx, dy):
+    """rasterize.py:75-76's power as written, op by op in float32."""
+    return lib().orc_literal_power(a, b, c, dx, dy)
+
+
 def raster_fwd(means2d, conics, opacities, feats, sorted_ids, tile_ranges, width, height,
-               bg=None, depths=None, tiles=None, threads=1):
+               bg=None, depths=None, tiles=None, threads=1, arith=0):
     means2d, conics, opacities, feats = map(_f32, (means2d, conics, opacities, feats))
     sorted_ids, tile_ranges = _i32(sorted_ids), _i32(tile_ranges)
     n, C = feats.shape
@@ -304,10 +317,11 @@ def raster_fwd(means2d, conics, opacities, feats, sorted_ids, tile_ranges, width
     final_T = np.zeros((height, width), np.float32)
     n_contrib = np.zeros((height, width), np.int32)
     depth_out = np.zeros((height, width), np.float32) if depths is not None else None
-    lib().orc_raster_fwd(n, C, _ptr(means2d), _ptr(conics), _ptr(opacities), _ptr(feats),
-                         _ptr(depths), _ptr(sorted_ids), _ptr(tile_ranges), _ptr(bg), width,
-                         height, _ptr(out), _ptr(final_T), _ptr(n_contrib), _ptr(depth_out),
-                         _ptr(tiles), 0 if tiles is None else tiles.size, threads)
+    lib().orc_raster_fwd_arith(n, C, _ptr(means2d), _ptr(conics), _ptr(opacities),
+                               _ptr(feats), _ptr(depths), _ptr(sorted_ids), _ptr(tile_ranges),
+                               _ptr(bg), width, height, _ptr(out), _ptr(final_T),
+                               _ptr(n_contrib), _ptr(depth_out), _ptr(tiles),
+                               0 if tiles is None else tiles.size, threads, int(arith))
     return dict(image=out, final_T=final_T, n_contrib=n_contrib, depth=depth_out)
 
 
