@@ -41,132 +41,199 @@ using gsx::kWave;
 // a symmetric window with zero padding:
 //   dS_mean/dp = (F(dS/dmu_p) + 2 p F(dS/dE_pp) + t F(dS/dE_pt)) / n.
 
-constexpr int kSsT = 16;                  // output tile edge (16 x 16 threads)
-constexpr int kSsThreads = kSsT * kSsT;
-constexpr int kSsMaxR = 7;                // window radius up to 7 (15 taps)
-constexpr int kSsMaxCh = 4;               // channels per launch
+constexpr int kSsMaxR = 7;   // window radius up to 7 (15 taps)
+constexpr int kSsMaxCh = 4;  // channels per launch
+constexpr int kSsWaves = 4;  // strips (one per wave) per workgroup
+constexpr int kSsThreads = kSsWaves * kWave;
 
 struct SsimWindow {
     float g[2 * kSsMaxR + 1];
 };
 
-template <int R>
-struct SsimTile {
-    static constexpr int kSpan = kSsT + 2 * R;
+// Strip geometry.  A wave owns ssim_cols(CH) image columns of CH channels
+// (lane = column * CH + channel) and walks down ssim_rows(R) input rows,
+// which complete ssim_rows(R) - 2R output rows.  The input rows come in
+// chunks of the window length K = 2R + 1, so the ring of the last K rows'
+// horizontal sums is indexed by compile-time constants.  Each row is read
+// once from global memory (the window's halo rows and columns being the only
+// re-reads: (K - 1) / ssim_rows(R) and 2R / ssim_cols(CH) of the strip).
+constexpr int ssim_cols(int ch) { return kWave / ch; }
+constexpr int ssim_rows(int r) { return (2 * r + 1) * ((44 + 2 * r) / (2 * r + 1)); }
+
+// Strip and lane bookkeeping shared by the two kernels.
+template <int R, int CH>
+struct SsimStrip {
+    static constexpr int K = 2 * R + 1;
+    static constexpr int COLS = ssim_cols(CH);
+    static constexpr int SPAN = (COLS + 2 * R) * CH;  // floats of one input row
+    static constexpr int NL = (SPAN + kWave - 1) / kWave;  // row floats per lane
+    static constexpr int ROWS = ssim_rows(R);
+    static constexpr int TB = ROWS - 2 * R;  // output rows
+    int x0, y0, xl, ch;
+    bool col_out;          // the lane's output column exists
+    int off[NL];           // offsets of the lane's row elements within an image row
+    bool ok[NL];           // and whether they lie inside the image
+    __device__ SsimStrip(int strip, int strips_x, int W, int C, int c0, int lane) {
+        const int sx = strip % strips_x, sy = strip / strips_x;
+        x0 = sx * COLS;
+        y0 = sy * TB;
+        xl = lane / CH;
+        ch = lane - xl * CH;
+        col_out = xl < COLS && x0 + xl < W;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int e = lane + kWave * j, col = e / CH, c = e - col * CH;
+            const int gx = x0 - R + col;
+            ok[j] = e < SPAN && gx >= 0 && gx < W;
+            off[j] = ok[j] ? gx * C + c0 + c : 0;
+        }
+    }
+    // index of tap k of the lane's column in a staged row
+    __device__ int tap(int k) const { return (xl + k) * CH + ch; }
 };
 
-// Tile of this workgroup: linear ids go round-robin over the XCDs, and the
-// remap gives each XCD a contiguous band of tiles, so the halo rows that
-// neighbouring tiles share are fetched into one L2.
-__device__ __forceinline__ void ssim_tile(int tiles_x, int& x0, int& y0) {
-    const int t = (int)gsx::xcd_remap(blockIdx.x, gridDim.x);
-    x0 = (t % tiles_x) * kSsT;
-    y0 = (t / tiles_x) * kSsT;
-}
-
-// Loads channels [c0, c0 + CH) of the (16 + 2R)^2 window around the tile into
-// dst[c][y][x], zero outside the image.  Consecutive threads read consecutive
-// floats of the interleaved (H, W, C) rows.
-template <int R, int CH>
-__device__ __forceinline__ void load_halo(float (*dst)[SsimTile<R>::kSpan][SsimTile<R>::kSpan + 1],
-                                          const float* __restrict__ src, int H, int W, int C,
-                                          int c0, int x0, int y0) {
-    constexpr int S = SsimTile<R>::kSpan;
-    for (int i = threadIdx.x; i < S * S * CH; i += kSsThreads) {
-        const int ly = i / (S * CH);
-        const int rem = i - ly * (S * CH);
-        const int lx = rem / CH, c = rem - lx * CH;
-        const int gy = y0 - R + ly, gx = x0 - R + lx;
-        float v = 0.0f;
-        if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = src[((int64_t)gy * W + gx) * C + c0 + c];
-        dst[c][ly][lx] = v;
+// One input row of one array into registers (zero outside the image).  The
+// loads are unconditional (outside the image they read element 0 and the
+// value is dropped): loads under branches would make the compiler wait for
+// every outstanding load, the prefetched rows included, at the next use.
+template <int NL>
+__device__ __forceinline__ void ssim_fetch(const float* __restrict__ src, int64_t row_base,
+                                           bool row_ok, const int (&off)[NL],
+                                           const bool (&ok)[NL], float (&v)[NL]) {
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const bool in = row_ok && ok[j];
+        const float x = src[in ? row_base + off[j] : 0];
+        v[j] = in ? x : 0.0f;
     }
 }
+
+// Keeps the compiler from moving the wave's LDS row accesses across the
+// point (lanes read what other lanes of the wave wrote; the hardware
+// executes one wave's LDS operations in order).
+__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
 
 template <int R, int CH>
 __global__ __launch_bounds__(kSsThreads) void k_ssim_fwd(
     const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C, int c0,
-    int tiles_x, SsimWindow win, float c1, float c2, float* __restrict__ maps,
+    int strips_x, int n_strips, SsimWindow win, float c1, float c2, float* __restrict__ maps,
     float* __restrict__ partials) {
-    constexpr int S = SsimTile<R>::kSpan;
-    constexpr int K = 2 * R + 1;
-    __shared__ float s_p[CH][S][S + 1];
-    __shared__ float s_t[CH][S][S + 1];
-    __shared__ float s_h[5][S][kSsT + 1];
-    __shared__ float s_red[2][kSsThreads / kWave];
+    using S = SsimStrip<R, CH>;
+    constexpr int K = S::K, NL = S::NL;
+    __shared__ float s_row[kSsWaves][2][NL * kWave];
+    __shared__ float s_red[2][kSsWaves];
 
-    const int tid = threadIdx.x;
-    const int tx = tid & (kSsT - 1), ty = tid / kSsT;
-    int x0, y0;
-    ssim_tile(tiles_x, x0, y0);
-    const int x = x0 + tx, y = y0 + ty;
-    const bool inside = x < W && y < H;
-    const int64_t plane = (int64_t)H * W * C;
-    const int64_t pix = ((int64_t)y * W + x) * C + c0;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int strip = (int)gsx::xcd_remap(blockIdx.x, gridDim.x) * kSsWaves + wave;
     float l1 = 0.0f, ssum = 0.0f;
-
-    load_halo<R, CH>(s_p, pred, H, W, C, c0, x0, y0);
-    load_halo<R, CH>(s_t, tgt, H, W, C, c0, x0, y0);
-    __syncthreads();
+    if (strip < n_strips) {
+        const S s(strip, strips_x, W, C, c0, lane);
+        float* sp = s_row[wave][0];
+        float* stt = s_row[wave][1];
+        const int64_t plane = (int64_t)H * W * C;
+        const int64_t rstride = (int64_t)W * C;
+        // rows i + 1 and i + 2 in flight while row i is filtered
+        float p0[NL], t0[NL], p1[NL], t1[NL], p2[NL], t2[NL];
+        auto fetch = [&](int i, float (&vp)[NL], float (&vt)[NL]) {
+            const int gy = s.y0 - R + i;
+            const bool row_ok = i < S::ROWS && gy >= 0 && gy < H;
+            const int64_t base = row_ok ? (int64_t)gy * rstride : 0;
+            ssim_fetch<NL>(pred, base, row_ok, s.off, s.ok, vp);
+            ssim_fetch<NL>(tgt, base, row_ok, s.off, s.ok, vt);
+        };
+        fetch(0, p1, t1);
+        fetch(1, p2, t2);
+        float ring[K][5];  // horizontal sums of the last K rows: p, t, pp, tt, pt
 #pragma unroll 1
-    for (int c = 0; c < CH; ++c) {
-        for (int i = tid; i < S * kSsT; i += kSsThreads) {
-            const int ly = i / kSsT, lx = i - ly * kSsT;
-            float a = 0.0f, b = 0.0f, pp = 0.0f, tt = 0.0f, pt = 0.0f;
+        for (int i0 = 0; i0 < S::ROWS; i0 += K) {
 #pragma unroll
-            for (int k = 0; k < K; ++k) {
-                const float w = win.g[k], p = s_p[c][ly][lx + k], t = s_t[c][ly][lx + k];
-                a = fmaf(w, p, a);
-                b = fmaf(w, t, b);
-                pp = fmaf(w, p * p, pp);
-                tt = fmaf(w, t * t, tt);
-                pt = fmaf(w, p * t, pt);
+            for (int u = 0; u < K; ++u) {
+                const int i = i0 + u;
+#pragma unroll
+                for (int j = 0; j < NL; ++j) {
+                    p0[j] = p1[j];
+                    t0[j] = t1[j];
+                    p1[j] = p2[j];
+                    t1[j] = t2[j];
+                }
+                fetch(i + 2, p2, t2);
+                wave_lds_order();
+#pragma unroll
+                for (int j = 0; j < NL; ++j) {
+                    sp[lane + kWave * j] = p0[j];
+                    stt[lane + kWave * j] = t0[j];
+                }
+                wave_lds_order();
+                float a = 0.0f, b = 0.0f, pp = 0.0f, tt = 0.0f, pt = 0.0f, pc = 0.0f, tc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    const float w = win.g[k], p = sp[s.tap(k)], t = stt[s.tap(k)];
+                    if (k == R) {
+                        pc = p;
+                        tc = t;
+                    }
+                    a = fmaf(w, p, a);
+                    b = fmaf(w, t, b);
+                    pp = fmaf(w, p * p, pp);
+                    tt = fmaf(w, t * t, tt);
+                    pt = fmaf(w, p * t, pt);
+                }
+                ring[u][0] = a;
+                ring[u][1] = b;
+                ring[u][2] = pp;
+                ring[u][3] = tt;
+                ring[u][4] = pt;
+                // |p - t| at the centre of output row i - R
+                const int oc = i - R;
+                if (s.col_out && oc >= 0 && oc < S::TB && s.y0 + oc < H) l1 += fabsf(pc - tc);
+                // output row o = i - 2R: rows o .. i sit in ring slots (u + 1 + k) mod K
+                const int o = i - 2 * R;
+                if (o >= 0 && o < S::TB) {
+                    float mp = 0.0f, mt = 0.0f, epp = 0.0f, ett = 0.0f, ept = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < K; ++k) {
+                        const int q = (u + 1 + k) % K;
+                        const float w = win.g[k];
+                        mp = fmaf(w, ring[q][0], mp);
+                        mt = fmaf(w, ring[q][1], mt);
+                        epp = fmaf(w, ring[q][2], epp);
+                        ett = fmaf(w, ring[q][3], ett);
+                        ept = fmaf(w, ring[q][4], ept);
+                    }
+                    const int y = s.y0 + o;
+                    if (s.col_out && y < H) {
+                        const float mpp = mp * mp, mtt = mt * mt, mpt = mp * mt;
+                        const float A = 2.0f * mpt + c1, B = mpp + mtt + c1;
+                        const float Cn = 2.0f * (ept - mpt) + c2, D = (epp - mpp) + (ett - mtt) + c2;
+                        // reciprocals to about 1 ulp (the loss is compared in
+                        // float32 against a double-precision restatement)
+                        const float rB = __builtin_amdgcn_rcpf(B), rD = __builtin_amdgcn_rcpf(D);
+                        const float cs = Cn * rD, l = A * rB;
+                        ssum += l * cs;
+                        const int64_t pix = (int64_t)y * rstride + (int64_t)(s.x0 + s.xl) * C + c0 +
+                                            s.ch;
+                        maps[pix] = 2.0f * (mt - l * mp) * cs * rB + 2.0f * l * (mp * cs - mt) * rD;
+                        maps[plane + pix] = -l * cs * rD;
+                        maps[2 * plane + pix] = 2.0f * l * rD;
+                    }
+                }
             }
-            s_h[0][ly][lx] = a;
-            s_h[1][ly][lx] = b;
-            s_h[2][ly][lx] = pp;
-            s_h[3][ly][lx] = tt;
-            s_h[4][ly][lx] = pt;
         }
-        __syncthreads();
-        float mp = 0.0f, mt = 0.0f, epp = 0.0f, ett = 0.0f, ept = 0.0f;
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const float w = win.g[k];
-            mp = fmaf(w, s_h[0][ty + k][tx], mp);
-            mt = fmaf(w, s_h[1][ty + k][tx], mt);
-            epp = fmaf(w, s_h[2][ty + k][tx], epp);
-            ett = fmaf(w, s_h[3][ty + k][tx], ett);
-            ept = fmaf(w, s_h[4][ty + k][tx], ept);
-        }
-        if (inside) {
-            const float p = s_p[c][ty + R][tx + R], t = s_t[c][ty + R][tx + R];
-            const float mpp = mp * mp, mtt = mt * mt, mpt = mp * mt;
-            const float A = 2.0f * mpt + c1, B = mpp + mtt + c1;
-            const float Cn = 2.0f * (ept - mpt) + c2, D = (epp - mpp) + (ett - mtt) + c2;
-            const float cs = Cn / D, l = A / B;
-            ssum += l * cs;
-            l1 += fabsf(p - t);
-            maps[pix + c] = 2.0f * (mt - l * mp) * cs / B + 2.0f * l * (mp * cs - mt) / D;
-            maps[plane + pix + c] = -l * cs / D;
-            maps[2 * plane + pix + c] = 2.0f * l / D;
-        }
-        __syncthreads();
     }
 #pragma unroll
     for (int o = kWave / 2; o > 0; o >>= 1) {
         l1 += __shfl_xor(l1, o, kWave);
         ssum += __shfl_xor(ssum, o, kWave);
     }
-    if ((tid & (kWave - 1)) == 0) {
-        s_red[0][tid / kWave] = l1;
-        s_red[1][tid / kWave] = ssum;
+    if (lane == 0) {
+        s_red[0][wave] = l1;
+        s_red[1][wave] = ssum;
     }
     __syncthreads();
-    if (tid == 0) {
+    if (threadIdx.x == 0) {
         float a = 0.0f, b = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kSsThreads / kWave; ++w) {
+        for (int w = 0; w < kSsWaves; ++w) {
             a += s_red[0][w];
             b += s_red[1][w];
         }
@@ -202,62 +269,93 @@ __global__ __launch_bounds__(256) void k_loss_reduce(const float* __restrict__ p
     }
 }
 
-// grad_pred = g_l1 sign(p - t) / n + g_ssim (F(dmu) + 2 p F(dpp) + t F(dpt)) / n
+// grad_pred = g_l1 sign(p - t) / n + g_ssim (F(dmu) + 2 p F(dpp) + t F(dpt)) / n,
+// F over the three maps in the strip walk of k_ssim_fwd.
 template <int R, int CH>
 __global__ __launch_bounds__(kSsThreads) void k_ssim_bwd(
     const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C, int c0,
-    int tiles_x, SsimWindow win, const float* __restrict__ maps, const float* __restrict__ grad_in,
-    float inv_n, float* __restrict__ grad) {
-    constexpr int S = SsimTile<R>::kSpan;
-    constexpr int K = 2 * R + 1;
-    __shared__ float s_m[3][CH][S][S + 1];
-    __shared__ float s_h[3][S][kSsT + 1];
+    int strips_x, int n_strips, SsimWindow win, const float* __restrict__ maps,
+    const float* __restrict__ grad_in, float inv_n, float* __restrict__ grad) {
+    using S = SsimStrip<R, CH>;
+    constexpr int K = S::K, NL = S::NL;
+    __shared__ float s_row[kSsWaves][3][NL * kWave];
 
-    const int tid = threadIdx.x;
-    const int tx = tid & (kSsT - 1), ty = tid / kSsT;
-    int x0, y0;
-    ssim_tile(tiles_x, x0, y0);
-    const int x = x0 + tx, y = y0 + ty;
-    const bool inside = x < W && y < H;
-    const int64_t plane = (int64_t)H * W * C;
-    const int64_t pix = ((int64_t)y * W + x) * C + c0;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int strip = (int)gsx::xcd_remap(blockIdx.x, gridDim.x) * kSsWaves + wave;
+    if (strip >= n_strips) return;
+    const S s(strip, strips_x, W, C, c0, lane);
     const float gl = grad_in[0] * inv_n, gs = grad_in[1] * inv_n;
-
+    const int64_t plane = (int64_t)H * W * C;
+    const int64_t rstride = (int64_t)W * C;
+    const int64_t col = (int64_t)(s.x0 + s.xl) * C + c0 + s.ch;
+    float* sm[3] = {s_row[wave][0], s_row[wave][1], s_row[wave][2]};
+    // row i + 1 and i + 2 of the maps in flight, with pred and target at
+    // the output pixel those rows complete
+    struct Row {
+        float m[3][NL];
+        float p, t;
+    };
+    Row r0, r1, r2;
+    auto fetch = [&](int i, Row& v) {
+        const int gy = s.y0 - R + i;
+        const bool row_ok = i < S::ROWS && gy >= 0 && gy < H;
+        const int64_t base = row_ok ? (int64_t)gy * rstride : 0;
 #pragma unroll
-    for (int q = 0; q < 3; ++q) load_halo<R, CH>(s_m[q], maps + q * plane, H, W, C, c0, x0, y0);
-    __syncthreads();
+        for (int q = 0; q < 3; ++q) ssim_fetch<NL>(maps + q * plane, base, row_ok, s.off, s.ok, v.m[q]);
+        const int yo = s.y0 + i - 2 * R;
+        const bool out_ok = s.col_out && i >= 2 * R && i < S::ROWS && yo < H;
+        const int64_t pix = out_ok ? (int64_t)yo * rstride + col : 0;
+        v.p = pred[pix];  // element 0 when out_ok is false: unused
+        v.t = tgt[pix];
+    };
+    fetch(0, r1);
+    fetch(1, r2);
+    float ring[K][3];
 #pragma unroll 1
-    for (int c = 0; c < CH; ++c) {
-        for (int i = tid; i < S * kSsT; i += kSsThreads) {
-            const int ly = i / kSsT, lx = i - ly * kSsT;
+    for (int i0 = 0; i0 < S::ROWS; i0 += K) {
+#pragma unroll
+        for (int u = 0; u < K; ++u) {
+            const int i = i0 + u;
+            r0 = r1;
+            r1 = r2;
+            fetch(i + 2, r2);
+            wave_lds_order();
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+#pragma unroll
+                for (int j = 0; j < NL; ++j) sm[q][lane + kWave * j] = r0.m[q][j];
+            wave_lds_order();
             float a = 0.0f, b = 0.0f, d = 0.0f;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
                 const float w = win.g[k];
-                a = fmaf(w, s_m[0][c][ly][lx + k], a);
-                b = fmaf(w, s_m[1][c][ly][lx + k], b);
-                d = fmaf(w, s_m[2][c][ly][lx + k], d);
+                a = fmaf(w, sm[0][s.tap(k)], a);
+                b = fmaf(w, sm[1][s.tap(k)], b);
+                d = fmaf(w, sm[2][s.tap(k)], d);
             }
-            s_h[0][ly][lx] = a;
-            s_h[1][ly][lx] = b;
-            s_h[2][ly][lx] = d;
-        }
-        __syncthreads();
-        float fm = 0.0f, fpp = 0.0f, fpt = 0.0f;
+            ring[u][0] = a;
+            ring[u][1] = b;
+            ring[u][2] = d;
+            const int o = i - 2 * R;
+            if (o >= 0 && o < S::TB) {
+                float fm = 0.0f, fpp = 0.0f, fpt = 0.0f;
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const float w = win.g[k];
-            fm = fmaf(w, s_h[0][ty + k][tx], fm);
-            fpp = fmaf(w, s_h[1][ty + k][tx], fpp);
-            fpt = fmaf(w, s_h[2][ty + k][tx], fpt);
+                for (int k = 0; k < K; ++k) {
+                    const int q = (u + 1 + k) % K;
+                    const float w = win.g[k];
+                    fm = fmaf(w, ring[q][0], fm);
+                    fpp = fmaf(w, ring[q][1], fpp);
+                    fpt = fmaf(w, ring[q][2], fpt);
+                }
+                const int y = s.y0 + o;
+                if (s.col_out && y < H) {
+                    const float p = r0.p, t = r0.t;
+                    const float sgn = (float)((p > t) - (p < t));
+                    const float gss = fm + 2.0f * p * fpp + t * fpt;
+                    grad[(int64_t)y * rstride + col] = fmaf(gs, gss, gl * sgn);
+                }
+            }
         }
-        if (inside) {
-            const float p = pred[pix + c], t = tgt[pix + c];
-            const float sgn = (float)((p > t) - (p < t));
-            const float gss = fm + 2.0f * p * fpp + t * fpt;
-            grad[pix + c] = fmaf(gs, gss, gl * sgn);
-        }
-        __syncthreads();
     }
 }
 
@@ -375,8 +473,30 @@ bool make_window(int32_t window_size, float sigma, SsimWindow& w) {
     return true;
 }
 
+// Strips of a launch over `ch` channels with window radius r, and its
+// workgroups (one partial pair each).
+struct SsimGeom {
+    int strips_x;
+    int n_strips;
+    int64_t blocks;
+};
+SsimGeom ssim_geom(int32_t H, int32_t W, int r, int ch) {
+    const int cols = ssim_cols(ch), tb = ssim_rows(r) - 2 * r;
+    SsimGeom g;
+    g.strips_x = (W + cols - 1) / cols;
+    const int64_t n = (int64_t)g.strips_x * ((H + tb - 1) / tb);
+    g.n_strips = (int)std::min<int64_t>(n, 0x7FFFFFFF);
+    g.blocks = (n + kSsWaves - 1) / kSsWaves;
+    return g;
+}
+
+// Partial pairs one launch may write, over every window radius and channel
+// count (the workspace does not depend on the window).
 int64_t photometric_blocks(int32_t H, int32_t W) {
-    return (int64_t)((W + kSsT - 1) / kSsT) * ((H + kSsT - 1) / kSsT);
+    int64_t m = 0;
+    for (int r = 0; r <= kSsMaxR; ++r)
+        for (int ch = 1; ch <= kSsMaxCh; ++ch) m = std::max(m, ssim_geom(H, W, r, ch).blocks);
+    return m;
 }
 
 int64_t photometric_groups(int32_t C) { return (C + kSsMaxCh - 1) / kSsMaxCh; }
@@ -525,19 +645,21 @@ int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const f
     float* maps = (float*)workspace;
     float* partials = (float*)((char*)workspace +
                                align256(3 * (int64_t)height * width * channels * 4));
-    const int tiles_x = (width + kSsT - 1) / kSsT;
-    const int64_t nblk = photometric_blocks(height, width);
     hipStream_t st = (hipStream_t)stream;
+    int64_t n_part = 0;  // partial pairs written so far, launches back to back
     for (int c0 = 0; c0 < channels; c0 += kSsMaxCh) {
         const int nc = std::min(kSsMaxCh, channels - c0);
-        float* part = partials + 2 * (c0 / kSsMaxCh) * nblk;
+        const SsimGeom g = ssim_geom(height, width, window_size / 2, nc);
+        if (g.blocks > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
+        float* part = partials + 2 * n_part;
+        n_part += g.blocks;
         const int key = (window_size / 2) * 8 + nc;
         switch (key) {
 #define GSX_SSIM_FWD(RR, CC)                                                                   \
     case RR * 8 + CC:                                                                          \
-        hipLaunchKernelGGL((k_ssim_fwd<RR, CC>), dim3((unsigned)nblk), dim3(kSsThreads), 0, st, \
-                           pred, target, height, width, channels, c0, tiles_x, win, c1, c2,     \
-                           maps, part);                                                        \
+        hipLaunchKernelGGL((k_ssim_fwd<RR, CC>), dim3((unsigned)g.blocks), dim3(kSsThreads), 0, \
+                           st, pred, target, height, width, channels, c0, g.strips_x,           \
+                           g.n_strips, win, c1, c2, maps, part);                               \
         break;
 #define GSX_SSIM_FWD_R(RR) GSX_SSIM_FWD(RR, 1) GSX_SSIM_FWD(RR, 2) GSX_SSIM_FWD(RR, 3) GSX_SSIM_FWD(RR, 4)
             GSX_SSIM_FWD_R(0)
@@ -556,8 +678,7 @@ int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const f
         GSX_LAUNCH_CHECK();
     }
     const double inv_n = 1.0 / ((double)height * width * channels);
-    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, partials,
-                       photometric_groups(channels) * nblk, inv_n, out);
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, partials, n_part, inv_n, out);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
@@ -574,19 +695,19 @@ int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const f
     if (workspace_bytes < gsx_photometric_workspace_bytes(height, width, channels))
         return GSX_ERR_WORKSPACE;
     const float inv_n = (float)(1.0 / ((double)height * width * channels));
-    const int tiles_x = (width + kSsT - 1) / kSsT;
-    const int64_t nblk = photometric_blocks(height, width);
     hipStream_t st = (hipStream_t)stream;
     const float* maps = (const float*)workspace;
     for (int c0 = 0; c0 < channels; c0 += kSsMaxCh) {
         const int nc = std::min(kSsMaxCh, channels - c0);
+        const SsimGeom g = ssim_geom(height, width, window_size / 2, nc);
+        if (g.blocks > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
         const int key = (window_size / 2) * 8 + nc;
         switch (key) {
 #define GSX_SSIM_BWD(RR, CC)                                                                   \
     case RR * 8 + CC:                                                                          \
-        hipLaunchKernelGGL((k_ssim_bwd<RR, CC>), dim3((unsigned)nblk), dim3(kSsThreads), 0, st, \
-                           pred, target, height, width, channels, c0, tiles_x, win, maps,       \
-                           grad_out, inv_n, grad_pred);                                        \
+        hipLaunchKernelGGL((k_ssim_bwd<RR, CC>), dim3((unsigned)g.blocks), dim3(kSsThreads), 0, \
+                           st, pred, target, height, width, channels, c0, g.strips_x,           \
+                           g.n_strips, win, maps, grad_out, inv_n, grad_pred);                 \
         break;
 #define GSX_SSIM_BWD_R(RR) GSX_SSIM_BWD(RR, 1) GSX_SSIM_BWD(RR, 2) GSX_SSIM_BWD(RR, 3) GSX_SSIM_BWD(RR, 4)
             GSX_SSIM_BWD_R(0)
