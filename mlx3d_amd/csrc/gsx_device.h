@@ -21,9 +21,9 @@ constexpr int kWave = 64;            // CDNA wavefront
 // exp(x): Cody-Waite reduction x = k ln2 + r (ln2 as a 16-bit head plus a
 // tail), degree-7 Taylor polynomial of e^r in Horner form with fused
 // multiply-adds, exact scaling by 2^k.  Returns 0 below -86 and +inf above
-// 88.  Stands in for metal::exp (rasterize.py:80,171,274) and for the
-// activations of model.py:116-122.  The CPU oracle evaluates the same
-// sequence of correctly rounded operations, so both agree bit for bit.
+// 88.  The exp of the activations of model.py:116-122 (the compositing
+// loops use their own splat_exp, raster.hip).  The CPU oracle evaluates the
+// same sequence of correctly rounded operations, so both agree bit for bit.
 __device__ __forceinline__ float dexp(float x) {
     if (x != x) return x;
     if (x < -86.0f) return 0.0f;
