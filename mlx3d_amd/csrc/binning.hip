@@ -408,7 +408,10 @@ __global__ __launch_bounds__(kScanThreads) void k_count_scan(
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) c[j] = i0 + j < n ? counts[gids[i0 + j]] : 0u;
     uint32_t total;
-    const uint32_t excl = block_excl_scan<kScanThreads>(c[0] + c[1] + c[2] + c[3], s_w, &total);
+    uint32_t csum = 0;
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) csum += c[j];
+    const uint32_t excl = block_excl_scan<kScanThreads>(csum, s_w, &total);
     if (tid == 0) {
         uint32_t prefix = 0;
         uint32_t* st = status + chunk;
