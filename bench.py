@@ -63,7 +63,7 @@ def _parse():
 KERNEL_SYMBOL = {"raster_fwd": "k_raster_fwd", "raster_bwd": "k_raster_bwd",
                  "preprocess_fwd": "k_preprocess_fwd", "preprocess_bwd": "k_preprocess_bwd",
                  "photometric_fwd": "k_ssim_fwd", "photometric_bwd": "k_ssim_bwd",
-                 "adam": "k_adam"}
+                 "adam": "k_adam", "preprocess_bwd_adam": "k_preprocess_bwd_adam"}
 COPY_PROBE_KERNEL = "k_debug_expf"
 
 
@@ -419,11 +419,15 @@ def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool,
     N = model.num_gaussians
     P = cams[0].width * cams[0].height
     floats = sum(int(v[0].numel()) for v in model.params.values())  # per Gaussian
+    # the fused preprocess VJP + Adam: parameters and both moments read and
+    # written (24 B per float), the rasterizer's per-Gaussian cotangents and
+    # the SH colours read (48 B per Gaussian)
     algo = {"photometric_fwd": 20 * P * 3, "photometric_bwd": 24 * P * 3,
-            "adam": 28 * N * floats}
+            "adam": 28 * N * floats, "preprocess_bwd_adam": N * (24 * floats + 48)}
     stages = {}
     for name in ("preprocess_fwd", "binning", "raster_fwd", "photometric_fwd",
-                 "photometric_bwd", "raster_bwd", "preprocess_bwd", "adam"):
+                 "photometric_bwd", "raster_bwd", "preprocess_bwd", "adam",
+                 "preprocess_bwd_adam"):
         t = timer.mean_ms(name)
         if math.isnan(t):
             continue
@@ -434,7 +438,8 @@ def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool,
                                  "algorithmic_bytes": int(algo[name]),
                                  "traffic": _traffic(name, workload)})
     return {"ms": round(ms, 4), "it_s": round(1e3 / ms, 3), "steps": steps,
-            "what": "GaussianTrainer.step: render fwd+bwd, L1 + 0.2 D-SSIM, Adam (6 groups)",
+            "what": "GaussianTrainer.step: render fwd+bwd, L1 + 0.2 D-SSIM, Adam (6 groups, "
+                    "fused into the preprocess backward)",
             "stages": stages}
 
 

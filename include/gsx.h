@@ -421,6 +421,27 @@ typedef struct gsx_adam_group {
 int gsx_adam_step(int32_t num_groups, const gsx_adam_group* groups,
                   float beta1, float beta2, float eps, void* stream);
 
+/* gsx_preprocess_bwd followed by gsx_adam_step on the six parameter groups
+ * of GaussianTrainer.step (trainer.py:339-342 after the autodiff VJP of
+ * render.py:73-80 / model.py:116-126), fused: every gradient goes from
+ * registers into the Adam update of its parameter, so the gradients are
+ * never written out and read back.  The reference has no single call for
+ * this; the updates are those gsx_adam_step applies to the gradients
+ * gsx_preprocess_bwd writes, bit for bit.  groups[6]: means, quats, scales,
+ * opacities, sh_dc, sh_rest (param = the tensor passed here, n = its float
+ * count, grad unused); SH in split layout with contiguous rows (sh_dc (N,3),
+ * sh_rest (N, 3 (K-1)), K >= 1), moments with the parameters' layouts,
+ * quats and its moments 16-byte aligned.  Parameters and moments are
+ * updated in place.  K = 1: groups[5] is not read. */
+int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, float* quats,
+                            float* scales, float* opacities, float* sh_dc, float* sh_rest,
+                            const float* colors_out, int32_t K, int32_t degree, uint32_t flags,
+                            float blur, const float* g_means2d, const float* g_conics,
+                            const float* g_opac_eff, const float* g_colors,
+                            const float* g_means2d_extra, const float* g_depths,
+                            const float* g_compensation, const gsx_adam_group* groups,
+                            float beta1, float beta2, float eps, void* stream);
+
 /* Replaces the density-control statistics of trainer.py:357-365:
  * grad_accum += |(g.x W/2, g.y H/2)| * (radii > 0); grad_count += (radii > 0).
  * g_means2d (N,2) is dL/dmeans2d of the rasterizer (the reference's

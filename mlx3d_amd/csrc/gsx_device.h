@@ -42,6 +42,18 @@ __device__ __forceinline__ float dexp(float x) {
     return ldexpf(p, (int)k);
 }
 
+// One Adam update (mlx.optimizers.Adam.apply_single without bias
+// correction, trainer.py:128, 339-342):
+//   m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g^2;  p = p - lr m / (sqrt(v) + eps)
+// in float32, each operation rounded once, in this order.
+__device__ __forceinline__ void adam_update(float& p, float g, float& m, float& v, float lr,
+                                            float b1, float omb1, float b2, float omb2,
+                                            float eps) {
+    m = b1 * m + omb1 * g;
+    v = b2 * v + omb2 * (g * g);
+    p = p - (lr * m) / (sqrtf(v) + eps);
+}
+
 // Sort key whose unsigned order is the float order of z (-0 folded onto +0,
 // NaN after +inf).
 __device__ __forceinline__ uint32_t depth_key(float z) {

@@ -333,6 +333,77 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     rects[i] = rect;
 }
 
+// Gradients of one Gaussian's stored parameters (means, quaternion, scales
+// and opacity as stored, before the activations `flags` select) from the
+// cotangents of the forward's outputs, and with SH the colour cotangent
+// after the clamp mask (gc), the basis (bk) and the active count (Ka).
+struct RawGrads {
+    float means[3], quat[4], scales[3], opacity;
+    float gc[3], bk[16];
+    int Ka;
+};
+
+template <bool UT>
+__device__ __forceinline__ void preprocess_vjp(
+    const gsx_camera& cam, int64_t i, float m0, float m1, float m2, float4 q, float r0, float r1,
+    float r2, float ro, uint32_t flags, float blur, bool aa, bool sh, int degree,
+    const float* __restrict__ colors_out, const float2* __restrict__ g_means2d,
+    const float* __restrict__ g_conics, const float* __restrict__ g_opac_eff,
+    const float* __restrict__ g_colors, const float2* __restrict__ g_means2d_extra,
+    const float* __restrict__ g_depths, const float* __restrict__ g_comp, RawGrads& G) {
+    const float sx = act_scale(r0, flags);
+    const float sy = act_scale(r1, flags);
+    const float sz = act_scale(r2, flags);
+    const float o = act_opacity(ro, flags);
+    typename ProjOf<UT>::T p;
+    project_any<UT>(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
+    const float goe = g_opac_eff[i];
+    const float g_o = goe * p.comp;
+    const float g_comp_total = (g_comp ? g_comp[i] : 0.0f) + goe * o;
+    float2 gm2 = g_means2d[i];
+    if (g_means2d_extra) {
+        const float2 e = g_means2d_extra[i];
+        gm2.x += e.x;
+        gm2.y += e.y;
+    }
+    float gs[3];
+    project_any_vjp<UT>(cam, p, m0, m1, m2, aa, gm2.x, gm2.y, g_conics[3 * i],
+                        g_conics[3 * i + 1], g_conics[3 * i + 2],
+                        g_depths ? g_depths[i] : 0.0f, g_comp_total, G.means, G.quat, gs);
+    const bool ls = flags & GSX_LOG_SCALES;
+    G.scales[0] = ls ? gs[0] * sx : gs[0];
+    G.scales[1] = ls ? gs[1] * sy : gs[1];
+    G.scales[2] = ls ? gs[2] * sz : gs[2];
+    G.opacity = (flags & GSX_LOGIT_OPACITY) ? g_o * o * (1.0f - o) : g_o;
+    G.Ka = 0;
+    if (sh) {
+        float dx, dy, dz;
+        view_dir(cam, m0, m1, m2, dx, dy, dz);
+        sh_basis(degree, dx, dy, dz, G.bk);
+        G.Ka = (degree + 1) * (degree + 1);
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch)
+            G.gc[ch] = (colors_out[3 * i + ch] > 0.0f) ? g_colors[3 * i + ch] : 0.0f;
+    }
+}
+
+// The SH coefficient gradients bk[k] gc (zero for k >= Ka) of coefficients
+// k0 .. K - 1 into dst[3 (k - k0) + ch].  The basis is indexed with
+// compile-time constants (a runtime index would move it to scratch); the
+// coefficients past 16 have no basis value, their gradient is zero.
+__device__ __forceinline__ void sh_grad_rows(const RawGrads& G, int K, int k0, float* dst) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        if (k < k0 || k >= K) continue;
+        const float bv = (k < G.Ka) ? G.bk[k] : 0.0f;
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) dst[3 * (k - k0) + ch] = bv * G.gc[ch];
+    }
+    for (int k = 16; k < K; ++k)
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) dst[3 * (k - k0) + ch] = 0.0f;
+}
+
 // VJP of k_preprocess_fwd, one Gaussian per lane.  SH gradients (zero for
 // coefficients >= Ka) are written through LDS rows in the same sh_mode
 // layouts as the forward reads.
@@ -353,63 +424,28 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
     const int64_t i = g0 + threadIdx.x;
     const int pad = sh_cols | 1;
     if (i < n) {
-        const float m0 = means[3 * i], m1 = means[3 * i + 1], m2 = means[3 * i + 2];
-        const float4 q = quats[i];
-        const float sx = act_scale(scales[3 * i], flags);
-        const float sy = act_scale(scales[3 * i + 1], flags);
-        const float sz = act_scale(scales[3 * i + 2], flags);
-        const float o = act_opacity(opacities[i], flags);
-        typename ProjOf<UT>::T p;
-        project_any<UT>(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
-        const float goe = g_opac_eff[i];
-        const float g_o = goe * p.comp;
-        const float g_comp_total = (g_comp ? g_comp[i] : 0.0f) + goe * o;
-        float2 gm2 = g_means2d[i];
-        if (g_means2d_extra) {
-            const float2 e = g_means2d_extra[i];
-            gm2.x += e.x;
-            gm2.y += e.y;
-        }
-        float gm[3], gq[4], gs[3];
-        project_any_vjp<UT>(cam, p, m0, m1, m2, aa, gm2.x, gm2.y, g_conics[3 * i],
-                            g_conics[3 * i + 1], g_conics[3 * i + 2],
-                            g_depths ? g_depths[i] : 0.0f, g_comp_total, gm, gq, gs);
-        g_means[3 * i] = gm[0];
-        g_means[3 * i + 1] = gm[1];
-        g_means[3 * i + 2] = gm[2];
-        g_quats[i] = make_float4(gq[0], gq[1], gq[2], gq[3]);
-        const bool ls = flags & GSX_LOG_SCALES;
-        g_scales[3 * i] = ls ? gs[0] * sx : gs[0];
-        g_scales[3 * i + 1] = ls ? gs[1] * sy : gs[1];
-        g_scales[3 * i + 2] = ls ? gs[2] * sz : gs[2];
-        g_opacities[i] = (flags & GSX_LOGIT_OPACITY) ? g_o * o * (1.0f - o) : g_o;
+        RawGrads G;
+        preprocess_vjp<UT>(cam, i, means[3 * i], means[3 * i + 1], means[3 * i + 2], quats[i],
+                           scales[3 * i], scales[3 * i + 1], scales[3 * i + 2], opacities[i],
+                           flags, blur, aa, g_sh0 != nullptr, degree, colors_out, g_means2d,
+                           g_conics, g_opac_eff, g_colors, g_means2d_extra, g_depths, g_comp, G);
+        g_means[3 * i] = G.means[0];
+        g_means[3 * i + 1] = G.means[1];
+        g_means[3 * i + 2] = G.means[2];
+        g_quats[i] = make_float4(G.quat[0], G.quat[1], G.quat[2], G.quat[3]);
+        g_scales[3 * i] = G.scales[0];
+        g_scales[3 * i + 1] = G.scales[1];
+        g_scales[3 * i + 2] = G.scales[2];
+        g_opacities[i] = G.opacity;
         if (g_sh0) {
-            float dx, dy, dz;
-            view_dir(cam, m0, m1, m2, dx, dy, dz);
-            float bk[16];
-            sh_basis(degree, dx, dy, dz, bk);
-            const int Ka = (degree + 1) * (degree + 1);
-            float gc[3];
-#pragma unroll
-            for (int ch = 0; ch < 3; ++ch)
-                gc[ch] = (colors_out[3 * i + ch] > 0.0f) ? g_colors[3 * i + ch] : 0.0f;
             float* row = s_sh + threadIdx.x * pad;
             if (sh_mode == kShPacked) {
-                for (int k = 0; k < K; ++k) {
-                    const float bv = (k < Ka) ? bk[k < 16 ? k : 0] : 0.0f;
-#pragma unroll
-                    for (int ch = 0; ch < 3; ++ch) row[3 * k + ch] = bv * gc[ch];
-                }
+                sh_grad_rows(G, K, 0, row);
             } else {
                 float* a = g_sh0 + i * s0;
 #pragma unroll
-                for (int ch = 0; ch < 3; ++ch) a[ch] = bk[0] * gc[ch];
-                float* b = sh_mode == kShSplit ? row : g_shr + i * sr;
-                for (int k = 1; k < K; ++k) {
-                    const float bv = (k < Ka) ? bk[k < 16 ? k : 0] : 0.0f;
-#pragma unroll
-                    for (int ch = 0; ch < 3; ++ch) b[3 * (k - 1) + ch] = bv * gc[ch];
-                }
+                for (int ch = 0; ch < 3; ++ch) a[ch] = G.bk[0] * G.gc[ch];
+                sh_grad_rows(G, K, 1, sh_mode == kShSplit ? row : g_shr + i * sr);
             }
         }
     }
@@ -418,6 +454,206 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
         const int rows = (int)min<int64_t>(kThreads, n - g0);
         lds_to_rows(s_sh, pad, sh_mode == kShPacked ? g_sh0 : g_shr,
                     sh_mode == kShPacked ? s0 : sr, g0, rows, sh_cols);
+    }
+}
+
+// The six parameter groups' Adam state for k_preprocess_bwd_adam, in the
+// trainer's order: means, quats, scales, opacities, SH DC, SH rest.
+struct AdamState6 {
+    float* m[6];
+    float* v[6];
+    float lr[6];
+};
+
+// One Adam update of a parameter whose value p the lane holds already; the
+// moments are read and written at M[k], V[k].  Returns the new value.
+__device__ __forceinline__ float adam_reg(float p, float* __restrict__ M, float* __restrict__ V,
+                                          int64_t k, float g, float lr, float b1, float omb1,
+                                          float b2, float omb2, float eps) {
+    float m = M[k], v = V[k];
+    adam_update(p, g, m, v, lr, b1, omb1, b2, omb2, eps);
+    M[k] = m;
+    V[k] = v;
+    return p;
+}
+
+__device__ __forceinline__ void adam4(float4& p, float4& m, float4& v, float4 g, float lr,
+                                      float b1, float omb1, float b2, float omb2, float eps) {
+    adam_update(p.x, g.x, m.x, v.x, lr, b1, omb1, b2, omb2, eps);
+    adam_update(p.y, g.y, m.y, v.y, lr, b1, omb1, b2, omb2, eps);
+    adam_update(p.z, g.z, m.z, v.z, lr, b1, omb1, b2, omb2, eps);
+    adam_update(p.w, g.w, m.w, v.w, lr, b1, omb1, b2, omb2, eps);
+}
+
+// The SH rest gradient of a Gaussian is rank one: coefficient k, channel ch
+// has bv(k) gc[ch] with bv(k) = bk[k] (0 from Ka on).  A workgroup stages
+// each lane's bv(1 .. 16) and gc(0 .. 2) as one LDS row of kRank1Stride
+// floats (odd, so each lane's own row hits distinct banks), and the SH rest
+// block is then streamed against it.
+constexpr int kRank1Stride = 19;
+
+__device__ __forceinline__ void stage_rank1(const RawGrads& G, float* row) {
+#pragma unroll
+    for (int k = 1; k < 16; ++k) row[k - 1] = (k < G.Ka) ? G.bk[k] : 0.0f;
+    row[15] = 0.0f;
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) row[16 + ch] = G.gc[ch];
+}
+
+// Gradient of SH rest column c (coefficient c / 3 + 1, channel c % 3) of a
+// staged row: the product sh_grad_rows forms (coefficient 16 has no basis
+// value and a gradient of +0, as there).
+__device__ __forceinline__ float rank1_grad(const float* row, int c) {
+    const int k1 = c / 3, ch = c - 3 * k1;
+    return k1 == 15 ? 0.0f : row[k1] * row[16 + ch];
+}
+
+// Gradients of elements e .. e + 3 of a workgroup's SH rest block (row-major,
+// `cols` per row).
+__device__ __forceinline__ float4 rank1_grad4(const float* s, int e, int cols, float inv) {
+    int r, c;
+    row_col(e, cols, inv, r, c);
+    float g[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        g[u] = rank1_grad(s + r * kRank1Stride, c);
+        if (++c == cols) {
+            c = 0;
+            ++r;
+        }
+    }
+    return make_float4(g[0], g[1], g[2], g[3]);
+}
+
+// The SH rest parameters and moments are read and written once per step, far
+// more data than the caches hold: non-temporal 16-byte loads and stores keep
+// the stream from evicting other data (measured on MI355X at 1M Gaussians,
+// K = 16: 297 -> 241 us for the fused kernel; the same on the stride-3
+// per-Gaussian moments made it slower, 339 us).  kStreamPieces 16-byte
+// pieces per lane are in flight at once (1: 277 us, 2: 242, 4: 238).
+constexpr int kStreamPieces = 4;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 stream_load(const float4* p) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void stream_store(float4* p, float4 a) {
+    const f32x4 v = {a.x, a.y, a.z, a.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+
+// k_preprocess_bwd followed by the Adam update of every parameter, fused:
+// each lane's gradients stay in registers and go straight into the update
+// of its Gaussian's parameters and moments, instead of being written out and
+// read back by a separate Adam launch.  The SH rest gradients' rank-one
+// factors go through LDS, and the workgroup then streams its contiguous
+// block of SH rest parameters and moments in 16-byte pieces (vec: all three
+// 16-byte aligned; otherwise element by element).  Parameters are read and
+// updated in place: each lane reads its own Gaussian's inputs before it
+// writes them, and no other lane reads them.  SH in split layout, contiguous rows: sh0 (N, 3),
+// shr (N, 3 (K - 1)); the moments share the parameters' layouts, the
+// quaternion moments 16-byte aligned.
+template <bool UT>
+__global__ __launch_bounds__(kThreads) void k_preprocess_bwd_adam(
+    gsx_camera cam, int64_t n, float* __restrict__ means, float4* __restrict__ quats,
+    float* __restrict__ scales, float* __restrict__ opacities, float* __restrict__ sh0,
+    float* __restrict__ shr, int K, int degree, uint32_t flags, float blur, bool aa, bool vec,
+    const float* __restrict__ colors_out, const float2* __restrict__ g_means2d,
+    const float* __restrict__ g_conics, const float* __restrict__ g_opac_eff,
+    const float* __restrict__ g_colors, const float2* __restrict__ g_means2d_extra,
+    const float* __restrict__ g_depths, const float* __restrict__ g_comp, AdamState6 st,
+    float b1, float omb1, float b2, float omb2, float eps) {
+    __shared__ float s_r1[kThreads * kRank1Stride];
+    const int64_t g0 = (int64_t)blockIdx.x * kThreads;
+    const int64_t i = g0 + threadIdx.x;
+    const int cols = 3 * (K - 1);
+    if (i < n) {
+        const float pm[3] = {means[3 * i], means[3 * i + 1], means[3 * i + 2]};
+        const float4 q = quats[i];
+        const float ps[3] = {scales[3 * i], scales[3 * i + 1], scales[3 * i + 2]};
+        const float ro = opacities[i];
+        RawGrads G;
+        preprocess_vjp<UT>(cam, i, pm[0], pm[1], pm[2], q, ps[0], ps[1], ps[2], ro, flags, blur,
+                           aa, true, degree, colors_out, g_means2d, g_conics, g_opac_eff,
+                           g_colors, g_means2d_extra, g_depths, g_comp, G);
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            means[3 * i + k] = adam_reg(pm[k], st.m[0], st.v[0], 3 * i + k, G.means[k], st.lr[0],
+                                        b1, omb1, b2, omb2, eps);
+        {
+            float4 p = q;
+            float4 m = reinterpret_cast<float4*>(st.m[1])[i];
+            float4 v = reinterpret_cast<float4*>(st.v[1])[i];
+            adam4(p, m, v, make_float4(G.quat[0], G.quat[1], G.quat[2], G.quat[3]), st.lr[1], b1,
+                  omb1, b2, omb2, eps);
+            quats[i] = p;
+            reinterpret_cast<float4*>(st.m[1])[i] = m;
+            reinterpret_cast<float4*>(st.v[1])[i] = v;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            scales[3 * i + k] = adam_reg(ps[k], st.m[2], st.v[2], 3 * i + k, G.scales[k],
+                                         st.lr[2], b1, omb1, b2, omb2, eps);
+        opacities[i] = adam_reg(ro, st.m[3], st.v[3], i, G.opacity, st.lr[3], b1, omb1, b2, omb2,
+                                eps);
+        float pd[3];
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) pd[ch] = sh0[3 * i + ch];
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch)
+            sh0[3 * i + ch] = adam_reg(pd[ch], st.m[4], st.v[4], 3 * i + ch, G.bk[0] * G.gc[ch],
+                                       st.lr[4], b1, omb1, b2, omb2, eps);
+        stage_rank1(G, s_r1 + threadIdx.x * kRank1Stride);
+    }
+    if (cols > 0) {
+        __syncthreads();
+        const int rows = (int)min<int64_t>(kThreads, n - g0);
+        const int total = rows * cols;
+        const float inv = 1.0f / (float)cols;
+        float* __restrict__ P = shr + g0 * cols;
+        float* __restrict__ M = st.m[5] + g0 * cols;
+        float* __restrict__ V = st.v[5] + g0 * cols;
+        const float lr = st.lr[5];
+        int done = 0;
+        if (vec) {  // g0 cols is a multiple of 4 (g0 of kThreads), the block 16-byte aligned
+            float4* P4 = reinterpret_cast<float4*>(P);
+            float4* M4 = reinterpret_cast<float4*>(M);
+            float4* V4 = reinterpret_cast<float4*>(V);
+            const int total4 = total >> 2;
+            for (int j = threadIdx.x; j < total4; j += kStreamPieces * kThreads) {
+                // loads of every piece are unconditional (a piece past the end
+                // re-reads the first), its stores guarded
+                int jj[kStreamPieces];
+                float4 pp[kStreamPieces], mm[kStreamPieces], vv[kStreamPieces];
+#pragma unroll
+                for (int u = 0; u < kStreamPieces; ++u) {
+                    jj[u] = j + u * kThreads < total4 ? j + u * kThreads : j;
+                    pp[u] = stream_load(P4 + jj[u]);
+                    mm[u] = stream_load(M4 + jj[u]);
+                    vv[u] = stream_load(V4 + jj[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < kStreamPieces; ++u)
+                    adam4(pp[u], mm[u], vv[u], rank1_grad4(s_r1, 4 * jj[u], cols, inv), lr, b1,
+                          omb1, b2, omb2, eps);
+#pragma unroll
+                for (int u = 0; u < kStreamPieces; ++u)
+                    if (u == 0 || j + u * kThreads < total4) {
+                        stream_store(P4 + jj[u], pp[u]);
+                        stream_store(M4 + jj[u], mm[u]);
+                        stream_store(V4 + jj[u], vv[u]);
+                    }
+            }
+            done = total4 << 2;
+        }
+        for (int e = done + threadIdx.x; e < total; e += kThreads) {
+            int r, c;
+            row_col(e, cols, inv, r, c);
+            P[e] = adam_reg(P[e], M, V, e, rank1_grad(s_r1 + r * kRank1Stride, c), lr, b1, omb1,
+                            b2, omb2, eps);
+        }
     }
 }
 
@@ -607,6 +843,58 @@ int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means, con
                        tiles_x, tiles_y,
                        (float2*)means2d, depths, radii, compensation, (float4*)conic_opacity,
                        colors_out, tile_counts, depth_keys, (uint2*)tile_rects);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, float* quats,
+                            float* scales, float* opacities, float* sh_dc, float* sh_rest,
+                            const float* colors_out, int32_t K, int32_t degree, uint32_t flags,
+                            float blur, const float* g_means2d, const float* g_conics,
+                            const float* g_opac_eff, const float* g_colors,
+                            const float* g_means2d_extra, const float* g_depths,
+                            const float* g_compensation, const gsx_adam_group* groups,
+                            float beta1, float beta2, float eps, void* stream) {
+    if (!cam || n < 0 || !lens_ok(cam) || !groups) return GSX_ERR_INVALID;
+    if (n == 0) return GSX_OK;
+    if (!means || !quats || !scales || !opacities || !sh_dc || !colors_out || !g_means2d ||
+        !g_conics || !g_opac_eff || !g_colors)
+        return GSX_ERR_INVALID;
+    if (degree < 0 || degree > 3 || K < (degree + 1) * (degree + 1) ||
+        3 * (K - 1) > kShMaxCols || (K > 1 && !sh_rest))
+        return GSX_ERR_INVALID;
+    // the groups name the same tensors, with the element counts of their layouts
+    float* const params[6] = {means, quats, scales, opacities, sh_dc, sh_rest};
+    const int64_t counts[6] = {3 * n, 4 * n, 3 * n, n, 3 * n, 3 * (int64_t)(K - 1) * n};
+    AdamState6 st;
+    for (int k = 0; k < 6; ++k) {
+        if (k == 5 && K == 1) {
+            st.m[k] = st.v[k] = nullptr;
+            st.lr[k] = 0.0f;
+            continue;
+        }
+        if (groups[k].param != params[k] || groups[k].n != counts[k] || !groups[k].m ||
+            !groups[k].v)
+            return GSX_ERR_INVALID;
+        st.m[k] = groups[k].m;
+        st.v[k] = groups[k].v;
+        st.lr[k] = groups[k].lr;
+    }
+    if (!aligned16(quats) || !aligned16(st.m[1]) || !aligned16(st.v[1]) ||
+        !aligned8(g_means2d) || (g_means2d_extra && !aligned8(g_means2d_extra)))
+        return GSX_ERR_INVALID;
+    const bool vec = K > 1 && aligned16(sh_rest) && aligned16(st.m[5]) && aligned16(st.v[5]);
+    // b1, 1 - b1, b2, 1 - b2 in float32 as gsx_adam_step rounds them
+    const float b1 = beta1, omb1 = (float)(1.0 - (double)beta1);
+    const float b2 = beta2, omb2 = (float)(1.0 - (double)beta2);
+    auto kern = (flags & GSX_PROJECT_UT) ? k_preprocess_bwd_adam<true>
+                                         : k_preprocess_bwd_adam<false>;
+    hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(kThreads), 0, (hipStream_t)stream, *cam, n,
+                       means, (float4*)quats, scales, opacities, sh_dc, sh_rest, K, degree, flags,
+                       blur, (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, vec, colors_out,
+                       (const float2*)g_means2d, g_conics, g_opac_eff, g_colors,
+                       (const float2*)g_means2d_extra, g_depths, g_compensation, st, b1, omb1,
+                       b2, omb2, eps);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }

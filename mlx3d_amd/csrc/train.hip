@@ -383,9 +383,7 @@ struct AdamArgs {
 
 __device__ __forceinline__ void adam_one(float& p, float g, float& m, float& v, float lr, float b1,
                                          float omb1, float b2, float omb2, float eps) {
-    m = b1 * m + omb1 * g;
-    v = b2 * v + omb2 * (g * g);
-    p = p - (lr * m) / (sqrtf(v) + eps);
+    gsx::adam_update(p, g, m, v, lr, b1, omb1, b2, omb2, eps);
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));

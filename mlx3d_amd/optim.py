@@ -26,7 +26,7 @@ import torch
 from . import _lib
 from .profiling import stage
 
-__all__ = ["Adam", "adam_step", "exponential_decay"]
+__all__ = ["Adam", "adam_step", "exponential_decay", "FusedAdam"]
 
 
 def exponential_decay(init: float, decay_rate: float) -> Callable[[int], float]:
@@ -87,6 +87,18 @@ class Adam:
             out.append((p, _lib.f32c(g), st["m"], st["v"], lr, self))
         return out
 
+    def _fused_group(self, name: str, p: torch.Tensor):
+        """The bookkeeping of one update of parameter ``name`` whose gradient
+        a kernel computes and applies itself: advances the schedule and
+        returns (param, m, v, lr)."""
+        if p.dtype != torch.float32 or not p.is_contiguous():
+            raise ValueError(f"parameter {name!r} must be contiguous float32")
+        lr = self._schedule(self.step)
+        self._last_lr = lr
+        self.step += 1
+        st = self._state_for(name, p)
+        return p, st["m"], st["v"], lr
+
     def apply_gradients(self, grads: dict[str, torch.Tensor],
                         params: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
         """Updates ``params`` in place (and returns them)."""
@@ -120,3 +132,24 @@ def adam_step(updates) -> None:
         with stage("adam"):
             _lib.check(L.gsx_adam_step(len(chunk), ctypes.cast(arr, ctypes.c_void_p), b1, b2,
                                        eps, _lib.stream_handle(dev)), "gsx_adam_step")
+
+
+class FusedAdam:
+    """One Adam update of several parameters applied by the kernel that
+    computes their gradients (``gsx_preprocess_bwd_adam``): built from
+    ``[(adam, name, param), ...]`` before the backward runs, it advances each
+    optimiser's schedule as ``adam_step`` would and holds the
+    ``gsx_adam_group`` records (gradient pointers unused)."""
+
+    def __init__(self, updates):
+        groups = [opt._fused_group(name, p) for opt, name, p in updates]
+        opts = [u[0] for u in updates]
+        self.betas, self.eps = opts[0].betas, opts[0].eps
+        if any(o.betas != self.betas or o.eps != self.eps for o in opts):
+            raise ValueError("FusedAdam: optimisers with different betas/eps")
+        self.tensors = [t for g in groups for t in g[:3]]  # kept alive with the records
+        self.records = (_lib.GsxAdamGroup * len(groups))()
+        for k, (p, m, v, lr) in enumerate(groups):
+            self.records[k] = _lib.GsxAdamGroup(p.data_ptr(), None, m.data_ptr(), v.data_ptr(),
+                                                p.numel(), lr)
+

@@ -14,6 +14,8 @@ expressions (what MLX autodiff computes for the reference).
 
 from __future__ import annotations
 
+import ctypes
+
 from dataclasses import dataclass
 
 import torch
@@ -43,6 +45,10 @@ class _Cfg:
     # (grad_accum, grad_count): the backward adds the density-control
     # statistics of dL/dmeans2d (trainer.py:357-365) to these in place.
     screen_stats: tuple | None = None
+    # optim.FusedAdam: the backward applies this Adam update to the six
+    # parameter groups itself (gsx_preprocess_bwd_adam) and returns no
+    # parameter gradients
+    adam: object | None = None
 
 
 def _sh_views(cfg: _Cfg, sh_a, sh_b):
@@ -130,6 +136,28 @@ class _RenderFn(torch.autograd.Function):
             _lib.check(_lib.load().gsx_accum_screen_grads(
                 n, _lib.ptr(g_m2), _lib.ptr(radii), cfg.width, cfg.height, _lib.ptr(acc),
                 _lib.ptr(cnt), _lib.stream_handle(dev)), "gsx_accum_screen_grads")
+        c = lambda t: None if t is None else _lib.f32c(t)  # noqa: E731
+        # The contiguous copies of the output cotangents (a stride-0 expand
+        # from .sum() is copied) must outlive the enqueued kernel: only their
+        # addresses cross the ABI, so they are bound to locals here.
+        gm2_in, gdep_in, gcomp_in = c(g_means2d), c(g_depths), c(g_comp)
+        L = _lib.load()
+        # The binning's final device status was copied behind it in the
+        # forward; a failed device-side check raises here, before any
+        # gradient or parameter update is produced.
+        ctx.bin_job.check()
+        if cfg.adam is not None:
+            opt = cfg.adam
+            with stage("preprocess_bwd_adam"):
+                _lib.check(L.gsx_preprocess_bwd_adam(
+                    cfg.cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
+                    _lib.ptr(opacities), _lib.ptr(sh_a), _lib.ptr(sh_b), _lib.ptr(feats), cfg.K,
+                    cfg.degree, cfg.flags, cfg.blur, _lib.ptr(g_m2), _lib.ptr(g_con),
+                    _lib.ptr(g_op), _lib.ptr(g_feat), _lib.ptr(gm2_in), _lib.ptr(gdep_in),
+                    _lib.ptr(gcomp_in), ctypes.cast(opt.records, ctypes.c_void_p),
+                    opt.betas[0], opt.betas[1], opt.eps, _lib.stream_handle(dev)),
+                    "gsx_preprocess_bwd_adam")
+            return None, None, None, None, None, None, None, None, None
         f = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)  # noqa: E731
         g_means, g_quats, g_scales, g_opac = f(n, 3), f(n, 4), f(n, 3), f(n)
         g_sh_a = g_sh_b = None
@@ -137,12 +165,6 @@ class _RenderFn(torch.autograd.Function):
             g_sh_a = torch.empty_like(sh_a)
             g_sh_b = torch.empty_like(sh_b) if cfg.sh_mode == "split" else None
         gs0, s0, gshr, sr = _sh_views(cfg, g_sh_a, g_sh_b)
-        c = lambda t: None if t is None else _lib.f32c(t)  # noqa: E731
-        # The contiguous copies of the output cotangents (a stride-0 expand
-        # from .sum() is copied) must outlive the enqueued kernel: only their
-        # addresses cross the ABI, so they are bound to locals here.
-        gm2_in, gdep_in, gcomp_in = c(g_means2d), c(g_depths), c(g_comp)
-        L = _lib.load()
         with stage("preprocess_bwd"):
             _lib.check(L.gsx_preprocess_bwd(
                 cfg.cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
@@ -152,10 +174,6 @@ class _RenderFn(torch.autograd.Function):
                 _lib.ptr(gdep_in), _lib.ptr(gcomp_in), _lib.ptr(g_means),
                 _lib.ptr(g_quats), _lib.ptr(g_scales), _lib.ptr(g_opac), _lib.ptr(gs0), s0, gshr,
                 sr, _lib.stream_handle(dev)), "gsx_preprocess_bwd")
-        # The binning's final device status was copied behind it in the
-        # forward; a failed device-side check raises here, before any
-        # optimizer sees these gradients.
-        ctx.bin_job.check()
         g_colors = None if cfg.sh_mode else g_feat
         return g_means, g_quats, g_scales, g_opac, g_sh_a, g_sh_b, g_colors, None, None
 
@@ -180,7 +198,7 @@ def _stats(screen_stats, n, dev):
 
 def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=None,
          sh_mode=None, K=0, degree=0, colors=None, background=None, flags=0, antialias=False,
-         blur=0.3, return_depth=False, refine_tiles=False, screen_stats=None):
+         blur=0.3, return_depth=False, refine_tiles=False, screen_stats=None, adam=None):
     n = means.shape[0]
     if means.ndim != 2 or means.shape[1] != 3:
         raise ValueError("means must have shape (N, 3).")
@@ -193,7 +211,9 @@ def _run(camera: Camera, means, quats, scales, opacities, *, sh_a=None, sh_b=Non
     cfg = _Cfg(cam=camera.to_gsx(), width=int(camera.width), height=int(camera.height),
                flags=flags, blur=float(blur), degree=int(degree), K=int(K), sh_mode=sh_mode,
                return_depth=bool(return_depth), refine=bool(refine_tiles),
-               screen_stats=_stats(screen_stats, n, dev))
+               screen_stats=_stats(screen_stats, n, dev), adam=adam)
+    if adam is not None and sh_mode != "split":
+        raise ValueError("a fused Adam update needs the split SH layout")
     c = _lib.f32c
     (image, final_T, alpha, n_contrib, means2d, depths, radii, comp, depth, ids,
      ranges) = _RenderFn.apply(c(means), c(quats), c(scales), c(opacities),

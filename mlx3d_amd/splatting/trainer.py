@@ -5,8 +5,10 @@ One ``GaussianTrainer.step`` on the vanilla and MCMC methods is
     fused render forward (preprocess, binning, raster)        libgsx
     photometric loss: mean L1 and mean SSIM in one pass       gsx_photometric_fwd
     backward: loss gradient, raster VJP (+ the screen-space    gsx_photometric_bwd,
-      gradient statistics of density control), preprocess VJP  gsx_raster_bwd, ...
-    Adam on all six parameter groups in one launch            gsx_adam_step
+      gradient statistics of density control)                  gsx_raster_bwd, ...
+    preprocess VJP with the Adam update of all six parameter   gsx_preprocess_bwd_adam
+      groups fused in (fuse_adam=False: the VJP, then one      (gsx_preprocess_bwd,
+      multi-group Adam launch)                                  gsx_adam_step)
 
 with no host synchronisation except the duplicate count of the binning;
 density control runs every ``densify_every`` steps on the device.
@@ -34,7 +36,7 @@ import torch
 
 from ..cameras import Camera
 from ..losses import photometric
-from ..optim import Adam, adam_step, exponential_decay
+from ..optim import Adam, FusedAdam, adam_step, exponential_decay
 from .. import _lib
 from .density import GROUPS
 from .geometry import geometry_loss, surfel_features, unprojection_maps
@@ -44,6 +46,9 @@ from .rasterize import rasterize, rasterize_features
 from .render import _check_common, _run
 from .sh import eval_sh
 from .tiles import bin_gaussians
+
+# parameter groups in the order gsx_preprocess_bwd_adam takes them
+_FUSED_ORDER = ("means", "quats", "scales", "opacities", "sh_dc", "sh_rest")
 
 __all__ = ["TrainerConfig", "GaussianTrainer"]
 
@@ -100,8 +105,13 @@ class GaussianTrainer:
     """Optimises a :class:`GaussianModel` against posed images (trainer.py:78-421)."""
 
     def __init__(self, model: GaussianModel, config: TrainerConfig | None = None,
-                 scene_extent: float = 1.0, generator: torch.Generator | None = None):
+                 scene_extent: float = 1.0, generator: torch.Generator | None = None,
+                 fuse_adam: bool = True):
         self.model = model
+        # vanilla / MCMC: the Adam update runs inside the preprocess backward
+        # (gsx_preprocess_bwd_adam, the same updates bit for bit); False keeps
+        # the separate gradient tensors and one gsx_adam_step launch
+        self.fuse_adam = bool(fuse_adam)
         self.config = config or TrainerConfig()
         if self.config.method not in {"vanilla", "mcmc", "2dgs"}:
             raise ValueError("TrainerConfig.method must be 'vanilla', 'mcmc', or '2dgs'")
@@ -172,16 +182,20 @@ class GaussianTrainer:
         the backward adds the screen statistics itself when ``collect``."""
         p = params
         stats = (self.grad_accum, self.grad_count) if collect else None
+        # with fuse_adam the backward applies this step's Adam update itself
+        # (the kernel's group order: means, quats, scales, opacities, DC, rest)
+        adam = (FusedAdam([(self.optimizers[k], k, p[k]) for k in _FUSED_ORDER])
+                if self.fuse_adam else None)
         out = _run(camera, p["means"], p["quats"], p["scales"], p["opacities"],
                    sh_a=p["sh_dc"], sh_b=p["sh_rest"], sh_mode="split",
                    K=p["sh_dc"].shape[1] + p["sh_rest"].shape[1],
                    degree=self.model.active_sh_degree, background=background,
                    flags=(_lib.LOG_SCALES | _lib.LOGIT_OPACITY
                           | _check_common(self.config.projection)),
-                   antialias=self.config.antialias, screen_stats=stats)
+                   antialias=self.config.antialias, screen_stats=stats, adam=adam)
         loss = self._photometric(out["image"], target)
         grads = torch.autograd.grad(loss, [p[k] for k in GROUPS], allow_unused=True)
-        return _StepResult(loss, grads, out["radii"])
+        return _StepResult(loss, None if adam is not None else grads, out["radii"])
 
     def _maps(self, camera: Camera, dev):
         key = (id(camera), camera.width, camera.height, str(dev))
@@ -280,10 +294,12 @@ class GaussianTrainer:
         else:
             res = self._fused_pass(leaves, camera, target, background, collect)
 
-        # every group in one Adam launch (trainer.py:339-342)
-        adam_step([(self.optimizers[k], {k: torch.zeros_like(model.params[k]) if g is None
-                                         else g}, {k: model.params[k].data})
-                   for k, g in zip(GROUPS, res.grads)])
+        # every group in one Adam launch (trainer.py:339-342), unless the
+        # backward has applied the update already
+        if res.grads is not None:
+            adam_step([(self.optimizers[k], {k: torch.zeros_like(model.params[k]) if g is None
+                                             else g}, {k: model.params[k].data})
+                       for k, g in zip(GROUPS, res.grads)])
         if cfg.method == "mcmc" and cfg.mcmc_noise_scale > 0:
             self._mcmc_noise()
         self._constrain()

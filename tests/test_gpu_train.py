@@ -12,6 +12,8 @@ and parameter gradients within max|d| / max|ref| < 1e-4 (loss) and 1e-3
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -208,6 +210,151 @@ def test_trainer_step_matches_oracle(degree):
     e = rel_err(host(tr.grad_accum), ra)
     say(f"  grad_accum rel {e:.2e}")
     assert e < 1e-3
+
+
+def _bwd_inputs(seed, n, K, with_extra):
+    """Parameters, forward colours and output cotangents for the preprocess
+    backward, plus nonzero Adam moments, as device tensors."""
+    cam, _, raw, sh = _model(seed, n)
+    rng = np.random.default_rng(seed + 1)
+    f = lambda *s, sc=1.0: cu((rng.standard_normal(s) * sc).astype(np.float32))  # noqa: E731
+    params = {k: cu(raw[k]) for k in ("means", "quats", "scales", "opacities")}
+    params["sh_dc"] = cu(sh[:, 0].copy())
+    params["sh_rest"] = cu(sh[:, 1:K].reshape(n, 3 * (K - 1)).copy())
+    cot = dict(colors=cu(rng.uniform(-0.2, 1.0, (n, 3)).astype(np.float32)),
+               g_m2=f(n, 2, sc=1e-2), g_con=f(n, 3, sc=1e-3), g_op=f(n, sc=1e-2),
+               g_col=f(n, 3, sc=1e-2), extra=f(n, 2, sc=1e-2) if with_extra else None,
+               g_dep=f(n, sc=1e-2) if with_extra else None,
+               g_comp=f(n, sc=1e-2) if with_extra else None)
+    moments = {k: (f(*v.shape, sc=1e-3),
+                   cu(rng.uniform(1e-8, 1e-6, v.shape).astype(np.float32)))
+               for k, v in params.items()}
+    return cam, params, cot, moments
+
+
+_ORDER = ("means", "quats", "scales", "opacities", "sh_dc", "sh_rest")
+_LRS = dict(means=1.6e-4, quats=1e-3, scales=5e-3, opacities=5e-2, sh_dc=2.5e-3,
+            sh_rest=1.25e-4)
+
+
+def _offset_copy(t):
+    """A copy of t that starts 4 bytes past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    buf[1:].copy_(t.reshape(-1))
+    return buf[1:].view(t.shape)
+
+
+@pytest.mark.parametrize("n,K,degree,flags,extra,misalign", [
+    (3001, 16, 3, 0, True, False), (3001, 16, 1, _lib.ANTIALIAS, False, False),
+    (2500, 9, 2, _lib.PROJECT_UT, True, False),
+    (777, 1, 0, _lib.PROJECT_UT | _lib.ANTIALIAS, True, False), (1, 4, 1, 0, False, False),
+    (3001, 16, 3, 0, True, True), (1500, 9, 2, 0, False, True)])
+def test_preprocess_bwd_adam_matches_bwd_then_adam(n, K, degree, flags, extra, misalign):
+    """gsx_preprocess_bwd_adam against gsx_preprocess_bwd + gsx_adam_step on
+    the same cotangents: parameters and both moments bit for bit (ragged last
+    block, degrees below the stored K, UT, antialiasing, optional inputs, SH
+    rest rows of odd and even width, and SH rest tensors off 16-byte
+    alignment, which take the element-wise path)."""
+    say(f"preprocess_bwd_adam n={n} K={K} degree={degree} flags={flags} extra={extra} "
+        f"misalign={misalign}")
+    cam, params, cot, moments = _bwd_inputs(50 + K, n, K, extra)
+    flags |= _lib.LOG_SCALES | _lib.LOGIT_OPACITY
+    L, ptr, st = _lib.load(), _lib.ptr, _lib.stream_handle(params["means"].device)
+    gcam = cam.to_gsx()
+    groups = [k for k in _ORDER if k != "sh_rest" or K > 1]
+    # separate: gradients written out, then one multi-group Adam launch
+    sep = {k: (params[k].clone(), moments[k][0].clone(), moments[k][1].clone()) for k in groups}
+    g = {k: torch.empty_like(params[k]) for k in _ORDER}
+    _lib.check(L.gsx_preprocess_bwd(
+        gcam, n, ptr(sep["means"][0]), ptr(sep["quats"][0]), ptr(sep["scales"][0]),
+        ptr(sep["opacities"][0]), ptr(cot["colors"]), K, degree, flags, 0.3, ptr(cot["g_m2"]),
+        ptr(cot["g_con"]), ptr(cot["g_op"]), ptr(cot["g_col"]), ptr(cot["extra"]),
+        ptr(cot["g_dep"]), ptr(cot["g_comp"]), ptr(g["means"]), ptr(g["quats"]),
+        ptr(g["scales"]), ptr(g["opacities"]), ptr(g["sh_dc"]), 3,
+        ptr(g["sh_rest"]) if K > 1 else None, 3 * (K - 1), st), "gsx_preprocess_bwd")
+    arr = (_lib.GsxAdamGroup * len(groups))()
+    for j, k in enumerate(groups):
+        p, m, v = sep[k]
+        arr[j] = _lib.GsxAdamGroup(p.data_ptr(), g[k].data_ptr(), m.data_ptr(), v.data_ptr(),
+                                   p.numel(), _LRS[k])
+    _lib.check(L.gsx_adam_step(len(groups), ctypes.cast(arr, ctypes.c_void_p), 0.9, 0.999,
+                               1e-15, st), "gsx_adam_step")
+    # fused
+    fus = {k: (params[k].clone(), moments[k][0].clone(), moments[k][1].clone()) for k in groups}
+    if misalign:
+        fus["sh_rest"] = tuple(_offset_copy(t) for t in fus["sh_rest"])
+    arr = (_lib.GsxAdamGroup * 6)()
+    for j, k in enumerate(groups):
+        p, m, v = fus[k]
+        arr[j] = _lib.GsxAdamGroup(p.data_ptr(), None, m.data_ptr(), v.data_ptr(), p.numel(),
+                                   _LRS[k])
+    _lib.check(L.gsx_preprocess_bwd_adam(
+        gcam, n, ptr(fus["means"][0]), ptr(fus["quats"][0]), ptr(fus["scales"][0]),
+        ptr(fus["opacities"][0]), ptr(fus["sh_dc"][0]),
+        ptr(fus["sh_rest"][0]) if K > 1 else None, ptr(cot["colors"]), K, degree, flags, 0.3,
+        ptr(cot["g_m2"]), ptr(cot["g_con"]), ptr(cot["g_op"]), ptr(cot["g_col"]),
+        ptr(cot["extra"]), ptr(cot["g_dep"]), ptr(cot["g_comp"]),
+        ctypes.cast(arr, ctypes.c_void_p), 0.9, 0.999, 1e-15, st), "gsx_preprocess_bwd_adam")
+    for k in groups:
+        for slot, a, b in zip(("param", "m", "v"), fus[k], sep[k]):
+            assert_bits(host(a), host(b), f"{slot} {k}")
+        assert not torch.equal(fus[k][0], params[k]), k  # the update ran
+
+
+def test_preprocess_bwd_adam_rejects_mismatched_groups():
+    cam, params, cot, moments = _bwd_inputs(60, 64, 4, False)
+    L, ptr, st = _lib.load(), _lib.ptr, _lib.stream_handle(params["means"].device)
+    arr = (_lib.GsxAdamGroup * 6)()
+    for j, k in enumerate(_ORDER):
+        arr[j] = _lib.GsxAdamGroup(params[k].data_ptr(), None, moments[k][0].data_ptr(),
+                                   moments[k][1].data_ptr(), params[k].numel(), 1e-3)
+    arr[2] = _lib.GsxAdamGroup(params["quats"].data_ptr(), None, moments["scales"][0].data_ptr(),
+                               moments["scales"][1].data_ptr(), params["scales"].numel(), 1e-3)
+
+    def call():
+        return L.gsx_preprocess_bwd_adam(
+            cam.to_gsx(), 64, ptr(params["means"]), ptr(params["quats"]),
+            ptr(params["scales"]), ptr(params["opacities"]), ptr(params["sh_dc"]),
+            ptr(params["sh_rest"]), ptr(cot["colors"]), 4, 1, _lib.LOG_SCALES, 0.3,
+            ptr(cot["g_m2"]), ptr(cot["g_con"]), ptr(cot["g_op"]), ptr(cot["g_col"]), None,
+            None, None, ctypes.cast(arr, ctypes.c_void_p), 0.9, 0.999, 1e-15, st)
+    before = host(params["means"])
+    assert call() != _lib.GSX_OK  # group 2 names the quaternions, not the scales
+    torch.cuda.synchronize()
+    assert_bits(host(params["means"]), before, "untouched means")
+
+
+@pytest.mark.parametrize("method,projection,degree", [("vanilla", "ewa", 3), ("vanilla", "ut", 1),
+                                                       ("mcmc", "ewa", 0)])
+def test_trainer_fused_adam_close_to_separate_update(method, projection, degree):
+    """GaussianTrainer with the update inside the backward against the
+    separate Adam launch over several steps.  The rasterizer backward adds
+    per-Gaussian cotangents with float atomics, so the two runs see gradients
+    that differ in the last bits; with eps 1e-15 a near-zero gradient whose
+    sign differs moves a parameter by about 3 lr the other way.  Bar: the
+    learning rates agree exactly, every parameter within 32 lr of its group
+    (four steps, plus 1e-6 relative), 99% of them within 1e-5 relative."""
+    say(f"fused adam trainer {method} {projection} degree {degree}")
+    models = [_model(41, 3000, degree)[1] for _ in range(2)]
+    cam = _model(41, 10, degree)[0]
+    cfg = TrainerConfig(method=method, projection=projection, densify_from=1 << 30,
+                        densify_until=1 << 30, opacity_reset_every=1 << 30,
+                        sh_increase_every=1 << 30, mcmc_noise_scale=0.0)
+    trs = [GaussianTrainer(m, cfg, fuse_adam=f) for m, f in zip(models, (True, False))]
+    rng = np.random.default_rng(5)
+    for step in range(4):
+        target = cu(rng.random((cam.height, cam.width, 3), dtype=np.float32))
+        infos = [tr.step(cam, target) for tr in trs]
+        assert abs(infos[0]["loss"] - infos[1]["loss"]) <= 1e-6 * abs(infos[1]["loss"]), step
+    for k in ("means", "quats", "scales", "opacities", "sh_dc", "sh_rest"):
+        assert trs[0].optimizers[k].learning_rate == trs[1].optimizers[k].learning_rate
+        lr = max(float(trs[0].optimizers[k].learning_rate), 1e-12)
+        a, b = host(models[0].params[k]), host(models[1].params[k])
+        d = np.abs(a.astype(np.float64) - b)
+        say(f"  {k}: max |d| {d.max():.3e} (lr {lr:.2e}), "
+            f"{int((d > 1e-5 * np.abs(b) + 1e-12).sum())} of {d.size} beyond 1e-5 rel")
+        assert (d <= 8 * 4 * lr + 1e-6 * np.abs(b)).all(), k
+        assert (d > 1e-5 * np.abs(b) + 1e-12).mean() < 0.01, k
 
 
 def test_densify_and_prune_matches_oracle():
