@@ -210,15 +210,19 @@ def summarize_prof(dirs, workload: str, command: str):
             counters.setdefault(r["Counter_Name"], []).append(
                 (_short(r["Kernel_Name"]), float(r["Counter_Value"]), int(r["Grid_Size"])))
     if "FETCH_SIZE" in counters and "WRITE_SIZE" in counters:
+        def is_kernel(name, sym):  # the symbol itself or an instantiation of it
+            return name == sym or name.startswith(sym + "<")
+
         def per_kernel(cname, sym):
-            v = [x[1] for x in counters[cname] if x[0].startswith(sym)]
+            v = [x[1] for x in counters[cname] if is_kernel(x[0], sym)]
             return sum(v) / len(v) if v else None
 
-        probe = [x for x in counters["FETCH_SIZE"] if x[0].startswith(COPY_PROBE_KERNEL)]
+        probe = [x for x in counters["FETCH_SIZE"] if is_kernel(x[0], COPY_PROBE_KERNEL)]
         n_probe = max(x[2] for x in probe)  # grid = elements of the largest probe launch
         known_kib = 4.0 * n_probe / 1024.0
         f_probe = max(x[1] for x in probe)
-        w_probe = max(x[1] for x in counters["WRITE_SIZE"] if x[0].startswith(COPY_PROBE_KERNEL))
+        w_probe = max(x[1] for x in counters["WRITE_SIZE"]
+                      if is_kernel(x[0], COPY_PROBE_KERNEL))
         f_scale, w_scale = known_kib / f_probe, known_kib / w_probe
         for stage, sym in KERNEL_SYMBOL.items():
             fk, wk = per_kernel("FETCH_SIZE", sym), per_kernel("WRITE_SIZE", sym)
