@@ -373,6 +373,27 @@ int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels,
                         const void* workspace, int64_t workspace_bytes,
                         const float* grad_out, float* grad_pred, void* stream);
 
+/* The trainer's objective loss = (1 - lambda) l1 + lambda (1 - ssim)
+ * (trainer.py:303-305) in one call: gsx_photometric_fwd, and out3 (3
+ * floats, device) = [l1, ssim, loss], the loss in the float32 steps of
+ * that expression with 1 - lambda and lambda each rounded once to float32
+ * (as the Python scalars reach float32 arithmetic).  0 <= lambda <= 1. */
+int gsx_photometric_loss_fwd(int32_t height, int32_t width, int32_t channels,
+                             const float* pred, const float* target,
+                             int32_t window_size, float sigma, float max_val,
+                             double lambda, void* workspace,
+                             int64_t workspace_bytes, float* out3, void* stream);
+
+/* Gradient of that loss: gsx_photometric_bwd with grad_out = (g (1 -
+ * lambda), -(g lambda)) formed on the device from the loss cotangent g
+ * (g_loss, 1 float, device), the values autodiff of the expression
+ * gives. */
+int gsx_photometric_loss_bwd(int32_t height, int32_t width, int32_t channels,
+                             const float* pred, const float* target,
+                             int32_t window_size, float sigma, double lambda,
+                             const void* workspace, int64_t workspace_bytes,
+                             const float* g_loss, float* grad_pred, void* stream);
+
 /* Replaces l1_loss(pred, target) = mean |pred - target|
  * (losses/image_metrics.py:13-14) for n contiguous floats: out (1 float,
  * device); partial sums in double, added in a fixed order.  The workspace

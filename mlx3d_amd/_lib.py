@@ -150,6 +150,10 @@ SIGNATURES = {
                                            _P]),
     "gsx_photometric_bwd": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, _F, _P, _I64, _P, _P,
                                            _P]),
+    "gsx_photometric_loss_fwd": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, _F, _F,
+                                                ctypes.c_double, _P, _I64, _P, _P]),
+    "gsx_photometric_loss_bwd": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, _F,
+                                                ctypes.c_double, _P, _I64, _P, _P, _P]),
     "gsx_l1_workspace_bytes": (_I64, [_I64]),
     "gsx_l1_fwd": (ctypes.c_int, [_I64, _P, _P, _P, _I64, _P, _P]),
     "gsx_l1_noalloc_max_elements": (_I64, []),

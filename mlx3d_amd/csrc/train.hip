@@ -242,11 +242,21 @@ __global__ __launch_bounds__(kSsThreads) void k_ssim_fwd(
     }
 }
 
+// The trainer's objective (1 - lambda) L1 + lambda (1 - SSIM) from the two
+// means, in the float32 steps torch takes for it (trainer.py:303-305 with
+// lambda a Python float): c_l1 = (float)(1 - lambda), c_ss = (float)lambda.
+struct LossMix {
+    float c_l1, c_ss;
+    bool on;
+};
+
 // Sums the per-tile partials in a fixed order (double accumulators) and
-// writes [mean |pred - target|, mean SSIM].
+// writes the first nout of [mean |pred - target|, mean SSIM]; with mix.on
+// also out[2] = the mixed objective.
 __global__ __launch_bounds__(256) void k_loss_reduce(const float* __restrict__ partials,
                                                      int64_t nblk, double inv_n,
-                                                     float* __restrict__ out) {
+                                                     float* __restrict__ out, int nout,
+                                                     LossMix mix) {
     __shared__ double s[2][256];
     double a = 0.0, b = 0.0;
     for (int64_t i = threadIdx.x; i < nblk; i += 256) {
@@ -264,8 +274,10 @@ __global__ __launch_bounds__(256) void k_loss_reduce(const float* __restrict__ p
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        out[0] = (float)(s[0][0] * inv_n);
-        out[1] = (float)(s[1][0] * inv_n);
+        const float l1 = (float)(s[0][0] * inv_n), ss = (float)(s[1][0] * inv_n);
+        out[0] = l1;
+        if (nout > 1) out[1] = ss;
+        if (mix.on) out[2] = mix.c_l1 * l1 + mix.c_ss * (1.0f - ss);
     }
 }
 
@@ -275,7 +287,7 @@ template <int R, int CH>
 __global__ __launch_bounds__(kSsThreads) void k_ssim_bwd(
     const float* __restrict__ pred, const float* __restrict__ tgt, int H, int W, int C, int c0,
     int strips_x, int n_strips, SsimWindow win, const float* __restrict__ maps,
-    const float* __restrict__ grad_in, float inv_n, float* __restrict__ grad) {
+    const float* __restrict__ grad_in, LossMix mix, float inv_n, float* __restrict__ grad) {
     using S = SsimStrip<R, CH>;
     constexpr int K = S::K, NL = S::NL;
     __shared__ float s_row[kSsWaves][3][NL * kWave];
@@ -284,7 +296,11 @@ __global__ __launch_bounds__(kSsThreads) void k_ssim_bwd(
     const int strip = (int)gsx::xcd_remap(blockIdx.x, gridDim.x) * kSsWaves + wave;
     if (strip >= n_strips) return;
     const S s(strip, strips_x, W, C, c0, lane);
-    const float gl = grad_in[0] * inv_n, gs = grad_in[1] * inv_n;
+    // (g_l1, g_ssim): given, or from the mixed objective's cotangent g as
+    // autograd forms them: (g c_l1, -(g c_ss))
+    const float g_l1 = mix.on ? grad_in[0] * mix.c_l1 : grad_in[0];
+    const float g_ss = mix.on ? -(grad_in[0] * mix.c_ss) : grad_in[1];
+    const float gl = g_l1 * inv_n, gs = g_ss * inv_n;
     const int64_t plane = (int64_t)H * W * C;
     const int64_t rstride = (int64_t)W * C;
     const int64_t col = (int64_t)(s.x0 + s.xl) * C + c0 + s.ch;
@@ -611,25 +627,22 @@ int l1_fwd_into(int64_t n, const float* pred, const float* target, float* partia
                            pred, target, partials);
     GSX_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, (const float*)partials, nblk,
-                       1.0 / (double)n, out);
+                       1.0 / (double)n, out, 1, LossMix{0.0f, 0.0f, false});
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int64_t gsx_photometric_workspace_bytes(int32_t height, int32_t width, int32_t channels) {
-    if (height <= 0 || width <= 0 || channels <= 0) return 0;
-    const int64_t maps = 3 * (int64_t)height * width * channels * (int64_t)sizeof(float);
-    return align256(maps) + align256(2 * photometric_groups(channels) *
-                                     photometric_blocks(height, width) * (int64_t)sizeof(float));
+LossMix loss_mix(double lambda) {
+    // the Python scalars 1 - lambda and lambda, each rounded once to float32
+    return LossMix{(float)(1.0 - lambda), (float)lambda, true};
 }
 
-int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const float* pred,
-                        const float* target, int32_t window_size, float sigma, float max_val,
-                        void* workspace, int64_t workspace_bytes, float* out, void* stream) {
+bool lambda_ok(double lambda) { return lambda >= 0.0 && lambda <= 1.0; }
+
+int photometric_fwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                    const float* target, int32_t window_size, float sigma, float max_val,
+                    void* workspace, int64_t workspace_bytes, float* out, LossMix mix,
+                    void* stream) {
     if (height <= 0 || width <= 0 || channels <= 0) return GSX_ERR_INVALID;
     if (!pred || !target || !out || !workspace) return GSX_ERR_INVALID;
     if ((int64_t)height * width * channels >= (int64_t(1) << 40)) return GSX_ERR_TOO_LARGE;
@@ -676,15 +689,16 @@ int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const f
         GSX_LAUNCH_CHECK();
     }
     const double inv_n = 1.0 / ((double)height * width * channels);
-    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, partials, n_part, inv_n, out);
+    hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, partials, n_part, inv_n, out,
+                       2, mix);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
 
-int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const float* pred,
-                        const float* target, int32_t window_size, float sigma,
-                        const void* workspace, int64_t workspace_bytes, const float* grad_out,
-                        float* grad_pred, void* stream) {
+int photometric_bwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                    const float* target, int32_t window_size, float sigma,
+                    const void* workspace, int64_t workspace_bytes, const float* grad_out,
+                    LossMix mix, float* grad_pred, void* stream) {
     if (height <= 0 || width <= 0 || channels <= 0) return GSX_ERR_INVALID;
     if (!pred || !target || !workspace || !grad_out || !grad_pred) return GSX_ERR_INVALID;
     if ((int64_t)height * width * channels >= (int64_t(1) << 40)) return GSX_ERR_TOO_LARGE;
@@ -705,7 +719,7 @@ int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const f
     case RR * 8 + CC:                                                                          \
         hipLaunchKernelGGL((k_ssim_bwd<RR, CC>), dim3((unsigned)g.blocks), dim3(kSsThreads), 0, \
                            st, pred, target, height, width, channels, c0, g.strips_x,           \
-                           g.n_strips, win, maps, grad_out, inv_n, grad_pred);                 \
+                           g.n_strips, win, maps, grad_out, mix, inv_n, grad_pred);            \
         break;
 #define GSX_SSIM_BWD_R(RR) GSX_SSIM_BWD(RR, 1) GSX_SSIM_BWD(RR, 2) GSX_SSIM_BWD(RR, 3) GSX_SSIM_BWD(RR, 4)
             GSX_SSIM_BWD_R(0)
@@ -724,6 +738,52 @@ int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const f
         GSX_LAUNCH_CHECK();
     }
     return GSX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t gsx_photometric_workspace_bytes(int32_t height, int32_t width, int32_t channels) {
+    if (height <= 0 || width <= 0 || channels <= 0) return 0;
+    const int64_t maps = 3 * (int64_t)height * width * channels * (int64_t)sizeof(float);
+    return align256(maps) + align256(2 * photometric_groups(channels) *
+                                     photometric_blocks(height, width) * (int64_t)sizeof(float));
+}
+
+
+int gsx_photometric_fwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                        const float* target, int32_t window_size, float sigma, float max_val,
+                        void* workspace, int64_t workspace_bytes, float* out, void* stream) {
+    return photometric_fwd(height, width, channels, pred, target, window_size, sigma, max_val,
+                           workspace, workspace_bytes, out, LossMix{0.0f, 0.0f, false}, stream);
+}
+
+int gsx_photometric_bwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                        const float* target, int32_t window_size, float sigma,
+                        const void* workspace, int64_t workspace_bytes, const float* grad_out,
+                        float* grad_pred, void* stream) {
+    return photometric_bwd(height, width, channels, pred, target, window_size, sigma, workspace,
+                           workspace_bytes, grad_out, LossMix{0.0f, 0.0f, false}, grad_pred,
+                           stream);
+}
+
+int gsx_photometric_loss_fwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                             const float* target, int32_t window_size, float sigma,
+                             float max_val, double lambda, void* workspace,
+                             int64_t workspace_bytes, float* out3, void* stream) {
+    if (!lambda_ok(lambda)) return GSX_ERR_INVALID;
+    return photometric_fwd(height, width, channels, pred, target, window_size, sigma, max_val,
+                           workspace, workspace_bytes, out3, loss_mix(lambda), stream);
+}
+
+int gsx_photometric_loss_bwd(int32_t height, int32_t width, int32_t channels, const float* pred,
+                             const float* target, int32_t window_size, float sigma,
+                             double lambda, const void* workspace, int64_t workspace_bytes,
+                             const float* g_loss, float* grad_pred, void* stream) {
+    if (!lambda_ok(lambda)) return GSX_ERR_INVALID;
+    return photometric_bwd(height, width, channels, pred, target, window_size, sigma, workspace,
+                           workspace_bytes, g_loss, loss_mix(lambda), grad_pred, stream);
 }
 
 int64_t gsx_l1_workspace_bytes(int64_t n) {

@@ -3,15 +3,19 @@
 One ``GaussianTrainer.step`` on the vanilla and MCMC methods is
 
     fused render forward (preprocess, binning, raster)        libgsx
-    photometric loss: mean L1 and mean SSIM in one pass       gsx_photometric_fwd
-    backward: loss gradient, raster VJP (+ the screen-space    gsx_photometric_bwd,
+    photometric loss: (1 - lambda) L1 + lambda (1 - SSIM)      gsx_photometric_loss_fwd
+      from one pass
+    backward: loss gradient, raster VJP (+ the screen-space    gsx_photometric_loss_bwd,
       gradient statistics of density control)                  gsx_raster_bwd, ...
     preprocess VJP with the Adam update of all six parameter   gsx_preprocess_bwd_adam
       groups fused in (fuse_adam=False: the VJP, then one      (gsx_preprocess_bwd,
       multi-group Adam launch)                                  gsx_adam_step)
 
-with no host synchronisation except the duplicate count of the binning;
-density control runs every ``densify_every`` steps on the device.
+with no host synchronisation except the duplicate count of the binning
+and the step's loss, which is copied to pinned memory right after the loss
+kernels: step() waits for that copy, not for the backward or the update,
+so the next step is queued while the GPU finishes this one.  Density
+control runs every ``densify_every`` steps on the device.
 
 The reference probes dL/dmeans2d by adding a zero (N, 2) array to means2d
 (trainer.py:264-275, 325, 337); here the backward hands the rasterizer's
@@ -35,7 +39,7 @@ import numpy as np
 import torch
 
 from ..cameras import Camera
-from ..losses import photometric
+from ..losses import photometric_loss
 from ..optim import Adam, FusedAdam, adam_step, exponential_decay
 from .. import _lib
 from .density import GROUPS
@@ -125,6 +129,11 @@ class GaussianTrainer:
         # random draws of the MCMC method (relocation jitter, position noise)
         self.generator = generator
         self._unproject = None  # (camera key, maps) of the last 2DGS view
+        # the step's scalar results (loss, geometry terms) land in pinned host
+        # memory behind the kernels that produce them (_queue_readback)
+        self._host_scalars = None
+        self._scalars_ready = None
+        self._consts = {}  # (name, device) -> small constant tensors reused every step
         self._constrain()
         self.optimizers = {name: Adam(learning_rate=rate, eps=1e-15)
                            for name, rate in self._group_rates().items()}
@@ -173,9 +182,41 @@ class GaussianTrainer:
 
     # ------------------------------------------------------------ forward+backward
     def _photometric(self, img: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
-        l1, s = photometric(img, target)
-        lam = self.config.lambda_dssim
-        return (1.0 - lam) * l1 + lam * (1.0 - s)
+        """(1 - lambda) L1 + lambda (1 - SSIM) (trainer.py:303-305) as one op."""
+        return photometric_loss(img, target, self.config.lambda_dssim)
+
+    def _queue_readback(self, values) -> None:
+        """Copies the step's scalars to pinned host memory right behind the
+        kernels that produce them, before the backward is queued: step()
+        then returns them without waiting for the backward and the parameter
+        update, and the host queues the next step while the GPU finishes
+        this one."""
+        if self._host_scalars is None:
+            self._host_scalars = torch.empty((4,), dtype=torch.float32, pin_memory=True)
+        src = torch.stack([v.detach().reshape(()) for v in values]) if len(values) > 1 \
+            else values[0].detach().reshape(1)
+        self._host_scalars[:len(values)].copy_(src, non_blocking=True)
+        self._scalars_ready = torch.cuda.Event()
+        self._scalars_ready.record(torch.cuda.current_stream(src.device))
+
+    def _const(self, name: str, dev, make):
+        """A small constant device tensor, built once per device (a per-step
+        fill would cost a launch in every step)."""
+        key = (name, str(dev))
+        t = self._consts.get(key)
+        if t is None:
+            t = self._consts[key] = make()
+        return t
+
+    def _grads(self, loss, wrt):
+        """dloss/dwrt with a cached unit cotangent."""
+        one = self._const("one", loss.device,
+                          lambda: torch.ones((), dtype=loss.dtype, device=loss.device))
+        return torch.autograd.grad(loss, wrt, grad_outputs=one, allow_unused=True)
+
+    def _read_back(self, count: int) -> list[float]:
+        self._scalars_ready.synchronize()
+        return self._host_scalars[:count].tolist()
 
     def _fused_pass(self, params, camera, target, background, collect: bool) -> _StepResult:
         """Vanilla / MCMC: the fused render, photometric loss and backward;
@@ -194,7 +235,8 @@ class GaussianTrainer:
                           | _check_common(self.config.projection)),
                    antialias=self.config.antialias, screen_stats=stats, adam=adam)
         loss = self._photometric(out["image"], target)
-        grads = torch.autograd.grad(loss, [p[k] for k in GROUPS], allow_unused=True)
+        self._queue_readback([loss])
+        grads = self._grads(loss, [p[k] for k in GROUPS])
         return _StepResult(loss, None if adam is not None else grads, out["radii"])
 
     def _maps(self, camera: Camera, dev):
@@ -234,8 +276,10 @@ class GaussianTrainer:
                 cfg.lambda_2d_depth_variance, cfg.lambda_2d_normal_consistency,
                 maps=self._maps(camera, dev))
             loss = loss + g_loss
+        self._queue_readback([loss] if geometry is None else
+                             [loss, geometry["depth_variance"], geometry["normal_consistency"]])
         wrt = [p[k] for k in GROUPS] + [probe]
-        grads = torch.autograd.grad(loss, wrt, allow_unused=True)
+        grads = self._grads(loss, wrt)
         return _StepResult(loss, grads[:-1], proj["radii"], grads[-1], geometry)
 
     # ------------------------------------------------------------ density control
@@ -285,7 +329,9 @@ class GaussianTrainer:
         model = self.model
         dev = model.params["means"].device
         target = _lib.f32c(torch.as_tensor(target, device=dev))
-        background = torch.full((3,), 1.0 if cfg.white_background else 0.0, device=dev)
+        white = bool(cfg.white_background)
+        background = self._const(f"background{int(white)}", dev,
+                                 lambda: torch.full((3,), 1.0 if white else 0.0, device=dev))
         collect = cfg.densify_from <= self.step_count <= cfg.densify_until
         leaves = {k: model.params[k].detach().requires_grad_(True) for k in GROUPS}
 
@@ -323,11 +369,12 @@ class GaussianTrainer:
         if sh_grew:
             model.one_up_sh_degree()
 
+        scalars = self._read_back(1 if res.geometry is None else 3)
         geometry = {"depth_variance": 0.0, "normal_consistency": 0.0}
         if res.geometry is not None:
-            geometry = {k: float(v) for k, v in res.geometry.items()}
+            geometry = {"depth_variance": scalars[1], "normal_consistency": scalars[2]}
         return {
-            "loss": float(res.loss.detach()),
+            "loss": scalars[0],
             "num_gaussians": model.num_gaussians,
             "step": self.step_count,
             "active_sh_degree": model.active_sh_degree,

@@ -20,7 +20,7 @@ import torch
 
 from gpu_util import assert_bits, cu, host, oracle_backward, oracle_forward, rel_err, say
 from mlx3d_amd import _lib
-from mlx3d_amd.losses import l1_loss, photometric, ssim
+from mlx3d_amd.losses import l1_loss, photometric, photometric_loss, ssim
 from mlx3d_amd.optim import Adam, adam_step, exponential_decay
 from mlx3d_amd.splatting import GaussianModel
 from mlx3d_amd.splatting.trainer import GaussianTrainer, TrainerConfig
@@ -49,6 +49,53 @@ def test_photometric_matches_oracle(H, W, C, ws, sigma):
     e = rel_err(host(pt.grad), rg)
     say(f"  grad rel {e:.2e}")
     assert e < 1e-4
+
+
+@pytest.mark.parametrize("H,W,C,lam,ws", [(64, 80, 3, 0.2, 11), (37, 53, 3, 0.0, 11),
+                                          (24, 20, 5, 1.0, 7), (1080, 1920, 3, 0.2, 11),
+                                          (48, 40, 1, 0.35, 3)])
+def test_photometric_loss_matches_expression(H, W, C, lam, ws):
+    """photometric_loss (gsx_photometric_loss_fwd/_bwd) against the
+    expression (1 - lam) l1 + lam (1 - ssim) over photometric()'s outputs
+    with torch autograd: loss value and gradient bit for bit."""
+    say(f"photometric_loss H={H} W={W} C={C} lam={lam}")
+    rng = np.random.default_rng(H * W + C)
+    p = rng.random((H, W, C), dtype=np.float32)
+    t = rng.random((H, W, C), dtype=np.float32)
+    a = cu(p).requires_grad_(True)
+    b = cu(p).requires_grad_(True)
+    fused = photometric_loss(a, cu(t), lam, window_size=ws)
+    l1, s = photometric(b, cu(t), window_size=ws)
+    expr = (1.0 - lam) * l1 + lam * (1.0 - s)
+    assert_bits(host(fused).reshape(1), host(expr).reshape(1), "loss")
+    (2.5 * fused).backward()
+    (2.5 * expr).backward()
+    assert_bits(host(a.grad), host(b.grad), "grad")
+    with pytest.raises(ValueError):
+        photometric_loss(a, cu(t), 1.5)
+
+
+def test_l1_writes_one_float():
+    """gsx_l1_fwd and gsx_l1_fwd_noalloc write exactly their one output
+    float (the neighbours of `out` inside a larger buffer stay untouched)."""
+    rng = np.random.default_rng(3)
+    n = 100003
+    p, t = cu(rng.random(n, dtype=np.float32)), cu(rng.random(n, dtype=np.float32))
+    L, st = _lib.load(), _lib.stream_handle(p.device)
+    want = float(np.abs(host(p).astype(np.float64) - host(t)).mean())
+    ws = torch.empty((int(L.gsx_l1_workspace_bytes(n)),), dtype=torch.uint8, device=p.device)
+    for call in ("gsx_l1_fwd", "gsx_l1_fwd_noalloc"):
+        buf = torch.full((8,), -7.0, device=p.device)
+        out = buf[3:4]
+        if call == "gsx_l1_fwd":
+            rc = L.gsx_l1_fwd(n, _lib.ptr(p), _lib.ptr(t), _lib.ptr(ws), ws.numel(),
+                              _lib.ptr(out), st)
+        else:
+            rc = L.gsx_l1_fwd_noalloc(n, _lib.ptr(p), _lib.ptr(t), _lib.ptr(out), st)
+        _lib.check(rc, call)
+        got = host(buf)
+        assert abs(float(got[3]) - want) < 1e-6, call
+        assert (np.delete(got, 3) == -7.0).all(), (call, got)
 
 
 def test_photometric_full_size_properties():
