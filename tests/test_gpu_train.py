@@ -371,6 +371,31 @@ def test_preprocess_bwd_adam_rejects_mismatched_groups():
     assert_bits(host(params["means"]), before, "untouched means")
 
 
+def test_trainer_fused_adam_sh_degree_zero_model():
+    """A model stored with SH degree 0 (K = 1: an empty sh_rest group): the
+    fused update leaves the empty group alone and matches the separate one."""
+    say("fused adam, SH degree 0 model")
+    cam, means, quats, scales, opac, _ = random_scene(61, n=2000, width=160, height=112)
+    rng = np.random.default_rng(62)
+    raw = dict(means=means, quats=quats, scales=np.log(scales).astype(np.float32),
+               opacities=np.clip(rng.standard_normal(2000), -4, 3).astype(np.float32),
+               sh_dc=(rng.standard_normal((2000, 1, 3)) * 0.2).astype(np.float32),
+               sh_rest=np.zeros((2000, 0, 3), np.float32))
+    models = [GaussianModel({k: cu(v) for k, v in raw.items()}, sh_degree=0) for _ in range(2)]
+    cfg = TrainerConfig(densify_from=1 << 30, densify_until=1 << 30, opacity_reset_every=1 << 30,
+                        sh_increase_every=1 << 30)
+    trs = [GaussianTrainer(m, cfg, fuse_adam=f) for m, f in zip(models, (True, False))]
+    target = cu(rng.random((cam.height, cam.width, 3), dtype=np.float32))
+    for _ in range(3):
+        infos = [tr.step(cam, target) for tr in trs]
+        assert abs(infos[0]["loss"] - infos[1]["loss"]) <= 1e-6 * abs(infos[1]["loss"])
+    for k in ("means", "quats", "scales", "opacities", "sh_dc"):
+        a, b = host(models[0].params[k]), host(models[1].params[k])
+        lr = float(trs[0].optimizers[k].learning_rate)
+        assert (np.abs(a.astype(np.float64) - b) <= 24 * lr + 1e-6 * np.abs(b)).all(), k
+    assert models[0].params["sh_rest"].shape == (2000, 0, 3)
+
+
 @pytest.mark.parametrize("method,projection,degree", [("vanilla", "ewa", 3), ("vanilla", "ut", 1),
                                                        ("mcmc", "ewa", 0)])
 def test_trainer_fused_adam_close_to_separate_update(method, projection, degree):
