@@ -172,12 +172,13 @@ def _short(name: str) -> str:
     return name.split("(")[0]
 
 
-def summarize_prof(dirs, workload: str, command: str):
-    """rocprofv3 csv output under dirs -> profiles/kernels_<workload>.md and,
-    with counter runs present, profiles/traffic_<kernel>_<workload>.json."""
+def summarize_prof(dirs, workload: str, command: str, out_dir: str | None = None):
+    """rocprofv3 csv output under dirs -> <out_dir>/kernels_<workload>.md and,
+    with counter runs present, <out_dir>/traffic_<kernel>_<workload>.json
+    (out_dir: profiles/ by default)."""
     import glob
 
-    out_dir = _profiles_dir()
+    out_dir = out_dir or _profiles_dir()
     os.makedirs(out_dir, exist_ok=True)
 
     def find(pattern):
