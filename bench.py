@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X Gaussian-splatting rasterizer.
 
-Metric (BASELINE.json): fwd+bwd iterations/s and forward FPS at 1M Gaussians,
+Metric: fwd+bwd iterations/s and forward FPS at 1M Gaussians,
 SH degree 3, 1920x1080 (config 3: antialias, 8 orbit views), plus the HBM
 roofline fraction.  A step is one view: GaussianModel.render -> L1 loss
 against a seeded U(0,1) target -> backward to every raw parameter.  Inputs,
@@ -68,9 +68,10 @@ COPY_PROBE_KERNEL = "k_debug_expf"
 
 
 def algorithmic_bytes(N, D, P, C, Ka, sh_path, depth):
-    """Compulsory HBM bytes per stage, SURVEY 8(d)'s formulas: each tensor
-    read or written once.  D is the number of (tile, Gaussian) duplicates
-    binning writes; the rasterizers are charged one gather per duplicate.
+    """Compulsory HBM bytes per stage (the path's measurement contract): each
+    tensor read or written once.  D is the number of (tile, Gaussian)
+    duplicates binning writes; the rasterizers are charged one gather per
+    duplicate.
 
         raster fwd   D (28 + 4C [+4 depth]) + P (4C + 8 [+4 depth])
         raster bwd   D (28 + 4C) + P (4C + 8) + N (24 + 4C)
@@ -98,7 +99,7 @@ def needed_bytes(Dn, N, P, C, depth):
     """The rasterizers' bytes when only the list entries a pixel can reach are
     charged: Dn = sum over tiles of the largest n_contrib (the backward
     replays exactly those; the forward reads at least those).  A secondary
-    figure beside SURVEY 8(d)'s, which charges every duplicate."""
+    figure beside algorithmic_bytes, which charges every duplicate."""
     dz = 4 if depth else 0
     return dict(raster_fwd=Dn * (28 + 4 * C + dz) + P * (4 * C + 12 + dz),
                 raster_bwd=Dn * (28 + 4 * C) + P * (4 * C + 8) + N * (24 + 4 * C))
@@ -624,7 +625,7 @@ def main():
                      "algorithmic_bytes": int(B[dom]), "mean_ms": stages[dom]["ms"],
                      "median_ms": stages[dom]["median_ms"],
                      "frac_median": stages[dom]["frac_median"],
-                     "bytes_formula": "SURVEY 8(d), every duplicate charged",
+                     "bytes_formula": "bench.py algorithmic_bytes: every duplicate charged",
                      "frac_needed_entries": stages[dom].get("frac_needed_entries"),
                      "issue": _issue(dom, workload, stages[dom]["ms"])},
         "stages": stages,

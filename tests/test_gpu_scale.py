@@ -1,5 +1,5 @@
-"""Parity at the benchmark configurations' full sizes (BASELINE.json configs
-1-5): GPU vs CPU oracle on the same seeded scenes.  Sorted ids, tile ranges
+"""Parity at the benchmark configurations' full sizes (configs 1-5 of
+mlx3d_amd.scenes): GPU vs CPU oracle on the same seeded scenes.  Sorted ids, tile ranges
 and n_contrib bit-exact; images/depth bit-exact; gradients to 1e-3
 relative.  Also size-independent invariants of the binning."""
 
