@@ -357,6 +357,57 @@ def test_rasterize_building_block_bitexact():
     assert_bits(host(d["depth"]), refd["depth"], "depth")
 
 
+@pytest.mark.parametrize("channels", [3, 12])
+def test_rasterize_non_plain_batches(channels):
+    """Batches holding a Gaussian outside the rasterizers' fast-path range
+    (a mean 2e6 px away; a 1e21 conic centred on a pixel, which takes G = 1
+    there and exp underflow everywhere else) run the kernels' general
+    path, with range-checked exp and selects, for every Gaussian of the
+    batch: image and n_contrib bit-exact, gradients <= 1e-3 against the
+    oracle.  Four tiles list all Gaussians, as a caller of the building
+    block may."""
+    W = H = 32
+    n = 90
+    rng = np.random.default_rng(41 + channels)
+    m2 = rng.uniform(0.0, 32.0, (n, 2)).astype(np.float32)
+    s = rng.uniform(0.5, 4.0, n)
+    con = np.stack([1 / s ** 2, rng.uniform(-0.2, 0.2, n) / s ** 2, 1 / s ** 2], 1)
+    con = con.astype(np.float32)
+    op = rng.uniform(0.05, 0.9, n).astype(np.float32)
+    m2[3] = [2.0e6, 8.0]
+    m2[1] = [8.5, 8.5]
+    con[1] = [1e21, 0.0, 1e21]
+    op[1] = 0.6
+    feats = rng.uniform(0.0, 1.0, (n, channels)).astype(np.float32)
+    ids = np.arange(n, dtype=np.int32)
+    ranges = np.tile(np.array([[0, n]], np.int32), (4, 1))
+    t = [cu(a).requires_grad_(True) for a in (m2, con, feats, op)]
+    if channels == 3:
+        out = rasterize(*t, cu(ids), cu(ranges), W, H, 2, 2)
+        img = out["image"]
+    else:
+        out = rasterize_features(*t, cu(ids), cu(ranges), W, H, 2, 2)
+        img = out["features"]
+    ref = O.raster_fwd(m2, con, op, feats, ids, ranges, W, H)
+    np.testing.assert_array_equal(host(out["n_contrib"]), ref["n_contrib"])
+    assert_bits(host(img), ref["image"], "image")
+    assert_bits(host(out["final_T"]), ref["final_T"], "final_T")
+    g_img = rng.standard_normal(ref["image"].shape).astype(np.float32)
+    g_a = rng.standard_normal(ref["final_T"].shape).astype(np.float32)
+    ((img * cu(g_img)).sum() + (out["alpha"] * cu(g_a)).sum()).backward()
+    rg = O.raster_bwd(m2, con, op, feats, ids, ranges, W, H, ref["final_T"], ref["n_contrib"],
+                      g_img, grad_final_T=-g_a)
+    for name, a, key in [("means2d", t[0], "means2d"), ("conics", t[1], "conics"),
+                         ("features", t[2], "features"), ("opacities", t[3], "opacities")]:
+        g = host(a.grad)
+        assert np.isfinite(g).all(), name
+        e = rel_err(g, rg[key])
+        say(f"non-plain C={channels} grad {name}: rel {e:.2e}")
+        assert e < 1e-3
+    # the pixel-centred Gaussian composites (at its own pixel only)
+    assert float(host(t[3].grad)[1]) != 0.0
+
+
 def test_rasterize_backward():
     cam, means, quats, scales, opac, colors = random_scene(3, n=3000, width=200, height=150)
     p = O.project(oracle_camera(cam), means, quats, scales)
