@@ -537,6 +537,41 @@ def test_normalized_features_match_depth():
     assert np.abs(host(feat["features"][..., 0])[~valid]).max(initial=0) < 1e-6
 
 
+def test_render_on_side_streams():
+    """Renders and their backward enqueued on two side streams back to back
+    (each stream has its own binning workspace and status words) match the
+    same renders run one after the other on the default stream: images and
+    n_contrib bit for bit, gradients up to the float atomics' order."""
+    scenes = [random_scene(seed, n=3000, width=200, height=150) for seed in (31, 32)]
+    rng = np.random.default_rng(33)
+    cot = [cu(rng.standard_normal((150, 200, 3)).astype(np.float32)) for _ in scenes]
+
+    def run(i):
+        cam, means, quats, scales, opac, colors = scenes[i]
+        t = [cu(a).requires_grad_(True) for a in (means, quats, scales, opac, colors)]
+        out = render_gaussians(cam, t[0], t[1], t[2], t[3], colors=t[4])
+        (out["image"] * cot[i]).sum().backward()
+        return out, t
+
+    want = [run(i) for i in range(2)]
+    torch.cuda.synchronize()
+    side = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    got = []
+    for i, s in enumerate(side):
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            got.append(run(i))
+    torch.cuda.synchronize()
+    for i in range(2):
+        (wo, wt), (go, gt) = want[i], got[i]
+        np.testing.assert_array_equal(host(go["n_contrib"]), host(wo["n_contrib"]))
+        assert_bits(host(go["image"]), host(wo["image"]), f"image {i}")
+        for name, a, b in zip(("means", "quats", "scales", "opacities", "colors"), gt, wt):
+            e = rel_err(host(a.grad), host(b.grad))
+            say(f"side stream {i} grad {name}: rel {e:.2e}")
+            assert e < 1e-5
+
+
 def test_empty_and_culled_render():
     cam, means, quats, scales, opac, colors = random_scene(8, n=10, width=64, height=48)
     means[:, 2] = -10.0  # all behind the camera
