@@ -65,6 +65,18 @@ def test_cpu_tensors_are_refused():
         bin_gaussians(torch.zeros(4, 2), torch.ones(4), torch.ones(4), 32, 32)
 
 
+def test_missing_library_raises(monkeypatch, tmp_path):
+    """Without a built libgsx.so the package raises on first use; there is
+    no other compute path to fall back to."""
+    from mlx3d_amd import _lib
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libgsx.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(ImportError, match="no fallback compute path"):
+        _lib.load()
+    with pytest.raises(ImportError, match="is missing"):
+        _lib.strerror(0)
+
+
 @pytest.mark.gpu
 def test_model_from_points_scales_and_layout():
     pts = torch.tensor([[0.0, 0, 0], [1.0, 0, 0], [0, 2.0, 0], [0, 0, 3.0], [1.0, 1.0, 0]])
