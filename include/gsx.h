@@ -22,7 +22,9 @@
  *  - Return value: GSX_OK (0) on success, > 0 = required capacity (retry
  *    with a larger buffer), < 0 = error code (gsx_strerror).
  *  - No C++ exception crosses the ABI.  Entry points are reentrant; calls
- *    on different streams may run concurrently.
+ *    on different streams may run concurrently, with one exception:
+ *    gsx_l1_fwd_noalloc shares one scratch array per GPU, so the caller
+ *    must order its calls on one GPU (overlapping calls race).
  */
 #ifndef GSX_H
 #define GSX_H

@@ -69,10 +69,15 @@ class Adam:
             self.state[name] = st
         return st
 
-    def _groups(self, grads: dict[str, torch.Tensor], params: dict[str, torch.Tensor]):
-        lr = self._schedule(self.step)
+    def _advance(self, lr: float) -> None:
+        """Records that the update at the current step (rate ``lr``) was
+        enqueued: called only after its launch succeeded, so a failed launch
+        leaves the schedule where it was."""
         self._last_lr = lr
         self.step += 1
+
+    def _groups(self, grads: dict[str, torch.Tensor], params: dict[str, torch.Tensor]):
+        lr = self._schedule(self.step)
         out = []
         for name, g in grads.items():
             p = params[name]
@@ -89,13 +94,12 @@ class Adam:
 
     def _fused_group(self, name: str, p: torch.Tensor):
         """The bookkeeping of one update of parameter ``name`` whose gradient
-        a kernel computes and applies itself: advances the schedule and
-        returns (param, m, v, lr)."""
+        a kernel computes and applies itself: returns (param, m, v, lr) at
+        the current step; the caller advances the schedule (``_advance``)
+        once the kernel is enqueued."""
         if p.dtype != torch.float32 or not p.is_contiguous():
             raise ValueError(f"parameter {name!r} must be contiguous float32")
         lr = self._schedule(self.step)
-        self._last_lr = lr
-        self.step += 1
         st = self._state_for(name, p)
         return p, st["m"], st["v"], lr
 
@@ -122,6 +126,8 @@ def adam_step(updates) -> None:
     dev = _lib.require_device(*[g[0] for g in groups])
     L = _lib.load()
     keep = []
+    # each optimiser's schedule advances once, after all its launches succeeded
+    advance = {id(opt): (opt, g[4]) for g in groups for opt in (g[5],)}
     for s in range(0, len(groups), _lib.ADAM_MAX_GROUPS):
         chunk = groups[s:s + _lib.ADAM_MAX_GROUPS]
         arr = (_lib.GsxAdamGroup * len(chunk))()
@@ -132,18 +138,24 @@ def adam_step(updates) -> None:
         with stage("adam"):
             _lib.check(L.gsx_adam_step(len(chunk), ctypes.cast(arr, ctypes.c_void_p), b1, b2,
                                        eps, _lib.stream_handle(dev)), "gsx_adam_step")
+    for opt, lr in advance.values():
+        opt._advance(lr)
 
 
 class FusedAdam:
     """One Adam update of several parameters applied by the kernel that
     computes their gradients (``gsx_preprocess_bwd_adam``): built from
-    ``[(adam, name, param), ...]`` before the backward runs, it advances each
-    optimiser's schedule as ``adam_step`` would and holds the
-    ``gsx_adam_group`` records (gradient pointers unused)."""
+    ``[(adam, name, param), ...]`` before the backward runs, it holds the
+    ``gsx_adam_group`` records (gradient pointers unused) with each
+    optimiser's rate at its current step.  ``commit()``, called once the
+    kernel is enqueued, advances each optimiser's schedule once, as
+    ``adam_step`` does; an update that never launched leaves them alone."""
 
     def __init__(self, updates):
         groups = [opt._fused_group(name, p) for opt, name, p in updates]
         opts = [u[0] for u in updates]
+        self._advance = {id(o): (o, g[3]) for o, g in zip(opts, groups)}
+        self.committed = False
         self.betas, self.eps = opts[0].betas, opts[0].eps
         if any(o.betas != self.betas or o.eps != self.eps for o in opts):
             raise ValueError("FusedAdam: optimisers with different betas/eps")
@@ -153,3 +165,10 @@ class FusedAdam:
             self.records[k] = _lib.GsxAdamGroup(p.data_ptr(), None, m.data_ptr(), v.data_ptr(),
                                                 p.numel(), lr)
 
+    def commit(self) -> None:
+        """Advances the schedules (once per update; later calls do nothing)."""
+        if self.committed:
+            return
+        self.committed = True
+        for opt, lr in self._advance.values():
+            opt._advance(lr)

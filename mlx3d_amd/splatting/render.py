@@ -157,6 +157,7 @@ class _RenderFn(torch.autograd.Function):
                     _lib.ptr(gcomp_in), ctypes.cast(opt.records, ctypes.c_void_p),
                     opt.betas[0], opt.betas[1], opt.eps, _lib.stream_handle(dev)),
                     "gsx_preprocess_bwd_adam")
+            opt.commit()
             return None, None, None, None, None, None, None, None, None
         f = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)  # noqa: E731
         g_means, g_quats, g_scales, g_opac = f(n, 3), f(n, 4), f(n, 3), f(n)

@@ -239,8 +239,19 @@ class GaussianTrainer:
         grads = self._grads(loss, [p[k] for k in GROUPS])
         return _StepResult(loss, None if adam is not None else grads, out["radii"])
 
+    @staticmethod
+    def _camera_key(camera: Camera, dev) -> tuple:
+        """Everything the unprojection maps depend on, by value: a Camera is
+        a mutable dataclass and a new one may reuse a freed one's id()."""
+        R = torch.as_tensor(camera.R, dtype=torch.float32).detach().cpu().contiguous()
+        t = torch.as_tensor(camera.t, dtype=torch.float32).detach().cpu().contiguous()
+        dist = None if camera.distortion is None else tuple(float(v) for v in camera.distortion)
+        return (R.numpy().tobytes(), t.numpy().tobytes(), float(camera.fx), float(camera.fy),
+                float(camera.cx), float(camera.cy), int(camera.width), int(camera.height), dist,
+                bool(camera.fisheye), bool(camera.orthographic), str(dev))
+
     def _maps(self, camera: Camera, dev):
-        key = (id(camera), camera.width, camera.height, str(dev))
+        key = GaussianTrainer._camera_key(camera, dev)
         if self._unproject is None or self._unproject[0] != key:
             self._unproject = (key, unprojection_maps(camera, dev))
         return self._unproject[1]
@@ -269,8 +280,12 @@ class GaussianTrainer:
         geometry = None
         if cfg.lambda_2d_depth_variance > 0 or cfg.lambda_2d_normal_consistency > 0:
             feats = surfel_features(p["means"], p["quats"], proj["depths"], camera)
-            rendered = rasterize_features(xy, proj["conics"], feats, opac, ids, ranges,
-                                          camera.width, camera.height, tx, ty, normalize=True)
+            # the geometry render reads the projection's means2d, not the
+            # probed ones (trainer.py:212-213): the probe carries only the
+            # photometric render's dL/dmeans2d into the density statistics
+            rendered = rasterize_features(proj["means2d"], proj["conics"], feats, opac, ids,
+                                          ranges, camera.width, camera.height, tx, ty,
+                                          normalize=True)
             g_loss, geometry = geometry_loss(
                 rendered["features"], rendered["alpha"], camera, cfg.geometry_min_alpha,
                 cfg.lambda_2d_depth_variance, cfg.lambda_2d_normal_consistency,

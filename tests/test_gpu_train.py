@@ -605,3 +605,34 @@ def test_trainer_loop(method):
         assert model.num_gaussians != 2000
     if method == "2dgs":
         assert float(model.params["scales"][:, 2].max()) <= np.log(1e-4 * 2.0) + 1e-6
+
+
+def test_2dgs_geometry_terms_leave_screen_stats_alone():
+    """The 2DGS geometry render reads the projection's means2d, not the
+    probed ones (trainer.py:212-213): from identical state, one step with the
+    geometry regularisers on gives the same density statistics as one with
+    them off.  The raster backward's float atomics add in run-dependent
+    order, so the comparison is relative (1e-5 of the largest entry), far
+    below the geometry gradient the probe would otherwise collect."""
+    say("2dgs screen statistics with and without geometry terms")
+    cam, gt, _, _ = _model(51, 3000)
+    with torch.no_grad():
+        target = gt.render(cam)["image"].detach()
+    stats = []
+    for lam_dv, lam_nc in ((0.0, 0.0), (0.5, 0.5)):
+        _, model, _, _ = _model(52, 2000, degree=0)
+        cfg = TrainerConfig(method="2dgs", densify_from=1, densify_until=100,
+                            densify_every=1000, opacity_reset_every=1000,
+                            lambda_2d_depth_variance=lam_dv,
+                            lambda_2d_normal_consistency=lam_nc)
+        tr = GaussianTrainer(model, cfg, scene_extent=2.0)
+        info = tr.step(cam, target)
+        assert np.isfinite(info["loss"])
+        torch.cuda.synchronize()
+        stats.append((host(tr.grad_accum), host(tr.grad_count)))
+    (a0, c0), (a1, c1) = stats
+    np.testing.assert_array_equal(c0, c1)
+    assert float(a0.max()) > 0
+    e = float(np.abs(a1 - a0).max() / np.abs(a0).max())
+    say(f"  grad_accum rel diff {e:.2e}")
+    assert e < 1e-5

@@ -129,3 +129,47 @@ def test_quat_scale_to_cov3d_closed_form():
     np.testing.assert_allclose(cov.numpy(), cov.transpose(1, 2).numpy(), atol=1e-6)
     np.testing.assert_allclose(torch.linalg.det(cov).numpy(),
                                (s.double() ** 2).prod(1).numpy(), rtol=1e-4)
+
+
+def test_unprojection_cache_follows_camera_content():
+    """The 2DGS unprojection maps are cached per camera *content*: a camera
+    edited in place (same id()) or a fresh camera gets fresh maps."""
+    from types import SimpleNamespace
+
+    from mlx3d_amd.splatting.geometry import unprojection_maps
+    from mlx3d_amd.splatting.trainer import GaussianTrainer
+
+    holder = SimpleNamespace(_unproject=None)
+    cam = Camera.look_at(eye=(0, 0, -3.0), width=24, height=16)
+    base0, dir0 = GaussianTrainer._maps(holder, cam, "cpu")
+    other = Camera.look_at(eye=(1.0, 0.5, -3.0), width=24, height=16)
+    cam.R, cam.t = other.R.clone(), other.t.clone()  # moved in place: same id()
+    base1, dir1 = GaussianTrainer._maps(holder, cam, "cpu")
+    want_b, want_d = unprojection_maps(cam, "cpu")
+    assert torch.equal(base1, want_b) and torch.equal(dir1, want_d)
+    assert not torch.equal(base0, base1)
+    cam.fx *= 1.5  # intrinsics edited in place
+    base2, dir2 = GaussianTrainer._maps(holder, cam, "cpu")
+    assert torch.equal(dir2, unprojection_maps(cam, "cpu")[1]) and not torch.equal(dir1, dir2)
+    # an equal camera reuses the cached maps (no rebuild)
+    assert GaussianTrainer._maps(holder, cam, "cpu")[0] is base2
+
+
+def test_adam_schedule_advances_only_after_launch():
+    """FusedAdam holds the current rates and advances each optimiser once, on
+    commit(); adam_step advances only after its launch, so an update that
+    raised before launching leaves the schedule where it was."""
+    from mlx3d_amd.optim import Adam, FusedAdam, adam_step, exponential_decay
+
+    opt = Adam(learning_rate=exponential_decay(1e-2, 0.5), eps=1e-15)
+    p = torch.zeros(8)
+    fused = FusedAdam([(opt, "p", p)])
+    assert opt.step == 0 and fused.records[0].lr == np.float32(1e-2)
+    fused.commit()
+    fused.commit()  # once only
+    assert opt.step == 1 and opt.learning_rate == 1e-2
+    fused = FusedAdam([(opt, "p", p)])
+    assert fused.records[0].lr == np.float32(0.5e-2) and opt.step == 1  # not committed: no advance
+    with pytest.raises(ValueError):  # CPU tensors are refused before any launch
+        adam_step([(opt, {"p": torch.ones(8)}, {"p": p})])
+    assert opt.step == 1 and opt.learning_rate == 1e-2
