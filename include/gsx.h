@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GSX_ABI_VERSION 3
+#define GSX_ABI_VERSION 4
 #define GSX_TILE_SIZE 16 /* tiles.py:14 */
 
 enum gsx_status {
@@ -168,7 +168,12 @@ int gsx_eval_sh_bwd(int64_t n, int32_t K, int32_t C, int32_t degree,
  * Outputs: means2d (N,2), depths (N), radii (N), compensation (N),
  * conic_opacity (N,4) = (conic a, b, c, opacity*compensation),
  * colors_out (N,3) (SH mode only), and for binning tile_counts (N),
- * depth_keys (N) and tile_rects (N,2) (packed xmin|ymin<<16, w|h<<16). */
+ * depth_keys (N) and tile_rects (N,2) (packed xmin|ymin<<16, w|h<<16).
+ * depth_keys order the binned Gaussians by depth: the orderable bits of z
+ * minus those of the camera's znear (binned Gaussians have z > znear), so
+ * the depth sort's top 2-bit pass is skipped for every z below about 2^30
+ * float32 ulps past znear; Gaussians with a zero tile count get key 0 and
+ * rectangle (0, 0). */
 int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means,
                        const float* quats, const float* scales,
                        const float* opacities, const float* sh0,
@@ -203,7 +208,8 @@ int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means,
  * Replaces bin_gaussians (splatting/tiles.py:19-182, refine_tiles off).
  *
  * gsx_bin_prepare: tiles.py:54-65 for externally supplied means2d (N,2),
- * radii (N), depths (N) -> tile_counts, depth_keys, tile_rects. */
+ * radii (N), depths (N) -> tile_counts, depth_keys (the orderable bits of
+ * any float depth; 0 for Gaussians with a zero count), tile_rects. */
 int gsx_bin_prepare(int64_t n, const float* means2d, const float* radii,
                     const float* depths, int32_t width, int32_t height,
                     uint32_t* tile_counts, uint32_t* depth_keys,
@@ -223,7 +229,17 @@ int64_t gsx_bin_workspace_bytes(int64_t n, int64_t capacity, int32_t num_tiles);
  * (refine_tiles, tiles.py:91-164).  Synchronises `stream` once to read D
  * into *num_dups.  Returns 1 if the duplicates exceed capacity (then
  * *num_dups is the capacity needed; retry with at least that).  n and
- * capacity < 2^30; sorted_ids must be 16-byte aligned. */
+ * capacity < 2^30; sorted_ids must be 16-byte aligned.  tile_rects of
+ * Gaussians with a zero tile count must be (0, 0) (as gsx_bin_prepare and
+ * gsx_preprocess_fwd write them).
+ *
+ * Up to 256 x 256 tiles without refine_tiles the duplicates are placed
+ * without a sort over them: Gaussians go into per-row lists by a stable
+ * radix pass over their rows, and each row's duplicates are ranked by
+ * column within 4096-duplicate segments whose per-column offsets a scan
+ * over the row has fixed.  Larger images and refine_tiles run the general
+ * path: emission of (tile, id) pairs and a stable radix sort of the tile
+ * ids. */
 int gsx_bin_sort(int64_t n, const uint32_t* tile_counts,
                  const uint32_t* depth_keys, const uint32_t* tile_rects,
                  const float* means2d, const float* conics, int64_t conic_stride,
@@ -232,15 +248,17 @@ int gsx_bin_sort(int64_t n, const uint32_t* tile_counts,
                  int32_t* sorted_ids, int32_t* tile_ranges,
                  int64_t* num_dups, void* stream);
 
-/* The same pipeline without the readback: bin_status (4 device words) gets
- * the number of duplicates emitted, the gsx_bin_error bits, the number
- * refine_tiles dropped (they sort after all kept ones) and the sum of the
- * tile counts (see gsx_bin_count_async).  If the emitted
- * duplicates exceed capacity, sorted_ids/tile_ranges hold an incomplete
- * (but in-bounds: ids < n, ranges within [0, capacity]) binning, so kernels
- * enqueued behind it stay safe; the caller copies bin_status to the host
- * when it needs D, checks it with gsx_bin_status_check and re-runs with a
- * larger capacity if asked to. */
+/* The same pipeline without the readback: bin_status (8 device words)
+ * gets [0] the number of duplicates emitted, [1] the gsx_bin_error bits,
+ * [2] the number refine_tiles dropped (they sort after all kept ones),
+ * [3] the sum of the tile counts and [4] the sum of the binned rectangles'
+ * heights (see gsx_bin_count_async); [5..7] are reserved (zero).  If the
+ * emitted duplicates exceed capacity, sorted_ids/tile_ranges hold an
+ * incomplete (but in-bounds: ids < n, ranges within [0, capacity]; on the
+ * row-placement path all ranges (0,0)) binning, so kernels enqueued behind
+ * it stay safe; the caller copies bin_status to the host when it needs D,
+ * checks it with gsx_bin_status_check and re-runs with a larger capacity if
+ * asked to. */
 int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts,
                        const uint32_t* depth_keys, const uint32_t* tile_rects,
                        const float* means2d, const float* conics,
@@ -253,41 +271,47 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts,
 /* The same pipeline in three calls, for callers that size the duplicate
  * buffers exactly instead of guessing a capacity.
  *
- * gsx_bin_count_async: zeroes tile_ranges and bin_status words 0, 2 and 3,
+ * gsx_bin_count_async: zeroes tile_ranges and bin_status words 0 and 2..7,
  * builds the depth keys' digit histograms in depth_ws
- * (gsx_bin_depth_workspace_bytes(n)) and adds the tile counts into
- * bin_status[3]: the number of duplicates emission will write (before
- * refine_tiles drops any), with GSX_BIN_ERR_OVERFLOW in bin_status[1] past
- * 2^30 - 1.  bin_status[1] is not cleared: the error bits of every call on
- * one bin_status accumulate until the caller clears the word, so a copy
- * made behind this call also reports the checks of earlier calls' tile
- * phases.  A caller that copies bin_status to the host right behind it and
- * enqueues gsx_bin_depth_async before waiting for that copy reads the count
- * while the device sorts.
+ * (gsx_bin_depth_workspace_bytes(n)), adds the tile counts into
+ * bin_status[3] (the number of duplicates emission will write before
+ * refine_tiles drops any, with GSX_BIN_ERR_OVERFLOW in bin_status[1] past
+ * 2^30 - 1) and the binned rectangles' heights into bin_status[4], and, for
+ * images up to 256 x 256 tiles, per-row histograms of the rectangles.
+ * bin_status[1] is not cleared: the error bits of every call on one
+ * bin_status accumulate until the caller clears the word, so a readback
+ * behind this call also reports the checks of earlier calls' tile phases.
  *
  * gsx_bin_depth_async: the stable depth sort (tiles.py:67-72) of the same
- * n depth keys in the same depth_ws.
+ * n depth keys in the same depth_ws, in passes of 10, 10, 10 and 2 bits
+ * (the last is skipped on the device when all keys share its digit, as
+ * the renderer's near-plane-relative keys do).  With host_status != NULL
+ * (pinned host memory of 8 uint64 words, e.g. the first half of
+ * gsx_host_status_alloc's 16) its first kernel writes host_status[k] =
+ * (uint64_t)seq << 32 | bin_status[k] for k = 0..7 after the count phase
+ * has finished: the host polls for `seq` instead of enqueueing a copy.
  *
- * gsx_bin_tiles_async: the rest of tiles.py:73-182 (scan of the counts in
- * depth order, emission, tile sort, ranges) on the depth sort's output,
- * with the same n, tile_counts, width and height and the same depth_ws,
- * plus tile_ws (gsx_bin_tile_workspace_bytes(capacity, num_tiles)).
- * bin_status then holds what gsx_bin_sort_async documents; with capacity =
- * bin_status[3] the duplicates always fit.
+ * gsx_bin_tiles_async: the rest of tiles.py:73-182 on the depth sort's
+ * output, with the same n, tile_counts, tile_rects, width and height and
+ * the same depth_ws, plus tile_ws (gsx_bin_tile_workspace_bytes(capacity,
+ * num_tiles)).  bin_status then holds what gsx_bin_sort_async documents;
+ * with capacity = bin_status[3] the duplicates always fit.  With
+ * host_status != NULL (8 words) its last kernel writes the final status
+ * there the same way.
  *
  * gsx_bin_sort_async is the three in sequence on one workspace (depth part
- * first, all four bin_status words cleared); gsx_bin_workspace_bytes is the
- * sum of the two sizes. */
+ * first, all bin_status words cleared); gsx_bin_workspace_bytes is the sum
+ * of the two sizes. */
 int64_t gsx_bin_depth_workspace_bytes(int64_t n);
 int64_t gsx_bin_tile_workspace_bytes(int64_t capacity, int32_t num_tiles);
 int gsx_bin_count_async(int64_t n, const uint32_t* tile_counts,
-                        const uint32_t* depth_keys, int32_t width,
-                        int32_t height, void* depth_ws,
+                        const uint32_t* depth_keys, const uint32_t* tile_rects,
+                        int32_t width, int32_t height, void* depth_ws,
                         int64_t depth_ws_bytes, int32_t* tile_ranges,
                         uint32_t* bin_status, void* stream);
 int gsx_bin_depth_async(int64_t n, const uint32_t* depth_keys, void* depth_ws,
                         int64_t depth_ws_bytes, uint32_t* bin_status,
-                        void* stream);
+                        uint64_t* host_status, uint32_t seq, void* stream);
 int gsx_bin_tiles_async(int64_t n, const uint32_t* tile_counts,
                         const uint32_t* tile_rects, const float* means2d,
                         const float* conics, int64_t conic_stride,
@@ -295,13 +319,20 @@ int gsx_bin_tiles_async(int64_t n, const uint32_t* tile_counts,
                         int64_t depth_ws_bytes, void* tile_ws,
                         int64_t tile_ws_bytes, int64_t capacity,
                         int32_t* sorted_ids, int32_t* tile_ranges,
-                        uint32_t* bin_status, void* stream);
+                        uint32_t* bin_status, uint64_t* host_status,
+                        uint32_t seq, void* stream);
 
-/* Host-side: interprets a host copy of the 4 bin_status words.  Returns
+/* Host-side: interprets a host copy of the bin_status words.  Returns
  * GSX_OK with *num_dups = D (duplicates kept), 1 with *num_dups = the
  * capacity needed, GSX_ERR_TOO_LARGE or GSX_ERR_DEVICE. */
 int gsx_bin_status_check(const uint32_t* host_status, int64_t capacity,
                          int64_t* num_dups);
+
+/* Pinned, device-coherent host memory of 16 uint64 words (two host_status
+ * targets), zeroed; the one allocation in this library, of host memory, for
+ * the status polling above.  Released with gsx_host_status_free. */
+int gsx_host_status_alloc(uint64_t** words);
+int gsx_host_status_free(uint64_t* words);
 
 /* ---------------------------------------------------------- rasterizer --
  * Packs conics (N,3) and opacities (N) into conic_opacity (N,4), the

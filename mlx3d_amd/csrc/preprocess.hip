@@ -360,7 +360,9 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_fwd(
     uint2 rect;
     const uint32_t cnt = tile_rect(p.u, p.v, p.radius, cam.width, cam.height, tiles_x, tiles_y, rect);
     counts[i] = cnt;
-    dkeys[i] = cnt ? depth_key(p.z) : 0xFFFFFFFFu;
+    // binned Gaussians have z > znear: the key is the distance from the
+    // near plane in orderable float bits (small for every realistic depth)
+    dkeys[i] = cnt ? depth_key(p.z) - depth_key(cam.znear) : 0u;
     rects[i] = rect;
 }
 
@@ -695,7 +697,7 @@ __global__ __launch_bounds__(kThreads) void k_bin_prepare(
     uint2 rect;
     const uint32_t cnt = tile_rect(m.x, m.y, radii[i], width, height, tiles_x, tiles_y, rect);
     counts[i] = cnt;
-    dkeys[i] = cnt ? depth_key(depths[i]) : 0xFFFFFFFFu;
+    dkeys[i] = cnt ? depth_key(depths[i]) : 0u;
     rects[i] = rect;
 }
 

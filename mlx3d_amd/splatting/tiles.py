@@ -4,15 +4,19 @@
 (D,) int32 in (tile, depth, index) order and ``tile_ranges`` (tiles, 2)
 int32 with (0, 0) for empty tiles.  The work runs in ``gsx_bin_prepare`` and
 ``gsx_bin_count_async`` / ``gsx_bin_depth_async`` / ``gsx_bin_tiles_async``
-(device radix sorts).  The host reads the duplicate count (the sum of the tile
-counts, which the reference reads at tiles.py:68) while the depth sort still
-runs, and sizes the tile phase's buffers exactly from it.
+(device radix passes and row placement).  The host reads the duplicate count
+(the sum of the tile counts, which the reference reads at tiles.py:68) while
+the depth sort still runs -- the depth sort's first kernel writes the status
+words into pinned host memory, which the host polls, so no copy or event
+sits between the kernels -- and sizes the tile phase's buffers exactly.
 """
 
 from __future__ import annotations
 
 import ctypes
 import threading
+import time
+import weakref
 
 import numpy as np
 import torch
@@ -23,13 +27,51 @@ TILE_SIZE = 16
 _BIN_ERR_OVERFLOW = 2  # gsx_bin_error
 _ERR_TOO_LARGE = -4    # gsx_status
 _ERR_DEVICE = -5
+_STATUS_WORDS = 8
+_WAIT_LIMIT_S = 120.0  # a device that never publishes is reported, not waited on forever
 
 __all__ = ["TILE_SIZE", "bin_gaussians"]
 
 
+class _HostStatus:
+    """Two pinned host targets of 8 status words each (count phase, final
+    status), which the binning's kernels write as (seq << 32 | word)."""
+
+    def __init__(self):
+        L = _lib.load()
+        p = ctypes.c_void_p()
+        _lib.check(L.gsx_host_status_alloc(ctypes.byref(p)), "gsx_host_status_alloc")
+        self.addr = p.value
+        self.words = np.ctypeslib.as_array(
+            (ctypes.c_uint64 * (2 * _STATUS_WORDS)).from_address(self.addr))
+        weakref.finalize(self, L.gsx_host_status_free, ctypes.c_void_p(self.addr))
+
+    def slot(self, k: int):
+        return ctypes.c_void_p(self.addr + 8 * _STATUS_WORDS * k)
+
+    def wait(self, k: int, seq: int) -> tuple[np.ndarray, int]:
+        """The words of target k once they carry `seq` or a later sequence
+        number (kernels of one stream publish in order), and that number."""
+        w = self.words[_STATUS_WORDS * k:_STATUS_WORDS * (k + 1)]
+        t0 = None
+        spins = 0
+        while True:
+            v = w.copy()
+            tags = (v >> np.uint64(32)).astype(np.uint32)
+            ahead = (tags - np.uint32(seq)).astype(np.uint32)  # modular: >= seq
+            if (ahead < np.uint32(1 << 31)).all() and (tags == tags[0]).all():
+                return (v & np.uint64(0xFFFFFFFF)).astype(np.uint32), int(tags[0])
+            spins += 1
+            if spins % 4096 == 0:
+                t0 = t0 or time.perf_counter()
+                if time.perf_counter() - t0 > _WAIT_LIMIT_S:
+                    _lib.check(_ERR_DEVICE, "binning status (no status from the device)")
+
+
 class _Workspace:
-    """Grow-only scratch buffers of the binning phases and the persistent
-    bin_status words, one set per (device, stream)."""
+    """Grow-only scratch buffers of the binning phases, the persistent
+    bin_status words and their pinned host targets, one set per (device,
+    stream)."""
 
     def __init__(self, dev):
         self.depth = None
@@ -37,7 +79,13 @@ class _Workspace:
         # device error bits accumulate here across jobs (gsx_bin_count_async
         # leaves word 1 alone), so each job's count readback also reports
         # the checks of the jobs before it
-        self.status = torch.zeros((4,), dtype=torch.int32, device=dev)
+        self.status = torch.zeros((_STATUS_WORDS,), dtype=torch.int32, device=dev)
+        self.host = _HostStatus()
+        self.seq = 0
+
+    def next_seq(self) -> int:
+        self.seq = (self.seq + 1) & 0xFFFFFFFF
+        return self.seq
 
     @staticmethod
     def _grow(buf, dev, need: int, what: str) -> torch.Tensor:
@@ -71,16 +119,6 @@ def _workspace_for(dev, stream) -> _Workspace:
     return ws
 
 
-def _pinned_status(status: torch.Tensor):
-    """Copy of the 4 status words into pinned host memory behind the work
-    enqueued so far, and the event that marks it."""
-    host = torch.empty((4,), dtype=torch.int32, pin_memory=True)
-    host.copy_(status, non_blocking=True)
-    ev = torch.cuda.Event()
-    ev.record()
-    return host, ev
-
-
 def _raise_on_errors(ws: _Workspace, err: int, what: str) -> None:
     if err == 0:
         return
@@ -95,15 +133,14 @@ class BinJob:
     """One binning on the device, sized exactly.
 
     gsx_bin_count_async sums the tile counts, the number of duplicates
-    emission writes; the job copies the status words to pinned memory,
-    enqueues the depth sort (gsx_bin_depth_async, which keeps the device
-    busy meanwhile) and waits for that copy only, allocates ``ids`` with
-    exactly that capacity and enqueues the rest (gsx_bin_tiles_async).
-    ``ids`` and ``ranges`` are usable by kernels enqueued behind the job
-    right away.  Without refine_tiles D is that count and no second host
-    sync is needed.  Every job copies its final status words to pinned
-    memory behind the tile phase (no wait); ``check()`` waits for that copy
-    and raises on a device-side error bit of the tile phase.  ``result()``
+    emission writes; gsx_bin_depth_async's first kernel copies the status
+    words to the workspace's pinned host target, which the host polls while
+    the device sorts; ``ids`` gets exactly that capacity and
+    gsx_bin_tiles_async is enqueued.  ``ids`` and ``ranges`` are usable by
+    kernels enqueued behind the job right away.  Without refine_tiles D is
+    that count and no second host wait is needed.  The tile phase's last
+    kernel writes the final status words to the second target; ``check()``
+    waits for them and raises on a device-side error bit.  ``result()``
     calls it when D is unknown (refine_tiles); the render backward calls it
     after enqueuing its kernels, so a failed binning raises before the
     gradients reach an optimizer.  A job nobody checks has its error bits
@@ -126,16 +163,18 @@ class BinJob:
         L = _lib.load()
         dws = ws.get_depth(self.dev, n)
         _lib.check(L.gsx_bin_count_async(
-            n, _lib.ptr(counts), _lib.ptr(dkeys), self.width, self.height, _lib.ptr(dws),
-            dws.numel(), _lib.ptr(self.ranges), _lib.ptr(status), stream),
+            n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), self.width, self.height,
+            _lib.ptr(dws), dws.numel(), _lib.ptr(self.ranges), _lib.ptr(status), stream),
             "gsx_bin_count_async")
-        host, ev = _pinned_status(status)
-        _lib.check(L.gsx_bin_depth_async(n, _lib.ptr(dkeys), _lib.ptr(dws), dws.numel(),
-                                         _lib.ptr(status), stream), "gsx_bin_depth_async")
-        ev.synchronize()
-        words = host.numpy().view(np.uint32)
-        _raise_on_errors(ws, int(words[1]), "gsx_bin_count_async")
-        self.cap = int(words[3])
+        self.seq = seq = ws.next_seq()
+        self.cap = 0
+        if n > 0:
+            _lib.check(L.gsx_bin_depth_async(n, _lib.ptr(dkeys), _lib.ptr(dws), dws.numel(),
+                                             _lib.ptr(status), ws.host.slot(0), seq, stream),
+                       "gsx_bin_depth_async")
+            words, _ = ws.host.wait(0, seq)
+            _raise_on_errors(ws, int(words[1]), "gsx_bin_count_async")
+            self.cap = int(words[3])
         tws = ws.get_tiles(self.dev, self.cap, num_tiles)
         self.ids = torch.empty((self.cap,), dtype=torch.int32, device=self.dev)
         m2, co = refine if refine is not None else (None, None)
@@ -143,27 +182,32 @@ class BinJob:
             n, _lib.ptr(counts), _lib.ptr(rects), _lib.ptr(m2), _lib.ptr(co),
             0 if co is None else co.shape[1], self.width, self.height, _lib.ptr(dws),
             dws.numel(), _lib.ptr(tws), tws.numel(), self.cap, _lib.ptr(self.ids),
-            _lib.ptr(self.ranges), _lib.ptr(status), stream), "gsx_bin_tiles_async")
-        self.host, self.ready = _pinned_status(status)
+            _lib.ptr(self.ranges), _lib.ptr(status), ws.host.slot(1), seq, stream),
+            "gsx_bin_tiles_async")
+        self.ready = n > 0  # n == 0 launches nothing after the count phase
         self.num_dups = None if (refine is not None or final) else self.cap
+        if n == 0:
+            self.num_dups = 0
 
     def check(self) -> None:
-        """With a final status copy: wait for the binning, raise GsxError if
-        a device-side check failed and set num_dups (duplicates kept)."""
-        if self.ready is None:
+        """Wait for the final status, raise GsxError if a device-side check
+        failed and set num_dups (duplicates kept)."""
+        if not self.ready:
             return
-        self.ready.synchronize()
-        self.ready = None
-        words = np.ascontiguousarray(self.host.numpy().view(np.uint32))
+        self.ready = False
+        words, seq = self.ws.host.wait(1, self.seq)
         _raise_on_errors(self.ws, int(words[1]), "gsx_bin_tiles_async")
+        if self.num_dups is not None:
+            return
+        if seq != self.seq:  # a later job on the stream overwrote the counts
+            raise _lib.GsxError("gsx_bin_tiles_async: status read after a later binning")
         nd = ctypes.c_int64(0)
         rc = _lib.check(_lib.load().gsx_bin_status_check(
             words.ctypes.data_as(ctypes.c_void_p), self.cap, ctypes.byref(nd)),
             "gsx_bin_tiles_async")
         if rc != _lib.GSX_OK:  # not reached: the capacity is the emitted count
             raise _lib.GsxError("gsx_bin_tiles_async: duplicates exceed the exact capacity")
-        if self.num_dups is None:
-            self.num_dups = int(nd.value)
+        self.num_dups = int(nd.value)
 
     def result(self):
         """(sorted_ids (D,), tile_ranges); waits for the binning only when D

@@ -33,7 +33,7 @@ def test_python_binding_covers_header():
 
 def test_status_strings_and_version():
     L = _lib.load()
-    assert L.gsx_abi_version() == 3
+    assert L.gsx_abi_version() == 4
     assert _lib.strerror(0) == "ok"
     assert "invalid" in _lib.strerror(-1)
     assert "capacity" in _lib.strerror(1)
@@ -83,7 +83,7 @@ def test_invalid_arguments_rejected_before_launch():
 
 
 def test_bin_status_check_is_host_only():
-    """gsx_bin_status_check interprets the four status words of
+    """gsx_bin_status_check interprets the status words of
     gsx_bin_sort_async: duplicates emitted, error bits (1 = wait bound,
     2 = overflow), duplicates dropped by refine_tiles."""
     L = _lib.load()
@@ -94,11 +94,11 @@ def test_bin_status_check_is_host_only():
         rc = L.gsx_bin_status_check(h.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(nd))
         return rc, nd.value
 
-    assert chk([123, 0, 0, 0], 123) == (0, 123)
-    assert chk([123, 0, 20, 0], 123) == (0, 103)   # kept = emitted - dropped
-    assert chk([124, 0, 0, 0], 123) == (1, 124)    # capacity needed
-    assert chk([5, 2, 0, 0], 100)[0] == -4
-    assert chk([5, 1, 0, 0], 100)[0] == -5
+    assert chk([123, 0, 0, 0, 0, 0, 0, 0], 123) == (0, 123)
+    assert chk([123, 0, 20, 0, 0, 0, 0, 0], 123) == (0, 103)   # kept = emitted - dropped
+    assert chk([124, 0, 0, 0, 0, 0, 0, 0], 123) == (1, 124)    # capacity needed
+    assert chk([5, 2, 0, 0, 0, 0, 0, 0], 100)[0] == -4
+    assert chk([5, 1, 0, 0, 0, 0, 0, 0], 100)[0] == -5
     assert L.gsx_strerror(-5).decode().startswith("device-side check")
     # binning entry points reject bad sizes before any launch
     nd = ctypes.c_int64(0)
@@ -108,21 +108,23 @@ def test_bin_status_check_is_host_only():
                           None, ctypes.byref(nd), None) == -4
     assert L.gsx_bin_sort_async(10, None, None, None, None, None, 0, 64, 64, None, 0, 100, None,
                                 None, None, None) == -1
-    # the two phases: null outputs / inputs, negative sizes, a short workspace
-    assert L.gsx_bin_count_async(10, None, None, 64, 64, None, 0, None, None, None) == -1
-    assert L.gsx_bin_count_async(-1, None, None, 64, 64, None, 0, None, None, None) == -1
-    assert L.gsx_bin_depth_async(-1, None, None, 0, None, None) == -1
-    assert L.gsx_bin_depth_async(10, None, None, 0, None, None) == -1
-    assert L.gsx_bin_depth_async(1 << 30, None, None, 0, None, None) == -4
-    st = np.zeros(4, np.uint32)
+    # the three phases: null outputs / inputs, negative sizes, a short workspace
+    assert L.gsx_bin_count_async(10, None, None, None, 64, 64, None, 0, None, None, None) == -1
+    assert L.gsx_bin_count_async(-1, None, None, None, 64, 64, None, 0, None, None, None) == -1
+    assert L.gsx_bin_depth_async(-1, None, None, 0, None, None, 0, None) == -1
+    assert L.gsx_bin_depth_async(10, None, None, 0, None, None, 0, None) == -1
+    assert L.gsx_bin_depth_async(1 << 30, None, None, 0, None, None, 0, None) == -4
+    st = np.zeros(8, np.uint32)
     rg = np.zeros(32, np.int32)
     p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731  (never dereferenced)
     assert L.gsx_bin_tiles_async(10, p(st), p(st), None, None, 0, 64, 64, p(st), 16, p(st), 16,
-                                 100, p(rg), p(rg), p(st), None) == -3
+                                 100, p(rg), p(rg), p(st), None, 0, None) == -3
     assert L.gsx_bin_tiles_async(10, None, None, None, None, 0, 64, 64, None, 0, None, 0, 100,
-                                 None, p(rg), p(st), None) == -1
+                                 None, p(rg), p(st), None, 0, None) == -1
     assert L.gsx_bin_tiles_async(10, None, None, None, None, 0, 64, 64, None, 0, None, 0,
-                                 1 << 30, None, p(rg), p(st), None) == -4
+                                 1 << 30, None, p(rg), p(st), None, 0, None) == -4
+    assert L.gsx_host_status_alloc(None) == -1
+    assert L.gsx_host_status_free(None) == 0
 
 
 def test_no_kernel_spills_registers():

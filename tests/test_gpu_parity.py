@@ -199,9 +199,13 @@ def test_bin_sort_sync_abi_and_capacity():
 
 def test_bin_two_phase_abi_exact_capacity():
     """gsx_bin_count_async reports the emitted duplicate count in
-    bin_status[3] before the sorts run; gsx_bin_depth_async and
-    gsx_bin_tiles_async with that capacity match the oracle bit for bit,
-    plain and with refine_tiles."""
+    bin_status[3] (and the row entries in [4]) before the sorts run;
+    gsx_bin_depth_async publishes those words to pinned host memory tagged
+    with the caller's sequence number; gsx_bin_tiles_async with that
+    capacity matches the oracle bit for bit, plain (row placement) and with
+    refine_tiles (general path), and publishes the final words."""
+    from mlx3d_amd.splatting.tiles import _HostStatus
+
     m, r, d, co = _elongated(9, n=4000)
     n = m.shape[0]
     L = _lib.load()
@@ -214,24 +218,30 @@ def test_bin_two_phase_abi_exact_capacity():
     _lib.check(L.gsx_bin_prepare(n, _lib.ptr(m2), _lib.ptr(rad), _lib.ptr(dep), 640, 360,
                                  _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), st),
                "prepare")
+    hr = host(rects).view(np.uint32)
+    heights = int(((hr[:, 1] >> 16) * (host(counts) > 0)).sum())
     full, _, tx, ty = O.bin_gaussians(m, r, d, 640, 360, threads=8)
-    for refine in (False, True):
+    hs = _HostStatus()
+    for seq, refine in ((7, False), (8, True)):
         rids, rranges, _, _ = O.bin_gaussians(m, r, d, 640, 360, threads=8,
                                               conics=co if refine else None)
         say(f"two-phase binning refine={refine}: emitted {full.shape[0]}, kept {rids.shape[0]}")
         dws = torch.empty(L.gsx_bin_depth_workspace_bytes(n), dtype=torch.uint8, device=dev)
         ranges = torch.empty((tx * ty, 2), dtype=torch.int32, device=dev)
-        # words 0, 2, 3 are cleared by the count call, the error word is not
-        status = torch.tensor([-1, 0, -1, -1], dtype=torch.int32, device=dev)
-        _lib.check(L.gsx_bin_count_async(n, _lib.ptr(counts), _lib.ptr(dkeys), 640, 360,
-                                         _lib.ptr(dws), dws.numel(), _lib.ptr(ranges),
+        # words 0 and 2..7 are cleared by the count call, the error word is not
+        status = torch.tensor([-1, 0, -1, -1, -1, -1, -1, -1], dtype=torch.int32, device=dev)
+        _lib.check(L.gsx_bin_count_async(n, _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects),
+                                         640, 360, _lib.ptr(dws), dws.numel(), _lib.ptr(ranges),
                                          _lib.ptr(status), st), "count")
         words = host(status).view(np.uint32)
-        assert words[0] == words[1] == words[2] == 0
+        assert words[0] == words[1] == words[2] == 0 and (words[5:] == 0).all()
         assert words[3] == full.shape[0] == int(host(counts).sum())
+        assert words[4] == heights
         _lib.check(L.gsx_bin_depth_async(n, _lib.ptr(dkeys), _lib.ptr(dws), dws.numel(),
-                                         _lib.ptr(status), st), "depth sort")
-        cap = int(words[3])
+                                         _lib.ptr(status), hs.slot(0), seq, st), "depth sort")
+        pub, tag = hs.wait(0, seq)
+        assert tag == seq and pub[3] == words[3] and pub[4] == heights and pub[1] == 0
+        cap = int(pub[3])
         tws = torch.empty(L.gsx_bin_tile_workspace_bytes(cap, tx * ty), dtype=torch.uint8,
                           device=dev)
         ids = torch.full((cap,), -1, dtype=torch.int32, device=dev)
@@ -239,13 +249,19 @@ def test_bin_two_phase_abi_exact_capacity():
             n, _lib.ptr(counts), _lib.ptr(rects), _lib.ptr(m2) if refine else None,
             _lib.ptr(con) if refine else None, 3 if refine else 0, 640, 360, _lib.ptr(dws),
             dws.numel(), _lib.ptr(tws), tws.numel(), cap, _lib.ptr(ids), _lib.ptr(ranges),
-            _lib.ptr(status), st), "tile phase")
+            _lib.ptr(status), hs.slot(1), seq, st), "tile phase")
+        final, tag = hs.wait(1, seq)
+        assert tag == seq
         words = host(status).view(np.uint32)
         nd = ctypes.c_int64(0)
         hw = np.ascontiguousarray(words)
         assert L.gsx_bin_status_check(hw.ctypes.data_as(ctypes.c_void_p), cap,
                                       ctypes.byref(nd)) == 0
         assert words[0] == cap and nd.value == rids.shape[0]
+        if refine:  # the general path publishes after its tile passes: dropped is final
+            np.testing.assert_array_equal(final[:3], words[:3])
+        else:  # the row path publishes D with its placement kernel
+            assert final[0] == cap and final[1] == 0
         np.testing.assert_array_equal(host(ids[:nd.value]), rids)
         np.testing.assert_array_equal(host(ranges), rranges)
 
