@@ -584,8 +584,12 @@ __global__ __launch_bounds__(kScanThreads) void k_row_scan(
     __shared__ uint32_t s_chunk, s_prefix;
     const int tid = threadIdx.x;
     uint32_t* err = status + 1;
-    // the row emission's look-back status words start at zero
-    for (int64_t k = (int64_t)blockIdx.x * kScanThreads + tid; k < n_clear;
+    // the row emission's look-back status words start at zero (those of
+    // the chunks the row entries -- status[4], final since the count
+    // phase -- will use)
+    const int64_t used = min<int64_t>(n_clear, ceil_div((int64_t)status[4], kRowChunk) *
+                                                   (2 * kMaxFastTiles));
+    for (int64_t k = (int64_t)blockIdx.x * kScanThreads + tid; k < used;
          k += (int64_t)gridDim.x * kScanThreads)
         clear[k] = 0u;
     if (tid == 0) s_chunk = atomicAdd(counter, 1u);
@@ -945,19 +949,21 @@ __device__ __forceinline__ bool find_segment(const RowPlan* __restrict__ plan,
 
 // Per segment and tile column: the number of its duplicates (range adds
 // over the columns its entries' clipped spans cover, then a prefix sum).
-__global__ __launch_bounds__(kEmitThreads) void k_seg_count(
+// One thread per column.
+__global__ __launch_bounds__(kMaxFastTiles) void k_seg_count(
     int64_t cap, const RowPlan* __restrict__ plan, const uint32_t* __restrict__ segrow,
     const uint32_t* __restrict__ segk0, int tiles_x, const uint32_t* __restrict__ e_pack,
     const uint32_t* __restrict__ e_doff, uint32_t* __restrict__ sc) {
     __shared__ uint32_t s_diff[kMaxFastTiles + 1];
-    __shared__ uint32_t s_w[kEmitThreads / 64];
+    __shared__ uint32_t s_w[kMaxFastTiles / 64];
     const int tid = threadIdx.x;
     if ((int64_t)plan->dups > cap) return;
     Segment sg;
     if (!find_segment(plan, segrow, segk0, blockIdx.x, sg)) return;
-    if (tid <= kMaxFastTiles) s_diff[tid] = 0u;
+    s_diff[tid] = 0u;
+    if (tid == 0) s_diff[kMaxFastTiles] = 0u;
     __syncthreads();
-    for (uint32_t k = sg.k0 + tid; k < sg.k1; k += kEmitThreads) {
+    for (uint32_t k = sg.k0 + tid; k < sg.k1; k += kMaxFastTiles) {
         const uint32_t doff = e_doff[sg.rb + k];
         if (doff >= sg.e) continue;
         const uint32_t p = e_pack[sg.rb + k];
@@ -969,32 +975,70 @@ __global__ __launch_bounds__(kEmitThreads) void k_seg_count(
     }
     __syncthreads();
     uint32_t tot;
-    const uint32_t v = tid < kMaxFastTiles ? s_diff[tid] : 0u;
-    const uint32_t incl = block_excl_scan<kEmitThreads>(v, s_w, &tot) + v;
+    const uint32_t v = s_diff[tid];
+    const uint32_t incl = block_excl_scan<kMaxFastTiles>(v, s_w, &tot) + v;
     if (tid < tiles_x) sc[(int64_t)blockIdx.x * kMaxFastTiles + tid] = incl;
 }
 
-// Per tile row (one workgroup, one thread per column): exclusive prefix of
-// each column's counts over the row's segments, the tile totals and their
-// exclusive scan along the row from the row's first output position, the
-// tile ranges, and sc[segment][x] = the segment's first output position
-// for column x.  Segments are read kBatch at a time (independent loads).
-__global__ __launch_bounds__(kMaxFastTiles) void k_tile_scan(
+// Per tile row (one workgroup; four threads per column, each over a
+// quarter of the row's segments): exclusive prefix of each column's counts
+// over the row's segments, the tile totals and their exclusive scan along
+// the row from the row's first output position, the tile ranges, and
+// sc[segment][x] = the segment's first output position for column x.
+constexpr int kScanParts = 4;
+__global__ __launch_bounds__(kScanParts * kMaxFastTiles) void k_tile_scan(
     int64_t cap, const RowPlan* __restrict__ plan, int tiles_x, uint32_t* __restrict__ sc,
     int2* __restrict__ ranges) {
     constexpr int kBatch = 8;
-    __shared__ uint32_t s_w[kMaxFastTiles / 64];
+    __shared__ uint32_t s_part[kScanParts][kMaxFastTiles];
+    __shared__ uint32_t s_start[kMaxFastTiles];
+    __shared__ uint32_t s_w[kScanParts * kMaxFastTiles / 64];
     const int tid = threadIdx.x;
+    const int x = tid % kMaxFastTiles, q = tid / kMaxFastTiles;
     if ((int64_t)plan->dups > cap) return;  // ranges stay zero
     const int y = blockIdx.x;
-    const uint32_t s0 = plan->segbase[y], s1 = plan->segbase[y + 1];
-    uint32_t run = 0;
-    if (tid < tiles_x) {
+    const uint32_t r0 = plan->segbase[y], r1 = plan->segbase[y + 1];
+    const uint32_t per = (r1 - r0 + kScanParts - 1) / kScanParts;
+    const uint32_t s0 = min(r0 + q * per, r1), s1 = min(s0 + per, r1);
+    const bool col = x < tiles_x;
+    uint32_t sum = 0;
+    if (col) {
         for (uint32_t s = s0; s < s1; s += kBatch) {
             uint32_t v[kBatch];
 #pragma unroll
             for (int k = 0; k < kBatch; ++k)
-                v[k] = s + k < s1 ? sc[(int64_t)(s + k) * kMaxFastTiles + tid] : 0u;
+                v[k] = s + k < s1 ? sc[(int64_t)(s + k) * kMaxFastTiles + x] : 0u;
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) sum += v[k];
+        }
+    }
+    s_part[q][x] = sum;
+    __syncthreads();
+    uint32_t total = 0, before = 0;
+#pragma unroll
+    for (int k = 0; k < kScanParts; ++k) {
+        const uint32_t t = s_part[k][x];
+        if (k < q) before += t;
+        total += t;
+    }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan<kScanParts * kMaxFastTiles>(
+        q == 0 && col ? total : 0u, s_w, &tot);
+    if (q == 0) {
+        const uint32_t start = plan->rowstart[y] + ex;
+        s_start[x] = start;
+        if (col)
+            ranges[(int64_t)y * tiles_x + x] =
+                total ? make_int2((int)start, (int)(start + total)) : make_int2(0, 0);
+    }
+    __syncthreads();
+    if (col) {
+        uint32_t run = s_start[x] + before;
+        for (uint32_t s = s0; s < s1; s += kBatch) {
+            uint32_t v[kBatch];
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k)
+                v[k] = s + k < s1 ? sc[(int64_t)(s + k) * kMaxFastTiles + x] : 0u;
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
                 const uint32_t t = v[k];
@@ -1003,17 +1047,8 @@ __global__ __launch_bounds__(kMaxFastTiles) void k_tile_scan(
             }
 #pragma unroll
             for (int k = 0; k < kBatch; ++k)
-                if (s + k < s1) sc[(int64_t)(s + k) * kMaxFastTiles + tid] = v[k];
+                if (s + k < s1) sc[(int64_t)(s + k) * kMaxFastTiles + x] = v[k];
         }
-    }
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan<kMaxFastTiles>(tid < tiles_x ? run : 0u, s_w, &tot);
-    if (tid < tiles_x) {
-        const uint32_t start = plan->rowstart[y] + ex;
-        ranges[(int64_t)y * tiles_x + tid] =
-            run ? make_int2((int)start, (int)(start + run)) : make_int2(0, 0);
-        // the kernel's own writes above: plain loads see them
-        for (uint32_t s = s0; s < s1; ++s) sc[(int64_t)s * kMaxFastTiles + tid] += start;
     }
 }
 
@@ -1697,11 +1732,12 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
                            n, capacity, (const uint32_t*)offs, (const uint32_t*)owner, gids,
                            (const uint2*)tile_rects, (const RowPlan*)plan, tiles_y, rstatus,
                            misc + 10, e_gid, e_pack, e_doff, segk0, L.segments, err);
-        hipLaunchKernelGGL(k_seg_count, dim3((unsigned)L.segments), dim3(kEmitThreads), 0, st,
+        hipLaunchKernelGGL(k_seg_count, dim3((unsigned)L.segments), dim3(kMaxFastTiles), 0, st,
                            capacity, (const RowPlan*)plan, (const uint32_t*)segrow,
                            (const uint32_t*)segk0, tiles_x, (const uint32_t*)e_pack,
                            (const uint32_t*)e_doff, sc);
-        hipLaunchKernelGGL(k_tile_scan, dim3((unsigned)tiles_y), dim3(kMaxFastTiles), 0, st,
+        hipLaunchKernelGGL(k_tile_scan, dim3((unsigned)tiles_y), dim3(kScanParts * kMaxFastTiles),
+                           0, st,
                            capacity, (const RowPlan*)plan, tiles_x, sc, (int2*)tile_ranges);
         hipLaunchKernelGGL(k_place, dim3((unsigned)L.segments), dim3(kEmitThreads), 0, st,
                            capacity, (const RowPlan*)plan, (const uint32_t*)segrow,
