@@ -187,7 +187,10 @@ int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means,
 
 /* VJP of gsx_preprocess_fwd (MLX autodiff of the same expressions,
  * render.py:75-80 with dirs under stop_gradient, colour clamp mask from
- * colors_out).  g_means2d/g_conics/g_opac_eff come from gsx_raster_bwd;
+ * colors_out).  g_means2d/g_conics/g_opac_eff/g_colors come from
+ * gsx_raster_bwd: four arrays with grad_stride = 0, or with grad_stride > 0
+ * its gradient record (g_means2d points at it, the other three are NULL;
+ * grad_stride a multiple of 4, at least 12 with SH, 8 without);
  * g_means2d_extra, g_depths, g_compensation are extra cotangents of the
  * returned means2d/depths/compensation and may be NULL.  g_sh0/g_sh_rest
  * use the strides of the forward; coefficients >= (degree+1)^2 are written
@@ -202,7 +205,7 @@ int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means,
                        const float* g_compensation, float* g_means,
                        float* g_quats, float* g_scales, float* g_opacities,
                        float* g_sh0, int64_t sh0_stride, float* g_sh_rest,
-                       int64_t sh_rest_stride, void* stream);
+                       int64_t sh_rest_stride, int32_t grad_stride, void* stream);
 
 /* ------------------------------------------------------------- binning --
  * Replaces bin_gaussians (splatting/tiles.py:19-182, refine_tiles off).
@@ -362,8 +365,13 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
 /* Replaces gs_rasterize_backward (rasterize.py:100-221) and the vjp wiring
  * of _rasterize_core (rasterize.py:364-403).  grad_out (H,W,C);
  * grad_final_T (H,W) or NULL.  Outputs (zeroed here, then accumulated):
- * g_means2d (N,2), g_conics (N,3), g_features (N,C), g_opacities (N).
- * No gradient is produced for the background (rasterize.py:401). */
+ * g_means2d (N,2), g_conics (N,3), g_features (N,C), g_opacities (N) with
+ * grad_stride = 0; with grad_stride > 0 (a multiple of 4, >= 6 + C) one
+ * 16-byte aligned record per Gaussian at g_means2d, [means2d 2 | conic 3 |
+ * opacity 1 | features C | padding], and the other three outputs NULL: a
+ * Gaussian's float atomics from one tile then land in one or two cache
+ * lines instead of one per array.  No gradient is produced for the
+ * background (rasterize.py:401). */
 int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
                    const int32_t* sorted_ids, int64_t num_ids,
@@ -372,7 +380,7 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
                    const float* final_T, const int32_t* n_contrib,
                    const float* grad_out, const float* grad_final_T,
                    float* g_means2d, float* g_conics, float* g_features,
-                   float* g_opacities, void* stream);
+                   float* g_opacities, int32_t grad_stride, void* stream);
 
 /* -------------------------------------------------------- training step --
  * The calls GaussianTrainer.step (splatting/trainer.py:319-421) makes
@@ -486,7 +494,8 @@ int gsx_adam_step(int32_t num_groups, const gsx_adam_group* groups,
  * count, grad unused); SH in split layout with contiguous rows (sh_dc (N,3),
  * sh_rest (N, 3 (K-1)), K >= 1), moments with the parameters' layouts,
  * quats and its moments 16-byte aligned.  Parameters and moments are
- * updated in place.  K = 1: groups[5] is not read. */
+ * updated in place.  K = 1: groups[5] is not read.  The rasterizer
+ * gradients come as in gsx_preprocess_bwd (grad_stride). */
 int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, float* quats,
                             float* scales, float* opacities, float* sh_dc, float* sh_rest,
                             const float* colors_out, int32_t K, int32_t degree, uint32_t flags,
@@ -494,15 +503,18 @@ int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, floa
                             const float* g_opac_eff, const float* g_colors,
                             const float* g_means2d_extra, const float* g_depths,
                             const float* g_compensation, const gsx_adam_group* groups,
-                            float beta1, float beta2, float eps, void* stream);
+                            float beta1, float beta2, float eps, int32_t grad_stride,
+                            void* stream);
 
 /* Replaces the density-control statistics of trainer.py:357-365:
  * grad_accum += |(g.x W/2, g.y H/2)| * (radii > 0); grad_count += (radii > 0).
  * g_means2d (N,2) is dL/dmeans2d of the rasterizer (the reference's
- * means2d probe gradient, trainer.py:264-275, 337). */
+ * means2d probe gradient, trainer.py:264-275, 337); with grad_stride > 0
+ * (even) the (x, y) pairs are grad_stride floats apart (a gradient record). */
 int gsx_accum_screen_grads(int64_t n, const float* g_means2d,
                            const float* radii, int32_t width, int32_t height,
-                           float* grad_accum, float* grad_count, void* stream);
+                           float* grad_accum, float* grad_count, int32_t grad_stride,
+                           void* stream);
 
 /* ------------------------------------------------------ table edits --
  * A Gaussian table: up to GSX_TABLE_MAX float32 tensors of N rows, tensor k

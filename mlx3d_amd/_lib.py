@@ -126,7 +126,7 @@ SIGNATURES = {
                                           _P]),
     "gsx_preprocess_bwd": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _P, _P, _I32, _I32, _U32, _F,
                                           _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
-                                          _P, _I64, _P]),
+                                          _P, _I64, _I32, _P]),
     "gsx_bin_prepare": (ctypes.c_int, [_I64, _P, _P, _P, _I32, _I32, _P, _P, _P, _P]),
     "gsx_bin_workspace_bytes": (_I64, [_I64, _I64, _I32]),
     "gsx_bin_sort": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I64, _I64,
@@ -146,7 +146,7 @@ SIGNATURES = {
     "gsx_raster_fwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32,
                                       _P, _P, _P, _P, _P, _P]),
     "gsx_raster_bwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32, _P,
-                                      _P, _P, _P, _P, _P, _P, _P, _P]),
+                                      _P, _P, _P, _P, _P, _P, _P, _I32, _P]),
     "gsx_photometric_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "gsx_photometric_fwd": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, _F, _F, _P, _I64, _P,
                                            _P]),
@@ -164,8 +164,8 @@ SIGNATURES = {
     "gsx_adam_step": (ctypes.c_int, [_I32, ctypes.c_void_p, _F, _F, _F, _P]),
     "gsx_preprocess_bwd_adam": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _P, _P, _P, _P, _I32,
                                                _I32, _U32, _F, _P, _P, _P, _P, _P, _P, _P,
-                                               ctypes.c_void_p, _F, _F, _F, _P]),
-    "gsx_accum_screen_grads": (ctypes.c_int, [_I64, _P, _P, _I32, _I32, _P, _P, _P]),
+                                               ctypes.c_void_p, _F, _F, _F, _I32, _P]),
+    "gsx_accum_screen_grads": (ctypes.c_int, [_I64, _P, _P, _I32, _I32, _P, _P, _I32, _P]),
     "gsx_knn_log_scale": (ctypes.c_int, [_I64, _P, _I64, _P, _I32, _F, _P, _P]),
     "gsx_density_workspace_bytes": (_I64, [_I64]),
     "gsx_density_classify": (ctypes.c_int, [_I64, _P, _P, _P, _P, _F, _F, _F, _F, _P, _I64,

@@ -376,32 +376,76 @@ struct RawGrads {
     int Ka;
 };
 
+// The rasterizer's per-Gaussian gradients: four arrays (means2d (N,2),
+// conics (N,3), effective opacity (N), colours (N,3)), or with stride > 0 one
+// record of `stride` floats per Gaussian, [means2d 2 | conic 3 | opacity 1 |
+// colour 3 | ...], 16-byte aligned (read as three float4).
+struct RasterGrads {
+    const float* m2;
+    const float* con;
+    const float* op;
+    const float* col;
+    int stride;
+};
+
+struct GradRow {
+    float gx, gy, ga, gb, gc, go;
+    float col[3];
+};
+
+__device__ __forceinline__ GradRow load_grads(const RasterGrads& g, int64_t i, bool sh) {
+    GradRow r;
+    if (g.stride > 0) {
+        const float4* p = reinterpret_cast<const float4*>(g.m2 + (int64_t)g.stride * i);
+        const float4 a = p[0], b = p[1];
+        r.gx = a.x;
+        r.gy = a.y;
+        r.ga = a.z;
+        r.gb = a.w;
+        r.gc = b.x;
+        r.go = b.y;
+        r.col[0] = b.z;
+        r.col[1] = b.w;
+        r.col[2] = sh ? p[2].x : 0.0f;
+    } else {
+        const float2 m = reinterpret_cast<const float2*>(g.m2)[i];
+        r.gx = m.x;
+        r.gy = m.y;
+        r.ga = g.con[3 * i];
+        r.gb = g.con[3 * i + 1];
+        r.gc = g.con[3 * i + 2];
+        r.go = g.op[i];
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) r.col[ch] = sh ? g.col[3 * i + ch] : 0.0f;
+    }
+    return r;
+}
+
 template <bool UT>
 __device__ __forceinline__ void preprocess_vjp(
     const gsx_camera& cam, int64_t i, float m0, float m1, float m2, float4 q, float r0, float r1,
     float r2, float ro, uint32_t flags, float blur, bool aa, bool sh, int degree,
-    const float* __restrict__ colors_out, const float2* __restrict__ g_means2d,
-    const float* __restrict__ g_conics, const float* __restrict__ g_opac_eff,
-    const float* __restrict__ g_colors, const float2* __restrict__ g_means2d_extra,
-    const float* __restrict__ g_depths, const float* __restrict__ g_comp, RawGrads& G) {
+    const float* __restrict__ colors_out, const RasterGrads& rg,
+    const float2* __restrict__ g_means2d_extra, const float* __restrict__ g_depths,
+    const float* __restrict__ g_comp, RawGrads& G) {
     const float sx = act_scale(r0, flags);
     const float sy = act_scale(r1, flags);
     const float sz = act_scale(r2, flags);
     const float o = act_opacity(ro, flags);
     typename ProjOf<UT>::T p;
     project_any<UT>(cam, m0, m1, m2, q.x, q.y, q.z, q.w, sx, sy, sz, blur, aa, p);
-    const float goe = g_opac_eff[i];
+    const GradRow gr = load_grads(rg, i, sh);
+    const float goe = gr.go;
     const float g_o = goe * p.comp;
     const float g_comp_total = (g_comp ? g_comp[i] : 0.0f) + goe * o;
-    float2 gm2 = g_means2d[i];
+    float2 gm2 = make_float2(gr.gx, gr.gy);
     if (g_means2d_extra) {
         const float2 e = g_means2d_extra[i];
         gm2.x += e.x;
         gm2.y += e.y;
     }
     float gs[3];
-    project_any_vjp<UT>(cam, p, m0, m1, m2, aa, gm2.x, gm2.y, g_conics[3 * i],
-                        g_conics[3 * i + 1], g_conics[3 * i + 2],
+    project_any_vjp<UT>(cam, p, m0, m1, m2, aa, gm2.x, gm2.y, gr.ga, gr.gb, gr.gc,
                         g_depths ? g_depths[i] : 0.0f, g_comp_total, G.means, G.quat, gs);
     const bool ls = flags & GSX_LOG_SCALES;
     G.scales[0] = ls ? gs[0] * sx : gs[0];
@@ -416,7 +460,7 @@ __device__ __forceinline__ void preprocess_vjp(
         G.Ka = (degree + 1) * (degree + 1);
 #pragma unroll
         for (int ch = 0; ch < 3; ++ch)
-            G.gc[ch] = (colors_out[3 * i + ch] > 0.0f) ? g_colors[3 * i + ch] : 0.0f;
+            G.gc[ch] = (colors_out[3 * i + ch] > 0.0f) ? gr.col[ch] : 0.0f;
     }
 }
 
@@ -445,9 +489,8 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
     gsx_camera cam, int64_t n, const float* __restrict__ means, const float4* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities,
     const float* __restrict__ colors_out, int K, int degree, int sh_mode, int sh_cols,
-    uint32_t flags, float blur, bool aa, const float2* __restrict__ g_means2d,
-    const float* __restrict__ g_conics, const float* __restrict__ g_opac_eff,
-    const float* __restrict__ g_colors, const float2* __restrict__ g_means2d_extra,
+    uint32_t flags, float blur, bool aa, RasterGrads rg,
+    const float2* __restrict__ g_means2d_extra,
     const float* __restrict__ g_depths, const float* __restrict__ g_comp,
     float* __restrict__ g_means, float4* __restrict__ g_quats, float* __restrict__ g_scales,
     float* __restrict__ g_opacities, float* __restrict__ g_sh0, int64_t s0,
@@ -460,8 +503,8 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd(
         RawGrads G;
         preprocess_vjp<UT>(cam, i, means[3 * i], means[3 * i + 1], means[3 * i + 2], quats[i],
                            scales[3 * i], scales[3 * i + 1], scales[3 * i + 2], opacities[i],
-                           flags, blur, aa, g_sh0 != nullptr, degree, colors_out, g_means2d,
-                           g_conics, g_opac_eff, g_colors, g_means2d_extra, g_depths, g_comp, G);
+                           flags, blur, aa, g_sh0 != nullptr, degree, colors_out, rg,
+                           g_means2d_extra, g_depths, g_comp, G);
         g_means[3 * i] = G.means[0];
         g_means[3 * i + 1] = G.means[1];
         g_means[3 * i + 2] = G.means[2];
@@ -590,9 +633,8 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd_adam(
     gsx_camera cam, int64_t n, float* __restrict__ means, float4* __restrict__ quats,
     float* __restrict__ scales, float* __restrict__ opacities, float* __restrict__ sh0,
     float* __restrict__ shr, int K, int degree, uint32_t flags, float blur, bool aa, bool vec,
-    const float* __restrict__ colors_out, const float2* __restrict__ g_means2d,
-    const float* __restrict__ g_conics, const float* __restrict__ g_opac_eff,
-    const float* __restrict__ g_colors, const float2* __restrict__ g_means2d_extra,
+    const float* __restrict__ colors_out, RasterGrads rg,
+    const float2* __restrict__ g_means2d_extra,
     const float* __restrict__ g_depths, const float* __restrict__ g_comp, AdamState6 st,
     float b1, float omb1, float b2, float omb2, float eps) {
     __shared__ float s_r1[kThreads * kRank1Stride];
@@ -606,8 +648,8 @@ __global__ __launch_bounds__(kThreads) void k_preprocess_bwd_adam(
         const float ro = opacities[i];
         RawGrads G;
         preprocess_vjp<UT>(cam, i, pm[0], pm[1], pm[2], q, ps[0], ps[1], ps[2], ro, flags, blur,
-                           aa, true, degree, colors_out, g_means2d, g_conics, g_opac_eff,
-                           g_colors, g_means2d_extra, g_depths, g_comp, G);
+                           aa, true, degree, colors_out, rg, g_means2d_extra, g_depths, g_comp,
+                           G);
 #pragma unroll
         for (int k = 0; k < 3; ++k)
             means[3 * i + k] = adam_reg(pm[k], st.m[0], st.v[0], 3 * i + k, G.means[k], st.lr[0],
@@ -877,6 +919,25 @@ int gsx_preprocess_fwd(const gsx_camera* cam, int64_t n, const float* means, con
     return GSX_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// The rasterizer gradients of gsx_preprocess_bwd(_adam): grad_stride 0 =
+// four arrays, > 0 = one record per Gaussian at g_means2d (the other three
+// pointers NULL).  Returns false for an invalid combination.
+bool raster_grads(const float* g_means2d, const float* g_conics, const float* g_opac_eff,
+                  const float* g_colors, int32_t grad_stride, bool sh, RasterGrads& rg) {
+    rg = RasterGrads{g_means2d, g_conics, g_opac_eff, g_colors, grad_stride};
+    if (!g_means2d || grad_stride < 0) return false;
+    if (grad_stride > 0)
+        return grad_stride % 4 == 0 && grad_stride >= (sh ? 12 : 8) && aligned16(g_means2d) &&
+               !g_conics && !g_opac_eff && !g_colors;
+    return g_conics && g_opac_eff && (!sh || g_colors) && aligned8(g_means2d);
+}
+}  // namespace
+
+extern "C" {
+
 int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, float* quats,
                             float* scales, float* opacities, float* sh_dc, float* sh_rest,
                             const float* colors_out, int32_t K, int32_t degree, uint32_t flags,
@@ -884,11 +945,13 @@ int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, floa
                             const float* g_opac_eff, const float* g_colors,
                             const float* g_means2d_extra, const float* g_depths,
                             const float* g_compensation, const gsx_adam_group* groups,
-                            float beta1, float beta2, float eps, void* stream) {
+                            float beta1, float beta2, float eps, int32_t grad_stride,
+                            void* stream) {
     if (!cam || n < 0 || !lens_ok(cam) || !groups) return GSX_ERR_INVALID;
     if (n == 0) return GSX_OK;
-    if (!means || !quats || !scales || !opacities || !sh_dc || !colors_out || !g_means2d ||
-        !g_conics || !g_opac_eff || !g_colors)
+    RasterGrads rg;
+    if (!means || !quats || !scales || !opacities || !sh_dc || !colors_out ||
+        !raster_grads(g_means2d, g_conics, g_opac_eff, g_colors, grad_stride, true, rg))
         return GSX_ERR_INVALID;
     if (degree < 0 || degree > 3 || K < (degree + 1) * (degree + 1) ||
         3 * (K - 1) > kShMaxCols || (K > 1 && !sh_rest))
@@ -911,7 +974,7 @@ int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, floa
         st.lr[k] = groups[k].lr;
     }
     if (!aligned16(quats) || !aligned16(st.m[1]) || !aligned16(st.v[1]) ||
-        !aligned8(g_means2d) || (g_means2d_extra && !aligned8(g_means2d_extra)))
+        (g_means2d_extra && !aligned8(g_means2d_extra)))
         return GSX_ERR_INVALID;
     const bool vec = K > 1 && aligned16(sh_rest) && aligned16(st.m[5]) && aligned16(st.v[5]);
     // b1, 1 - b1, b2, 1 - b2 in float32 as gsx_adam_step rounds them
@@ -921,8 +984,7 @@ int gsx_preprocess_bwd_adam(const gsx_camera* cam, int64_t n, float* means, floa
                                          : k_preprocess_bwd_adam<false>;
     hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(kThreads), 0, (hipStream_t)stream, *cam, n,
                        means, (float4*)quats, scales, opacities, sh_dc, sh_rest, K, degree, flags,
-                       blur, (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, vec, colors_out,
-                       (const float2*)g_means2d, g_conics, g_opac_eff, g_colors,
+                       blur, (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, vec, colors_out, rg,
                        (const float2*)g_means2d_extra, g_depths, g_compensation, st, b1, omb1,
                        b2, omb2, eps);
     GSX_LAUNCH_CHECK();
@@ -937,19 +999,21 @@ int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means, con
                        const float* g_depths, const float* g_compensation, float* g_means,
                        float* g_quats, float* g_scales, float* g_opacities, float* g_sh0,
                        int64_t sh0_stride, float* g_sh_rest, int64_t sh_rest_stride,
-                       void* stream) {
+                       int32_t grad_stride, void* stream) {
     if (!cam || n < 0 || !lens_ok(cam)) return GSX_ERR_INVALID;
     if (n == 0) return GSX_OK;
-    if (!means || !quats || !scales || !opacities || !g_means2d || !g_conics || !g_opac_eff ||
-        !g_means || !g_quats || !g_scales || !g_opacities)
+    RasterGrads rg;
+    if (!means || !quats || !scales || !opacities || !g_means || !g_quats || !g_scales ||
+        !g_opacities ||
+        !raster_grads(g_means2d, g_conics, g_opac_eff, g_colors, grad_stride, g_sh0 != nullptr,
+                      rg))
         return GSX_ERR_INVALID;
     if (g_sh0) {
-        if (!colors_out || !g_colors || degree < 0 || degree > 3 ||
-            K < (degree + 1) * (degree + 1))
+        if (!colors_out || degree < 0 || degree > 3 || K < (degree + 1) * (degree + 1))
             return GSX_ERR_INVALID;
         if (K > 1 && !g_sh_rest) return GSX_ERR_INVALID;
     }
-    if (!aligned16(quats) || !aligned16(g_quats) || !aligned8(g_means2d) ||
+    if (!aligned16(quats) || !aligned16(g_quats) ||
         (g_means2d_extra && !aligned8(g_means2d_extra)))
         return GSX_ERR_INVALID;
     int sh_mode = kShDirect, sh_cols = 1;
@@ -967,8 +1031,8 @@ int gsx_preprocess_bwd(const gsx_camera* cam, int64_t n, const float* means, con
     hipLaunchKernelGGL(kern, dim3(grid_for(n)), dim3(kThreads), 0,
                        (hipStream_t)stream, *cam, n, means, (const float4*)quats, scales,
                        opacities, colors_out, K, degree, sh_mode, sh_cols, flags, blur,
-                       (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, (const float2*)g_means2d,
-                       g_conics, g_opac_eff, g_colors, (const float2*)g_means2d_extra, g_depths,
+                       (flags & GSX_ANTIALIAS) != 0 && blur > 0.0f, rg,
+                       (const float2*)g_means2d_extra, g_depths,
                        g_compensation, g_means, (float4*)g_quats, g_scales, g_opacities, g_sh0,
                        sh0_stride, g_sh_rest, sh_rest_stride);
     GSX_LAUNCH_CHECK();

@@ -844,7 +844,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     const float* __restrict__ final_T, const int* __restrict__ n_contrib,
     const float* __restrict__ grad_out, const float* __restrict__ grad_T,
     float* __restrict__ g_xy, float* __restrict__ g_conic, float* __restrict__ g_feat,
-    float* __restrict__ g_opac) {
+    float* __restrict__ g_opac, int gstride) {
     constexpr int F4 = (CH + 3) / 4;
     constexpr int NV = CH + 6;             // u, w, u dx, u dy, w dy, opacity term, channels
     constexpr int NV4 = (NV + 3) / 4;
@@ -1011,15 +1011,17 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
         }
         __syncthreads();
         // 2. the global atomics, component-major across the lanes: a wave's
-        //    atomic instruction covers about 64 / NV Gaussians, each touching
-        //    one cache line per gradient array, instead of 64 Gaussians with
-        //    one line each per component
+        //    atomic instruction covers about 64 / NV Gaussians.  With a
+        //    gradient record (gstride > 0) each Gaussian's components are
+        //    adjacent words of one record; with separate arrays each
+        //    Gaussian touches one cache line per array
         for (int item = tid; item < BB * NV; item += kThreads) {
             const int j = item / NV, k = item - j * NV;
             const int g = __float_as_int(s_r1[j].w);
             const float v = reinterpret_cast<const float*>(s_part[0][j])[k];
             if (g < 0 || v == 0.0f || (k >= 6 && k - 6 >= nc)) continue;
-            float* dst = k < 2 ? g_xy + 2 * (int64_t)g + k
+            float* dst = gstride > 0 ? g_xy + (int64_t)gstride * g + (k < 6 ? k : c0 + k)
+                       : k < 2 ? g_xy + 2 * (int64_t)g + k
                        : k < 5 ? g_conic + 3 * (int64_t)g + (k - 2)
                        : k == 5 ? g_opac + g
                                 : g_feat + (int64_t)g * C + c0 + (k - 6);
@@ -1072,10 +1074,10 @@ void launch_bwd(dim3 grid, hipStream_t st, const float2* xy, const float4* co, c
                 int C, int c0, int nc, const int* ids, const int2* ranges, int64_t n,
                 int64_t n_ids, const float* bg, int W, int H, int tiles_x, const float* fT,
                 const int* ncon, const float* gout, const float* gT, float* gxy, float* gcon,
-                float* gfeat, float* gop) {
+                float* gfeat, float* gop, int gstride) {
     hipLaunchKernelGGL((k_raster_bwd<CH>), grid, dim3(kThreads), 0, st, xy, co, feat, C, c0, nc,
                        ids, ranges, n, n_ids, bg, W, H, tiles_x, fT, ncon, gout, gT, gxy, gcon,
-                       gfeat, gop);
+                       gfeat, gop, gstride);
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1136,11 +1138,16 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
                    const float* background, int32_t width, int32_t height, const float* final_T,
                    const int32_t* n_contrib, const float* grad_out, const float* grad_final_T,
                    float* g_means2d, float* g_conics, float* g_features, float* g_opacities,
-                   void* stream) {
+                   int32_t grad_stride, void* stream) {
     if (n < 0 || num_ids < 0 || C <= 0 || width <= 0 || height <= 0) return GSX_ERR_INVALID;
     if (!tile_ranges || !final_T || !n_contrib || !grad_out) return GSX_ERR_INVALID;
-    if (n > 0 && (!means2d || !conic_opacity || !features || !g_means2d || !g_conics ||
-                  !g_features || !g_opacities))
+    const bool rec = grad_stride > 0;
+    if (grad_stride < 0 || (rec && (grad_stride % 4 != 0 || grad_stride < 6 + C ||
+                                    !aligned16(g_means2d) || g_conics || g_features ||
+                                    g_opacities)))
+        return GSX_ERR_INVALID;
+    if (n > 0 && (!means2d || !conic_opacity || !features || !g_means2d ||
+                  (!rec && (!g_conics || !g_features || !g_opacities))))
         return GSX_ERR_INVALID;
     if (num_ids > 0 && !sorted_ids) return GSX_ERR_INVALID;
     if (!aligned8(means2d) || !aligned16(conic_opacity) || !aligned8(tile_ranges))
@@ -1148,10 +1155,15 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
     hipStream_t st = (hipStream_t)stream;
     if (n == 0) return GSX_OK;
     {
-        const int64_t most = std::max<int64_t>((int64_t)C, 3) * n;
+        const int64_t most = rec ? (int64_t)grad_stride * n : std::max<int64_t>((int64_t)C, 3) * n;
         const unsigned blocks = (unsigned)std::min<int64_t>((most + 255) / 256, 8192);
-        hipLaunchKernelGGL(k_zero_grads, dim3(blocks), dim3(256), 0, st, g_means2d, 2 * n,
-                           g_conics, 3 * n, g_features, (int64_t)C * n, g_opacities, n);
+        if (rec)
+            hipLaunchKernelGGL(k_zero_grads, dim3(blocks), dim3(256), 0, st, g_means2d,
+                               (int64_t)grad_stride * n, (float*)nullptr, (int64_t)0,
+                               (float*)nullptr, (int64_t)0, (float*)nullptr, (int64_t)0);
+        else
+            hipLaunchKernelGGL(k_zero_grads, dim3(blocks), dim3(256), 0, st, g_means2d, 2 * n,
+                               g_conics, 3 * n, g_features, (int64_t)C * n, g_opacities, n);
         GSX_LAUNCH_CHECK();
     }
     const int tiles_x = (width + kTile - 1) / kTile;
@@ -1165,7 +1177,7 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
         launch_bwd<V>(grid, st, (const float2*)means2d, (const float4*)conic_opacity, features,  \
                       C, c0, nc, sorted_ids, (const int2*)tile_ranges, n, num_ids, background,   \
                       width, height, tiles_x, final_T, n_contrib, grad_out, grad_final_T,        \
-                      g_means2d, g_conics, g_features, g_opacities);                             \
+                      g_means2d, g_conics, g_features, g_opacities, grad_stride);                \
         break;
             GSX_BWD_CASE(1)
             GSX_BWD_CASE(2)

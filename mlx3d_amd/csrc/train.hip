@@ -450,15 +450,16 @@ __global__ __launch_bounds__(kAdamThreads) void k_adam(AdamArgs a, float b1, flo
 // ------------------------------------------- density-control statistics --
 // trainer.py:358-365: gx = g_x (W / 2), gy = g_y (H / 2),
 // accum += sqrt(gx gx + gy gy) * visible, count += visible, visible = radii > 0.
-__global__ __launch_bounds__(256) void k_accum_screen_grads(int64_t n,
-                                                            const float2* __restrict__ g,
+// g: (x, y) pairs `stride` floats apart.
+__global__ __launch_bounds__(256) void k_accum_screen_grads(int64_t n, const float* __restrict__ g,
+                                                            int stride,
                                                             const float* __restrict__ radii,
                                                             float half_w, float half_h,
                                                             float* __restrict__ accum,
                                                             float* __restrict__ count) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float2 d = g[i];
+    const float2 d = *reinterpret_cast<const float2*>(g + (int64_t)stride * i);
     const float gx = d.x * half_w, gy = d.y * half_h;
     const float norm = sqrtf(gx * gx + gy * gy);
     const float vis = radii[i] > 0.0f ? 1.0f : 0.0f;
@@ -878,15 +879,17 @@ int gsx_adam_step(int32_t num_groups, const gsx_adam_group* groups, float beta1,
 }
 
 int gsx_accum_screen_grads(int64_t n, const float* g_means2d, const float* radii, int32_t width,
-                           int32_t height, float* grad_accum, float* grad_count, void* stream) {
+                           int32_t height, float* grad_accum, float* grad_count,
+                           int32_t grad_stride, void* stream) {
     if (n < 0 || width <= 0 || height <= 0) return GSX_ERR_INVALID;
     if (n == 0) return GSX_OK;
     if (!g_means2d || !radii || !grad_accum || !grad_count) return GSX_ERR_INVALID;
-    if (((uintptr_t)g_means2d & 7u) != 0) return GSX_ERR_INVALID;
+    if (((uintptr_t)g_means2d & 7u) != 0 || grad_stride < 0 || (grad_stride & 1) != 0)
+        return GSX_ERR_INVALID;
     const unsigned blocks = (unsigned)((n + 255) / 256);
     hipLaunchKernelGGL(k_accum_screen_grads, dim3(blocks), dim3(256), 0, (hipStream_t)stream, n,
-                       (const float2*)g_means2d, radii, (float)(width / 2.0),
-                       (float)(height / 2.0), grad_accum, grad_count);
+                       g_means2d, grad_stride > 0 ? (int)grad_stride : 2, radii,
+                       (float)(width / 2.0), (float)(height / 2.0), grad_accum, grad_count);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }

@@ -52,15 +52,35 @@ def t_cotangent(g_final_T, g_alpha):
     return -g_alpha if g_final_T is None else g_final_T - g_alpha
 
 
+def grad_record_stride(C: int) -> int:
+    """Floats per Gaussian of the rasterizer's gradient record: means2d (2),
+    conic (3), opacity (1), C features, padded to whole 16-byte groups (at
+    least 12, which the preprocess VJP reads)."""
+    return max(12, 4 * ((6 + C + 3) // 4))
+
+
 def raster_backward(means2d, conic_opac, feats, sorted_ids, tile_ranges, background, width,
-                    height, final_T, n_contrib, g_out, g_final_T):
-    """gsx_raster_bwd: gradients w.r.t. means2d, conics, features, opacity."""
+                    height, final_T, n_contrib, g_out, g_final_T, record: bool = False):
+    """gsx_raster_bwd: gradients w.r.t. means2d, conics, features, opacity.
+
+    With ``record`` the kernel accumulates into one (N, stride) record per
+    Gaussian (its atomics for a Gaussian then share a cache line or two);
+    the four gradients are returned as strided views of it, and the record
+    and its stride as two more values."""
     dev = means2d.device
     n, C = feats.shape
-    g_m = _empty((n, 2), dev)
-    g_c = _empty((n, 3), dev)
-    g_f = _empty((n, C), dev)
-    g_o = _empty((n,), dev)
+    if record:
+        stride = grad_record_stride(C)
+        rec = _empty((n, stride), dev)
+        g_m, g_c, g_o, g_f = rec[:, 0:2], rec[:, 2:5], rec[:, 5], rec[:, 6:6 + C]
+        outs = (rec, None, None, None)
+    else:
+        stride = 0
+        g_m = _empty((n, 2), dev)
+        g_c = _empty((n, 3), dev)
+        g_f = _empty((n, C), dev)
+        g_o = _empty((n,), dev)
+        outs = (g_m, g_c, g_f, g_o)
     if g_out is None:
         g_out = torch.zeros((height, width, C), dtype=torch.float32, device=dev)
     g_out = _lib.f32c(g_out)
@@ -70,9 +90,11 @@ def raster_backward(means2d, conic_opac, feats, sorted_ids, tile_ranges, backgro
                                 _lib.ptr(sorted_ids), sorted_ids.numel(), _lib.ptr(tile_ranges),
                                 _lib.ptr(background),
                                 width, height, _lib.ptr(final_T), _lib.ptr(n_contrib),
-                                _lib.ptr(g_out), _lib.ptr(g_final_T), _lib.ptr(g_m), _lib.ptr(g_c),
-                                _lib.ptr(g_f), _lib.ptr(g_o), _lib.stream_handle(dev)),
+                                _lib.ptr(g_out), _lib.ptr(g_final_T), *[_lib.ptr(t) for t in outs],
+                                stride, _lib.stream_handle(dev)),
                "gsx_raster_bwd")
+    if record:
+        return g_m, g_c, g_f, g_o, rec, stride
     return g_m, g_c, g_f, g_o
 
 

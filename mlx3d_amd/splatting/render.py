@@ -126,16 +126,17 @@ class _RenderFn(torch.autograd.Function):
         cfg = ctx.cfg
         dev = means.device
         n = means.shape[0]
+        # the rasterizer's gradients go into one record per Gaussian, which
+        # the screen statistics and the preprocess VJP read in place
         with stage("raster_bwd"):
-            g_m2, g_con, g_feat, g_op = raster_backward(means2d, co, feats, ids, ranges,
-                                                        background, cfg.width, cfg.height,
-                                                        final_T, n_contrib, g_image,
-                                                        t_cotangent(g_final_T, g_alpha))
+            _, _, g_feat, _, grec, gstride = raster_backward(
+                means2d, co, feats, ids, ranges, background, cfg.width, cfg.height, final_T,
+                n_contrib, g_image, t_cotangent(g_final_T, g_alpha), record=True)
         if cfg.screen_stats is not None:
             acc, cnt = cfg.screen_stats
             _lib.check(_lib.load().gsx_accum_screen_grads(
-                n, _lib.ptr(g_m2), _lib.ptr(radii), cfg.width, cfg.height, _lib.ptr(acc),
-                _lib.ptr(cnt), _lib.stream_handle(dev)), "gsx_accum_screen_grads")
+                n, _lib.ptr(grec), _lib.ptr(radii), cfg.width, cfg.height, _lib.ptr(acc),
+                _lib.ptr(cnt), gstride, _lib.stream_handle(dev)), "gsx_accum_screen_grads")
         c = lambda t: None if t is None else _lib.f32c(t)  # noqa: E731
         # The contiguous copies of the output cotangents (a stride-0 expand
         # from .sum() is copied) must outlive the enqueued kernel: only their
@@ -152,10 +153,10 @@ class _RenderFn(torch.autograd.Function):
                 _lib.check(L.gsx_preprocess_bwd_adam(
                     cfg.cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
                     _lib.ptr(opacities), _lib.ptr(sh_a), _lib.ptr(sh_b), _lib.ptr(feats), cfg.K,
-                    cfg.degree, cfg.flags, cfg.blur, _lib.ptr(g_m2), _lib.ptr(g_con),
-                    _lib.ptr(g_op), _lib.ptr(g_feat), _lib.ptr(gm2_in), _lib.ptr(gdep_in),
+                    cfg.degree, cfg.flags, cfg.blur, _lib.ptr(grec), None, None, None,
+                    _lib.ptr(gm2_in), _lib.ptr(gdep_in),
                     _lib.ptr(gcomp_in), ctypes.cast(opt.records, ctypes.c_void_p),
-                    opt.betas[0], opt.betas[1], opt.eps, _lib.stream_handle(dev)),
+                    opt.betas[0], opt.betas[1], opt.eps, gstride, _lib.stream_handle(dev)),
                     "gsx_preprocess_bwd_adam")
             opt.commit()
             return None, None, None, None, None, None, None, None, None
@@ -170,11 +171,10 @@ class _RenderFn(torch.autograd.Function):
             _lib.check(L.gsx_preprocess_bwd(
                 cfg.cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
                 _lib.ptr(opacities), _lib.ptr(feats if cfg.sh_mode else None), cfg.K, cfg.degree,
-                cfg.flags, cfg.blur, _lib.ptr(g_m2), _lib.ptr(g_con), _lib.ptr(g_op),
-                _lib.ptr(g_feat if cfg.sh_mode else None), _lib.ptr(gm2_in),
+                cfg.flags, cfg.blur, _lib.ptr(grec), None, None, None, _lib.ptr(gm2_in),
                 _lib.ptr(gdep_in), _lib.ptr(gcomp_in), _lib.ptr(g_means),
                 _lib.ptr(g_quats), _lib.ptr(g_scales), _lib.ptr(g_opac), _lib.ptr(gs0), s0, gshr,
-                sr, _lib.stream_handle(dev)), "gsx_preprocess_bwd")
+                sr, gstride, _lib.stream_handle(dev)), "gsx_preprocess_bwd")
         g_colors = None if cfg.sh_mode else g_feat
         return g_means, g_quats, g_scales, g_opac, g_sh_a, g_sh_b, g_colors, None, None
 

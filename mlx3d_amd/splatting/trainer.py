@@ -371,7 +371,7 @@ class GaussianTrainer:
                 g2, r2 = _lib.f32c(res.probe_grad), _lib.f32c(res.radii.detach())
                 _lib.check(_lib.load().gsx_accum_screen_grads(
                     g2.shape[0], _lib.ptr(g2), _lib.ptr(r2), camera.width, camera.height,
-                    _lib.ptr(self.grad_accum), _lib.ptr(self.grad_count),
+                    _lib.ptr(self.grad_accum), _lib.ptr(self.grad_count), 0,
                     _lib.stream_handle(dev)), "gsx_accum_screen_grads")
             if self.step_count % cfg.densify_every == 0 and self.step_count > cfg.densify_from:
                 densify = self._density_event()

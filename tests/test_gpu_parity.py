@@ -691,3 +691,35 @@ def test_render_direct_output_cotangents():
         e = rel_err(host(a.grad), g[key])
         say(f"direct cotangents grad {name}: rel {e:.2e}")
         assert e < 1e-3
+
+
+@pytest.mark.parametrize("C", [3, 5, 32])
+def test_raster_backward_gradient_record(C):
+    """gsx_raster_bwd into one gradient record per Gaussian (grad_stride > 0)
+    against the four separate arrays: the same sums (float atomics add in
+    run-dependent order, so to 1e-6 of the largest entry), padding zero."""
+    from mlx3d_amd.splatting.rasterize import raster_backward, raster_forward
+
+    say(f"gradient record C={C}")
+    cam, means, quats, scales, opac, _ = random_scene(31 + C, n=4000, width=320, height=200)
+    rng = np.random.default_rng(C)
+    feats = cu(rng.random((means.shape[0], C), dtype=np.float32))
+    proj = project_gaussians(cam, cu(means), cu(quats), cu(scales))
+    ids, ranges, _, _ = bin_gaussians(proj["means2d"], proj["radii"], proj["depths"], 320, 200)
+    co = torch.cat([proj["conics"], (cu(opac) * proj["compensation"])[:, None]], 1).contiguous()
+    m2 = proj["means2d"].contiguous()
+    bg = torch.zeros(C, device=m2.device)
+    _, final_T, n_contrib, _, _ = raster_forward(m2, co, feats, ids, ranges, bg, 320, 200)
+    g_out = cu(rng.normal(size=(200, 320, C)).astype(np.float32))
+    g_T = cu(rng.normal(size=(200, 320)).astype(np.float32))
+    sep = raster_backward(m2, co, feats, ids, ranges, bg, 320, 200, final_T, n_contrib, g_out,
+                          g_T)
+    rec = raster_backward(m2, co, feats, ids, ranges, bg, 320, 200, final_T, n_contrib, g_out,
+                          g_T, record=True)
+    for name, a, b in zip(("means2d", "conics", "features", "opacities"), sep, rec[:4]):
+        e = float((a - b).abs().max() / a.abs().max().clamp_min(1e-30))
+        say(f"  {name}: rel {e:.2e}")
+        assert e < 1e-6, name
+    stride = rec[5]
+    assert stride % 4 == 0 and stride >= 6 + C
+    assert float(rec[4][:, 6 + C:].abs().max() if stride > 6 + C else 0.0) == 0.0

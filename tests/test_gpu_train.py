@@ -195,7 +195,7 @@ def test_accum_screen_grads_bitexact():
     acc, cnt = cu(acc0), cu(cnt0)
     gd, rd = cu(g), cu(radii)  # alive until the kernel has run
     _lib.check(_lib.load().gsx_accum_screen_grads(
-        n, _lib.ptr(gd), _lib.ptr(rd), 1279, 720, _lib.ptr(acc), _lib.ptr(cnt),
+        n, _lib.ptr(gd), _lib.ptr(rd), 1279, 720, _lib.ptr(acc), _lib.ptr(cnt), 0,
         _lib.stream_handle(acc.device)), "accum")
     ra, rc = O.accum_screen_grads(g, radii, 1279, 720, acc0, cnt0)
     assert_bits(host(acc), ra, "grad_accum")
@@ -318,7 +318,23 @@ def test_preprocess_bwd_adam_matches_bwd_then_adam(n, K, degree, flags, extra, m
         ptr(cot["g_con"]), ptr(cot["g_op"]), ptr(cot["g_col"]), ptr(cot["extra"]),
         ptr(cot["g_dep"]), ptr(cot["g_comp"]), ptr(g["means"]), ptr(g["quats"]),
         ptr(g["scales"]), ptr(g["opacities"]), ptr(g["sh_dc"]), 3,
-        ptr(g["sh_rest"]) if K > 1 else None, 3 * (K - 1), st), "gsx_preprocess_bwd")
+        ptr(g["sh_rest"]) if K > 1 else None, 3 * (K - 1), 0, st), "gsx_preprocess_bwd")
+    # the same VJP from the rasterizer's gradient record (12 floats per
+    # Gaussian: means2d, conic, opacity, colour): bit-identical gradients
+    rec = torch.zeros((n, 12), dtype=torch.float32, device=cot["g_m2"].device)
+    rec[:, 0:2] = cot["g_m2"]
+    rec[:, 2:5] = cot["g_con"]
+    rec[:, 5] = cot["g_op"]
+    rec[:, 6:9] = cot["g_col"]
+    g2 = {k: torch.empty_like(params[k]) for k in _ORDER}
+    _lib.check(L.gsx_preprocess_bwd(
+        gcam, n, ptr(sep["means"][0]), ptr(sep["quats"][0]), ptr(sep["scales"][0]),
+        ptr(sep["opacities"][0]), ptr(cot["colors"]), K, degree, flags, 0.3, ptr(rec), None,
+        None, None, ptr(cot["extra"]), ptr(cot["g_dep"]), ptr(cot["g_comp"]), ptr(g2["means"]),
+        ptr(g2["quats"]), ptr(g2["scales"]), ptr(g2["opacities"]), ptr(g2["sh_dc"]), 3,
+        ptr(g2["sh_rest"]) if K > 1 else None, 3 * (K - 1), 12, st), "gsx_preprocess_bwd rec")
+    for k in groups:
+        assert_bits(host(g2[k]), host(g[k]), f"record-layout gradient {k}")
     arr = (_lib.GsxAdamGroup * len(groups))()
     for j, k in enumerate(groups):
         p, m, v = sep[k]
@@ -341,7 +357,7 @@ def test_preprocess_bwd_adam_matches_bwd_then_adam(n, K, degree, flags, extra, m
         ptr(fus["sh_rest"][0]) if K > 1 else None, ptr(cot["colors"]), K, degree, flags, 0.3,
         ptr(cot["g_m2"]), ptr(cot["g_con"]), ptr(cot["g_op"]), ptr(cot["g_col"]),
         ptr(cot["extra"]), ptr(cot["g_dep"]), ptr(cot["g_comp"]),
-        ctypes.cast(arr, ctypes.c_void_p), 0.9, 0.999, 1e-15, st), "gsx_preprocess_bwd_adam")
+        ctypes.cast(arr, ctypes.c_void_p), 0.9, 0.999, 1e-15, 0, st), "gsx_preprocess_bwd_adam")
     for k in groups:
         for slot, a, b in zip(("param", "m", "v"), fus[k], sep[k]):
             assert_bits(host(a), host(b), f"{slot} {k}")
@@ -364,7 +380,7 @@ def test_preprocess_bwd_adam_rejects_mismatched_groups():
             ptr(params["scales"]), ptr(params["opacities"]), ptr(params["sh_dc"]),
             ptr(params["sh_rest"]), ptr(cot["colors"]), 4, 1, _lib.LOG_SCALES, 0.3,
             ptr(cot["g_m2"]), ptr(cot["g_con"]), ptr(cot["g_op"]), ptr(cot["g_col"]), None,
-            None, None, ctypes.cast(arr, ctypes.c_void_p), 0.9, 0.999, 1e-15, st)
+            None, None, ctypes.cast(arr, ctypes.c_void_p), 0.9, 0.999, 1e-15, 0, st)
     before = host(params["means"])
     assert call() != _lib.GSX_OK  # group 2 names the quaternions, not the scales
     torch.cuda.synchronize()
