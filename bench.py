@@ -53,6 +53,9 @@ def _parse():
     ap.add_argument("--train-steps", type=int, default=12,
                     help="also time GaussianTrainer.step (SH configs with a backward); 0 = off")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB")
+    ap.add_argument("--reference-suite", action="store_true",
+                    help="time the reference's own published benchmark cases "
+                         "(examples/benchmark.py) and print them as one JSON line")
     ap.add_argument("--summarize-prof", metavar="DIR", nargs="+")
     ap.add_argument("--workload", default="c3_1m_sh3_aa_1080p_8views")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
@@ -449,8 +452,94 @@ def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool,
             "stages": stages}
 
 
+# The reference's published Apple-GPU figures (docs/benchmarks.md:17-22),
+# per-call latency in ms, for the cases of examples/benchmark.py:44-85.
+REFERENCE_PUBLISHED_MS = {
+    "hard rasterizer 20480 faces @ 256px": 4.3,
+    "hard rasterizer 20480 faces @ 512px": 6.2,
+    "hard rasterizer 20480 faces @ 1024px": 17.9,
+    "gaussian splatting 10000 splats @ 512px": 12.5,
+    "gaussian splatting 100000 splats @ 720px": 100.0,
+}
+
+
+def reference_suite():
+    """examples/benchmark.py:68-85 (and :44-56 for the mesh rasterizer) on
+    this GPU: the same inputs (points N(0, 1) * 0.6 with U(0, 1) colours
+    through GaussianModel.from_points at SH degree 0; a 20 480-face
+    icosphere), cameras and outputs.  `latency_ms` is the reference's
+    measure -- each call waits for its result, as mx.eval does -- averaged
+    over 50 calls after 5 warmups; `pipelined_ms` is the same calls
+    enqueued back to back.  Synthetic data from numpy's PCG64 (MLX's
+    generator is not available), so the splat sets are statistically, not
+    bitwise, the reference's."""
+    import numpy as np
+    import torch
+
+    from mlx3d_amd import scenes
+    from mlx3d_amd.cameras import Camera
+    from mlx3d_amd.renderer import interpolate_face_attributes, rasterize_meshes
+    from mlx3d_amd.splatting import GaussianModel
+
+    dev = torch.device("cuda:0")
+    rows = []
+
+    def timed(name, fn, iters=50, warmup=5):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+            torch.cuda.synchronize()
+        lat = (time.perf_counter() - t0) / iters * 1e3
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        pipe = (time.perf_counter() - t0) / iters * 1e3
+        ref = REFERENCE_PUBLISHED_MS[name]
+        rows.append({"case": name, "latency_ms": round(lat, 4), "fps": round(1e3 / lat, 1),
+                     "pipelined_ms": round(pipe, 4), "reference_ms": ref,
+                     "speedup_vs_reference": round(ref / lat, 1)})
+
+    verts, faces = scenes.ico_sphere(level=5, radius=1.0)
+    v = torch.as_tensor(verts, device=dev)
+    f = torch.as_tensor(faces, device=dev)
+    vc = 0.5 * v + 0.5
+    for size in (256, 512, 1024):
+        cam = Camera.look_at(eye=(2.2, 1.6, 2.2), at=(0, 0, 0), fov=45.0, width=size,
+                             height=size)
+
+        def hard(cam=cam):
+            frag = rasterize_meshes(cam, v, f)
+            return interpolate_face_attributes(frag, vc)
+
+        with torch.no_grad():
+            timed(f"hard rasterizer {faces.shape[0]} faces @ {size}px", hard)
+    rng = np.random.default_rng(0)
+    for n, size in ((10_000, 512), (100_000, 720)):
+        pts = torch.as_tensor((rng.standard_normal((n, 3)) * 0.6).astype(np.float32), device=dev)
+        col = torch.as_tensor(rng.random((n, 3), dtype=np.float32), device=dev)
+        model = GaussianModel.from_points(pts, col, sh_degree=0)
+        cam = Camera.look_at(eye=(0, 0, -3.0), at=(0, 0, 0), fov=60.0, width=size, height=size)
+        with torch.no_grad():
+            timed(f"gaussian splatting {n} splats @ {size}px",
+                  lambda model=model, cam=cam: model.render(cam)["image"])
+    return {"metric": "reference benchmark cases (examples/benchmark.py), per-call latency",
+            "unit": "ms", "device": torch.cuda.get_device_name(dev), "rows": rows,
+            "reference_device": "Apple-Silicon GPU (docs/benchmarks.md, chip not named)"}
+
+
 def main():
     args = _parse()
+    if args.reference_suite:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from mlx3d_amd import _lib
+
+        _lib.load()
+        print(json.dumps(reference_suite()), flush=True)
+        return
     if args.summarize_prof:
         summarize_prof(args.summarize_prof, args.workload, args.command)
         return
