@@ -1030,6 +1030,384 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     }
 }
 
+// ------------------------------------------------- matrix-core backward --
+// The backward for wide channel blocks (CH = 32) with its channel work on
+// the matrix cores.  Per (Gaussian, pixel) pair the replay is the same VALU
+// arithmetic as bwd_values -- every alpha / T / early-stop decision and the
+// per-pixel running state are unchanged -- except that the two channel
+// contractions come from v_mfma_f32_16x16x4_f32 products over groups of 16
+// list entries:
+//   A. cg[g][p] = sum_c f[g][c] g[p][c], (16 x 32) x (32 x 64), before the
+//      group's replay (the features are staged; the pixels' cotangents are
+//      held in registers in the B-operand layout for the whole walk), and
+//   B. dL/dc[g][c] = sum over the wave's 64 pixels of aT[g][p] g[p][c],
+//      (16 x 64) x (64 x 32), after it (aT = alpha T of each pair).
+// One LDS tile per wave carries cg[g][p] to the replay, which overwrites
+// entry (g, p) with aT[g][p] once read.  The replay itself produces only
+// the six geometric values (u, w, u dx, u dy, w dy, G dL/dalpha), reduced
+// across the wave as before.  Operand layouts (checked on the GPU):
+// A[row = l % 16][k = l / 16], B[k = l / 16][col = l % 16]; the result's lane
+// l holds rows 4 (l / 16) + i, column l % 16.  The features are staged
+// channel-major (row stride 65) and the tile with row stride 68, so the
+// operand reads and result writes of a wave hit distinct LDS banks.  Sums
+// from the four quadrant waves meet in one LDS slot per Gaussian through LDS
+// float atomics.  The
+// contractions add in a different order than the VALU path, so gradients
+// agree with it to float32 rounding, not bitwise; no decision depends on
+// them.
+constexpr int kMxGroup = 16;   // Gaussians per matrix-core group
+constexpr int kMxPad = 68;     // row stride (floats) of a wave's tile: 4 r + q bank spread
+constexpr int kMxFPad = 65;    // row stride (floats) of the channel-major features
+constexpr int kMxGeo = 6;      // geometric values per Gaussian
+
+typedef float mx_floatx4 __attribute__((ext_vector_type(4)));
+
+struct MxPixel {
+    float T;  // transmittance in front of the current Gaussian
+    float Q;
+    int last;
+};
+
+// The replay of one (pixel, Gaussian) pair given cg = c . g: the geometric
+// values into v (zeros where the pixel does not composite the Gaussian) and
+// alpha T into aT (zero likewise).  Returns whether any lane of the wave
+// passes the first tests (v and aT are zero when it does not).
+template <bool PLAIN>
+__device__ __forceinline__ bool bwd_geo(const float4& r0, const float4& r1, float cg, int off,
+                                        int lim, float pxf, float pyf, MxPixel& px,
+                                        float (&v)[8], float& aT_out) {
+    const float dx = r0.x - pxf, dy = r0.y - pyf;
+    const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
+    const bool c1 = off < lim, c2 = !(power > 0.0f), c3 = !(power < r0.z);
+    bool ok = c1 && c2 && c3;
+    const uint64_t m123 = __ballot(c1) & __ballot(c2) & __ballot(c3);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = 0.0f;
+    aT_out = 0.0f;
+    if (m123 == 0ull) return false;
+    const float G = PLAIN ? splat_exp_core(power) : splat_exp_sel(power);
+    const float alpha = fminf(0.99f, r0.w * G);
+    const bool c4 = !(alpha < 1.0f / 255.0f);
+    ok = ok && c4;
+    if ((m123 & __ballot(c4)) == 0ull) return false;
+    float ga, aT;
+    if constexpr (PLAIN) {
+        const float Gs = ok ? G : 0.0f;
+        const float as = ok ? alpha : 0.0f;
+        const float rcp = __builtin_amdgcn_rcpf(1.0f - as);
+        px.T = px.T * rcp;
+        const float dL_dalpha = fmaf(cg, px.T, -(px.Q * rcp));
+        aT = as * px.T;
+        px.Q = fmaf(aT, cg, px.Q);
+        ga = Gs * dL_dalpha;
+    } else {
+        const float rcp = __builtin_amdgcn_rcpf(1.0f - alpha);
+        px.T = ok ? px.T * rcp : px.T;
+        float dL_dalpha = fmaf(cg, px.T, -(px.Q * rcp));
+        dL_dalpha = ok ? dL_dalpha : 0.0f;
+        aT = ok ? alpha * px.T : 0.0f;
+        px.Q = ok ? fmaf(aT, cg, px.Q) : px.Q;
+        ga = G * dL_dalpha;
+    }
+    const float u = ga * dx, w = ga * dy;
+    v[0] = (PLAIN || ok) ? u : 0.0f;
+    v[1] = (PLAIN || ok) ? w : 0.0f;
+    v[2] = (PLAIN || ok) ? u * dx : 0.0f;
+    v[3] = (PLAIN || ok) ? u * dy : 0.0f;
+    v[4] = (PLAIN || ok) ? w * dy : 0.0f;
+    v[5] = (PLAIN || ok) ? ga : 0.0f;
+    aT_out = aT;  // zero for lanes that do not composite (PLAIN: as = 0)
+    return true;
+}
+
+// The walk of one quadrant wave for the matrix-core backward: groups of up
+// to 16 list entries (back to front): product A into the tile, the replay
+// pair by pair, product B into the Gaussians' LDS slots.  gA[pb][ks] =
+// g(pixel 16 pb + l % 16, channel 4 ks + l / 16); gB[ks][cb] = g(pixel
+// 4 ks + l / 16, channel 16 cb + l % 16).
+template <bool PLAIN>
+__device__ __forceinline__ void bwd_walk_mx(const uint16_t* list, int cnt, int lim,
+                                            const float4* s_r0, const float4* s_r1,
+                                            const float* s_feat, int pad_slot,
+                                            float (*sum)[40], float (*tile)[kMxPad],
+                                            const float (&gA)[4][8], const float (&gB)[16][2],
+                                            float pxf, float pyf, int lane, MxPixel& px) {
+#pragma unroll 1
+    for (int i0 = 0; i0 < cnt; i0 += kMxGroup) {
+        const int ng = min(kMxGroup, cnt - i0);
+        // A: the features of entry l % 16 (the padding record's zeros past
+        // the group), channels 4 ks + l / 16
+        const int row = lane & 15;
+        const int slot = row < ng ? (list[i0 + row] >> 4) : pad_slot;
+        float fa[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) fa[ks] = s_feat[(4 * ks + (lane >> 4)) * kMxFPad + slot];
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) {
+            mx_floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[ks], gA[pb][ks], acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tile[4 * (lane >> 4) + i][16 * pb + row] = acc[i];
+        }
+        // the wave's LDS accesses complete in order; the fence keeps the
+        // compiler from moving the reads below above the writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        // the replay two entries at a time (a = j, b = j + 1; past the group
+        // the padding record, which contributes nothing), their geometric
+        // values interleaved (a's at even, b's at odd positions) into one
+        // reduction, the next pair's records read before this pair is
+        // evaluated
+        const int pad = pad_slot * 16;
+        int oa = 0 < ng ? list[i0] : pad, ob = 1 < ng ? list[i0 + 1] : pad;
+        float4 a0 = rec_at(s_r0, oa), a1 = rec_at(s_r1, oa);
+        float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
+        float cga = tile[0][lane], cgb = tile[1][lane];
+#pragma unroll 1
+        for (int j = 0; j < kMxGroup; j += 2) {
+            const int na = j + 2 < ng ? list[i0 + j + 2] : pad;
+            const int nb = j + 3 < ng ? list[i0 + j + 3] : pad;
+            // the next pair's rows are not overwritten before they are read
+            const float nca = j + 2 < kMxGroup ? tile[j + 2][lane] : 0.0f;
+            const float ncb = j + 3 < kMxGroup ? tile[j + 3][lane] : 0.0f;
+            float va[8], vb[8], aTa, aTb;
+            const bool ha = bwd_geo<PLAIN>(a0, a1, cga, oa, lim, pxf, pyf, px, va, aTa);
+            const bool hb = bwd_geo<PLAIN>(b0, b1, cgb, ob, lim, pxf, pyf, px, vb, aTb);
+            tile[j][lane] = aTa;
+            tile[j + 1][lane] = aTb;
+            a0 = rec_at(s_r0, na);
+            a1 = rec_at(s_r1, na);
+            b0 = rec_at(s_r0, nb);
+            b1 = rec_at(s_r1, nb);
+            if (ha || hb) {
+                float w[12], tot[3];
+#pragma unroll
+                for (int q = 0; q < kMxGeo; ++q) {
+                    w[2 * q] = va[q];
+                    w[2 * q + 1] = vb[q];
+                }
+                wave_reduce_rows<12, 12>(w, tot);
+                if ((lane & 15) == 15) {
+                    // rows with row_value 0 and 2 hold a's values 2m and
+                    // 2m + 1, rows with 1 and 3 b's
+                    const int rv = row_value(lane >> 4);
+                    float* dst = sum[((rv & 1) ? ob : oa) >> 4] + (rv >> 1);
+#pragma unroll
+                    for (int m = 0; m < 3; ++m) atomicAdd(dst + 2 * m, tot[m]);
+                }
+            }
+            oa = na;
+            ob = nb;
+            cga = nca;
+            cgb = ncb;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        mx_floatx4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {
+            const float a = tile[row][4 * ks + (lane >> 4)];
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, gB[ks][0], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, gB[ks][1], acc1, 0, 0, 0);
+        }
+        // lane l holds the sums of entries 4 (l / 16) + i, channels l % 16
+        // and 16 + l % 16
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int g = 4 * (lane >> 4) + i;
+            if (g < ng) {
+                float* dst = sum[list[i0 + g] >> 4] + kMxGeo + row;
+                if (acc0[i] != 0.0f) atomicAdd(dst, acc0[i]);
+                if (acc1[i] != 0.0f) atomicAdd(dst + 16, acc1[i]);
+            }
+        }
+        // the next group's product A overwrites the tile
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    }
+}
+
+template <int CH>
+__global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
+    const float2* __restrict__ xy, const float4* __restrict__ co, const float* __restrict__ feat,
+    int C, int c0, int nc, const int* __restrict__ ids, const int2* __restrict__ ranges,
+    int64_t n, int64_t n_ids, const float* __restrict__ bg, int W, int H, int tiles_x,
+    const float* __restrict__ final_T, const int* __restrict__ n_contrib,
+    const float* __restrict__ grad_out, const float* __restrict__ grad_T,
+    float* __restrict__ g_xy, float* __restrict__ g_conic, float* __restrict__ g_feat,
+    float* __restrict__ g_opac, int gstride) {
+    static_assert(CH == 32, "the matrix-core backward covers 32-channel blocks");
+    constexpr int F4 = CH / 4;
+    constexpr int NV = CH + kMxGeo;  // slot values
+    constexpr int SP = CH + 8;       // slot stride (floats)
+    constexpr int BB = 64;
+    constexpr int NLW = BB / kWave;
+    __shared__ float4 s_r0[BB + 1];
+    __shared__ float4 s_r1[BB + 1];  // -a/2, -b, -c/2 (conic), Gaussian id (int bits)
+    __shared__ float s_fT[CH * kMxFPad];              // features, channel-major (column BB: zeros)
+    __shared__ float s_sum[BB + 1][SP];               // summed over the waves (LDS atomics)
+    __shared__ float s_tile[kWaves][kMxGroup][kMxPad];  // per-wave cg / aT tiles
+    __shared__ uint64_t s_mask[kWaves][NLW];
+    __shared__ uint16_t s_list[kWaves][BB + 4];
+    __shared__ int s_last[kWaves];
+    __shared__ __align__(16) uint32_t s_plain[kWaves];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tile = (int)xcd_remap(blockIdx.x, gridDim.x);
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const int px0 = tx * kTile, py0 = ty * kTile;
+    const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;
+    const int px = qx0 + (lane & 7);
+    const int py = qy0 + (lane >> 3);
+    const bool inside = px < W && py < H;
+    const float pxf = (float)px + 0.5f, pyf = (float)py + 0.5f;
+    const int64_t pid = (int64_t)py * W + px;
+
+    int start, num;
+    tile_span(ranges[tile], n_ids, start, num);
+
+    MxPixel st;
+    const float T_final = inside ? final_T[pid] : 1.0f;
+    st.T = T_final;
+    st.last = inside ? n_contrib[pid] : 0;
+    float bg_dot = 0.0f;
+    for (int ch = 0; ch < nc; ++ch)
+        bg_dot = bg_dot + (bg ? bg[c0 + ch] : 0.0f) * (inside ? grad_out[pid * C + c0 + ch] : 0.0f);
+    if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + grad_T[pid];
+    st.Q = T_final * bg_dot;
+    // the quadrant's cotangents in the two B-operand layouts (pixel q of
+    // the quadrant is (q % 8, q / 8))
+    auto gval = [&](int q, int ch) {
+        const int bx = qx0 + (q & 7), by = qy0 + (q >> 3);
+        return (bx < W && by < H && ch < nc) ? grad_out[((int64_t)by * W + bx) * C + c0 + ch]
+                                             : 0.0f;
+    };
+    float gA[4][8], gB[16][2];
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) gA[pb][ks] = gval(16 * pb + (lane & 15), 4 * ks + (lane >> 4));
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) gB[ks][cb] = gval(4 * ks + (lane >> 4), 16 * cb + (lane & 15));
+
+    if (tid == 0) {
+        s_r0[BB] = make_float4(0.0f, 0.0f, __builtin_huge_valf(), 0.0f);
+        s_r1[BB] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (tid < CH) s_fT[tid * kMxFPad + BB] = 0.0f;
+    {
+        int m = st.last;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, kWave));
+        if (lane == 0) s_last[wave] = m;
+    }
+    __syncthreads();
+    int quad_last[kWaves];
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) quad_last[q] = s_last[q];
+    const int max_last = max(max(quad_last[0], quad_last[1]), max(quad_last[2], quad_last[3]));
+    const int n_batches = (max_last + BB - 1) / BB;
+
+    for (int b = n_batches - 1; b >= 0; --b) {
+        __syncthreads();
+        uint32_t qm = 0;
+        bool plain = true;
+        for (int k = tid; k < (BB + 1) * SP; k += kThreads) (&s_sum[0][0])[k] = 0.0f;
+        if (tid < BB) {
+            const int k = b * BB + tid;
+            float4 r1 = make_float4(0.0f, 0.0f, 0.0f, __int_as_float(-1));
+            if (k < num) {
+                const int g = ids[start + k];
+                if ((uint32_t)g < (uint64_t)n) {
+                    const float2 m = xy[g];
+                    const float4 c = co[g];
+                    const float thr = alpha_floor_power(c.w);
+                    s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
+                    r1 = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, __int_as_float(g));
+                    qm = quadrant_mask(m.x, m.y, c, px0, py0);
+#pragma unroll
+                    for (int q = 0; q < kWaves; ++q)
+                        if (k >= quad_last[q]) qm &= ~(1u << q);
+                    plain = plain_gaussian<0>(m.x, m.y, c, thr, nullptr);
+                }
+            }
+            s_r1[tid] = r1;
+        }
+        if (wave < NLW) {
+#pragma unroll
+            for (int q = 0; q < kWaves; ++q) {
+                const uint64_t bq = __ballot((qm >> q) & 1u);
+                if (lane == 0) s_mask[q][wave] = bq;
+            }
+        }
+        // the features: every thread stages two of the batch's float4
+        // pieces (the ids come from the records above), so no thread holds a
+        // Gaussian's 32 channels beside the walk's cotangent registers
+        __syncthreads();
+        for (int k = tid; k < BB * F4; k += kThreads) {
+            const int j = k / F4, q = k - j * F4;
+            const int g = __float_as_int(s_r1[j].w);
+            if (g >= 0) {
+                const float* f = feat + (int64_t)g * C + c0 + 4 * q;
+                float4 v;
+                v.x = 4 * q < nc ? f[0] : 0.0f;
+                v.y = 4 * q + 1 < nc ? f[1] : 0.0f;
+                v.z = 4 * q + 2 < nc ? f[2] : 0.0f;
+                v.w = 4 * q + 3 < nc ? f[3] : 0.0f;
+                float* d = s_fT + (4 * q) * kMxFPad + j;
+                d[0] = v.x;
+                d[kMxFPad] = v.y;
+                d[2 * kMxFPad] = v.z;
+                d[3 * kMxFPad] = v.w;
+                plain = plain && fabsf(v.x) < 1e30f && fabsf(v.y) < 1e30f &&
+                        fabsf(v.z) < 1e30f && fabsf(v.w) < 1e30f;
+            }
+        }
+        const uint64_t np = __ballot(!plain);
+        if (lane == 0) s_plain[wave] = np == 0ull;
+        __syncthreads();
+        const uint4 pl = *reinterpret_cast<const uint4*>(s_plain);
+        const bool batch_plain = (pl.x & pl.y & pl.z & pl.w) != 0u;
+        const int cnt = build_list<NLW, true>(s_mask[wave], s_list[wave], lane, BB * 16);
+        const int lim = 16 * max(0, min(st.last - b * BB, BB));
+        const float* sfeat = s_fT;
+        if (batch_plain)
+            bwd_walk_mx<true>(s_list[wave], cnt, lim, s_r0, s_r1, sfeat, BB, s_sum, s_tile[wave],
+                              gA, gB, pxf, pyf, lane, st);
+        else
+            bwd_walk_mx<false>(s_list[wave], cnt, lim, s_r0, s_r1, sfeat, BB, s_sum,
+                               s_tile[wave], gA, gB, pxf, pyf, lane, st);
+        __syncthreads();
+        // one thread per Gaussian turns the sums into the reference's
+        // gradient components (rasterize.py:197-218 in terms of the sums)
+        if (tid < BB) {
+            float* e = s_sum[tid];
+            const float4 c = s_r1[tid];
+            const float o = s_r0[tid].w;
+            const float e0 = e[0], e1 = e[1];
+            e[0] = o * (2.0f * c.x * e0 + c.y * e1);
+            e[1] = o * (c.y * e0 + 2.0f * c.z * e1);
+            e[2] = -0.5f * o * e[2];
+            e[3] = -o * e[3];
+            e[4] = -0.5f * o * e[4];
+        }
+        __syncthreads();
+        for (int item = tid; item < BB * NV; item += kThreads) {
+            const int j = item / NV, k = item - j * NV;
+            const int g = __float_as_int(s_r1[j].w);
+            const float v = s_sum[j][k];
+            if (g < 0 || v == 0.0f || (k >= 6 && k - 6 >= nc)) continue;
+            float* dst = gstride > 0 ? g_xy + (int64_t)gstride * g + (k < 6 ? k : c0 + k)
+                       : k < 2 ? g_xy + 2 * (int64_t)g + k
+                       : k < 5 ? g_conic + 3 * (int64_t)g + (k - 2)
+                       : k == 5 ? g_opac + g
+                                : g_feat + (int64_t)g * C + c0 + (k - 6);
+            atomicAdd(dst, v);
+        }
+    }
+}
+
 // Clears the four gradient outputs in one launch (a fill kernel rather than
 // hipMemsetAsync, so the call can sit inside a captured graph).
 __global__ __launch_bounds__(256) void k_zero_grads(float* __restrict__ a, int64_t na,
@@ -1075,9 +1453,14 @@ void launch_bwd(dim3 grid, hipStream_t st, const float2* xy, const float4* co, c
                 int64_t n_ids, const float* bg, int W, int H, int tiles_x, const float* fT,
                 const int* ncon, const float* gout, const float* gT, float* gxy, float* gcon,
                 float* gfeat, float* gop, int gstride) {
-    hipLaunchKernelGGL((k_raster_bwd<CH>), grid, dim3(kThreads), 0, st, xy, co, feat, C, c0, nc,
-                       ids, ranges, n, n_ids, bg, W, H, tiles_x, fT, ncon, gout, gT, gxy, gcon,
-                       gfeat, gop, gstride);
+    if constexpr (CH == 32)
+        hipLaunchKernelGGL((k_raster_bwd_mx<CH>), grid, dim3(kThreads), 0, st, xy, co, feat, C,
+                           c0, nc, ids, ranges, n, n_ids, bg, W, H, tiles_x, fT, ncon, gout, gT,
+                           gxy, gcon, gfeat, gop, gstride);
+    else
+        hipLaunchKernelGGL((k_raster_bwd<CH>), grid, dim3(kThreads), 0, st, xy, co, feat, C, c0,
+                           nc, ids, ranges, n, n_ids, bg, W, H, tiles_x, fT, ncon, gout, gT, gxy,
+                           gcon, gfeat, gop, gstride);
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
