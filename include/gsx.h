@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GSX_ABI_VERSION 4
+#define GSX_ABI_VERSION 5
 #define GSX_TILE_SIZE 16 /* tiles.py:14 */
 
 enum gsx_status {
@@ -352,7 +352,14 @@ int gsx_pack_conic_opacity(int64_t n, const float* conics,
  * are treated as transparent, so malformed inputs cannot read out of
  * bounds; background (C) or NULL (zeros); out (H,W,C); final_T (H,W);
  * n_contrib (H,W) int32; depth_out (H,W) when depths != NULL; alpha_out
- * (H,W) = 1 - final_T (rasterize.py:443) or NULL. */
+ * (H,W) = 1 - final_T (rasterize.py:443) or NULL.
+ * tile_order: NULL (tiles in launch order), or 2 * T int32 words (T =
+ * ceil(W/16) ceil(H/16)) that the call fills: words [0, T) the order the
+ * workgroups take the tiles in (within each XCD's contiguous share of the
+ * tiles, longest tile lists first), words [T, 2T) each tile's largest
+ * n_contrib, which gsx_raster_bwd orders its tiles by.  The outputs do not
+ * depend on the order; the buffer has no counterpart in the reference
+ * (whose Metal dispatch has no such control). */
 int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
                    const float* depths, const int32_t* sorted_ids,
@@ -360,7 +367,7 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
                    const float* background,
                    int32_t width, int32_t height, float* out, float* final_T,
                    int32_t* n_contrib, float* depth_out, float* alpha_out,
-                   void* stream);
+                   int32_t* tile_order, void* stream);
 
 /* Replaces gs_rasterize_backward (rasterize.py:100-221) and the vjp wiring
  * of _rasterize_core (rasterize.py:364-403).  grad_out (H,W,C);
@@ -371,7 +378,11 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
  * opacity 1 | features C | padding], and the other three outputs NULL: a
  * Gaussian's float atomics from one tile then land in one or two cache
  * lines instead of one per array.  No gradient is produced for the
- * background (rasterize.py:401). */
+ * background (rasterize.py:401).  tile_order: NULL (launch order), or the
+ * buffer gsx_raster_fwd filled for this frame: words [0, T) are rewritten
+ * with the tiles ordered by the contributor bounds in [T, 2T) (largest
+ * first within each XCD's share).  Any contents give a valid order; the
+ * gradients do not depend on it beyond float atomic ordering. */
 int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
                    const int32_t* sorted_ids, int64_t num_ids,
@@ -380,7 +391,8 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
                    const float* final_T, const int32_t* n_contrib,
                    const float* grad_out, const float* grad_final_T,
                    float* g_means2d, float* g_conics, float* g_features,
-                   float* g_opacities, int32_t grad_stride, void* stream);
+                   float* g_opacities, int32_t grad_stride,
+                   int32_t* tile_order, void* stream);
 
 /* -------------------------------------------------------- training step --
  * The calls GaussianTrainer.step (splatting/trainer.py:319-421) makes

@@ -144,9 +144,9 @@ SIGNATURES = {
     "gsx_host_status_free": (ctypes.c_int, [_P]),
     "gsx_pack_conic_opacity": (ctypes.c_int, [_I64, _P, _P, _P, _P]),
     "gsx_raster_fwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32,
-                                      _P, _P, _P, _P, _P, _P]),
+                                      _P, _P, _P, _P, _P, _P, _P]),
     "gsx_raster_bwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32, _P,
-                                      _P, _P, _P, _P, _P, _P, _P, _I32, _P]),
+                                      _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P]),
     "gsx_photometric_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "gsx_photometric_fwd": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, _F, _F, _P, _I64, _P,
                                            _P]),

@@ -329,6 +329,34 @@ __device__ __forceinline__ void tile_span(int2 rg, int64_t n_ids, int& start, in
     num = (int)(s1 - s0);
 }
 
+// Tile processing order.  Workgroups go round-robin over the 8 XCDs and
+// each XCD starts its workgroups in launch order as slots free, so the
+// kernel ends when the last XCD drains its share.  xcd_remap gives each XCD
+// a contiguous range of tiles (neighbours share its L2); `order`, when
+// given, permutes each range so that the XCD starts its heaviest tiles
+// first (longest-processing-time-first list scheduling), which keeps long
+// tiles out of the drain.  The heavy tiles of a frame are its crowded
+// regions: up to 2.2x the mean work per tile at 720p/1080p here.
+__device__ __forceinline__ int tile_at(const int* order, uint32_t b, uint32_t nb) {
+    const uint32_t p = xcd_remap(b, nb);
+    return order ? order[p] : (int)p;
+}
+
+// The workgroup's largest contributor count (n_contrib) into work[tile]:
+// the number of list entries the backward replays for the tile.  Every
+// thread of the workgroup calls it.
+__device__ __forceinline__ void store_tile_work(int* work, int tile, int last, int wave,
+                                                int lane) {
+    __shared__ int s_wmax[kWaves];
+    int m = last;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o, kWave));
+    if (lane == 0) s_wmax[wave] = m;
+    __syncthreads();
+    if (wave == 0 && lane == 0)
+        work[tile] = max(max(s_wmax[0], s_wmax[1]), max(s_wmax[2], s_wmax[3]));
+}
+
 // A quadrant wave's walk list: the staged Gaussians whose bit is set in the
 // quadrant's NW mask words (loader wave lw, lane l <-> staged index
 // 64 lw + l), compacted in LDS as 16-bit record byte offsets (16 x index)
@@ -471,7 +499,8 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     int C, int c0, int nc, const float* __restrict__ depths, const int* __restrict__ ids,
     const int2* __restrict__ ranges, int64_t n, int64_t n_ids, const float* __restrict__ bg,
     int W, int H, int tiles_x, float* __restrict__ out, float* __restrict__ final_T,
-    int* __restrict__ n_contrib, float* __restrict__ depth_out, float* __restrict__ alpha_out) {
+    int* __restrict__ n_contrib, float* __restrict__ depth_out, float* __restrict__ alpha_out,
+    const int* __restrict__ order, int* __restrict__ work) {
     constexpr int F4 = (CH + 3) / 4;
     // entry kThreads of the records is the walk lists' padding: a record no
     // pixel can take (alpha bound +inf)
@@ -488,7 +517,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = (int)xcd_remap(blockIdx.x, gridDim.x);
+    const int tile = tile_at(order, blockIdx.x, gridDim.x);
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int px = px0 + (wave & 1) * 8 + (lane & 7);
@@ -573,6 +602,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
             }
         }
     }
+    if (work) store_tile_work(work, tile, last, wave, lane);
 }
 
 // Per-pixel state of the back-to-front replay.
@@ -844,7 +874,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     const float* __restrict__ final_T, const int* __restrict__ n_contrib,
     const float* __restrict__ grad_out, const float* __restrict__ grad_T,
     float* __restrict__ g_xy, float* __restrict__ g_conic, float* __restrict__ g_feat,
-    float* __restrict__ g_opac, int gstride) {
+    float* __restrict__ g_opac, int gstride, const int* __restrict__ order) {
     constexpr int F4 = (CH + 3) / 4;
     constexpr int NV = CH + 6;             // u, w, u dx, u dy, w dy, opacity term, channels
     constexpr int NV4 = (NV + 3) / 4;
@@ -866,7 +896,7 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = (int)xcd_remap(blockIdx.x, gridDim.x);
+    const int tile = tile_at(order, blockIdx.x, gridDim.x);
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int px = px0 + (wave & 1) * 8 + (lane & 7);
@@ -1234,7 +1264,7 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     const float* __restrict__ final_T, const int* __restrict__ n_contrib,
     const float* __restrict__ grad_out, const float* __restrict__ grad_T,
     float* __restrict__ g_xy, float* __restrict__ g_conic, float* __restrict__ g_feat,
-    float* __restrict__ g_opac, int gstride) {
+    float* __restrict__ g_opac, int gstride, const int* __restrict__ order) {
     static_assert(CH == 32, "the matrix-core backward covers 32-channel blocks");
     constexpr int F4 = CH / 4;
     constexpr int NV = CH + kMxGeo;  // slot values
@@ -1252,7 +1282,7 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = (int)xcd_remap(blockIdx.x, gridDim.x);
+    const int tile = tile_at(order, blockIdx.x, gridDim.x);
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;
@@ -1408,6 +1438,365 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     }
 }
 
+// Matrix-core forward for 32-channel blocks.  The per-pixel loop keeps every
+// decision of fwd_pair on the vector ALU (power, exp, alpha, the early stop,
+// T, depth, the last contributor), so final_T, n_contrib, alpha and depth
+// are the VALU path's bits; only the channel sums move.  For a group of 16
+// list entries the replay writes each pair's weight w = alpha T (zero where
+// the pixel does not composite) into a per-wave LDS tile, then
+//   out[c][p] += sum over the group of f[g][c] w[g][p]
+// runs as 32 v_mfma_f32_16x16x4_f32 (A = features, 16 channels x 4 entries;
+// B = weights, 4 entries x 16 pixels; 2 channel blocks x 4 pixel blocks of
+// accumulators).  Lane l holds channels 16 cb + 4 (l / 16) + i of quadrant
+// pixel 16 pb + l % 16.  The features are staged row-major with a row
+// stride of 48 floats (rows four slots apart share no bank window) and the
+// tile with a row stride of 80 (the four rows one operand read touches hit
+// disjoint banks).  The sums add in another order than the sequential
+// multiply-adds of fwd_pair: channels agree with it to float32 rounding.
+// Batches holding a non-finite (or |f| >= 1e30) feature add their groups on
+// the vector ALU into the same accumulators, pair by pair in list order and
+// only where w != 0, so 0 * inf never reaches a pixel that skipped the
+// Gaussian.
+constexpr int kMfBatch = 128;  // list entries staged per batch
+constexpr int kMfFeat = 48;    // feature row stride (floats)
+constexpr int kMfTile = 80;    // weight tile row stride (floats)
+
+// One (pixel, Gaussian) step of fwd_pair without the channel sums: returns
+// the weight the pixel gives the Gaussian (zero unless it composites).
+template <bool DEPTH, bool PLAIN>
+__device__ __forceinline__ float fwd_weight(const float4& r0, const float4& r1, int off,
+                                            float pxf, float pyf, float& T, float& dacc,
+                                            int& last_off, uint64_t& alive) {
+    const float dx = r0.x - pxf, dy = r0.y - pyf;
+    const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
+    const uint64_t live = alive & __ballot(!(power > 0.0f)) & __ballot(!(power < r0.z));
+    const float e = PLAIN ? splat_exp_core(power) : splat_exp_sel(power);
+    const float alpha = fminf(0.99f, r0.w * e);
+    const uint64_t pass = live & __ballot(!(alpha < 1.0f / 255.0f));
+    const float next_T = T * (1.0f - alpha);
+    const uint64_t lt = __ballot(next_T < 1e-4f);
+    alive &= ~(pass & lt);
+    const bool add = __builtin_amdgcn_inverse_ballot_w64(pass & ~lt);
+    const float w = alpha * T;
+    const float wa = add ? w : 0.0f;
+    if (DEPTH) {
+        if (PLAIN) {
+            dacc = fmaf(r1.w, wa, dacc);
+        } else {
+            const float d2 = fmaf(r1.w, w, dacc);
+            dacc = add ? d2 : dacc;
+        }
+    }
+    T = add ? next_T : T;
+    last_off = add ? off : last_off;
+    return wa;
+}
+
+// The walk of one quadrant wave for the matrix-core forward, in groups of
+// 16 list entries: the replay (two entries per round, the next pair's
+// records read before this pair is evaluated) fills the weight tile; rows
+// past the entries replayed (the group's end, or the wave's early stop)
+// are zero.  FINITE: every staged feature is finite and below 1e30.
+template <bool DEPTH, bool PLAIN, bool FINITE>
+__device__ __forceinline__ void fwd_walk_mx(const uint16_t* list, int cnt, const float4* s_r0,
+                                            const float4* s_r1, const float* s_feat,
+                                            int pad_slot, float (*tile)[kMfTile], float pxf,
+                                            float pyf, int lane, float& T, float& dacc,
+                                            int& last_off, uint64_t& alive,
+                                            mx_floatx4 (&acc)[2][4]) {
+    const int pad = pad_slot * 16;
+    const int row = lane & 15, kq = lane >> 4;
+#pragma unroll 1
+    for (int i0 = 0; i0 < cnt; i0 += kMxGroup) {
+        const int ng = min(kMxGroup, cnt - i0);
+        int oa = list[i0], ob = 1 < ng ? list[i0 + 1] : pad;
+        float4 a0 = rec_at(s_r0, oa), a1 = rec_at(s_r1, oa);
+        int j = 0;
+#pragma unroll 1
+        while (j < ng) {
+            const int na = j + 2 < ng ? list[i0 + j + 2] : pad;
+            const int nb = j + 3 < ng ? list[i0 + j + 3] : pad;
+            const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
+            tile[j][lane] =
+                fwd_weight<DEPTH, PLAIN>(a0, a1, oa, pxf, pyf, T, dacc, last_off, alive);
+            a0 = rec_at(s_r0, na);
+            a1 = rec_at(s_r1, na);
+            tile[j + 1][lane] =
+                fwd_weight<DEPTH, PLAIN>(b0, b1, ob, pxf, pyf, T, dacc, last_off, alive);
+            oa = na;
+            ob = nb;
+            j += 2;
+            if (alive == 0ull) break;
+        }
+#pragma unroll 1
+        for (; j < kMxGroup; ++j) tile[j][lane] = 0.0f;
+        // the wave's LDS accesses complete in order; the fence keeps the
+        // compiler from moving the reads below above the writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        if constexpr (FINITE) {
+#pragma unroll 1
+            for (int ks = 0; ks < 4; ++ks) {
+                const int r = 4 * ks + kq;
+                const int slot = r < ng ? (list[i0 + r] >> 4) : pad_slot;
+                const float fa0 = s_feat[slot * kMfFeat + row];
+                const float fa1 = s_feat[slot * kMfFeat + 16 + row];
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) {
+                    const float wb = tile[r][16 * pb + row];
+                    acc[0][pb] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0, wb, acc[0][pb], 0, 0, 0);
+                    acc[1][pb] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1, wb, acc[1][pb], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll 1
+            for (int r = 0; r < ng; ++r) {
+                const int slot = list[i0 + r] >> 4;
+                float wv[4];
+#pragma unroll
+                for (int pb = 0; pb < 4; ++pb) wv[pb] = tile[r][16 * pb + row];
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    const float4 f =
+                        *reinterpret_cast<const float4*>(s_feat + slot * kMfFeat + 16 * cb + 4 * kq);
+#pragma unroll
+                    for (int pb = 0; pb < 4; ++pb) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float v = fmaf(comp4(f, i), wv[pb], acc[cb][pb][i]);
+                            acc[cb][pb][i] = wv[pb] != 0.0f ? v : acc[cb][pb][i];
+                        }
+                    }
+                }
+            }
+        }
+        // the next group's replay overwrites the tile
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        if (alive == 0ull) return;
+    }
+}
+
+template <bool DEPTH>
+__global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
+    const float2* __restrict__ xy, const float4* __restrict__ co, const float* __restrict__ feat,
+    int C, int c0, int nc, const float* __restrict__ depths, const int* __restrict__ ids,
+    const int2* __restrict__ ranges, int64_t n, int64_t n_ids, const float* __restrict__ bg,
+    int W, int H, int tiles_x, float* __restrict__ out, float* __restrict__ final_T,
+    int* __restrict__ n_contrib, float* __restrict__ depth_out, float* __restrict__ alpha_out,
+    const int* __restrict__ order, int* __restrict__ work) {
+    constexpr int BB = kMfBatch;
+    constexpr int NLW = BB / kWave;  // waves that stage records
+    constexpr int F4 = 8;            // float4 pieces of a 32-channel row
+    // entry BB of the records (and feature row BB, zeros) is the padding
+    __shared__ float4 s_r0[BB + 1];  // mean x, mean y, log-alpha bound, opacity
+    __shared__ float4 s_r1[BB + 1];  // -a/2, -b, -c/2 (conic), depth
+    __shared__ __align__(16) float s_feat[(BB + 1) * kMfFeat];
+    __shared__ float s_tile[kWaves][kMxGroup][kMfTile];
+    __shared__ uint64_t s_mask[kWaves][NLW];
+    __shared__ uint16_t s_list[kWaves][BB + 4];
+    __shared__ __align__(16) uint32_t s_alive[kWaves];
+    __shared__ __align__(16) uint32_t s_plain[kWaves];
+    __shared__ __align__(16) uint32_t s_finite[kWaves];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tile = tile_at(order, blockIdx.x, gridDim.x);
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const int px0 = tx * kTile, py0 = ty * kTile;
+    const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;
+    const int px = qx0 + (lane & 7);
+    const int py = qy0 + (lane >> 3);
+    const bool inside = px < W && py < H;
+    const float pxf = (float)px + 0.5f, pyf = (float)py + 0.5f;
+
+    int start, num;
+    tile_span(ranges[tile], n_ids, start, num);
+
+    float T = 1.0f, dacc = 0.0f;
+    mx_floatx4 acc[2][4];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) acc[cb][pb] = mx_floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    int last = 0;
+    uint64_t alive = __ballot(inside);
+    if (tid == 0) {
+        s_r0[BB] = make_float4(0.0f, 0.0f, __builtin_huge_valf(), 0.0f);
+        s_r1[BB] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (tid < kMfFeat) s_feat[BB * kMfFeat + tid] = 0.0f;
+
+    for (int base = 0; base < num; base += BB) {
+        if (lane == 0) s_alive[wave] = alive != 0ull;
+        __syncthreads();
+        const uint4 al = *reinterpret_cast<const uint4*>(s_alive);
+        if ((al.x | al.y | al.z | al.w) == 0u) break;  // all 256 pixels done
+        uint32_t qm = 0;
+        bool plain = true, finite = true;
+        if (tid < BB) {
+            const int k = base + tid;
+            if (k < num) {
+                const int g = ids[start + k];
+                if ((uint32_t)g < (uint64_t)n) {
+                    const float2 m = xy[g];
+                    const float4 c = co[g];
+                    const float thr = alpha_floor_power(c.w);
+                    s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
+                    const float dz = DEPTH ? depths[g] : 0.0f;
+                    s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, dz);
+                    qm = quadrant_mask(m.x, m.y, c, px0, py0);
+                    plain = plain_gaussian<0>(m.x, m.y, c, thr, nullptr) && fabsf(dz) < 1e30f;
+                }
+            }
+        }
+        // the features: thread t stages piece t % 8 of entries t / 8 + 32 i
+#pragma unroll
+        for (int it = 0; it < BB * F4 / kThreads; ++it) {
+            const int j = (tid >> 3) + (kThreads / F4) * it, q = tid & 7;
+            const int k = base + j;
+            if (k < num) {
+                const int g = ids[start + k];
+                if ((uint32_t)g < (uint64_t)n) {
+                    const float* f = feat + (int64_t)g * C + c0 + 4 * q;
+                    float4 v;
+                    v.x = 4 * q < nc ? f[0] : 0.0f;
+                    v.y = 4 * q + 1 < nc ? f[1] : 0.0f;
+                    v.z = 4 * q + 2 < nc ? f[2] : 0.0f;
+                    v.w = 4 * q + 3 < nc ? f[3] : 0.0f;
+                    *reinterpret_cast<float4*>(s_feat + j * kMfFeat + 4 * q) = v;
+                    finite = finite && fabsf(v.x) < 1e30f && fabsf(v.y) < 1e30f &&
+                             fabsf(v.z) < 1e30f && fabsf(v.w) < 1e30f;
+                }
+            }
+        }
+        if (wave < NLW) {
+#pragma unroll
+            for (int q = 0; q < kWaves; ++q) {
+                const uint64_t b = __ballot((qm >> q) & 1u);
+                if (lane == 0) s_mask[q][wave] = b;
+            }
+        }
+        const uint64_t np = __ballot(!plain), nf = __ballot(!finite);
+        if (lane == 0) {
+            s_plain[wave] = np == 0ull;
+            s_finite[wave] = nf == 0ull;
+        }
+        __syncthreads();
+        const uint4 pl = *reinterpret_cast<const uint4*>(s_plain);
+        const uint4 fi = *reinterpret_cast<const uint4*>(s_finite);
+        const bool batch_plain = (pl.x & pl.y & pl.z & pl.w) != 0u;
+        const bool batch_finite = (fi.x & fi.y & fi.z & fi.w) != 0u;
+        if (alive == 0ull) continue;
+        const int cnt = build_list<NLW, false>(s_mask[wave], s_list[wave], lane, BB * 16);
+        int last_off = -1;
+        if (batch_finite) {
+            if (batch_plain)
+                fwd_walk_mx<DEPTH, true, true>(s_list[wave], cnt, s_r0, s_r1, s_feat, BB,
+                                               s_tile[wave], pxf, pyf, lane, T, dacc, last_off,
+                                               alive, acc);
+            else
+                fwd_walk_mx<DEPTH, false, true>(s_list[wave], cnt, s_r0, s_r1, s_feat, BB,
+                                                s_tile[wave], pxf, pyf, lane, T, dacc, last_off,
+                                                alive, acc);
+        } else {
+            fwd_walk_mx<DEPTH, false, false>(s_list[wave], cnt, s_r0, s_r1, s_feat, BB,
+                                             s_tile[wave], pxf, pyf, lane, T, dacc, last_off,
+                                             alive, acc);
+        }
+        if (last_off >= 0) last = base + (last_off >> 4) + 1;
+    }
+    if (inside && c0 == 0) {
+        const int64_t pid = (int64_t)py * W + px;
+        final_T[pid] = T;
+        n_contrib[pid] = last;
+        if (alpha_out) alpha_out[pid] = 1.0f - T;
+        if (DEPTH) {
+            const float al = 1.0f - T;
+            depth_out[pid] = al > 1e-6f ? dacc / al : 0.0f;
+        }
+    }
+    if (work) store_tile_work(work, tile, last, wave, lane);
+    // channel results: lane l holds quadrant pixel 16 pb + l % 16, channels
+    // 16 cb + 4 (l / 16) + i; that pixel's T is lane (16 pb + l % 16)'s
+    const int row = lane & 15, kq = lane >> 4;
+    // whole 16-byte pieces when the block is 32 aligned channels
+    const bool vec_out = nc == 32 && (C & 3) == 0 && (c0 & 3) == 0 &&
+                         (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+        const int q = 16 * pb + row;
+        const float Tq = __shfl(T, q, kWave);
+        const int bx = qx0 + (q & 7), by = qy0 + (q >> 3);
+        if (bx < W && by < H) {
+            float* o = out + ((int64_t)by * W + bx) * C + c0;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const int ch0 = 16 * cb + 4 * kq;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v[i] = acc[cb][pb][i] + Tq * (bg && ch0 + i < nc ? bg[c0 + ch0 + i] : 0.0f);
+                if (vec_out) {
+                    *reinterpret_cast<float4*>(o + ch0) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (ch0 + i < nc) o[ch0 + i] = v[i];
+                }
+            }
+        }
+    }
+}
+
+// The tile order for tile_at: one workgroup per XCD range, a counting sort
+// of the range's tiles by a work estimate in descending quarter-octave
+// buckets (4 log2(w + 1), 64 buckets): the list length (ranges) for the
+// forward, the contributor bound the forward stored (work) for the
+// backward.  Order within a bucket follows LDS atomics and is not fixed;
+// results do not depend on it (each tile's outputs are its own, and the
+// backward's cross-tile sums are float atomics in any case).  Every tile of
+// the range is placed exactly once, whatever the estimates hold.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBuckets = 64;
+
+__device__ __forceinline__ int order_key(int w) {
+    const uint32_t v = (uint32_t)max(w, 0) + 1u;
+    const int e = 31 - __clz(v);
+    const int frac = e >= 2 ? (int)((v >> (e - 2)) & 3u) : (int)((v << (2 - e)) & 3u);
+    return kOrderBuckets - 1 - min(kOrderBuckets - 1, 4 * e + frac);  // heaviest first
+}
+
+__global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __restrict__ ranges,
+                                                              const int* __restrict__ work,
+                                                              int64_t n_ids, int tiles,
+                                                              int* __restrict__ order) {
+    __shared__ int s_cnt[kOrderBuckets];
+    constexpr int kXcd = 8;
+    const int x = blockIdx.x, tid = threadIdx.x;
+    const int q = tiles / kXcd, r = tiles % kXcd;
+    const int lo = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+    const int hi = lo + q + (x < r ? 1 : 0);
+    auto key = [&](int t) {
+        int w;
+        if (work) {
+            w = work[t];
+        } else {
+            int start, num;
+            tile_span(ranges[t], n_ids, start, num);
+            w = num;
+        }
+        return order_key(w);
+    };
+    if (tid < kOrderBuckets) s_cnt[tid] = 0;
+    __syncthreads();
+    for (int t = lo + tid; t < hi; t += kOrderThreads) atomicAdd(&s_cnt[key(t)], 1);
+    __syncthreads();
+    if (tid < kWave) {
+        const int v = s_cnt[tid];
+        s_cnt[tid] = (int)wave_incl_scan((uint32_t)v) - v;
+    }
+    __syncthreads();
+    for (int t = lo + tid; t < hi; t += kOrderThreads) order[lo + atomicAdd(&s_cnt[key(t)], 1)] = t;
+}
+
 // Clears the four gradient outputs in one launch (a fill kernel rather than
 // hipMemsetAsync, so the call can sit inside a captured graph).
 __global__ __launch_bounds__(256) void k_zero_grads(float* __restrict__ a, int64_t na,
@@ -1436,15 +1825,26 @@ template <int CH>
 void launch_fwd(dim3 grid, hipStream_t st, bool depth, const float2* xy, const float4* co,
                 const float* feat, int C, int c0, int nc, const float* depths, const int* ids,
                 const int2* ranges, int64_t n, int64_t n_ids, const float* bg, int W, int H,
-                int tiles_x, float* out, float* fT, int* ncon, float* dout, float* aout) {
-    if (depth)
+                int tiles_x, float* out, float* fT, int* ncon, float* dout, float* aout,
+                const int* order, int* work) {
+    if constexpr (CH == 32) {
+        if (depth)
+            hipLaunchKernelGGL((k_raster_fwd_mx<true>), grid, dim3(kThreads), 0, st, xy, co, feat,
+                               C, c0, nc, depths, ids, ranges, n, n_ids, bg, W, H, tiles_x, out,
+                               fT, ncon, dout, aout, order, work);
+        else
+            hipLaunchKernelGGL((k_raster_fwd_mx<false>), grid, dim3(kThreads), 0, st, xy, co,
+                               feat, C, c0, nc, depths, ids, ranges, n, n_ids, bg, W, H, tiles_x,
+                               out, fT, ncon, dout, aout, order, work);
+    } else if (depth) {
         hipLaunchKernelGGL((k_raster_fwd<CH, true>), grid, dim3(kThreads), 0, st, xy, co, feat, C,
                            c0, nc, depths, ids, ranges, n, n_ids, bg, W, H, tiles_x, out, fT,
-                           ncon, dout, aout);
-    else
+                           ncon, dout, aout, order, work);
+    } else {
         hipLaunchKernelGGL((k_raster_fwd<CH, false>), grid, dim3(kThreads), 0, st, xy, co, feat, C,
                            c0, nc, depths, ids, ranges, n, n_ids, bg, W, H, tiles_x, out, fT,
-                           ncon, dout, aout);
+                           ncon, dout, aout, order, work);
+    }
 }
 
 template <int CH>
@@ -1452,15 +1852,15 @@ void launch_bwd(dim3 grid, hipStream_t st, const float2* xy, const float4* co, c
                 int C, int c0, int nc, const int* ids, const int2* ranges, int64_t n,
                 int64_t n_ids, const float* bg, int W, int H, int tiles_x, const float* fT,
                 const int* ncon, const float* gout, const float* gT, float* gxy, float* gcon,
-                float* gfeat, float* gop, int gstride) {
+                float* gfeat, float* gop, int gstride, const int* order) {
     if constexpr (CH == 32)
         hipLaunchKernelGGL((k_raster_bwd_mx<CH>), grid, dim3(kThreads), 0, st, xy, co, feat, C,
                            c0, nc, ids, ranges, n, n_ids, bg, W, H, tiles_x, fT, ncon, gout, gT,
-                           gxy, gcon, gfeat, gop, gstride);
+                           gxy, gcon, gfeat, gop, gstride, order);
     else
         hipLaunchKernelGGL((k_raster_bwd<CH>), grid, dim3(kThreads), 0, st, xy, co, feat, C, c0,
                            nc, ids, ranges, n, n_ids, bg, W, H, tiles_x, fT, ncon, gout, gT, gxy,
-                           gcon, gfeat, gop, gstride);
+                           gcon, gfeat, gop, gstride, order);
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1475,7 +1875,7 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d, const float* coni
                    int64_t num_ids, const int32_t* tile_ranges, const float* background,
                    int32_t width,
                    int32_t height, float* out, float* final_T, int32_t* n_contrib,
-                   float* depth_out, float* alpha_out, void* stream) {
+                   float* depth_out, float* alpha_out, int32_t* tile_order, void* stream) {
     if (n < 0 || num_ids < 0 || C <= 0 || width <= 0 || height <= 0) return GSX_ERR_INVALID;
     if (!tile_ranges || !out || !final_T || !n_contrib) return GSX_ERR_INVALID;
     if (n > 0 && (!means2d || !conic_opacity || !features)) return GSX_ERR_INVALID;
@@ -1488,16 +1888,24 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d, const float* coni
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
     const dim3 grid((unsigned)(tiles_x * tiles_y));
+    const int tiles = tiles_x * tiles_y;
+    if (tile_order) {
+        hipLaunchKernelGGL(k_tile_order, dim3(8), dim3(kOrderThreads), 0, st,
+                           (const int2*)tile_ranges, (const int*)nullptr, num_ids, tiles,
+                           tile_order);
+        GSX_LAUNCH_CHECK();
+    }
     for (int c0 = 0; c0 < C; c0 += kMaxChunk) {
         const int nc = (C - c0 < kMaxChunk) ? C - c0 : kMaxChunk;
         const bool depth = depths && c0 == 0;
+        int* work = (tile_order && c0 == 0) ? tile_order + tiles : nullptr;
         switch (pick_ch(nc)) {
 #define GSX_FWD_CASE(V)                                                                          \
     case V:                                                                                      \
         launch_fwd<V>(grid, st, depth, (const float2*)means2d, (const float4*)conic_opacity,     \
                       features, C, c0, nc, depths, sorted_ids, (const int2*)tile_ranges, n,      \
                       num_ids, background, width, height, tiles_x, out, final_T, n_contrib,      \
-                      depth_out, alpha_out);                                                     \
+                      depth_out, alpha_out, tile_order, work);                                   \
         break;
             GSX_FWD_CASE(1)
             GSX_FWD_CASE(2)
@@ -1521,7 +1929,7 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
                    const float* background, int32_t width, int32_t height, const float* final_T,
                    const int32_t* n_contrib, const float* grad_out, const float* grad_final_T,
                    float* g_means2d, float* g_conics, float* g_features, float* g_opacities,
-                   int32_t grad_stride, void* stream) {
+                   int32_t grad_stride, int32_t* tile_order, void* stream) {
     if (n < 0 || num_ids < 0 || C <= 0 || width <= 0 || height <= 0) return GSX_ERR_INVALID;
     if (!tile_ranges || !final_T || !n_contrib || !grad_out) return GSX_ERR_INVALID;
     const bool rec = grad_stride > 0;
@@ -1552,6 +1960,13 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
     const dim3 grid((unsigned)(tiles_x * tiles_y));
+    const int tiles = tiles_x * tiles_y;
+    if (tile_order) {
+        hipLaunchKernelGGL(k_tile_order, dim3(8), dim3(kOrderThreads), 0, st,
+                           (const int2*)nullptr, (const int*)(tile_order + tiles), num_ids, tiles,
+                           tile_order);
+        GSX_LAUNCH_CHECK();
+    }
     for (int c0 = 0; c0 < C; c0 += kMaxChunk) {
         const int nc = (C - c0 < kMaxChunk) ? C - c0 : kMaxChunk;
         switch (pick_ch(nc)) {
@@ -1560,7 +1975,7 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
         launch_bwd<V>(grid, st, (const float2*)means2d, (const float4*)conic_opacity, features,  \
                       C, c0, nc, sorted_ids, (const int2*)tile_ranges, n, num_ids, background,   \
                       width, height, tiles_x, final_T, n_contrib, grad_out, grad_final_T,        \
-                      g_means2d, g_conics, g_features, g_opacities, grad_stride);                \
+                      g_means2d, g_conics, g_features, g_opacities, grad_stride, tile_order);    \
         break;
             GSX_BWD_CASE(1)
             GSX_BWD_CASE(2)

@@ -24,10 +24,21 @@ def _empty(shape, dev, dtype=torch.float32):
     return torch.empty(shape, dtype=dtype, device=dev)
 
 
+def tile_order_buffer(width, height, dev):
+    """The rasterizers' tile-order buffer for a width x height image: 2 T
+    int32 words (T tiles), filled by the forward and reused by the
+    backward of the same frame."""
+    tiles = ((width + TILE_SIZE - 1) // TILE_SIZE) * ((height + TILE_SIZE - 1) // TILE_SIZE)
+    return _empty((2 * tiles,), dev, torch.int32)
+
+
 def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, background, width,
-                   height, depths=None):
+                   height, depths=None, tile_order=None):
     """gsx_raster_fwd on prepared float32 contiguous tensors (no autograd):
-    (out, final_T, n_contrib, depth_map or None, alpha = 1 - final_T)."""
+    (out, final_T, n_contrib, depth_map or None, alpha = 1 - final_T).
+    With ``tile_order`` (tile_order_buffer) the workgroups take the heaviest
+    tiles first and the buffer keeps the per-tile bounds for
+    raster_backward."""
     dev = means2d.device
     n, C = feats.shape
     out = _empty((height, width, C), dev)
@@ -41,7 +52,8 @@ def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, backgrou
                                 _lib.ptr(tile_ranges),
                                 _lib.ptr(background), width, height, _lib.ptr(out),
                                 _lib.ptr(final_T), _lib.ptr(n_contrib), _lib.ptr(depth_map),
-                                _lib.ptr(alpha), _lib.stream_handle(dev)), "gsx_raster_fwd")
+                                _lib.ptr(alpha), _lib.ptr(tile_order), _lib.stream_handle(dev)),
+               "gsx_raster_fwd")
     return out, final_T, n_contrib, depth_map, alpha
 
 
@@ -60,8 +72,10 @@ def grad_record_stride(C: int) -> int:
 
 
 def raster_backward(means2d, conic_opac, feats, sorted_ids, tile_ranges, background, width,
-                    height, final_T, n_contrib, g_out, g_final_T, record: bool = False):
+                    height, final_T, n_contrib, g_out, g_final_T, record: bool = False,
+                    tile_order=None):
     """gsx_raster_bwd: gradients w.r.t. means2d, conics, features, opacity.
+    ``tile_order``: the buffer the frame's raster_forward filled, or None.
 
     With ``record`` the kernel accumulates into one (N, stride) record per
     Gaussian (its atomics for a Gaussian then share a cache line or two);
@@ -91,7 +105,7 @@ def raster_backward(means2d, conic_opac, feats, sorted_ids, tile_ranges, backgro
                                 _lib.ptr(background),
                                 width, height, _lib.ptr(final_T), _lib.ptr(n_contrib),
                                 _lib.ptr(g_out), _lib.ptr(g_final_T), *[_lib.ptr(t) for t in outs],
-                                stride, _lib.stream_handle(dev)),
+                                stride, _lib.ptr(tile_order), _lib.stream_handle(dev)),
                "gsx_raster_bwd")
     if record:
         return g_m, g_c, g_f, g_o, rec, stride
@@ -114,10 +128,12 @@ class _Rasterize(torch.autograd.Function):
                 width, height):
         _lib.require_device(means2d, conics, feats, opacities, sorted_ids, tile_ranges, background)
         co = pack_conic_opacity(conics, opacities)
+        order = tile_order_buffer(width, height, means2d.device)
         out, final_T, n_contrib, _, alpha = raster_forward(means2d, co, feats, sorted_ids,
-                                                           tile_ranges, background, width, height)
+                                                           tile_ranges, background, width, height,
+                                                           tile_order=order)
         ctx.save_for_backward(means2d, co, feats, sorted_ids, tile_ranges, background, final_T,
-                              n_contrib)
+                              n_contrib, order)
         ctx.size = (width, height)
         ctx.mark_non_differentiable(n_contrib)
         ctx.set_materialize_grads(False)  # unused outputs: no zero-filled cotangents
@@ -125,11 +141,11 @@ class _Rasterize(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_out, g_final_T, g_alpha, _g_nc):
-        means2d, co, feats, ids, ranges, bg, final_T, n_contrib = ctx.saved_tensors
+        means2d, co, feats, ids, ranges, bg, final_T, n_contrib, order = ctx.saved_tensors
         width, height = ctx.size
         g_m, g_c, g_f, g_o = raster_backward(means2d, co, feats, ids, ranges, bg, width, height,
                                              final_T, n_contrib, g_out,
-                                             t_cotangent(g_final_T, g_alpha))
+                                             t_cotangent(g_final_T, g_alpha), tile_order=order)
         return g_m, g_c, g_f, g_o, None, None, None, None, None
 
 
@@ -214,5 +230,7 @@ def rasterize_depth(means2d, conics, opacities, depths, sorted_ids, tile_ranges,
         _, final_T, _, depth, alpha = raster_forward(_lib.f32c(means2d), co,
                                                      d[:, None].contiguous(), _ids(sorted_ids),
                                                      _ids(tile_ranges), None, width, height,
-                                                     depths=d)
+                                                     depths=d,
+                                                     tile_order=tile_order_buffer(
+                                                         width, height, means2d.device))
     return {"depth": depth, "alpha": alpha, "final_T": final_T}

@@ -23,7 +23,8 @@ import torch
 from .. import _lib
 from ..cameras import Camera
 from ..profiling import count, stage
-from .rasterize import background_tensor, raster_backward, raster_forward, t_cotangent
+from .rasterize import (background_tensor, raster_backward, raster_forward, t_cotangent,
+                        tile_order_buffer)
 from .sh import num_sh_bases
 from .tiles import BinJob
 
@@ -86,10 +87,13 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
         job = BinJob(counts, dkeys, rects, cfg.width, cfg.height,
                      refine=(means2d, co) if cfg.refine else None)
 
+    order = tile_order_buffer(cfg.width, cfg.height, dev)
+
     def raster(ids):
         with stage("raster_fwd"):
             return raster_forward(means2d, co, feats, ids, job.ranges, background, cfg.width,
-                                  cfg.height, depths=depths if cfg.return_depth else None)
+                                  cfg.height, depths=depths if cfg.return_depth else None,
+                                  tile_order=order)
 
     # The rasterizer runs on the id buffer (its ranges never reach past D);
     # only refine_tiles needs the final status for D, read after it has been
@@ -99,7 +103,7 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
     count("duplicates", ids.shape[0])
     return dict(means2d=means2d, depths=depths, radii=radii, compensation=comp, conic_opac=co,
                 feats=feats, sorted_ids=ids, tile_ranges=ranges, image=image, final_T=final_T,
-                alpha=alpha, n_contrib=n_contrib, depth=depth_map, job=job)
+                alpha=alpha, n_contrib=n_contrib, depth=depth_map, job=job, tile_order=order)
 
 
 class _RenderFn(torch.autograd.Function):
@@ -110,7 +114,8 @@ class _RenderFn(torch.autograd.Function):
         ctx.bin_job = r["job"]
         ctx.save_for_backward(means, quats, scales, opacities, sh_a, sh_b, r["feats"],
                               r["means2d"], r["conic_opac"], r["sorted_ids"], r["tile_ranges"],
-                              r["final_T"], r["n_contrib"], background, r["radii"])
+                              r["final_T"], r["n_contrib"], background, r["radii"],
+                              r["tile_order"])
         depth = r["depth"] if r["depth"] is not None else r["final_T"].new_empty((0,))
         ctx.mark_non_differentiable(r["radii"], r["n_contrib"], depth, r["sorted_ids"],
                                     r["tile_ranges"])
@@ -122,7 +127,7 @@ class _RenderFn(torch.autograd.Function):
     def backward(ctx, g_image, g_final_T, g_alpha, _g_nc, g_means2d, g_depths, _g_radii, g_comp,
                  _g_depth, _g_ids, _g_ranges):
         (means, quats, scales, opacities, sh_a, sh_b, feats, means2d, co, ids, ranges, final_T,
-         n_contrib, background, radii) = ctx.saved_tensors
+         n_contrib, background, radii, order) = ctx.saved_tensors
         cfg = ctx.cfg
         dev = means.device
         n = means.shape[0]
@@ -131,7 +136,8 @@ class _RenderFn(torch.autograd.Function):
         with stage("raster_bwd"):
             _, _, g_feat, _, grec, gstride = raster_backward(
                 means2d, co, feats, ids, ranges, background, cfg.width, cfg.height, final_T,
-                n_contrib, g_image, t_cotangent(g_final_T, g_alpha), record=True)
+                n_contrib, g_image, t_cotangent(g_final_T, g_alpha), record=True,
+                tile_order=order)
         if cfg.screen_stats is not None:
             acc, cnt = cfg.screen_stats
             _lib.check(_lib.load().gsx_accum_screen_grads(

@@ -42,6 +42,38 @@ def assert_bits(a, b, what=""):
                              f"gpu={a[bad][:5]} oracle={b[bad][:5]}")
 
 
+def matrix_core_channels(C: int) -> np.ndarray:
+    """Channels that the rasterizers sum on the matrix cores: those of the
+    32-channel blocks that hold 17 to 32 channels."""
+    mask = np.zeros(C, bool)
+    for c0 in range(0, C, 32):
+        nc = min(32, C - c0)
+        if nc > 16:
+            mask[c0:c0 + nc] = True
+    return mask
+
+
+def assert_features(a, b, what="features", atol=1e-5):
+    """Rendered channels against the oracle: bitwise where the channel sums
+    run on the vector ALU (the oracle's order of multiply-adds), within
+    `atol` absolute (the north star's image tolerance) where a 32-channel
+    block sums on the matrix cores in another order.  Non-finite values
+    must sit at the same places with the same value."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} vs {b.shape}"
+    mask = matrix_core_channels(a.shape[-1])
+    assert_bits(a[..., ~mask], b[..., ~mask], what)
+    am, bm = a[..., mask], b[..., mask]
+    fin = np.isfinite(bm)
+    np.testing.assert_array_equal(np.isfinite(am), fin, err_msg=what)
+    np.testing.assert_array_equal(np.isnan(am), np.isnan(bm), err_msg=what)
+    np.testing.assert_array_equal(am[np.isinf(bm)], bm[np.isinf(bm)], err_msg=what)
+    if fin.any():
+        err = float(np.abs(am[fin].astype(np.float64) - bm[fin]).max())
+        assert err <= atol, f"{what}: max abs error {err:.3e} > {atol}"
+
+
 def rel_err(a, b) -> float:
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import (assert_bits, cu, host, oracle_backward, oracle_forward, rel_err, say)
+from gpu_util import (assert_bits, assert_features, cu, host, oracle_backward, oracle_forward,
+                      rel_err, say)
 from mlx3d_amd import _lib
 from mlx3d_amd.splatting import (GaussianModel, bin_gaussians, eval_sh, project_gaussians,
                                  rasterize, rasterize_depth, rasterize_features,
@@ -373,7 +374,7 @@ def test_rasterize_building_block_bitexact():
     assert_bits(host(d["depth"]), refd["depth"], "depth")
 
 
-@pytest.mark.parametrize("channels", [3, 12])
+@pytest.mark.parametrize("channels", [3, 12, 32])
 def test_rasterize_non_plain_batches(channels):
     """Batches holding a Gaussian outside the rasterizers' fast-path range
     (a mean 2e6 px away; a 1e21 conic centred on a pixel, which takes G = 1
@@ -406,7 +407,7 @@ def test_rasterize_non_plain_batches(channels):
         img = out["features"]
     ref = O.raster_fwd(m2, con, op, feats, ids, ranges, W, H)
     np.testing.assert_array_equal(host(out["n_contrib"]), ref["n_contrib"])
-    assert_bits(host(img), ref["image"], "image")
+    assert_features(host(img), ref["image"], "image")
     assert_bits(host(out["final_T"]), ref["final_T"], "final_T")
     g_img = rng.standard_normal(ref["image"].shape).astype(np.float32)
     g_a = rng.standard_normal(ref["final_T"].shape).astype(np.float32)
@@ -513,6 +514,52 @@ def test_model_render_sh_raw_params(degree):
         assert e < 1e-3
 
 
+@pytest.mark.parametrize("channels", [32, 37])
+def test_features_non_finite_forward(channels):
+    """A batch holding an infinite, a NaN and a huge (1e31) feature adds its
+    channel sums on the vector ALU inside the matrix-core forward, only
+    where a pixel composites the Gaussian: the non-finite values land
+    exactly where the oracle's multiply-adds put them (no 0 * inf at pixels
+    that skip the Gaussian), every other value within 1e-5, n_contrib,
+    final_T and depth bit-exact."""
+    W = H = 32
+    n = 90
+    rng = np.random.default_rng(7 + channels)
+    m2 = rng.uniform(0.0, 32.0, (n, 2)).astype(np.float32)
+    s = rng.uniform(0.5, 4.0, n)
+    con = np.stack([1 / s ** 2, rng.uniform(-0.2, 0.2, n) / s ** 2, 1 / s ** 2], 1)
+    con = con.astype(np.float32)
+    op = rng.uniform(0.05, 0.9, n).astype(np.float32)
+    feats = rng.standard_normal((n, channels)).astype(np.float32)
+    feats[5, 3] = np.inf
+    feats[17, 20] = -np.inf
+    feats[40, 9] = np.nan
+    feats[41, 30] = 1e31
+    depths = rng.uniform(1.0, 5.0, n).astype(np.float32)
+    ids = np.arange(n, dtype=np.int32)
+    ranges = np.tile(np.array([[0, n]], np.int32), (4, 1))
+    out = torch.empty((H, W, channels), device="cuda")
+    fT = torch.empty((H, W), device="cuda")
+    nct = torch.empty((H, W), dtype=torch.int32, device="cuda")
+    dout = torch.empty((H, W), device="cuda")
+    aout = torch.empty((H, W), device="cuda")
+    dm2, dcon, dfe, ddp, dids, drg = (cu(a) for a in (m2, np.concatenate([con, op[:, None]], 1),
+                                                      feats, depths, ids, ranges))
+    L = _lib.load()
+    P = _lib.ptr
+    _lib.check(L.gsx_raster_fwd(n, channels, P(dm2), P(dcon), P(dfe), P(ddp), P(dids), n,
+                                P(drg), None, W, H, P(out), P(fT), P(nct), P(dout), P(aout),
+                                None, _lib.stream_handle(out.device)), "raster_fwd")
+    torch.cuda.synchronize()
+    ref = O.raster_fwd(m2, con, op, feats, ids, ranges, W, H, depths=depths)
+    np.testing.assert_array_equal(host(nct), ref["n_contrib"])
+    assert_bits(host(fT), ref["final_T"], "final_T")
+    assert_bits(host(dout), ref["depth"], "depth")
+    img = host(out)
+    assert not np.isfinite(ref["image"]).all()  # the non-finite values reach pixels
+    assert_features(img, ref["image"], "features")
+
+
 @pytest.mark.parametrize("channels", [1, 2, 4, 5, 12, 32, 37])
 def test_features(channels):
     cam, means, quats, scales, opac, _ = random_scene(6, n=3000, width=128, height=96)
@@ -526,7 +573,7 @@ def test_features(channels):
                                             depth=True)
     assert out["features"].shape == (96, 128, channels)
     np.testing.assert_array_equal(host(out["n_contrib"]), r["n_contrib"])
-    assert_bits(host(out["features"]), r["image"], "features")
+    assert_features(host(out["features"]), r["image"], "features")
     assert_bits(host(out["depth"]), r["depth"], "depth")
     g_img = rng.standard_normal(r["image"].shape).astype(np.float32)
     g_a = rng.standard_normal(r["final_T"].shape).astype(np.float32)
@@ -723,3 +770,58 @@ def test_raster_backward_gradient_record(C):
     stride = rec[5]
     assert stride % 4 == 0 and stride >= 6 + C
     assert float(rec[4][:, 6 + C:].abs().max() if stride > 6 + C else 0.0) == 0.0
+
+
+@pytest.mark.parametrize("C", [3, 32])
+def test_tile_order(C):
+    """The rasterizers' tile order (heaviest tiles first within each XCD's
+    share): the forward's outputs are bit-identical with and without it;
+    the buffer holds a permutation of the tiles in XCD-contiguous ranges and
+    each tile's largest n_contrib; the backward gives the same gradients in
+    launch order, in the forward's order and with the bound words replaced
+    by arbitrary values (float atomics: to 1e-6 of the largest entry)."""
+    from mlx3d_amd.splatting.rasterize import (raster_backward, raster_forward,
+                                               tile_order_buffer)
+
+    W, H = 328, 200  # 21 x 13 tiles: 273 = 8 * 34 + 1, one XCD range longer
+    cam, means, quats, scales, opac, _ = random_scene(57 + C, n=5000, width=W, height=H)
+    rng = np.random.default_rng(C)
+    feats = cu(rng.standard_normal((means.shape[0], C)).astype(np.float32))
+    proj = project_gaussians(cam, cu(means), cu(quats), cu(scales))
+    ids, ranges, _, _ = bin_gaussians(proj["means2d"], proj["radii"], proj["depths"], W, H)
+    co = torch.cat([proj["conics"], (cu(opac) * proj["compensation"])[:, None]], 1).contiguous()
+    m2 = proj["means2d"].contiguous()
+    bg = torch.linspace(-0.1, 0.1, C, device=m2.device)
+    base = raster_forward(m2, co, feats, ids, ranges, bg, W, H)
+    order = tile_order_buffer(W, H, m2.device)
+    ordered = raster_forward(m2, co, feats, ids, ranges, bg, W, H, tile_order=order)
+    for name, a, b in zip(("out", "final_T", "n_contrib", "alpha"),
+                          (base[0], base[1], base[2], base[4]),
+                          (ordered[0], ordered[1], ordered[2], ordered[4])):
+        assert torch.equal(a, b), name
+    T = 21 * 13
+    o = host(order)
+    perm, work = o[:T], o[T:]
+    assert np.array_equal(np.sort(perm), np.arange(T))
+    q, r = divmod(T, 8)
+    lo = 0
+    for x in range(8):  # each XCD's range holds its own tiles
+        hi = lo + q + (1 if x < r else 0)
+        assert np.array_equal(np.sort(perm[lo:hi]), np.arange(lo, hi))
+        lo = hi
+    nc = np.zeros((13 * 16, 21 * 16), np.int32)
+    nc[:H, :W] = host(base[2])
+    want = nc.reshape(13, 16, 21, 16).max(axis=(1, 3)).ravel()
+    np.testing.assert_array_equal(work, want)
+    g_out = cu(rng.normal(size=(H, W, C)).astype(np.float32))
+    g_T = cu(rng.normal(size=(H, W)).astype(np.float32))
+    ref = raster_backward(m2, co, feats, ids, ranges, bg, W, H, base[1], base[2], g_out, g_T)
+    scrambled = order.clone()
+    scrambled[T:] = cu(rng.integers(-2**31, 2**31 - 1, T, dtype=np.int64).astype(np.int32))
+    for buf in (order, scrambled):
+        got = raster_backward(m2, co, feats, ids, ranges, bg, W, H, base[1], base[2], g_out,
+                              g_T, tile_order=buf)
+        assert np.array_equal(np.sort(host(buf)[:T]), np.arange(T))
+        for name, a, b in zip(("means2d", "conics", "features", "opacities"), ref, got):
+            e = float((a - b).abs().max() / a.abs().max().clamp_min(1e-30))
+            assert e < 1e-6, name

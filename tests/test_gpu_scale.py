@@ -7,7 +7,8 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import assert_bits, cu, host, oracle_backward, oracle_forward, rel_err, say
+from gpu_util import (assert_bits, assert_features, cu, host, oracle_backward, oracle_forward,
+                      rel_err, say)
 from mlx3d_amd import scenes
 from mlx3d_amd.splatting import GaussianModel, render_gaussian_features
 from oracle import oracle as O
@@ -120,7 +121,7 @@ def test_config5_features_depth():
     say(f"  D={ids.shape[0]}")
     np.testing.assert_array_equal(host(out["sorted_ids"]), ids)
     np.testing.assert_array_equal(host(out["n_contrib"]), r["n_contrib"])
-    assert_bits(host(out["features"]), r["image"], "features")
+    assert_features(host(out["features"]), r["image"], "features")
     assert_bits(host(out["depth"]), r["depth"], "depth")
     target = scene.target(cam)
     (out["features"] - cu(target)).abs().mean().backward()
