@@ -355,8 +355,8 @@ int gsx_pack_conic_opacity(int64_t n, const float* conics,
  * (H,W) = 1 - final_T (rasterize.py:443) or NULL.
  * tile_order: NULL (tiles in launch order), or 2 * T int32 words (T =
  * ceil(W/16) ceil(H/16)) that the call fills: words [0, T) the order the
- * workgroups take the tiles in (within each XCD's contiguous share of the
- * tiles, longest tile lists first), words [T, 2T) each tile's largest
+ * workgroups take the tiles in (longest tile lists first), words [T, 2T)
+ * each tile's largest
  * n_contrib, which gsx_raster_bwd orders its tiles by.  The outputs do not
  * depend on the order; the buffer has no counterpart in the reference
  * (whose Metal dispatch has no such control). */
@@ -381,7 +381,7 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
  * background (rasterize.py:401).  tile_order: NULL (launch order), or the
  * buffer gsx_raster_fwd filled for this frame: words [0, T) are rewritten
  * with the tiles ordered by the contributor bounds in [T, 2T) (largest
- * first within each XCD's share).  Any contents give a valid order; the
+ * first).  Any contents give a valid order; the
  * gradients do not depend on it beyond float atomic ordering. */
 int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,

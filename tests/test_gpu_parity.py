@@ -774,16 +774,17 @@ def test_raster_backward_gradient_record(C):
 
 @pytest.mark.parametrize("C", [3, 32])
 def test_tile_order(C):
-    """The rasterizers' tile order (heaviest tiles first within each XCD's
-    share): the forward's outputs are bit-identical with and without it;
-    the buffer holds a permutation of the tiles in XCD-contiguous ranges and
-    each tile's largest n_contrib; the backward gives the same gradients in
+    """The rasterizers' tile order (heaviest tiles first): the forward's
+    outputs are bit-identical with and without it; the buffer holds a
+    permutation of the tiles, ordered by non-increasing list length (in
+    quarter-octave buckets), and each tile's largest n_contrib; the
+    backward gives the same gradients in
     launch order, in the forward's order and with the bound words replaced
     by arbitrary values (float atomics: to 1e-6 of the largest entry)."""
     from mlx3d_amd.splatting.rasterize import (raster_backward, raster_forward,
                                                tile_order_buffer)
 
-    W, H = 328, 200  # 21 x 13 tiles: 273 = 8 * 34 + 1, one XCD range longer
+    W, H = 328, 200  # 21 x 13 tiles, the last column and row partial
     cam, means, quats, scales, opac, _ = random_scene(57 + C, n=5000, width=W, height=H)
     rng = np.random.default_rng(C)
     feats = cu(rng.standard_normal((means.shape[0], C)).astype(np.float32))
@@ -803,12 +804,12 @@ def test_tile_order(C):
     o = host(order)
     perm, work = o[:T], o[T:]
     assert np.array_equal(np.sort(perm), np.arange(T))
-    q, r = divmod(T, 8)
-    lo = 0
-    for x in range(8):  # each XCD's range holds its own tiles
-        hi = lo + q + (1 if x < r else 0)
-        assert np.array_equal(np.sort(perm[lo:hi]), np.arange(lo, hi))
-        lo = hi
+    rg = host(ranges)
+    v = (rg[:, 1] - rg[:, 0]).astype(np.int64) + 1
+    e = np.array([int(x).bit_length() - 1 for x in v])
+    frac = np.where(e >= 2, v >> np.maximum(e - 2, 0), v << np.maximum(2 - e, 0)) & 3
+    bucket = np.minimum(4 * e + frac, 63)  # the exponent and two bits below the leading one
+    assert (np.diff(bucket[perm]) <= 0).all()
     nc = np.zeros((13 * 16, 21 * 16), np.int32)
     nc[:H, :W] = host(base[2])
     want = nc.reshape(13, 16, 21, 16).max(axis=(1, 3)).ravel()
