@@ -356,10 +356,9 @@ int gsx_pack_conic_opacity(int64_t n, const float* conics,
  * tile_order: NULL (tiles in launch order), or 2 * T int32 words (T =
  * ceil(W/16) ceil(H/16)) that the call fills: words [0, T) the order the
  * workgroups take the tiles in (longest tile lists first), words [T, 2T)
- * each tile's largest
- * n_contrib, which gsx_raster_bwd orders its tiles by.  The outputs do not
- * depend on the order; the buffer has no counterpart in the reference
- * (whose Metal dispatch has no such control). */
+ * each tile's largest n_contrib, which gsx_raster_bwd orders its tiles by.
+ * The outputs do not depend on the order.  The buffer has no counterpart
+ * in the reference (whose Metal dispatch has no such control). */
 int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
                    const float* depths, const int32_t* sorted_ids,

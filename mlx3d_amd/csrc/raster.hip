@@ -334,11 +334,13 @@ __device__ __forceinline__ void tile_span(int2 rg, int64_t n_ids, int& start, in
 // tiles differ in work by 2-3x (crowded regions of the frame).  Without
 // `order` the tiles go by xcd_remap (each XCD a contiguous range of
 // tiles); with it, workgroup b takes tile order[b], the frame's tiles by
-// decreasing work estimate (longest-processing-time-first list
-// scheduling), so no long tile starts late.  Measured at 1080p and 720p,
-// ordering the whole frame beat ordering within each XCD's contiguous
-// range: the lost L2 sharing between neighbouring tiles costs less than
-// the better balance gains.
+// decreasing work (longest-processing-time-first list scheduling), so no
+// long tile starts late.  The forward orders by list length (which
+// predicts its work loosely, yet gains more than the sort costs), the
+// backward by the exact work the forward recorded.  Measured at 1080p and
+// 720p, ordering the whole frame
+// beat ordering within each XCD's contiguous range: the lost L2 sharing
+// between neighbouring tiles costs less than the better balance gains.
 __device__ __forceinline__ int tile_at(const int* order, uint32_t b, uint32_t nb) {
     return order ? order[b] : (int)xcd_remap(b, nb);
 }
@@ -1747,16 +1749,23 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
     }
 }
 
-// The tile order for tile_at: one workgroup, a counting sort of the
-// tiles by a work estimate in descending quarter-octave buckets
-// (4 log2(w + 1), 64 buckets): the list length (ranges) for the forward,
-// the contributor bound the forward stored (work) for the backward.  Order
-// within a bucket follows LDS atomics and is not fixed; results do not
-// depend on it (each tile's outputs are its own, and the backward's
-// cross-tile sums are float atomics in any case).  Every tile is placed
-// exactly once, whatever the estimates hold.
+// The tile order for tile_at: one workgroup, a counting sort of the tiles
+// by a work estimate in descending quarter-octave buckets (4 log2(w + 1),
+// 64 buckets): the list length (ranges) for the forward, the contributor
+// bound the forward stored (work, the entries the backward replays) for the
+// backward.  Each bucket has 16
+// counters, lane l of every wave using counter l % 16, so at most four
+// lanes of one LDS atomic hit the same word (same-address lanes serialize).
+// A first pass counts, a scan over (bucket, counter) gives each counter its
+// start, a second pass places through the same counters.  The order within
+// a bucket follows the atomics and is not fixed; results do not depend on
+// it (each tile's outputs are its own, and the backward's cross-tile sums
+// are float atomics in any case).  Every tile is placed exactly once,
+// whatever the estimates hold.
 constexpr int kOrderThreads = 1024;
+constexpr int kOrderItems = 16;   // tiles per thread and round, read at once
 constexpr int kOrderBuckets = 64;
+constexpr int kOrderCopies = kOrderThreads / kOrderBuckets;  // 16: one scan entry per thread
 
 __device__ __forceinline__ int order_key(int w) {
     const uint32_t v = (uint32_t)max(w, 0) + 1u;
@@ -1765,33 +1774,61 @@ __device__ __forceinline__ int order_key(int w) {
     return kOrderBuckets - 1 - min(kOrderBuckets - 1, 4 * e + frac);  // heaviest first
 }
 
+template <bool WORK>
 __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __restrict__ ranges,
                                                               const int* __restrict__ work,
                                                               int64_t n_ids, int tiles,
                                                               int* __restrict__ order) {
-    __shared__ int s_cnt[kOrderBuckets];
-    const int tid = threadIdx.x;
-    auto key = [&](int t) {
-        int w;
-        if (work) {
-            w = work[t];
-        } else {
-            int start, num;
-            tile_span(ranges[t], n_ids, start, num);
-            w = num;
+    __shared__ uint32_t s_cnt[kOrderBuckets][kOrderCopies];  // bucket-major: the scan order
+    __shared__ uint32_t s_w[kOrderThreads / kWave];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int copy = lane % kOrderCopies;
+    // the round's keys: every load issued before the first is used (the
+    // index is clamped, not branched on, so none waits for another)
+    auto keys_of = [&](int t0, int (&keys)[kOrderItems]) {
+        int w[kOrderItems];
+#pragma unroll
+        for (int k = 0; k < kOrderItems; ++k) {
+            const int t = min(t0 + tid + k * kOrderThreads, tiles - 1);
+            if constexpr (WORK) {
+                w[k] = work[t];
+            } else {
+                int start, num;
+                tile_span(ranges[t], n_ids, start, num);
+                w[k] = num;
+            }
         }
-        return order_key(w);
+#pragma unroll
+        for (int k = 0; k < kOrderItems; ++k)
+            keys[k] = t0 + tid + k * kOrderThreads < tiles ? order_key(w[k]) : -1;
     };
-    if (tid < kOrderBuckets) s_cnt[tid] = 0;
+    auto pass = [&](int t0, bool place) {
+        int keys[kOrderItems];
+        keys_of(t0, keys);
+#pragma unroll
+        for (int k = 0; k < kOrderItems; ++k) {
+            if (keys[k] < 0) continue;
+            if (place)
+                order[atomicAdd(&s_cnt[keys[k]][copy], 1u)] = t0 + tid + k * kOrderThreads;
+            else
+                atomicAdd(&s_cnt[keys[k]][copy], 1u);
+        }
+    };
+    s_cnt[tid / kOrderCopies][tid % kOrderCopies] = 0u;
     __syncthreads();
-    for (int t = tid; t < tiles; t += kOrderThreads) atomicAdd(&s_cnt[key(t)], 1);
+    for (int t0 = 0; t0 < tiles; t0 += kOrderItems * kOrderThreads) pass(t0, false);
     __syncthreads();
-    if (tid < kWave) {
-        const int v = s_cnt[tid];
-        s_cnt[tid] = (int)wave_incl_scan((uint32_t)v) - v;
+    {
+        const uint32_t c = s_cnt[tid / kOrderCopies][tid % kOrderCopies];
+        const uint32_t incl = wave_incl_scan(c);
+        if (lane == kWave - 1) s_w[wave] = incl;
+        __syncthreads();
+        uint32_t base = incl - c;
+        for (int w = 0; w < wave; ++w) base += s_w[w];
+        s_cnt[tid / kOrderCopies][tid % kOrderCopies] = base;
     }
     __syncthreads();
-    for (int t = tid; t < tiles; t += kOrderThreads) order[atomicAdd(&s_cnt[key(t)], 1)] = t;
+    for (int t0 = 0; t0 < tiles; t0 += kOrderItems * kOrderThreads) pass(t0, true);
 }
 
 // Clears the four gradient outputs in one launch (a fill kernel rather than
@@ -1887,7 +1924,7 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d, const float* coni
     const dim3 grid((unsigned)(tiles_x * tiles_y));
     const int tiles = tiles_x * tiles_y;
     if (tile_order) {
-        hipLaunchKernelGGL(k_tile_order, dim3(1), dim3(kOrderThreads), 0, st,
+        hipLaunchKernelGGL(k_tile_order<false>, dim3(1), dim3(kOrderThreads), 0, st,
                            (const int2*)tile_ranges, (const int*)nullptr, num_ids, tiles,
                            tile_order);
         GSX_LAUNCH_CHECK();
@@ -1959,7 +1996,7 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
     const dim3 grid((unsigned)(tiles_x * tiles_y));
     const int tiles = tiles_x * tiles_y;
     if (tile_order) {
-        hipLaunchKernelGGL(k_tile_order, dim3(1), dim3(kOrderThreads), 0, st,
+        hipLaunchKernelGGL(k_tile_order<true>, dim3(1), dim3(kOrderThreads), 0, st,
                            (const int2*)nullptr, (const int*)(tile_order + tiles), num_ids, tiles,
                            tile_order);
         GSX_LAUNCH_CHECK();

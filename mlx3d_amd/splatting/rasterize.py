@@ -26,8 +26,9 @@ def _empty(shape, dev, dtype=torch.float32):
 
 def tile_order_buffer(width, height, dev):
     """The rasterizers' tile-order buffer for a width x height image: 2 T
-    int32 words (T tiles), filled by the forward and reused by the
-    backward of the same frame."""
+    int32 words (T tiles): each call writes its tile order (heaviest tiles
+    first), the forward also the per-tile contributor bounds that the
+    backward of the same frame orders by."""
     tiles = ((width + TILE_SIZE - 1) // TILE_SIZE) * ((height + TILE_SIZE - 1) // TILE_SIZE)
     return _empty((2 * tiles,), dev, torch.int32)
 
@@ -36,9 +37,9 @@ def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, backgrou
                    height, depths=None, tile_order=None):
     """gsx_raster_fwd on prepared float32 contiguous tensors (no autograd):
     (out, final_T, n_contrib, depth_map or None, alpha = 1 - final_T).
-    With ``tile_order`` (tile_order_buffer) the workgroups take the heaviest
-    tiles first and the buffer keeps the per-tile bounds for
-    raster_backward."""
+    With ``tile_order`` (tile_order_buffer) the workgroups take the tiles
+    with the longest lists first, and the kernel records each tile's
+    contributor bound there, which raster_backward orders its tiles by."""
     dev = means2d.device
     n, C = feats.shape
     out = _empty((height, width, C), dev)

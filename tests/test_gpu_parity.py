@@ -775,12 +775,12 @@ def test_raster_backward_gradient_record(C):
 @pytest.mark.parametrize("C", [3, 32])
 def test_tile_order(C):
     """The rasterizers' tile order (heaviest tiles first): the forward's
-    outputs are bit-identical with and without it; the buffer holds a
-    permutation of the tiles, ordered by non-increasing list length (in
-    quarter-octave buckets), and each tile's largest n_contrib; the
-    backward gives the same gradients in
-    launch order, in the forward's order and with the bound words replaced
-    by arbitrary values (float atomics: to 1e-6 of the largest entry)."""
+    outputs are bit-identical with and without the order buffer; it orders
+    the tiles by non-increasing list length (quarter-octave buckets) and
+    records each tile's largest n_contrib; the backward orders by those
+    bounds and gives the same gradients as in launch order, also when the
+    bound words hold arbitrary values (float atomics: to 1e-6 of the
+    largest entry)."""
     from mlx3d_amd.splatting.rasterize import (raster_backward, raster_forward,
                                                tile_order_buffer)
 
@@ -801,19 +801,21 @@ def test_tile_order(C):
                           (ordered[0], ordered[1], ordered[2], ordered[4])):
         assert torch.equal(a, b), name
     T = 21 * 13
-    o = host(order)
-    perm, work = o[:T], o[T:]
+
+    def buckets(w):  # the kernel's key: the exponent and two bits below the leading one
+        v = np.maximum(w.astype(np.int64), 0) + 1
+        e = np.array([int(x).bit_length() - 1 for x in v])
+        frac = np.where(e >= 2, v >> np.maximum(e - 2, 0), v << np.maximum(2 - e, 0)) & 3
+        return np.minimum(4 * e + frac, 63)
+
+    perm = host(order)[:T]
     assert np.array_equal(np.sort(perm), np.arange(T))
     rg = host(ranges)
-    v = (rg[:, 1] - rg[:, 0]).astype(np.int64) + 1
-    e = np.array([int(x).bit_length() - 1 for x in v])
-    frac = np.where(e >= 2, v >> np.maximum(e - 2, 0), v << np.maximum(2 - e, 0)) & 3
-    bucket = np.minimum(4 * e + frac, 63)  # the exponent and two bits below the leading one
-    assert (np.diff(bucket[perm]) <= 0).all()
+    assert (np.diff(buckets(rg[:, 1] - rg[:, 0])[perm]) <= 0).all()
     nc = np.zeros((13 * 16, 21 * 16), np.int32)
     nc[:H, :W] = host(base[2])
     want = nc.reshape(13, 16, 21, 16).max(axis=(1, 3)).ravel()
-    np.testing.assert_array_equal(work, want)
+    np.testing.assert_array_equal(host(order)[T:], want)
     g_out = cu(rng.normal(size=(H, W, C)).astype(np.float32))
     g_T = cu(rng.normal(size=(H, W)).astype(np.float32))
     ref = raster_backward(m2, co, feats, ids, ranges, bg, W, H, base[1], base[2], g_out, g_T)
@@ -822,7 +824,10 @@ def test_tile_order(C):
     for buf in (order, scrambled):
         got = raster_backward(m2, co, feats, ids, ranges, bg, W, H, base[1], base[2], g_out,
                               g_T, tile_order=buf)
-        assert np.array_equal(np.sort(host(buf)[:T]), np.arange(T))
+        o = host(buf)
+        perm, work = o[:T], o[T:]
+        assert np.array_equal(np.sort(perm), np.arange(T))
+        assert (np.diff(buckets(work)[perm]) <= 0).all()
         for name, a, b in zip(("means2d", "conics", "features", "opacities"), ref, got):
             e = float((a - b).abs().max() / a.abs().max().clamp_min(1e-30))
             assert e < 1e-6, name
