@@ -39,23 +39,31 @@ constexpr int kThreads = kTilePixels;
 constexpr int kWaves = kThreads / kWave;  // 4 quadrant waves
 
 // The compositing loops' exp (stands in for metal::exp at rasterize.py:80,
-// 171): k = rint(x log2 e), r = x - k ln2 with ln2 rounded to float32 (one
-// multiply-add), e^r by the degree-5 polynomial 1 + r q(r) whose
-// coefficients were fitted for least maximum relative error on |r| <= ln2/2,
-// then exact scaling by 2^k.  At most 2.02 ulp from exp for x in [-6, 0]
-// (every power that can pass the alpha test), 4.75 ulp on [-87, 0], and
-// exp(0) = 1.  splat_exp_core is the sequence without range handling
-// (callers that know x lies in [-86, 88]); splat_exp_sel adds it with
-// selects: 0 below -86, +inf above 88, NaN unchanged.
+// 171), nine instructions: k = the integer nearest x log2 e from one fused
+// multiply-add with the rounding constant 1.5 * 2^23 (j lies in
+// [2^23, 2^24), where floats are spaced 1 apart, so j - 1.5 * 2^23 = k
+// exactly); r = x - k ln2 with ln2 rounded to float32 (one multiply-add);
+// e^r by the degree-5 polynomial p = 1 + r q(r) whose coefficients were
+// fitted for least maximum relative error on |r| <= ln2/2; then 2^k p by
+// one shift-and-add of j's encoding into p's (its low nine bits are
+// k mod 2^9, so the shift adds k to the exponent field modulo 2^32; for x in
+// [-86, 88] the result is normal and the add is the exact scaling).  At
+// most 2.02 ulp from exp for x in [-6, 0] (every power that can pass the
+// alpha test), 4.75 ulp on [-87, 0], and exp(0) = 1.  splat_exp_core is the
+// sequence without range handling (callers that know x lies in [-86, 88]);
+// splat_exp_sel adds it with selects: 0 below -86, +inf above 88, NaN
+// unchanged.
 __device__ __forceinline__ float splat_exp_core(float x) {
-    const float k = rintf(x * 1.44269504088896341f);
+    const float j = fmaf(x, 1.44269504088896341f, 12582912.0f);
+    const float k = j - 12582912.0f;
     const float r = fmaf(k, -0.693147182464599609375f, x);
     float q = 8.290260538610955e-03f;
     q = fmaf(q, r, 4.189814578274823e-02f);
     q = fmaf(q, r, 1.6667638172664237e-01f);
     q = fmaf(q, r, 4.9999147944277167e-01f);
     q = fmaf(q, r, 9.999997063356061e-01f);
-    return ldexpf(fmaf(q, r, 1.0f), (int)k);
+    const float p = fmaf(q, r, 1.0f);
+    return __uint_as_float(__float_as_uint(p) + (__float_as_uint(j) << 23));
 }
 
 __device__ __forceinline__ float splat_exp_sel(float x) {
@@ -362,14 +370,14 @@ __device__ __forceinline__ void store_tile_work(int* work, int tile, int last, i
 
 // A quadrant wave's walk list: the staged Gaussians whose bit is set in the
 // quadrant's NW mask words (loader wave lw, lane l <-> staged index
-// 64 lw + l), compacted in LDS as 16-bit record byte offsets (16 x index)
+// 64 lw + l), compacted in LDS as 32-bit record byte offsets (16 x index)
 // so the walk is a counted loop over uniform offsets.  Built by the wave
 // itself after the workgroup barrier that publishes the masks; ascending
 // index order (REV: descending).  list[cnt] and list[cnt + 1] are set to
 // pad, a valid record offset, for the walks' look-ahead.  Returns cnt
 // (uniform).
 template <int NW, bool REV>
-__device__ __forceinline__ int build_list(const uint64_t* words, uint16_t* list, int lane,
+__device__ __forceinline__ int build_list(const uint64_t* words, uint32_t* list, int lane,
                                           int pad) {
     int total = 0;
     const uint64_t below = (1ull << lane) - 1ull;
@@ -379,10 +387,10 @@ __device__ __forceinline__ int build_list(const uint64_t* words, uint16_t* list,
         const int lw = REV ? NW - 1 - k : k;
         const uint64_t m = uniform64(words[lw]);
         if ((m >> lane) & 1ull)
-            list[total + __popcll(m & (REV ? above : below))] = (uint16_t)((lw * kWave + lane) * 16);
+            list[total + __popcll(m & (REV ? above : below))] = (uint32_t)((lw * kWave + lane) * 16);
         total += __popcll(m);
     }
-    if (lane < 2) list[total + lane] = (uint16_t)pad;
+    if (lane < 2) list[total + lane] = (uint32_t)pad;
     return total;
 }
 
@@ -469,7 +477,7 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
 // last_off gets the offset of each pixel's last composited Gaussian of this
 // batch.
 template <int CH, bool DEPTH, bool PLAIN>
-__device__ __forceinline__ void fwd_walk(const uint16_t* list, int cnt, const float4* s_r0,
+__device__ __forceinline__ void fwd_walk(const uint32_t* list, int cnt, const float4* s_r0,
                                          const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
                                          float pxf, float pyf, float& T, float* acc, float& dacc,
                                          int& last_off, uint64_t& alive) {
@@ -511,7 +519,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     __shared__ float4 s_r1[kThreads + 1];     // -a/2, -b, -c/2 (conic), depth
     __shared__ float4 s_f[kThreads + 1][F4];  // channels, zero padded
     __shared__ uint64_t s_mask[kWaves][kWaves];  // [quadrant][loader wave]
-    __shared__ uint16_t s_list[kWaves][kThreads + 4];  // walk lists (+ look-ahead room)
+    __shared__ uint32_t s_list[kWaves][kThreads + 4];  // walk lists (+ look-ahead room)
     // one word per wave, written before a barrier and read by every thread
     // after it (a 16-byte read): some pixel of the wave still composites /
     // every Gaussian the wave staged is plain.  Each batch's reads come
@@ -520,7 +528,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = tile_at(order, blockIdx.x, gridDim.x);
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int px = px0 + (wave & 1) * 8 + (lane & 7);
@@ -776,7 +784,7 @@ __device__ __forceinline__ void bwd_reduce2(float (&w)[4 * ((CH + 7) / 2)], int 
 // index), records and list entries read ahead as in fwd_walk, one
 // reduction per contributing Gaussian.
 template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_walk1(const uint16_t* list, int cnt, int lim,
+__device__ __forceinline__ void bwd_walk1(const uint32_t* list, int cnt, int lim,
                                           const float4* s_r0, const float4* s_r1,
                                           const float4 (*s_f)[(CH + 3) / 4],
                                           float4 (*part)[((CH + 6) + 3) / 4], float pxf,
@@ -816,7 +824,7 @@ __device__ __forceinline__ void bwd_walk1(const uint16_t* list, int cnt, int lim
 // the next a's before b is.  An odd count pairs the last Gaussian with the
 // padding record, which contributes nothing and owns a slot of its own.
 template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_walk2(const uint16_t* list, int cnt, int lim,
+__device__ __forceinline__ void bwd_walk2(const uint32_t* list, int cnt, int lim,
                                           const float4* s_r0, const float4* s_r1,
                                           const float4 (*s_f)[(CH + 3) / 4],
                                           float4 (*part)[((CH + 6) + 3) / 4], float pxf,
@@ -849,7 +857,7 @@ __device__ __forceinline__ void bwd_walk2(const uint16_t* list, int cnt, int lim
 // channel blocks reduce one Gaussian at a time, where padding is a small
 // share and two value sets would not fit the register budget.
 template <int CH, bool PLAIN>
-__device__ __forceinline__ void bwd_walk(const uint16_t* list, int cnt, int lim,
+__device__ __forceinline__ void bwd_walk(const uint32_t* list, int cnt, int lim,
                                          const float4* s_r0, const float4* s_r1,
                                          const float4 (*s_f)[(CH + 3) / 4],
                                          float4 (*part)[((CH + 6) + 3) / 4], float pxf, float pyf,
@@ -892,14 +900,14 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     __shared__ float4 s_f[BB + 1][F4];
     __shared__ float4 s_part[kWaves][BB + 1][NV4];  // per-wave gradient sums per Gaussian
     __shared__ uint64_t s_mask[kWaves][NLW];
-    __shared__ uint16_t s_list[kWaves][BB + 4];  // walk lists (+ look-ahead room)
+    __shared__ uint32_t s_list[kWaves][BB + 4];  // walk lists (+ look-ahead room)
     __shared__ int s_last[kWaves];
     // per wave: every Gaussian it staged is plain (written before the staging
     // barrier, read by all after it; the loop-top barrier orders batches)
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = tile_at(order, blockIdx.x, gridDim.x);
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int px = px0 + (wave & 1) * 8 + (lane & 7);
@@ -1159,7 +1167,7 @@ __device__ __forceinline__ bool bwd_geo(const float4& r0, const float4& r1, floa
 // g(pixel 16 pb + l % 16, channel 4 ks + l / 16); gB[ks][cb] = g(pixel
 // 4 ks + l / 16, channel 16 cb + l % 16).
 template <bool PLAIN>
-__device__ __forceinline__ void bwd_walk_mx(const uint16_t* list, int cnt, int lim,
+__device__ __forceinline__ void bwd_walk_mx(const uint32_t* list, int cnt, int lim,
                                             const float4* s_r0, const float4* s_r1,
                                             const float* s_feat, int pad_slot,
                                             float (*sum)[40], float (*tile)[kMxPad],
@@ -1280,12 +1288,12 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     __shared__ float s_sum[BB + 1][SP];               // summed over the waves (LDS atomics)
     __shared__ float s_tile[kWaves][kMxGroup][kMxPad];  // per-wave cg / aT tiles
     __shared__ uint64_t s_mask[kWaves][NLW];
-    __shared__ uint16_t s_list[kWaves][BB + 4];
+    __shared__ uint32_t s_list[kWaves][BB + 4];
     __shared__ int s_last[kWaves];
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = tile_at(order, blockIdx.x, gridDim.x);
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;
@@ -1501,7 +1509,7 @@ __device__ __forceinline__ float fwd_weight(const float4& r0, const float4& r1, 
 // past the entries replayed (the group's end, or the wave's early stop)
 // are zero.  FINITE: every staged feature is finite and below 1e30.
 template <bool DEPTH, bool PLAIN, bool FINITE>
-__device__ __forceinline__ void fwd_walk_mx(const uint16_t* list, int cnt, const float4* s_r0,
+__device__ __forceinline__ void fwd_walk_mx(const uint32_t* list, int cnt, const float4* s_r0,
                                             const float4* s_r1, const float* s_feat,
                                             int pad_slot, float (*tile)[kMfTile], float pxf,
                                             float pyf, int lane, float& T, float& dacc,
@@ -1595,13 +1603,13 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
     __shared__ __align__(16) float s_feat[(BB + 1) * kMfFeat];
     __shared__ float s_tile[kWaves][kMxGroup][kMfTile];
     __shared__ uint64_t s_mask[kWaves][NLW];
-    __shared__ uint16_t s_list[kWaves][BB + 4];
+    __shared__ uint32_t s_list[kWaves][BB + 4];
     __shared__ __align__(16) uint32_t s_alive[kWaves];
     __shared__ __align__(16) uint32_t s_plain[kWaves];
     __shared__ __align__(16) uint32_t s_finite[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = tile_at(order, blockIdx.x, gridDim.x);
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;

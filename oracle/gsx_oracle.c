@@ -56,26 +56,40 @@ void orc_expf_array(int64_t n, const float* x, float* y) {
 
 /* ------------------------------------------------------- splat exp/power --
  * The compositing loops' exp (metal::exp at rasterize.py:80,171,274): k =
- * rint(x log2 e), r = x - k ln2 with ln2 rounded to float32 (one fused
- * multiply-add), e^r by the degree-5 polynomial 1 + r q(r) whose
+ * the integer nearest x log2 e, from one fused multiply-add with the
+ * rounding constant 1.5 * 2^23 (j = x log2 e + 1.5 * 2^23 rounded to float
+ * lies in [2^23, 2^24), where the float spacing is 1, so j - 1.5 * 2^23 = k
+ * exactly); r = x - k ln2 with ln2 rounded to float32 (one fused
+ * multiply-add); e^r by the degree-5 polynomial p = 1 + r q(r) whose
  * coefficients were fitted for least maximum relative error on
- * |r| <= ln2/2, then exact scaling by 2^k.  Same range handling as orc_expf.
- * At most 2.02 ulp from exp on [-6, 0] (every power that can pass the alpha
- * test), 2.19 on [-12, 0] and 4.75 on [-87, 0] (exhaustive float32 sweeps),
- * exp(0) = 1.
+ * |r| <= ln2/2; then 2^k p by adding k to p's exponent field (the low nine
+ * bits of j's encoding are k mod 2^9, so j's bits shifted left by 23 add k
+ * to the field modulo 2^32; for x in [-86, 88] the result is a normal
+ * float, so the add is the exact scaling).  Same range handling as
+ * orc_expf.  At most 2.02 ulp from exp on [-6, 0] (every power that can
+ * pass the alpha test), 2.19 on [-12, 0] and 4.75 on [-87, 0] (float32
+ * sweeps), exp(0) = 1.
  */
 float orc_splat_expf(float x) {
     if (x != x) return x;
     if (x < -86.0f) return 0.0f;
     if (x > 88.0f) return INFINITY;
-    const float k = rintf(x * 1.44269504088896341f);
+    const float j = fmaf(x, 1.44269504088896341f, 12582912.0f);
+    const float k = j - 12582912.0f;
     const float r = fmaf(k, -0.693147182464599609375f, x);
     float q = 8.290260538610955e-03f;
     q = fmaf(q, r, 4.189814578274823e-02f);
     q = fmaf(q, r, 1.6667638172664237e-01f);
     q = fmaf(q, r, 4.9999147944277167e-01f);
     q = fmaf(q, r, 9.999997063356061e-01f);
-    return ldexpf(fmaf(q, r, 1.0f), (int)k);
+    const float p = fmaf(q, r, 1.0f);
+    uint32_t pb, jb;
+    memcpy(&pb, &p, 4);
+    memcpy(&jb, &j, 4);
+    pb += jb << 23;
+    float y;
+    memcpy(&y, &pb, 4);
+    return y;
 }
 
 void orc_splat_expf_array(int64_t n, const float* x, float* y) {
