@@ -1100,6 +1100,16 @@ constexpr int kMxGroup = 16;   // Gaussians per matrix-core group
 constexpr int kMxPad = 68;     // row stride (floats) of a wave's tile: 4 r + q bank spread
 constexpr int kMxFPad = 65;    // row stride (floats) of the channel-major features
 constexpr int kMxGeo = 6;      // geometric values per Gaussian
+constexpr int kMxGeoStride = 8;   // slot stride (floats) of the geometric sums
+
+// Where a Gaussian's feature gradients go: base + stride * id + offset + c
+// for channels c < nc of the block.
+struct MxFeatOut {
+    float* base;
+    int64_t stride;
+    int offset;
+    int nc;
+};
 
 typedef float mx_floatx4 __attribute__((ext_vector_type(4)));
 
@@ -1170,7 +1180,8 @@ template <bool PLAIN>
 __device__ __forceinline__ void bwd_walk_mx(const uint32_t* list, int cnt, int lim,
                                             const float4* s_r0, const float4* s_r1,
                                             const float* s_feat, int pad_slot,
-                                            float (*sum)[40], float (*tile)[kMxPad],
+                                            float (*sum)[kMxGeoStride], const MxFeatOut& fo,
+                                            float (*tile)[kMxPad],
                                             const float (&gA)[4][8], const float (&gB)[16][2],
                                             float pxf, float pyf, int lane, MxPixel& px) {
 #pragma unroll 1
@@ -1252,14 +1263,19 @@ __device__ __forceinline__ void bwd_walk_mx(const uint32_t* list, int cnt, int l
             acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, gB[ks][1], acc1, 0, 0, 0);
         }
         // lane l holds the sums of entries 4 (l / 16) + i, channels l % 16
-        // and 16 + l % 16
+        // and 16 + l % 16: added straight into the Gaussians' feature
+        // gradients (one instruction covers four Gaussians' 16 consecutive
+        // channels; zero sums are skipped)
+        const uint4 gl = *reinterpret_cast<const uint4*>(list + i0 + 4 * (lane >> 4));
+        const uint32_t gi[4] = {gl.x, gl.y, gl.z, gl.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int g = 4 * (lane >> 4) + i;
             if (g < ng) {
-                float* dst = sum[list[i0 + g] >> 4] + kMxGeo + row;
-                if (acc0[i] != 0.0f) atomicAdd(dst, acc0[i]);
-                if (acc1[i] != 0.0f) atomicAdd(dst + 16, acc1[i]);
+                const int gid = __float_as_int(s_r1[gi[i] >> 4].w);
+                float* dst = fo.base + (int64_t)fo.stride * gid + fo.offset + row;
+                if (acc0[i] != 0.0f && row < fo.nc) atomicAdd(dst, acc0[i]);
+                if (acc1[i] != 0.0f && row + 16 < fo.nc) atomicAdd(dst + 16, acc1[i]);
             }
         }
         // the next group's product A overwrites the tile
@@ -1278,17 +1294,17 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     float* __restrict__ g_opac, int gstride, const int* __restrict__ order) {
     static_assert(CH == 32, "the matrix-core backward covers 32-channel blocks");
     constexpr int F4 = CH / 4;
-    constexpr int NV = CH + kMxGeo;  // slot values
-    constexpr int SP = CH + 8;       // slot stride (floats)
     constexpr int BB = 64;
     constexpr int NLW = BB / kWave;
     __shared__ float4 s_r0[BB + 1];
     __shared__ float4 s_r1[BB + 1];  // -a/2, -b, -c/2 (conic), Gaussian id (int bits)
     __shared__ float s_fT[CH * kMxFPad];              // features, channel-major (column BB: zeros)
-    __shared__ float s_sum[BB + 1][SP];               // summed over the waves (LDS atomics)
+    __shared__ float s_sum[BB + 1][kMxGeoStride];     // geometric sums over the waves
     __shared__ float s_tile[kWaves][kMxGroup][kMxPad];  // per-wave cg / aT tiles
     __shared__ uint64_t s_mask[kWaves][NLW];
-    __shared__ uint32_t s_list[kWaves][BB + 4];
+    // walk lists; a group's 16 entries are read as four 16-byte pieces, so
+    // each row has room for a whole group past the last entry
+    __shared__ __align__(16) uint32_t s_list[kWaves][BB + kMxGroup];
     __shared__ int s_last[kWaves];
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
@@ -1349,12 +1365,14 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     for (int q = 0; q < kWaves; ++q) quad_last[q] = s_last[q];
     const int max_last = max(max(quad_last[0], quad_last[1]), max(quad_last[2], quad_last[3]));
     const int n_batches = (max_last + BB - 1) / BB;
+    const MxFeatOut fout = gstride > 0 ? MxFeatOut{g_xy, gstride, kMxGeo + c0, nc}
+                                       : MxFeatOut{g_feat, C, c0, nc};
 
     for (int b = n_batches - 1; b >= 0; --b) {
         __syncthreads();
         uint32_t qm = 0;
         bool plain = true;
-        for (int k = tid; k < (BB + 1) * SP; k += kThreads) (&s_sum[0][0])[k] = 0.0f;
+        for (int k = tid; k < (BB + 1) * kMxGeoStride; k += kThreads) (&s_sum[0][0])[k] = 0.0f;
         if (tid < BB) {
             const int k = b * BB + tid;
             float4 r1 = make_float4(0.0f, 0.0f, 0.0f, __int_as_float(-1));
@@ -1414,10 +1432,10 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
         const int lim = 16 * max(0, min(st.last - b * BB, BB));
         const float* sfeat = s_fT;
         if (batch_plain)
-            bwd_walk_mx<true>(s_list[wave], cnt, lim, s_r0, s_r1, sfeat, BB, s_sum, s_tile[wave],
-                              gA, gB, pxf, pyf, lane, st);
+            bwd_walk_mx<true>(s_list[wave], cnt, lim, s_r0, s_r1, sfeat, BB, s_sum, fout,
+                              s_tile[wave], gA, gB, pxf, pyf, lane, st);
         else
-            bwd_walk_mx<false>(s_list[wave], cnt, lim, s_r0, s_r1, sfeat, BB, s_sum,
+            bwd_walk_mx<false>(s_list[wave], cnt, lim, s_r0, s_r1, sfeat, BB, s_sum, fout,
                                s_tile[wave], gA, gB, pxf, pyf, lane, st);
         __syncthreads();
         // one thread per Gaussian turns the sums into the reference's
@@ -1434,16 +1452,15 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
             e[4] = -0.5f * o * e[4];
         }
         __syncthreads();
-        for (int item = tid; item < BB * NV; item += kThreads) {
-            const int j = item / NV, k = item - j * NV;
+        for (int item = tid; item < BB * kMxGeo; item += kThreads) {
+            const int j = item / kMxGeo, k = item - j * kMxGeo;
             const int g = __float_as_int(s_r1[j].w);
             const float v = s_sum[j][k];
-            if (g < 0 || v == 0.0f || (k >= 6 && k - 6 >= nc)) continue;
-            float* dst = gstride > 0 ? g_xy + (int64_t)gstride * g + (k < 6 ? k : c0 + k)
+            if (g < 0 || v == 0.0f) continue;
+            float* dst = gstride > 0 ? g_xy + (int64_t)gstride * g + k
                        : k < 2 ? g_xy + 2 * (int64_t)g + k
                        : k < 5 ? g_conic + 3 * (int64_t)g + (k - 2)
-                       : k == 5 ? g_opac + g
-                                : g_feat + (int64_t)g * C + c0 + (k - 6);
+                                : g_opac + g;
             atomicAdd(dst, v);
         }
     }
