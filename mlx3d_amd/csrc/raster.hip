@@ -1090,12 +1090,16 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
 // A[row = l % 16][k = l / 16], B[k = l / 16][col = l % 16]; the result's lane
 // l holds rows 4 (l / 16) + i, column l % 16.  The features are staged
 // channel-major (row stride 65) and the tile with row stride 68, so the
-// operand reads and result writes of a wave hit distinct LDS banks.  Sums
-// from the four quadrant waves meet in one LDS slot per Gaussian through LDS
-// float atomics.  The
-// contractions add in a different order than the VALU path, so gradients
-// agree with it to float32 rounding, not bitwise; no decision depends on
-// them.
+// operand reads and result writes of a wave hit distinct LDS banks.  The
+// geometric sums of the four quadrant waves meet in one LDS slot per
+// Gaussian through LDS float atomics (three per pair); product B's channel
+// sums go straight to the gradient record with global float atomics, one
+// instruction covering four Gaussians' 16 consecutive channels -- LDS
+// float atomics for them (eight per group and lane) cost more than the
+// whole global flush, and per-wave LDS slots instead (34 KB) cut the
+// workgroups per CU from three to two, slower still.  The contractions add
+// in a different order than the VALU path, so gradients agree with it to
+// float32 rounding, not bitwise; no decision depends on them.
 constexpr int kMxGroup = 16;   // Gaussians per matrix-core group
 constexpr int kMxPad = 68;     // row stride (floats) of a wave's tile: 4 r + q bank spread
 constexpr int kMxFPad = 65;    // row stride (floats) of the channel-major features
