@@ -286,7 +286,7 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts,
  * behind this call also reports the checks of earlier calls' tile phases.
  *
  * gsx_bin_depth_async: the stable depth sort (tiles.py:67-72) of the same
- * n depth keys in the same depth_ws, in passes of 10, 10, 10 and 2 bits
+ * n depth keys in the same depth_ws, in passes of 9, 9, 9 and 5 bits
  * (the last is skipped on the device when all keys share its digit, as
  * the renderer's near-plane-relative keys do).  With host_status != NULL
  * (pinned host memory of 8 uint64 words, e.g. the first half of
@@ -353,12 +353,13 @@ int gsx_pack_conic_opacity(int64_t n, const float* conics,
  * bounds; background (C) or NULL (zeros); out (H,W,C); final_T (H,W);
  * n_contrib (H,W) int32; depth_out (H,W) when depths != NULL; alpha_out
  * (H,W) = 1 - final_T (rasterize.py:443) or NULL.
- * tile_order: NULL (tiles in launch order), or 2 * T int32 words (T =
- * ceil(W/16) ceil(H/16)) that the call fills: words [0, T) the order the
- * workgroups take the tiles in (longest tile lists first), words [T, 2T)
- * each tile's largest n_contrib, which gsx_raster_bwd orders its tiles by.
- * The outputs do not depend on the order.  The buffer has no counterpart
- * in the reference (whose Metal dispatch has no such control). */
+ * tile_order: NULL (tiles in launch order), or gsx_tile_order_words(W, H)
+ * int32 words that the call fills: words [0, T) (T = ceil(W/16)
+ * ceil(H/16)) each tile's largest n_contrib, which gsx_raster_bwd orders
+ * its tiles by; words [T, 2T) the order the workgroups take the tiles in
+ * (each XCD's contiguous band of tiles, longest lists first).  The outputs
+ * do not depend on the order.  The buffer has no counterpart in the
+ * reference (whose Metal dispatch has no such control). */
 int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
                    const float* depths, const int32_t* sorted_ids,
@@ -378,10 +379,15 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
  * Gaussian's float atomics from one tile then land in one or two cache
  * lines instead of one per array.  No gradient is produced for the
  * background (rasterize.py:401).  tile_order: NULL (launch order), or the
- * buffer gsx_raster_fwd filled for this frame: words [0, T) are rewritten
- * with the tiles ordered by the contributor bounds in [T, 2T) (largest
- * first).  Any contents give a valid order; the
- * gradients do not depend on it beyond float atomic ordering. */
+ * buffer gsx_raster_fwd filled for this frame: from the contributor bounds
+ * in words [0, T) the call writes its order to the words after them (the
+ * tiles cut into 8 contiguous bands of equal work, one per XCD, each band
+ * heaviest first).  Any contents give a valid order; the gradients do not
+ * depend on it beyond float atomic ordering. */
+/* Size in int32 words of the rasterizers' tile_order buffer for a
+ * width x height image: T + 16 ceil(T / 8) (0 for an empty image). */
+int64_t gsx_tile_order_words(int32_t width, int32_t height);
+
 int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
                    const int32_t* sorted_ids, int64_t num_ids,

@@ -145,6 +145,7 @@ SIGNATURES = {
     "gsx_pack_conic_opacity": (ctypes.c_int, [_I64, _P, _P, _P, _P]),
     "gsx_raster_fwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32,
                                       _P, _P, _P, _P, _P, _P, _P]),
+    "gsx_tile_order_words": (_I64, [_I32, _I32]),
     "gsx_raster_bwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32, _P,
                                       _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P]),
     "gsx_photometric_workspace_bytes": (_I64, [_I32, _I32, _I32]),

@@ -337,20 +337,25 @@ __device__ __forceinline__ void tile_span(int2 rg, int64_t n_ids, int& start, in
     num = (int)(s1 - s0);
 }
 
-// Tile processing order.  A workgroup slot that frees takes the next
-// workgroup in launch order, so the kernel ends when the last slot drains;
-// tiles differ in work by 2-3x (crowded regions of the frame).  Without
-// `order` the tiles go by xcd_remap (each XCD a contiguous range of
-// tiles); with it, workgroup b takes tile order[b], the frame's tiles by
-// decreasing work (longest-processing-time-first list scheduling), so no
-// long tile starts late.  The forward orders by list length (which
-// predicts its work loosely, yet gains more than the sort costs), the
-// backward by the exact work the forward recorded.  Measured at 1080p and
-// 720p, ordering the whole frame
-// beat ordering within each XCD's contiguous range: the lost L2 sharing
-// between neighbouring tiles costs less than the better balance gains.
-__device__ __forceinline__ int tile_at(const int* order, uint32_t b, uint32_t nb) {
-    return order ? order[b] : (int)xcd_remap(b, nb);
+// Tile processing order.  Workgroups go round-robin over the 8 XCDs and a
+// workgroup slot that frees takes the next workgroup of its XCD, so the
+// kernel ends when the last XCD drains its share; tiles differ in work by
+// 2-3x (crowded regions of the frame).  xcd_remap gives each XCD a
+// contiguous band of tiles (neighbours share its L2: the same Gaussians'
+// records).  With an order (k_tile_order) the bands stay contiguous, each
+// XCD takes its band's heaviest tiles first (longest-processing-time-first
+// list scheduling), and for the backward, whose per-tile work the forward
+// recorded exactly, the bands are cut to equal work rather than equal tile
+// counts, with up to twice the mean tiles per band: the backward then
+// launches 16 ceil(T / 8) workgroups, those past a band's end exit at once.
+// Ordering the whole frame instead, heaviest first regardless of bands,
+// balanced as well but doubled the rasterizers' HBM traffic (1.05 GB per
+// C3 backward instead of 0.47: neighbouring tiles on different XCDs).
+// by_block: order is indexed by workgroup (the backward's layout), else by
+// xcd_remap position; -1 = no tile.
+__device__ __forceinline__ int tile_at(const int* order, uint32_t b, uint32_t nb, bool by_block) {
+    if (!order) return (int)xcd_remap(b, nb);
+    return order[by_block ? b : xcd_remap(b, nb)];
 }
 
 // The workgroup's largest contributor count (n_contrib) into work[tile]:
@@ -528,7 +533,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x, false));
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int px = px0 + (wave & 1) * 8 + (lane & 7);
@@ -907,7 +912,8 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x, true));
+    if (tile < 0) return;  // past the end of this XCD's band
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int px = px0 + (wave & 1) * 8 + (lane & 7);
@@ -1313,7 +1319,8 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     __shared__ __align__(16) uint32_t s_plain[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x, true));
+    if (tile < 0) return;  // past the end of this XCD's band
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;
@@ -1630,7 +1637,7 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
     __shared__ __align__(16) uint32_t s_finite[kWaves];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x));
+    const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x, false));
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;
@@ -1778,86 +1785,170 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
     }
 }
 
-// The tile order for tile_at: one workgroup, a counting sort of the tiles
-// by a work estimate in descending quarter-octave buckets (4 log2(w + 1),
-// 64 buckets): the list length (ranges) for the forward, the contributor
-// bound the forward stored (work, the entries the backward replays) for the
-// backward.  Each bucket has 16
-// counters, lane l of every wave using counter l % 16, so at most four
-// lanes of one LDS atomic hit the same word (same-address lanes serialize).
-// A first pass counts, a scan over (bucket, counter) gives each counter its
-// start, a second pass places through the same counters.  The order within
-// a bucket follows the atomics and is not fixed; results do not depend on
-// it (each tile's outputs are its own, and the backward's cross-tile sums
-// are float atomics in any case).  Every tile is placed exactly once,
-// whatever the estimates hold.
+// The tile order for tile_at: one workgroup per band (XCD) x.  Each tile
+// gets a band and a work estimate; band x's workgroup lists its tiles by
+// descending quarter-octave bucket of the estimate (4 log2(w + 1), 64
+// buckets) with a counting sort.  Forward (BWD false): the estimate is the
+// list length (ranges), the bands are xcd_remap's (equal tile counts), and
+// tile t lands at order[band start + its rank in the band].  Backward: the
+// estimate is the contributor bound the forward stored (work, the entries
+// the backward replays); up to 16384 tiles the bands are cut at equal
+// shares of sum(min(w, 2^16) + 16) (the 16 stands for a tile's fixed cost;
+// every workgroup computes the same cuts from the whole frame), each
+// capped at cap = 2 ceil(T / 8) tiles, and tile t lands at
+// order[8 rank + band], so workgroup b = 8 i + x (XCD x) takes band x's
+// i-th tile; band x's other entries of the 8 cap hold -1.  Each bucket has
+// 16 LDS counters, lane l using counter l % 16, so at most four lanes of
+// one LDS atomic hit the same word (same-address lanes serialize).  The
+// order within a bucket follows the atomics and is not fixed; results do
+// not depend on it (each tile's outputs are its own, and the backward's
+// cross-tile sums are float atomics in any case).  Every tile is placed
+// exactly once, whatever the estimates hold.
 constexpr int kOrderThreads = 1024;
-constexpr int kOrderItems = 16;   // tiles per thread and round, read at once
+constexpr int kOrderItems = 16;   // tiles per thread of the band cut, read at once
 constexpr int kOrderBuckets = 64;
-constexpr int kOrderCopies = kOrderThreads / kOrderBuckets;  // 16: one scan entry per thread
+constexpr int kOrderBands = 8;
+constexpr int kOrderCopies = kOrderThreads / kOrderBuckets;      // 16: one counter per thread
+constexpr int kOrderBalanced = kOrderThreads * kOrderItems;     // most tiles cut by work
 
-__device__ __forceinline__ int order_key(int w) {
+__device__ __forceinline__ int order_bucket(int w) {
     const uint32_t v = (uint32_t)max(w, 0) + 1u;
     const int e = 31 - __clz(v);
     const int frac = e >= 2 ? (int)((v >> (e - 2)) & 3u) : (int)((v << (2 - e)) & 3u);
     return kOrderBuckets - 1 - min(kOrderBuckets - 1, 4 * e + frac);  // heaviest first
 }
 
-template <bool WORK>
+// Words of a tile-order buffer for T tiles: T bounds, then 16 ceil(T / 8)
+// order entries.
+__host__ __device__ inline int64_t tile_order_words(int64_t tiles) {
+    return tiles + 16 * ((tiles + kOrderBands - 1) / kOrderBands);
+}
+
+template <bool BWD>
 __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __restrict__ ranges,
                                                               const int* __restrict__ work,
                                                               int64_t n_ids, int tiles,
                                                               int* __restrict__ order) {
-    __shared__ uint32_t s_cnt[kOrderBuckets][kOrderCopies];  // bucket-major: the scan order
+    __shared__ uint32_t s_cnt[kOrderBuckets * kOrderCopies];  // bucket-major: the scan order
     __shared__ uint32_t s_w[kOrderThreads / kWave];
+    __shared__ int s_start[kOrderBands + 1];  // first tile of each band
+    const int band = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int copy = lane % kOrderCopies;
-    // the round's keys: every load issued before the first is used (the
-    // index is clamped, not branched on, so none waits for another)
-    auto keys_of = [&](int t0, int (&keys)[kOrderItems]) {
+    const int cap = 2 * ((tiles + kOrderBands - 1) / kOrderBands);
+    auto estimate = [&](int t) {
+        if constexpr (BWD) {
+            return work[t];
+        } else {
+            int start, num;
+            tile_span(ranges[t], n_ids, start, num);
+            return num;
+        }
+    };
+    // equal-count bands (xcd_remap's ranges)
+    const int q = tiles / kOrderBands, r = tiles % kOrderBands;
+    if (tid <= kOrderBands)
+        s_start[tid] = tid < r ? tid * (q + 1) : r * (q + 1) + (tid - r) * q;
+    if (BWD)  // this band's unused entries say "no tile"
+        for (int i = tid; i < cap; i += kOrderThreads) order[kOrderBands * i + band] = -1;
+    s_cnt[tid] = 0u;
+    if (BWD && tiles <= kOrderBalanced) {
+        // bands of equal work: exclusive prefix of the weights over the
+        // tiles in raster order (thread tid: tiles 16 tid .. 16 tid + 15)
         int w[kOrderItems];
 #pragma unroll
+        for (int k = 0; k < kOrderItems; ++k)
+            w[k] = work[min(tid * kOrderItems + k, tiles - 1)];
+        uint32_t v[kOrderItems], sum = 0;
+#pragma unroll
         for (int k = 0; k < kOrderItems; ++k) {
-            const int t = min(t0 + tid + k * kOrderThreads, tiles - 1);
-            if constexpr (WORK) {
-                w[k] = work[t];
-            } else {
-                int start, num;
-                tile_span(ranges[t], n_ids, start, num);
-                w[k] = num;
+            const int t = tid * kOrderItems + k;
+            v[k] = t < tiles ? (uint32_t)min(max(w[k], 0), 1 << 16) + 16u : 0u;
+            sum += v[k];
+        }
+        const uint32_t incl = wave_incl_scan(sum);
+        if (lane == kWave - 1) s_w[wave] = incl;
+        __syncthreads();
+        if (tid > 0 && tid <= kOrderBands) s_start[tid] = tiles;
+        uint32_t pe = incl - sum, total = 0;
+#pragma unroll
+        for (int x = 0; x < kOrderThreads / kWave; ++x) {
+            if (x < wave) pe += s_w[x];
+            total += s_w[x];
+        }
+        __syncthreads();
+        // band of tile t: floor(8 pe / total); the first tile of each band
+        // (the smallest t with that band) recorded with atomicMin
+        int prev = -1;
+#pragma unroll
+        for (int k = 0; k < kOrderItems; ++k) {
+            const int t = tid * kOrderItems + k;
+            if (t < tiles) {
+                const int x = (int)min<uint64_t>(kOrderBands - 1,
+                                                 (uint64_t)pe * kOrderBands / max(total, 1u));
+                if (x != prev && x > 0) atomicMin(&s_start[x], t);
+                prev = x;
+            }
+            pe += v[k];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            // empty bands start where the next one does; then every band
+            // holds at most cap tiles (the cuts move forward, then back)
+            int b[kOrderBands + 1];
+#pragma unroll
+            for (int x = 1; x < kOrderBands; ++x) b[x] = s_start[x];
+            b[0] = 0;
+            b[kOrderBands] = tiles;
+#pragma unroll
+            for (int x = kOrderBands - 1; x > 0; --x) b[x] = min(b[x], b[x + 1]);
+#pragma unroll
+            for (int x = 1; x < kOrderBands; ++x) b[x] = min(b[x], b[x - 1] + cap);
+#pragma unroll
+            for (int x = kOrderBands - 1; x > 0; --x) b[x] = max(b[x], b[x + 1] - cap);
+#pragma unroll
+            for (int x = 0; x <= kOrderBands; ++x) s_start[x] = b[x];
+        }
+    }
+    __syncthreads();
+    const int lo = s_start[band], hi = s_start[band + 1];
+    const int copy = lane % kOrderCopies;
+    // this band's tiles, up to four per thread read at once (bands of more
+    // than 4096 tiles loop)
+    constexpr int kBandItems = 4;
+    auto pass = [&](bool place) {
+        for (int t0 = lo; t0 < hi; t0 += kBandItems * kOrderThreads) {
+            int w[kBandItems];
+#pragma unroll
+            for (int k = 0; k < kBandItems; ++k)
+                w[k] = estimate(min(t0 + tid + k * kOrderThreads, hi - 1));
+#pragma unroll
+            for (int k = 0; k < kBandItems; ++k) {
+                const int t = t0 + tid + k * kOrderThreads;
+                if (t >= hi) continue;
+                uint32_t* c = &s_cnt[order_bucket(w[k]) * kOrderCopies + copy];
+                if (!place) {
+                    atomicAdd(c, 1u);
+                } else {
+                    const int rank = (int)atomicAdd(c, 1u);
+                    order[BWD ? kOrderBands * rank + band : lo + rank] = t;
+                }
             }
         }
-#pragma unroll
-        for (int k = 0; k < kOrderItems; ++k)
-            keys[k] = t0 + tid + k * kOrderThreads < tiles ? order_key(w[k]) : -1;
     };
-    auto pass = [&](int t0, bool place) {
-        int keys[kOrderItems];
-        keys_of(t0, keys);
-#pragma unroll
-        for (int k = 0; k < kOrderItems; ++k) {
-            if (keys[k] < 0) continue;
-            if (place)
-                order[atomicAdd(&s_cnt[keys[k]][copy], 1u)] = t0 + tid + k * kOrderThreads;
-            else
-                atomicAdd(&s_cnt[keys[k]][copy], 1u);
-        }
-    };
-    s_cnt[tid / kOrderCopies][tid % kOrderCopies] = 0u;
-    __syncthreads();
-    for (int t0 = 0; t0 < tiles; t0 += kOrderItems * kOrderThreads) pass(t0, false);
+    if (lo < hi) pass(false);
     __syncthreads();
     {
-        const uint32_t c = s_cnt[tid / kOrderCopies][tid % kOrderCopies];
+        // exclusive scan of the counters (bucket-major), one per thread
+        const uint32_t c = s_cnt[tid];
         const uint32_t incl = wave_incl_scan(c);
         if (lane == kWave - 1) s_w[wave] = incl;
         __syncthreads();
         uint32_t base = incl - c;
-        for (int w = 0; w < wave; ++w) base += s_w[w];
-        s_cnt[tid / kOrderCopies][tid % kOrderCopies] = base;
+        for (int x = 0; x < wave; ++x) base += s_w[x];
+        s_cnt[tid] = base;
     }
     __syncthreads();
-    for (int t0 = 0; t0 < tiles; t0 += kOrderItems * kOrderThreads) pass(t0, true);
+    if (lo < hi) pass(true);
 }
 
 // Clears the four gradient outputs in one launch (a fill kernel rather than
@@ -1952,23 +2043,24 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d, const float* coni
     const int tiles_y = (height + kTile - 1) / kTile;
     const dim3 grid((unsigned)(tiles_x * tiles_y));
     const int tiles = tiles_x * tiles_y;
-    if (tile_order) {
-        hipLaunchKernelGGL(k_tile_order<false>, dim3(1), dim3(kOrderThreads), 0, st,
-                           (const int2*)tile_ranges, (const int*)nullptr, num_ids, tiles,
-                           tile_order);
+    // tile_order: [0, T) the bounds this call writes, [T, 2T) its order
+    int* const order = tile_order ? tile_order + tiles : nullptr;
+    if (order) {
+        hipLaunchKernelGGL(k_tile_order<false>, dim3(kOrderBands), dim3(kOrderThreads), 0, st,
+                           (const int2*)tile_ranges, (const int*)nullptr, num_ids, tiles, order);
         GSX_LAUNCH_CHECK();
     }
     for (int c0 = 0; c0 < C; c0 += kMaxChunk) {
         const int nc = (C - c0 < kMaxChunk) ? C - c0 : kMaxChunk;
         const bool depth = depths && c0 == 0;
-        int* work = (tile_order && c0 == 0) ? tile_order + tiles : nullptr;
+        int* work = (tile_order && c0 == 0) ? tile_order : nullptr;
         switch (pick_ch(nc)) {
 #define GSX_FWD_CASE(V)                                                                          \
     case V:                                                                                      \
         launch_fwd<V>(grid, st, depth, (const float2*)means2d, (const float4*)conic_opacity,     \
                       features, C, c0, nc, depths, sorted_ids, (const int2*)tile_ranges, n,      \
                       num_ids, background, width, height, tiles_x, out, final_T, n_contrib,      \
-                      depth_out, alpha_out, tile_order, work);                                   \
+                      depth_out, alpha_out, order, work);                                        \
         break;
             GSX_FWD_CASE(1)
             GSX_FWD_CASE(2)
@@ -1984,6 +2076,13 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d, const float* coni
         GSX_LAUNCH_CHECK();
     }
     return GSX_OK;
+}
+
+int64_t gsx_tile_order_words(int32_t width, int32_t height) {
+    if (width <= 0 || height <= 0) return 0;
+    const int64_t tiles =
+        (int64_t)((width + kTile - 1) / kTile) * (int64_t)((height + kTile - 1) / kTile);
+    return tile_order_words(tiles);
 }
 
 int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* conic_opacity,
@@ -2022,12 +2121,14 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
     }
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
-    const dim3 grid((unsigned)(tiles_x * tiles_y));
     const int tiles = tiles_x * tiles_y;
-    if (tile_order) {
-        hipLaunchKernelGGL(k_tile_order<true>, dim3(1), dim3(kOrderThreads), 0, st,
-                           (const int2*)nullptr, (const int*)(tile_order + tiles), num_ids, tiles,
-                           tile_order);
+    // tile_order: [0, T) the forward's bounds, [T, T + 16 ceil(T / 8)) this
+    // call's order, one entry per workgroup
+    int* const order = tile_order ? tile_order + tiles : nullptr;
+    const dim3 grid((unsigned)(order ? tile_order_words(tiles) - tiles : tiles));
+    if (order) {
+        hipLaunchKernelGGL(k_tile_order<true>, dim3(kOrderBands), dim3(kOrderThreads), 0, st,
+                           (const int2*)nullptr, (const int*)tile_order, num_ids, tiles, order);
         GSX_LAUNCH_CHECK();
     }
     for (int c0 = 0; c0 < C; c0 += kMaxChunk) {
@@ -2038,7 +2139,7 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
         launch_bwd<V>(grid, st, (const float2*)means2d, (const float4*)conic_opacity, features,  \
                       C, c0, nc, sorted_ids, (const int2*)tile_ranges, n, num_ids, background,   \
                       width, height, tiles_x, final_T, n_contrib, grad_out, grad_final_T,        \
-                      g_means2d, g_conics, g_features, g_opacities, grad_stride, tile_order);    \
+                      g_means2d, g_conics, g_features, g_opacities, grad_stride, order);         \
         break;
             GSX_BWD_CASE(1)
             GSX_BWD_CASE(2)

@@ -25,12 +25,12 @@ def _empty(shape, dev, dtype=torch.float32):
 
 
 def tile_order_buffer(width, height, dev):
-    """The rasterizers' tile-order buffer for a width x height image: 2 T
-    int32 words (T tiles): each call writes its tile order (heaviest tiles
-    first), the forward also the per-tile contributor bounds that the
-    backward of the same frame orders by."""
-    tiles = ((width + TILE_SIZE - 1) // TILE_SIZE) * ((height + TILE_SIZE - 1) // TILE_SIZE)
-    return _empty((2 * tiles,), dev, torch.int32)
+    """The rasterizers' tile-order buffer for a width x height image
+    (gsx_tile_order_words int32 words): each call writes its tile order
+    (heaviest tiles first within each XCD's band of tiles), the forward
+    also the per-tile contributor bounds that the backward of the same frame
+    orders by."""
+    return _empty((int(_lib.load().gsx_tile_order_words(width, height)),), dev, torch.int32)
 
 
 def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, background, width,

@@ -62,6 +62,10 @@ def test_workspace_query_is_host_only():
     assert L.gsx_bin_depth_workspace_bytes(-1) < 0
     assert L.gsx_bin_tile_workspace_bytes(-1, 100) < 0
     assert L.gsx_bin_tile_workspace_bytes(10, 0) < 0
+    # the rasterizers' tile-order buffer: T bounds + 16 ceil(T / 8) order entries
+    assert L.gsx_tile_order_words(328, 200) == 21 * 13 + 16 * 35
+    assert L.gsx_tile_order_words(16, 16) == 1 + 16
+    assert L.gsx_tile_order_words(0, 16) == 0
 
 
 def test_invalid_arguments_rejected_before_launch():

@@ -774,17 +774,20 @@ def test_raster_backward_gradient_record(C):
 
 @pytest.mark.parametrize("C", [3, 32])
 def test_tile_order(C):
-    """The rasterizers' tile order (heaviest tiles first): the forward's
-    outputs are bit-identical with and without the order buffer; it orders
-    the tiles by non-increasing list length (quarter-octave buckets) and
-    records each tile's largest n_contrib; the backward orders by those
-    bounds and gives the same gradients as in launch order, also when the
-    bound words hold arbitrary values (float atomics: to 1e-6 of the
-    largest entry)."""
+    """The rasterizers' tile order: the forward's outputs are bit-identical
+    with and without the order buffer; the forward records each tile's
+    largest n_contrib and orders each XCD's contiguous band of tiles
+    (xcd_remap's equal-count bands) by non-increasing list length
+    (quarter-octave buckets); the backward cuts the tiles into 8 contiguous
+    bands of equal work (at most 2 ceil(T / 8) tiles each), lists each band
+    heaviest first at entries 8 i + band, -1 past a band's end, and gives
+    the same gradients as in launch order, also when the bound words hold
+    arbitrary values (float atomics: to 1e-6 of the largest entry)."""
     from mlx3d_amd.splatting.rasterize import (raster_backward, raster_forward,
                                                tile_order_buffer)
 
     W, H = 328, 200  # 21 x 13 tiles, the last column and row partial
+    T = 21 * 13
     cam, means, quats, scales, opac, _ = random_scene(57 + C, n=5000, width=W, height=H)
     rng = np.random.default_rng(C)
     feats = cu(rng.standard_normal((means.shape[0], C)).astype(np.float32))
@@ -795,12 +798,13 @@ def test_tile_order(C):
     bg = torch.linspace(-0.1, 0.1, C, device=m2.device)
     base = raster_forward(m2, co, feats, ids, ranges, bg, W, H)
     order = tile_order_buffer(W, H, m2.device)
+    cap = 2 * ((T + 7) // 8)
+    assert order.numel() == T + 8 * cap
     ordered = raster_forward(m2, co, feats, ids, ranges, bg, W, H, tile_order=order)
     for name, a, b in zip(("out", "final_T", "n_contrib", "alpha"),
                           (base[0], base[1], base[2], base[4]),
                           (ordered[0], ordered[1], ordered[2], ordered[4])):
         assert torch.equal(a, b), name
-    T = 21 * 13
 
     def buckets(w):  # the kernel's key: the exponent and two bits below the leading one
         v = np.maximum(w.astype(np.int64), 0) + 1
@@ -808,26 +812,40 @@ def test_tile_order(C):
         frac = np.where(e >= 2, v >> np.maximum(e - 2, 0), v << np.maximum(2 - e, 0)) & 3
         return np.minimum(4 * e + frac, 63)
 
-    perm = host(order)[:T]
-    assert np.array_equal(np.sort(perm), np.arange(T))
-    rg = host(ranges)
-    assert (np.diff(buckets(rg[:, 1] - rg[:, 0])[perm]) <= 0).all()
+    o = host(order)
     nc = np.zeros((13 * 16, 21 * 16), np.int32)
     nc[:H, :W] = host(base[2])
-    want = nc.reshape(13, 16, 21, 16).max(axis=(1, 3)).ravel()
-    np.testing.assert_array_equal(host(order)[T:], want)
+    np.testing.assert_array_equal(o[:T], nc.reshape(13, 16, 21, 16).max(axis=(1, 3)).ravel())
+    fwd = o[T:2 * T]
+    rg = host(ranges)
+    lens = buckets(rg[:, 1] - rg[:, 0])
+    q, r = divmod(T, 8)
+    lo = 0
+    for x in range(8):  # each XCD's band holds its own tiles, longest lists first
+        hi = lo + q + (1 if x < r else 0)
+        assert np.array_equal(np.sort(fwd[lo:hi]), np.arange(lo, hi))
+        assert (np.diff(lens[fwd[lo:hi]]) <= 0).all()
+        lo = hi
     g_out = cu(rng.normal(size=(H, W, C)).astype(np.float32))
     g_T = cu(rng.normal(size=(H, W)).astype(np.float32))
     ref = raster_backward(m2, co, feats, ids, ranges, bg, W, H, base[1], base[2], g_out, g_T)
     scrambled = order.clone()
-    scrambled[T:] = cu(rng.integers(-2**31, 2**31 - 1, T, dtype=np.int64).astype(np.int32))
+    scrambled[:T] = cu(rng.integers(-2**31, 2**31 - 1, T, dtype=np.int64).astype(np.int32))
     for buf in (order, scrambled):
         got = raster_backward(m2, co, feats, ids, ranges, bg, W, H, base[1], base[2], g_out,
                               g_T, tile_order=buf)
         o = host(buf)
-        perm, work = o[:T], o[T:]
-        assert np.array_equal(np.sort(perm), np.arange(T))
-        assert (np.diff(buckets(work)[perm]) <= 0).all()
+        work, slots = o[:T], o[T:].reshape(cap, 8)  # slots[i, x]: band x's i-th tile
+        placed = slots[slots >= 0]
+        assert np.array_equal(np.sort(placed), np.arange(T))
+        start = 0
+        for x in range(8):
+            col = slots[:, x]
+            size = int((col >= 0).sum())
+            assert (col[:size] >= 0).all() and (col[size:] < 0).all()
+            assert np.array_equal(np.sort(col[:size]), np.arange(start, start + size))
+            assert (np.diff(buckets(work)[col[:size]]) <= 0).all()
+            start += size
         for name, a, b in zip(("means2d", "conics", "features", "opacities"), ref, got):
             e = float((a - b).abs().max() / a.abs().max().clamp_min(1e-30))
             assert e < 1e-6, name
