@@ -1797,18 +1797,14 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
 // every workgroup computes the same cuts from the whole frame), each
 // capped at cap = 2 ceil(T / 8) tiles, and tile t lands at
 // order[8 rank + band], so workgroup b = 8 i + x (XCD x) takes band x's
-// i-th tile; band x's other entries of the 8 cap hold -1.  Each bucket has
-// 16 LDS counters, lane l using counter l % 16, so at most four lanes of
-// one LDS atomic hit the same word (same-address lanes serialize).  The
-// order within a bucket follows the atomics and is not fixed; results do
-// not depend on it (each tile's outputs are its own, and the backward's
-// cross-tile sums are float atomics in any case).  Every tile is placed
-// exactly once, whatever the estimates hold.
+// i-th tile; band x's other entries of the 8 cap hold -1.  The sort is
+// stable (tiles of one bucket keep their raster order) and uses no LDS
+// atomics (same-address lanes of one would serialize).  Every tile is
+// placed exactly once, whatever the estimates hold.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderItems = 16;   // tiles per thread of the band cut, read at once
 constexpr int kOrderBuckets = 64;
 constexpr int kOrderBands = 8;
-constexpr int kOrderCopies = kOrderThreads / kOrderBuckets;      // 16: one counter per thread
 constexpr int kOrderBalanced = kOrderThreads * kOrderItems;     // most tiles cut by work
 
 __device__ __forceinline__ int order_bucket(int w) {
@@ -1829,7 +1825,8 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __rest
                                                               const int* __restrict__ work,
                                                               int64_t n_ids, int tiles,
                                                               int* __restrict__ order) {
-    __shared__ uint32_t s_cnt[kOrderBuckets * kOrderCopies];  // bucket-major: the scan order
+    constexpr int kBandItems = 4;
+    __shared__ uint32_t s_cnt[kOrderBuckets * kBandItems * (kOrderThreads / kWave)];
     __shared__ uint32_t s_w[kOrderThreads / kWave];
     __shared__ int s_start[kOrderBands + 1];  // first tile of each band
     const int band = blockIdx.x;
@@ -1850,7 +1847,8 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __rest
         s_start[tid] = tid < r ? tid * (q + 1) : r * (q + 1) + (tid - r) * q;
     if (BWD)  // this band's unused entries say "no tile"
         for (int i = tid; i < cap; i += kOrderThreads) order[kOrderBands * i + band] = -1;
-    s_cnt[tid] = 0u;
+    for (int k = tid; k < kOrderBuckets * kBandItems * (kOrderThreads / kWave); k += kOrderThreads)
+        s_cnt[k] = 0u;
     if (BWD && tiles <= kOrderBalanced) {
         // bands of equal work: exclusive prefix of the weights over the
         // tiles in raster order (thread tid: tiles 16 tid .. 16 tid + 15)
@@ -1911,44 +1909,75 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __rest
     }
     __syncthreads();
     const int lo = s_start[band], hi = s_start[band + 1];
-    const int copy = lane % kOrderCopies;
-    // this band's tiles, up to four per thread read at once (bands of more
-    // than 4096 tiles loop)
-    constexpr int kBandItems = 4;
-    auto pass = [&](bool place) {
-        for (int t0 = lo; t0 < hi; t0 += kBandItems * kOrderThreads) {
-            int w[kBandItems];
+    // this band's tiles: item k of thread tid is tile lo + k * 1024 + tid, so
+    // tile order is (k, wave, lane) order.  A stable counting sort: per
+    // item, the lanes of the wave holding the same bucket (ballots over its
+    // six bits) give the rank within the wave; counts per (bucket, item,
+    // wave), scanned in that order, give each wave's start.  Within a
+    // bucket the tiles keep their raster order, so neighbouring tiles of
+    // similar work run close together in time and share the XCD's L2.
+    // Bands of more than kBandItems * 1024 tiles are placed in rounds, each
+    // round sorted on its own (the rounds in raster order).
+    for (int r0 = lo; r0 < hi; r0 += kBandItems * kOrderThreads) {
+        int bk[kBandItems];
+        uint32_t rk[kBandItems];
 #pragma unroll
-            for (int k = 0; k < kBandItems; ++k)
-                w[k] = estimate(min(t0 + tid + k * kOrderThreads, hi - 1));
+        for (int k = 0; k < kBandItems; ++k) {
+            const int t = r0 + k * kOrderThreads + tid;
+            bk[k] = t < hi ? order_bucket(estimate(t)) : -1;
+        }
+#pragma unroll
+        for (int k = 0; k < kBandItems; ++k) {
+            const bool valid = bk[k] >= 0;
+            uint64_t m = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < 6; ++b) {
+                const bool bit = (bk[k] >> b) & 1;
+                const uint64_t ones = __ballot(bit);
+                m &= bit ? ones : ~ones;
+            }
+            rk[k] = (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+            // the lowest lane of each bucket group writes the group's count
+            if (valid && rk[k] == 0u)
+                s_cnt[(bk[k] * kBandItems + k) * (kOrderThreads / kWave) + wave] =
+                    (uint32_t)__popcll(m);
+        }
+        __syncthreads();
+        {
+            // exclusive scan of the (bucket, item, wave) counts, 4 per thread
+            uint32_t c[kBandItems], sum = 0;
 #pragma unroll
             for (int k = 0; k < kBandItems; ++k) {
-                const int t = t0 + tid + k * kOrderThreads;
-                if (t >= hi) continue;
-                uint32_t* c = &s_cnt[order_bucket(w[k]) * kOrderCopies + copy];
-                if (!place) {
-                    atomicAdd(c, 1u);
-                } else {
-                    const int rank = (int)atomicAdd(c, 1u);
-                    order[BWD ? kOrderBands * rank + band : lo + rank] = t;
-                }
+                c[k] = s_cnt[tid * kBandItems + k];
+                sum += c[k];
+            }
+            const uint32_t incl = wave_incl_scan(sum);
+            if (lane == kWave - 1) s_w[wave] = incl;
+            __syncthreads();
+            uint32_t base = incl - sum;
+            for (int x = 0; x < wave; ++x) base += s_w[x];
+#pragma unroll
+            for (int k = 0; k < kBandItems; ++k) {
+                s_cnt[tid * kBandItems + k] = base;
+                base += c[k];
             }
         }
-    };
-    if (lo < hi) pass(false);
-    __syncthreads();
-    {
-        // exclusive scan of the counters (bucket-major), one per thread
-        const uint32_t c = s_cnt[tid];
-        const uint32_t incl = wave_incl_scan(c);
-        if (lane == kWave - 1) s_w[wave] = incl;
         __syncthreads();
-        uint32_t base = incl - c;
-        for (int x = 0; x < wave; ++x) base += s_w[x];
-        s_cnt[tid] = base;
+#pragma unroll
+        for (int k = 0; k < kBandItems; ++k) {
+            if (bk[k] < 0) continue;
+            const int t = r0 + k * kOrderThreads + tid;
+            const int rank = (int)(s_cnt[(bk[k] * kBandItems + k) * (kOrderThreads / kWave) + wave] +
+                                   rk[k]) + (r0 - lo);
+            order[BWD ? kOrderBands * rank + band : lo + rank] = t;
+        }
+        __syncthreads();
+        // counters back to zero for the next round
+        for (int k = tid; k < kOrderBuckets * kBandItems * (kOrderThreads / kWave);
+             k += kOrderThreads)
+            s_cnt[k] = 0u;
+        __syncthreads();
     }
-    __syncthreads();
-    if (lo < hi) pass(true);
 }
 
 // Clears the four gradient outputs in one launch (a fill kernel rather than
