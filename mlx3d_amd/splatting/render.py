@@ -131,17 +131,28 @@ class _RenderFn(torch.autograd.Function):
         cfg = ctx.cfg
         dev = means.device
         n = means.shape[0]
-        # the rasterizer's gradients go into one record per Gaussian, which
-        # the screen statistics and the preprocess VJP read in place
+        # The rasterizer's gradients go into one record per Gaussian, which
+        # the screen statistics and the preprocess VJP read in place.  A
+        # feature render hands its feature gradient to autograd instead: a
+        # strided view of the record would be copied there, so it takes the
+        # four-array layout (a contiguous (N, C) feature gradient).
+        record = bool(cfg.sh_mode) or cfg.adam is not None
         with stage("raster_bwd"):
-            _, _, g_feat, _, grec, gstride = raster_backward(
+            r = raster_backward(
                 means2d, co, feats, ids, ranges, background, cfg.width, cfg.height, final_T,
-                n_contrib, g_image, t_cotangent(g_final_T, g_alpha), record=True,
+                n_contrib, g_image, t_cotangent(g_final_T, g_alpha), record=record,
                 tile_order=order)
+        if record:
+            _, _, g_feat, _, grec, gstride = r
+            g_in = (grec, None, None)  # g_means2d (the record), g_conics, g_opac_eff
+        else:
+            g_m2r, g_con, g_feat, g_op = r
+            gstride = 0
+            g_in = (g_m2r, g_con, g_op)
         if cfg.screen_stats is not None:
             acc, cnt = cfg.screen_stats
             _lib.check(_lib.load().gsx_accum_screen_grads(
-                n, _lib.ptr(grec), _lib.ptr(radii), cfg.width, cfg.height, _lib.ptr(acc),
+                n, _lib.ptr(g_in[0]), _lib.ptr(radii), cfg.width, cfg.height, _lib.ptr(acc),
                 _lib.ptr(cnt), gstride, _lib.stream_handle(dev)), "gsx_accum_screen_grads")
         c = lambda t: None if t is None else _lib.f32c(t)  # noqa: E731
         # The contiguous copies of the output cotangents (a stride-0 expand
@@ -159,7 +170,7 @@ class _RenderFn(torch.autograd.Function):
                 _lib.check(L.gsx_preprocess_bwd_adam(
                     cfg.cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
                     _lib.ptr(opacities), _lib.ptr(sh_a), _lib.ptr(sh_b), _lib.ptr(feats), cfg.K,
-                    cfg.degree, cfg.flags, cfg.blur, _lib.ptr(grec), None, None, None,
+                    cfg.degree, cfg.flags, cfg.blur, *[_lib.ptr(t) for t in g_in], None,
                     _lib.ptr(gm2_in), _lib.ptr(gdep_in),
                     _lib.ptr(gcomp_in), ctypes.cast(opt.records, ctypes.c_void_p),
                     opt.betas[0], opt.betas[1], opt.eps, gstride, _lib.stream_handle(dev)),
@@ -177,7 +188,7 @@ class _RenderFn(torch.autograd.Function):
             _lib.check(L.gsx_preprocess_bwd(
                 cfg.cam, n, _lib.ptr(means), _lib.ptr(quats), _lib.ptr(scales),
                 _lib.ptr(opacities), _lib.ptr(feats if cfg.sh_mode else None), cfg.K, cfg.degree,
-                cfg.flags, cfg.blur, _lib.ptr(grec), None, None, None, _lib.ptr(gm2_in),
+                cfg.flags, cfg.blur, *[_lib.ptr(t) for t in g_in], None, _lib.ptr(gm2_in),
                 _lib.ptr(gdep_in), _lib.ptr(gcomp_in), _lib.ptr(g_means),
                 _lib.ptr(g_quats), _lib.ptr(g_scales), _lib.ptr(g_opac), _lib.ptr(gs0), s0, gshr,
                 sr, gstride, _lib.stream_handle(dev)), "gsx_preprocess_bwd")
