@@ -196,6 +196,46 @@ __device__ __forceinline__ uint32_t look_back(const uint32_t* status, int64_t ch
     return prefix;
 }
 
+// The same for a single counter column (stride 1, column 0), walked by one
+// whole wave: each round reads the 64 statuses before the current position
+// at once (lane l: chunk c - l) and adds them up to the nearest inclusive
+// one, stopping before the first unpublished one (polled again, bounded as
+// above).  A lone thread's 8-status window needs ~n/8 round trips for the
+// n-th chunk when all chunks start together; the wave needs ~n/64.  Every
+// lane of the wave calls it; the result is uniform.
+__device__ __forceinline__ uint32_t wave_look_back(const uint32_t* status, int64_t chunk,
+                                                   uint32_t* err) {
+    const int lane = lane_id();
+    uint32_t prefix = 0;
+    uint32_t spins = 0;
+    int64_t c = chunk - 1;
+    while (c >= 0) {
+        const int64_t idx = c - lane;  // before chunk 0: an inclusive zero
+        const uint32_t s = idx >= 0 ? status_load(status + idx) : kFlagInc;
+        const uint32_t flag = s & ~kCountMask;
+        const uint64_t pend = __ballot(flag == 0u);
+        const uint64_t inc = __ballot(flag == kFlagInc);
+        const int first_pend = pend ? __ffsll((unsigned long long)pend) - 1 : kWave;
+        const int first_inc = inc ? __ffsll((unsigned long long)inc) - 1 : kWave;
+        const bool done = first_inc < first_pend;
+        const int take = done ? first_inc + 1 : first_pend;  // lanes [0, take)
+        uint32_t v = lane < take ? (s & kCountMask) : 0u;
+#pragma unroll
+        for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        prefix += v;
+        if (done) break;
+        c -= take;
+        if (take == 0) {
+            if (++spins > kSpinLimit) {
+                if (lane == 0) atomicOr(err, GSX_BIN_ERR_LOOKBACK);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    return prefix;
+}
+
 // min(n_host, *n_dev) when the live length is only known on the device.
 __device__ __forceinline__ int64_t live_count(int64_t n_host, const uint32_t* n_dev) {
     if (!n_dev) return n_host;
@@ -566,80 +606,18 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
 }
 
 // ------------------------------------------------------- fast tile phase --
-// Exclusive scan of the rectangles' heights (row entries) in depth order:
-// roffs[i] = row entries of depth-ordered Gaussians 0..i-1, roffs[n] = the
-// total; owner[b] for every row-emission workgroup b that has entries: the
-// depth-ordered Gaussian that owns entry b * kRowChunk.  (Rectangles of
-// Gaussians with a zero count are (0, 0): height 0.)  Workgroup 0, after its
-// chunk, also writes the row plan from the row histograms, the row of every
-// segment (segrow) and status[0] = D; the row emission, launched after this
-// kernel, is its first reader.
-__global__ __launch_bounds__(kScanThreads) void k_row_scan(
-    int64_t n, const uint2* __restrict__ rects, const uint32_t* __restrict__ gids,
-    uint32_t* __restrict__ sstatus, uint32_t* __restrict__ counter, uint32_t* __restrict__ roffs,
-    uint32_t* __restrict__ owner, int64_t n_owner, uint32_t* __restrict__ status,
-    uint32_t* __restrict__ clear, int64_t n_clear, const uint32_t* __restrict__ row_diff,
-    int tiles_y, RowPlan* __restrict__ plan, uint32_t* __restrict__ segrow, int64_t max_segs) {
-    __shared__ uint32_t s_w[kScanThreads / 64];
-    __shared__ uint32_t s_chunk, s_prefix;
+// The row plan (workgroup-wide; every thread calls it): row histograms from
+// their difference form (summed over the copies, then prefix-summed over
+// the rows), then the exclusive scans of the row entries, the duplicates
+// and the segments; the row of every segment; status[0] = D.
+__device__ __forceinline__ void row_plan(const uint32_t* __restrict__ row_diff, int tiles_y,
+                                         RowPlan* __restrict__ plan,
+                                         uint32_t* __restrict__ segrow, int64_t max_segs,
+                                         uint32_t* __restrict__ status, uint32_t* s_w) {
     const int tid = threadIdx.x;
-    uint32_t* err = status + 1;
-    // the row emission's look-back status words start at zero (those of
-    // the chunks the row entries -- status[4], final since the count
-    // phase -- will use)
-    const int64_t used = min<int64_t>(n_clear, ceil_div((int64_t)status[4], kRowChunk) *
-                                                   (2 * kMaxFastTiles));
-    for (int64_t k = (int64_t)blockIdx.x * kScanThreads + tid; k < used;
-         k += (int64_t)gridDim.x * kScanThreads)
-        clear[k] = 0u;
-    if (tid == 0) s_chunk = atomicAdd(counter, 1u);
-    __syncthreads();
-    const int64_t chunk = s_chunk;
-    const int64_t nchunks = ceil_div(n, kScanChunk);
-    if (chunk < nchunks) {  // always: the grid has exactly nchunks workgroups
-        const int64_t i0 = chunk * kScanChunk + (int64_t)tid * kScanItems;
-        uint32_t c[kScanItems];
-#pragma unroll
-        for (int j = 0; j < kScanItems; ++j) c[j] = i0 + j < n ? rects[gids[i0 + j]].y >> 16 : 0u;
-        uint32_t total;
-        uint32_t csum = 0;
-#pragma unroll
-        for (int j = 0; j < kScanItems; ++j) csum += c[j];
-        const uint32_t excl = block_excl_scan<kScanThreads>(csum, s_w, &total);
-        if (tid == 0) {
-            uint32_t prefix = 0;
-            uint32_t* st = sstatus + chunk;
-            if (chunk == 0) {
-                status_store(st, kFlagInc | (total & kCountMask));
-            } else {
-                status_store(st, kFlagAgg | (total & kCountMask));
-                prefix = look_back(sstatus, chunk, 1, 0, err);
-                status_store(st, kFlagInc | ((prefix + total) & kCountMask));
-            }
-            s_prefix = prefix;
-            if (chunk == nchunks - 1) roffs[n] = prefix + total;
-        }
-        __syncthreads();
-        uint32_t run = s_prefix + excl;
-#pragma unroll
-        for (int j = 0; j < kScanItems; ++j) {
-            if (i0 + j < n) {
-                roffs[i0 + j] = run;
-                for (int64_t b = ceil_div((int64_t)run, kRowChunk);
-                     b * kRowChunk < (int64_t)run + c[j] && b < n_owner; ++b)
-                    owner[b] = (uint32_t)(i0 + j);
-            }
-            run += c[j];
-        }
-    }
-    if (blockIdx.x != 0) return;
-    // row plan: row histograms from their difference form (summed over the
-    // copies, then prefix-summed over the rows), then the exclusive scans
-    // of the row entries, the duplicates and the segments
-    __syncthreads();
     uint32_t dc = 0, dw = 0;
-    if (tid < tiles_y) {
-#pragma unroll 4
+    if (tid < tiles_y) {  // the 32 loads issued together
+#pragma unroll
         for (int c = 0; c < kHistCopies; ++c) {
             dc += row_diff[c * 2 * kRowWords + tid];
             dw += row_diff[c * 2 * kRowWords + kRowWords + tid];
@@ -673,6 +651,81 @@ __global__ __launch_bounds__(kScanThreads) void k_row_scan(
         plan->dups = dup_tot;
         plan->segments = seg_tot;
         status[0] = dup_tot;
+    }
+}
+
+// Exclusive scan of the rectangles' heights (row entries) in depth order:
+// roffs[i] = row entries of depth-ordered Gaussians 0..i-1, roffs[n] = the
+// total; owner[b] for every row-emission workgroup b that has entries: the
+// depth-ordered Gaussian that owns entry b * kRowChunk.  (Rectangles of
+// Gaussians with a zero count are (0, 0): height 0.)  The grid has one
+// workgroup more than chunks: the last one writes the row plan from the row
+// histograms (the count phase's, so it starts at once, beside the scan),
+// the row of every segment (segrow) and status[0] = D; the row emission,
+// launched after this kernel, is its first reader.
+__global__ __launch_bounds__(kScanThreads) void k_row_scan(
+    int64_t n, const uint2* __restrict__ rects, const uint32_t* __restrict__ gids,
+    uint32_t* __restrict__ sstatus, uint32_t* __restrict__ counter, uint32_t* __restrict__ roffs,
+    uint32_t* __restrict__ owner, int64_t n_owner, uint32_t* __restrict__ status,
+    uint32_t* __restrict__ clear, int64_t n_clear, const uint32_t* __restrict__ row_diff,
+    int tiles_y, RowPlan* __restrict__ plan, uint32_t* __restrict__ segrow, int64_t max_segs) {
+    __shared__ uint32_t s_w[kScanThreads / 64];
+    __shared__ uint32_t s_chunk, s_prefix;
+    const int tid = threadIdx.x;
+    uint32_t* err = status + 1;
+    // the row emission's look-back status words start at zero (those of
+    // the chunks the row entries -- status[4], final since the count
+    // phase -- will use)
+    const int64_t used = min<int64_t>(n_clear, ceil_div((int64_t)status[4], kRowChunk) *
+                                                   (2 * kMaxFastTiles));
+    for (int64_t k = (int64_t)blockIdx.x * kScanThreads + tid; k < used;
+         k += (int64_t)gridDim.x * kScanThreads)
+        clear[k] = 0u;
+    const int64_t nchunks = ceil_div(n, kScanChunk);
+    if (blockIdx.x == gridDim.x - 1) {  // the row plan's workgroup
+        row_plan(row_diff, tiles_y, plan, segrow, max_segs, status, s_w);
+        return;
+    }
+    if (tid == 0) s_chunk = atomicAdd(counter, 1u);
+    __syncthreads();
+    const int64_t chunk = s_chunk;
+    if (chunk < nchunks) {  // always: the other workgroups are exactly nchunks
+        const int64_t i0 = chunk * kScanChunk + (int64_t)tid * kScanItems;
+        uint32_t c[kScanItems];
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) c[j] = i0 + j < n ? rects[gids[i0 + j]].y >> 16 : 0u;
+        uint32_t total;
+        uint32_t csum = 0;
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) csum += c[j];
+        const uint32_t excl = block_excl_scan<kScanThreads>(csum, s_w, &total);
+        if (tid < kWave) {  // wave 0 walks the look-back
+            uint32_t prefix = 0;
+            uint32_t* st = sstatus + chunk;
+            if (chunk == 0) {
+                if (tid == 0) status_store(st, kFlagInc | (total & kCountMask));
+            } else {
+                if (tid == 0) status_store(st, kFlagAgg | (total & kCountMask));
+                prefix = wave_look_back(sstatus, chunk, err);
+                if (tid == 0) status_store(st, kFlagInc | ((prefix + total) & kCountMask));
+            }
+            if (tid == 0) {
+                s_prefix = prefix;
+                if (chunk == nchunks - 1) roffs[n] = prefix + total;
+            }
+        }
+        __syncthreads();
+        uint32_t run = s_prefix + excl;
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) {
+            if (i0 + j < n) {
+                roffs[i0 + j] = run;
+                for (int64_t b = ceil_div((int64_t)run, kRowChunk);
+                     b * kRowChunk < (int64_t)run + c[j] && b < n_owner; ++b)
+                    owner[b] = (uint32_t)(i0 + j);
+            }
+            run += c[j];
+        }
     }
 }
 
@@ -1208,22 +1261,26 @@ __global__ __launch_bounds__(kScanThreads) void k_count_scan(
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) csum += c[j];
     const uint32_t excl = block_excl_scan<kScanThreads>(csum, s_w, &total);
-    if (tid == 0) {
+    if (tid < kWave) {  // wave 0 walks the look-back
         uint32_t prefix = 0;
         uint32_t* st = status + chunk;
-        if (total > kCountMask) atomicOr(err, GSX_BIN_ERR_OVERFLOW);
+        if (tid == 0 && total > kCountMask) atomicOr(err, GSX_BIN_ERR_OVERFLOW);
         if (chunk == 0) {
-            status_store(st, kFlagInc | (total & kCountMask));
+            if (tid == 0) status_store(st, kFlagInc | (total & kCountMask));
         } else {
-            status_store(st, kFlagAgg | (total & kCountMask));
-            prefix = look_back(status, chunk, 1, 0, err);
-            if ((uint64_t)prefix + total > kCountMask) atomicOr(err, GSX_BIN_ERR_OVERFLOW);
-            status_store(st, kFlagInc | ((prefix + total) & kCountMask));
+            if (tid == 0) status_store(st, kFlagAgg | (total & kCountMask));
+            prefix = wave_look_back(status, chunk, err);
+            if (tid == 0) {
+                if ((uint64_t)prefix + total > kCountMask) atomicOr(err, GSX_BIN_ERR_OVERFLOW);
+                status_store(st, kFlagInc | ((prefix + total) & kCountMask));
+            }
         }
-        s_prefix = prefix;
-        if (chunk == nchunks - 1) {
-            *d_total = prefix + total;
-            offs[n] = prefix + total;
+        if (tid == 0) {
+            s_prefix = prefix;
+            if (chunk == nchunks - 1) {
+                *d_total = prefix + total;
+                offs[n] = prefix + total;
+            }
         }
     }
     __syncthreads();
@@ -1717,7 +1774,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
         uint32_t* sc = at<uint32_t>(tile_ws, L.sc);
         uint32_t* segrow = at<uint32_t>(tile_ws, L.segrow);
         uint32_t* segk0 = at<uint32_t>(tile_ws, L.segk0);
-        hipLaunchKernelGGL(k_row_scan, dim3((unsigned)D.scan_chunks), dim3(kScanThreads), 0, st,
+        hipLaunchKernelGGL(k_row_scan, dim3((unsigned)D.scan_chunks + 1u), dim3(kScanThreads), 0, st,
                            n, (const uint2*)tile_rects, gids, sstatus, misc + 9, offs, owner,
                            L.row_chunks, bin_status, rstatus, L.rstatus_words,
                            (const uint32_t*)(misc + kMiscRowDiff), tiles_y, plan, segrow,
