@@ -3,7 +3,7 @@
 The render functions run the fused pipeline
 
     gsx_preprocess_fwd -> gsx_bin_count_async -> gsx_bin_depth_async
-        -> (read the duplicate count) -> gsx_bin_tiles_async -> gsx_raster_fwd
+        -> gsx_bin_tiles_async -> gsx_raster_fwd -> (read the duplicate count)
     gsx_raster_bwd -> gsx_preprocess_bwd            (backward)
 
 inside one ``torch.autograd.Function``: activations, projection, opacity
@@ -95,10 +95,15 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
                                   cfg.height, depths=depths if cfg.return_depth else None,
                                   tile_order=order)
 
-    # The rasterizer runs on the id buffer (its ranges never reach past D);
-    # only refine_tiles needs the final status for D, read after it has been
-    # enqueued.
+    # The rasterizer runs on the id buffer (its ranges never reach past D)
+    # and is enqueued before the host reads D.  If D exceeded the guessed
+    # capacity, the first run saw empty ranges and the binning has been
+    # enqueued again with the exact capacity: the rasterizer runs again
+    # behind it.  Only refine_tiles needs the final status for D, read after
+    # everything has been enqueued.
     image, final_T, n_contrib, depth_map, alpha = raster(job.ids)
+    if job.settle():
+        image, final_T, n_contrib, depth_map, alpha = raster(job.ids)
     ids, ranges = job.result()
     count("duplicates", ids.shape[0])
     return dict(means2d=means2d, depths=depths, radii=radii, compensation=comp, conic_opac=co,

@@ -4,15 +4,18 @@
 (D,) int32 in (tile, depth, index) order and ``tile_ranges`` (tiles, 2)
 int32 with (0, 0) for empty tiles.  The work runs in ``gsx_bin_prepare`` and
 ``gsx_bin_count_async`` / ``gsx_bin_depth_async`` / ``gsx_bin_tiles_async``
-(device radix passes and row placement).  The host reads the duplicate count
-(the sum of the tile counts, which the reference reads at tiles.py:68) while
-the depth sort still runs -- the depth sort's first kernel writes the status
-words into pinned host memory, which the host polls, so no copy or event
-sits between the kernels -- and sizes the tile phase's buffers exactly.
+(device radix passes and row placement).  The duplicate count D (the sum of
+the tile counts, which the reference reads at tiles.py:68) reaches the host
+without a copy or an event: the depth sort's first kernel writes the status
+words into pinned host memory, which the host polls.  A render enqueues the
+tile phase with a capacity guessed from the stream's latest counts and reads
+D after its rasterizer has been enqueued, so nothing waits between kernels;
+a count above the guess re-runs that frame's binning with the exact size.
 """
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import threading
 import time
@@ -29,6 +32,7 @@ _ERR_TOO_LARGE = -4    # gsx_status
 _ERR_DEVICE = -5
 _STATUS_WORDS = 8
 _WAIT_LIMIT_S = 120.0  # a device that never publishes is reported, not waited on forever
+_HINT_WINDOW = 16      # jobs whose duplicate counts size the next capacity guess
 
 __all__ = ["TILE_SIZE", "bin_gaussians"]
 
@@ -82,6 +86,18 @@ class _Workspace:
         self.status = torch.zeros((_STATUS_WORDS,), dtype=torch.int32, device=dev)
         self.host = _HostStatus()
         self.seq = 0
+        self.recent = collections.deque(maxlen=_HINT_WINDOW)  # D of the latest jobs
+
+    def capacity_hint(self) -> int | None:
+        """Duplicate capacity for a job whose D is not read yet: 1.25x the
+        largest D of the latest jobs on this stream (None before the first)."""
+        if not self.recent:
+            return None
+        d = max(self.recent)
+        return d + d // 4 + 1024
+
+    def note_dups(self, d: int) -> None:
+        self.recent.append(int(d))
 
     def next_seq(self) -> int:
         self.seq = (self.seq + 1) & 0xFFFFFFFF
@@ -130,36 +146,53 @@ def _raise_on_errors(ws: _Workspace, err: int, what: str) -> None:
 
 
 class BinJob:
-    """One binning on the device, sized exactly.
+    """One binning on the device.
 
-    gsx_bin_count_async sums the tile counts, the number of duplicates
+    gsx_bin_count_async sums the tile counts, the number of duplicates D
     emission writes; gsx_bin_depth_async's first kernel copies the status
-    words to the workspace's pinned host target, which the host polls while
-    the device sorts; ``ids`` gets exactly that capacity and
-    gsx_bin_tiles_async is enqueued.  ``ids`` and ``ranges`` are usable by
-    kernels enqueued behind the job right away.  Without refine_tiles D is
-    that count and no second host wait is needed.  The tile phase's last
-    kernel writes the final status words to the second target; ``check()``
-    waits for them and raises on a device-side error bit.  ``result()``
-    calls it when D is unknown (refine_tiles); the render backward calls it
-    after enqueuing its kernels, so a failed binning raises before the
-    gradients reach an optimizer.  A job nobody checks has its error bits
-    reported by the next job's count readback on the same stream.
+    words (D among them) to the workspace's pinned host target.  When the
+    stream has binned before (and without refine_tiles or ``final``), the
+    tile phase is enqueued at once with a guessed capacity (1.25x the
+    largest D of the latest jobs) and ``ids`` of that length: nothing waits
+    between the phases, and ``ids`` and ``ranges`` are usable by kernels
+    enqueued behind the job right away.  ``settle()`` then reads D from the
+    host target; if D exceeds the guess the tile phase has written an
+    in-bounds, empty binning (all ranges (0, 0)), and the whole binning is
+    enqueued again with the exact capacity -- ``settle()`` returns True and
+    the caller enqueues its consumers again.  Otherwise (the first job on a
+    stream, refine_tiles, ``final``) the host polls for D before it
+    enqueues the tile phase with exactly that capacity.  The tile phase's
+    last kernel writes the final status words to the second target;
+    ``check()`` waits for them and raises on a device-side error bit.
+    ``result()`` calls it when D is unknown (refine_tiles); the render
+    backward calls it after enqueuing its kernels, so a failed binning
+    raises before the gradients reach an optimizer.  A job nobody checks
+    has its error bits reported by the next job's count readback on the
+    same stream.
     """
 
     def __init__(self, counts, dkeys, rects, width: int, height: int, refine=None,
                  final: bool = False):
         """``refine`` = (means2d (N,2), conics (N,k>=3)) enables refine_tiles."""
         self.dev = counts.device
-        self.n = n = counts.shape[0]
+        self.n = counts.shape[0]
         self.width, self.height = int(width), int(height)
         self.tiles_x = (self.width + TILE_SIZE - 1) // TILE_SIZE
         self.tiles_y = (self.height + TILE_SIZE - 1) // TILE_SIZE
-        num_tiles = self.tiles_x * self.tiles_y
-        stream = _lib.stream_handle(self.dev)
-        ws = self.ws = _workspace_for(self.dev, stream)
+        self.stream = _lib.stream_handle(self.dev)
+        self.ws = _workspace_for(self.dev, self.stream)
+        self.ranges = torch.empty((self.tiles_x * self.tiles_y, 2), dtype=torch.int32,
+                                  device=self.dev)
+        self.inputs = (counts, dkeys, rects, refine)
+        self.exact = refine is not None or final  # D read before the tile phase, kept as is
+        self._enqueue(None if self.exact else self.ws.capacity_hint())
+
+    def _enqueue(self, guess: int | None) -> None:
+        """Count phase, depth sort and tile phase, with capacity `guess`, or
+        with the D read back in between when `guess` is None."""
+        counts, dkeys, rects, refine = self.inputs
+        n, ws, stream = self.n, self.ws, self.stream
         status = ws.status
-        self.ranges = torch.empty((num_tiles, 2), dtype=torch.int32, device=self.dev)
         L = _lib.load()
         dws = ws.get_depth(self.dev, n)
         _lib.check(L.gsx_bin_count_async(
@@ -168,14 +201,16 @@ class BinJob:
             "gsx_bin_count_async")
         self.seq = seq = ws.next_seq()
         self.cap = 0
+        self.guessed = False
         if n > 0:
             _lib.check(L.gsx_bin_depth_async(n, _lib.ptr(dkeys), _lib.ptr(dws), dws.numel(),
                                              _lib.ptr(status), ws.host.slot(0), seq, stream),
                        "gsx_bin_depth_async")
-            words, _ = ws.host.wait(0, seq)
-            _raise_on_errors(ws, int(words[1]), "gsx_bin_count_async")
-            self.cap = int(words[3])
-        tws = ws.get_tiles(self.dev, self.cap, num_tiles)
+            if guess is None:
+                self.cap = self._read_count()
+            else:
+                self.cap, self.guessed = int(guess), True
+        tws = ws.get_tiles(self.dev, self.cap, self.tiles_x * self.tiles_y)
         self.ids = torch.empty((self.cap,), dtype=torch.int32, device=self.dev)
         m2, co = refine if refine is not None else (None, None)
         _lib.check(L.gsx_bin_tiles_async(
@@ -185,9 +220,36 @@ class BinJob:
             _lib.ptr(self.ranges), _lib.ptr(status), ws.host.slot(1), seq, stream),
             "gsx_bin_tiles_async")
         self.ready = n > 0  # n == 0 launches nothing after the count phase
-        self.num_dups = None if (refine is not None or final) else self.cap
+        self.num_dups = None if (self.exact or self.guessed) else self.cap
         if n == 0:
             self.num_dups = 0
+
+    def _read_count(self) -> int:
+        """D of this job from the count phase's status words (first host
+        target), which raises on device-side error bits."""
+        words, tag = self.ws.host.wait(0, self.seq)
+        if tag != self.seq:  # a later job on the stream overwrote the counts
+            raise _lib.GsxError("gsx_bin_count_async: count read after a later binning")
+        _raise_on_errors(self.ws, int(words[1]), "gsx_bin_count_async")
+        d = int(words[3])
+        self.ws.note_dups(d)
+        return d
+
+    def settle(self) -> bool:
+        """Read D when the capacity was guessed.  Returns True when it
+        exceeded the guess and the binning has been enqueued again with the
+        exact capacity: work enqueued behind the first run (which saw empty
+        ranges) must be enqueued again.  False otherwise, and for jobs sized
+        exactly from the start."""
+        if not self.guessed:
+            return False
+        self.guessed = False
+        d = self._read_count()
+        if d <= self.cap:
+            self.num_dups = d
+            return False
+        self._enqueue(None)
+        return True
 
     def check(self) -> None:
         """Wait for the final status, raise GsxError if a device-side check
@@ -210,8 +272,10 @@ class BinJob:
         self.num_dups = int(nd.value)
 
     def result(self):
-        """(sorted_ids (D,), tile_ranges); waits for the binning only when D
-        is not yet known (refine_tiles)."""
+        """(sorted_ids (D,), tile_ranges); reads D first when the capacity
+        was guessed (see settle()) and waits for the whole binning when D
+        is not known before it ends (refine_tiles)."""
+        self.settle()
         if self.num_dups is None:
             self.check()
         return self.ids[:self.num_dups], self.ranges
