@@ -162,6 +162,8 @@ SIGNATURES = {
     "gsx_l1_noalloc_max_elements": (_I64, []),
     "gsx_l1_fwd_noalloc": (ctypes.c_int, [_I64, _P, _P, _P, _P]),
     "gsx_l1_bwd": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P]),
+    "gsx_l1_fwd_signs": (ctypes.c_int, [_I64, _P, _P, _P, _I64, _P, _P, _P]),
+    "gsx_l1_bwd_signs": (ctypes.c_int, [_I64, _P, _P, _P, _P, _P, _P]),
     "gsx_adam_step": (ctypes.c_int, [_I32, ctypes.c_void_p, _F, _F, _F, _P]),
     "gsx_preprocess_bwd_adam": (ctypes.c_int, [_CAM, _I64, _P, _P, _P, _P, _P, _P, _P, _I32,
                                                _I32, _U32, _F, _P, _P, _P, _P, _P, _P, _P,

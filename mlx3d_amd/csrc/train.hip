@@ -259,9 +259,23 @@ __global__ __launch_bounds__(256) void k_loss_reduce(const float* __restrict__ p
                                                      LossMix mix) {
     __shared__ double s[2][256];
     double a = 0.0, b = 0.0;
-    for (int64_t i = threadIdx.x; i < nblk; i += 256) {
-        a += (double)partials[2 * i];
-        b += (double)partials[2 * i + 1];
+    // each thread adds partials threadIdx.x + 256 k in increasing k; the
+    // loads of eight of them are issued together
+    constexpr int kBatch = 8;
+    for (int64_t i0 = threadIdx.x; i0 < nblk; i0 += 256 * kBatch) {
+        float2 v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {  // unconditional (clamped) loads
+            const int64_t i = min(i0 + 256 * k, nblk - 1);
+            v[k] = *reinterpret_cast<const float2*>(partials + 2 * i);
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            if (i0 + 256 * k < nblk) {
+                a += (double)v[k].x;
+                b += (double)v[k].y;
+            }
+        }
     }
     s[0][threadIdx.x] = a;
     s[1][threadIdx.x] = b;
@@ -523,27 +537,67 @@ int64_t photometric_groups(int32_t C) { return (C + kSsMaxCh - 1) / kSsMaxCh; }
 // in one elementwise pass.
 constexpr int kL1Threads = 256, kL1Per = 16, kL1Block = kL1Threads * kL1Per;
 
+// Sign code of d = pred - target, one byte per element: 0 for d > 0, 1 for
+// d < 0, 2 for d == 0, 3 for NaN (the gradient is then d itself).
+__device__ __forceinline__ uint32_t l1_sign_code(float d) {
+    return d > 0.0f ? 0u : (d < 0.0f ? 1u : (d == 0.0f ? 2u : 3u));
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(kL1Threads) void k_l1_partial(int64_t n,
                                                            const float* __restrict__ p,
                                                            const float* __restrict__ t,
-                                                           float* __restrict__ partials) {
+                                                           float* __restrict__ partials,
+                                                           uint8_t* __restrict__ signs) {
     __shared__ double s[kL1Threads];
     const int64_t base = (int64_t)blockIdx.x * kL1Block;
     double acc = 0.0;
+    if (VEC && base + kL1Block <= n) {
+        // a whole block: every load issued before the sums (same order)
+        float4 a[kL1Per / 4], b[kL1Per / 4];
+#pragma unroll
+        for (int k = 0; k < kL1Per / 4; ++k) {
+            const int64_t i = base + 4 * ((int64_t)k * kL1Threads + threadIdx.x);
+            a[k] = *reinterpret_cast<const float4*>(p + i);
+            b[k] = *reinterpret_cast<const float4*>(t + i);
+        }
+#pragma unroll
+        for (int k = 0; k < kL1Per / 4; ++k) {
+            const int64_t i = base + 4 * ((int64_t)k * kL1Threads + threadIdx.x);
+            const float4 d = make_float4(a[k].x - b[k].x, a[k].y - b[k].y, a[k].z - b[k].z,
+                                         a[k].w - b[k].w);
+            acc += (double)fabsf(d.x) + (double)fabsf(d.y) + (double)fabsf(d.z) +
+                   (double)fabsf(d.w);
+            if (signs)
+                *reinterpret_cast<uint32_t*>(signs + i) =
+                    l1_sign_code(d.x) | (l1_sign_code(d.y) << 8) | (l1_sign_code(d.z) << 16) |
+                    (l1_sign_code(d.w) << 24);
+        }
+    } else {
 #pragma unroll
     for (int k = 0; k < kL1Per / 4; ++k) {
         const int64_t i = base + 4 * ((int64_t)k * kL1Threads + threadIdx.x);
         if (VEC && i + 3 < n) {
             const float4 a = *reinterpret_cast<const float4*>(p + i);
             const float4 b = *reinterpret_cast<const float4*>(t + i);
-            acc += (double)fabsf(a.x - b.x) + (double)fabsf(a.y - b.y) +
-                   (double)fabsf(a.z - b.z) + (double)fabsf(a.w - b.w);
+            const float4 d = make_float4(a.x - b.x, a.y - b.y, a.z - b.z, a.w - b.w);
+            acc += (double)fabsf(d.x) + (double)fabsf(d.y) + (double)fabsf(d.z) +
+                   (double)fabsf(d.w);
+            if (signs)  // VEC: 4-byte aligned
+                *reinterpret_cast<uint32_t*>(signs + i) =
+                    l1_sign_code(d.x) | (l1_sign_code(d.y) << 8) | (l1_sign_code(d.z) << 16) |
+                    (l1_sign_code(d.w) << 24);
         } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (i + e < n) acc += (double)fabsf(p[i + e] - t[i + e]);
+            for (int e = 0; e < 4; ++e) {
+                if (i + e < n) {
+                    const float d = p[i + e] - t[i + e];
+                    acc += (double)fabsf(d);
+                    if (signs) signs[i + e] = (uint8_t)l1_sign_code(d);
+                }
+            }
         }
+    }
     }
     s[threadIdx.x] = acc;
     __syncthreads();
@@ -582,6 +636,52 @@ __global__ __launch_bounds__(kL1Threads) void k_l1_bwd(int64_t n, const float* _
     }
 }
 
+// The same gradient from the sign codes k_l1_partial wrote: one byte read
+// per element instead of two floats (pred and target are read only where
+// the code is NaN).
+template <bool VEC>
+__global__ __launch_bounds__(kL1Threads) void k_l1_bwd_signs(int64_t n,
+                                                             const uint8_t* __restrict__ signs,
+                                                             const float* __restrict__ p,
+                                                             const float* __restrict__ t,
+                                                             const float* __restrict__ g,
+                                                             float nf, float* __restrict__ grad) {
+    const float sc = g[0] / nf;
+    auto val = [&](uint32_t code, int64_t i) {
+        return code == 0u ? sc : (code == 1u ? -sc : (code == 2u ? 0.0f : p[i] - t[i]));
+    };
+    const int64_t base = (int64_t)blockIdx.x * kL1Block;
+    if (VEC && base + kL1Block <= n) {  // a whole block: the code loads issued together
+        uint32_t c[kL1Per / 4];
+#pragma unroll
+        for (int k = 0; k < kL1Per / 4; ++k)
+            c[k] = *reinterpret_cast<const uint32_t*>(
+                signs + base + 4 * ((int64_t)k * kL1Threads + threadIdx.x));
+#pragma unroll
+        for (int k = 0; k < kL1Per / 4; ++k) {
+            const int64_t i = base + 4 * ((int64_t)k * kL1Threads + threadIdx.x);
+            *reinterpret_cast<float4*>(grad + i) =
+                make_float4(val(c[k] & 0xFFu, i), val((c[k] >> 8) & 0xFFu, i + 1),
+                            val((c[k] >> 16) & 0xFFu, i + 2), val(c[k] >> 24, i + 3));
+        }
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < kL1Per / 4; ++k) {
+        const int64_t i = base + 4 * ((int64_t)k * kL1Threads + threadIdx.x);
+        if (VEC && i + 3 < n) {
+            const uint32_t c = *reinterpret_cast<const uint32_t*>(signs + i);
+            *reinterpret_cast<float4*>(grad + i) =
+                make_float4(val(c & 0xFFu, i), val((c >> 8) & 0xFFu, i + 1),
+                            val((c >> 16) & 0xFFu, i + 2), val(c >> 24, i + 3));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (i + e < n) grad[i + e] = val(signs[i + e], i + e);
+        }
+    }
+}
+
 inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
 // Scratch of gsx_l1_fwd_noalloc: the per-workgroup partial sums of at most
@@ -616,16 +716,17 @@ float* scratch_on(int dev) {
 }
 
 // The L1 forward on given partials storage (the workspace or the scratch).
-int l1_fwd_into(int64_t n, const float* pred, const float* target, float* partials, float* out,
-                hipStream_t st) {
+int l1_fwd_into(int64_t n, const float* pred, const float* target, float* partials,
+                uint8_t* signs, float* out, hipStream_t st) {
     const int64_t nblk = (n + kL1Block - 1) / kL1Block;
-    const bool vec = (((uintptr_t)pred | (uintptr_t)target) & 15u) == 0;
+    const bool vec =
+        (((uintptr_t)pred | (uintptr_t)target) & 15u) == 0 && ((uintptr_t)signs & 3u) == 0;
     if (vec)
         hipLaunchKernelGGL(k_l1_partial<true>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
-                           pred, target, partials);
+                           pred, target, partials, signs);
     else
         hipLaunchKernelGGL(k_l1_partial<false>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
-                           pred, target, partials);
+                           pred, target, partials, signs);
     GSX_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_loss_reduce, dim3(1), dim3(256), 0, st, (const float*)partials, nblk,
                        1.0 / (double)n, out, 1, LossMix{0.0f, 0.0f, false});
@@ -798,7 +899,16 @@ int gsx_l1_fwd(int64_t n, const float* pred, const float* target, void* workspac
     if (workspace_bytes < gsx_l1_workspace_bytes(n)) return GSX_ERR_WORKSPACE;
     const int64_t nblk = (n + kL1Block - 1) / kL1Block;
     if (nblk > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
-    return l1_fwd_into(n, pred, target, (float*)workspace, out, (hipStream_t)stream);
+    return l1_fwd_into(n, pred, target, (float*)workspace, nullptr, out, (hipStream_t)stream);
+}
+
+int gsx_l1_fwd_signs(int64_t n, const float* pred, const float* target, void* workspace,
+                     int64_t workspace_bytes, uint8_t* signs, float* out, void* stream) {
+    if (n <= 0 || !pred || !target || !workspace || !signs || !out) return GSX_ERR_INVALID;
+    if (workspace_bytes < gsx_l1_workspace_bytes(n)) return GSX_ERR_WORKSPACE;
+    const int64_t nblk = (n + kL1Block - 1) / kL1Block;
+    if (nblk > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
+    return l1_fwd_into(n, pred, target, (float*)workspace, signs, out, (hipStream_t)stream);
 }
 
 int64_t gsx_l1_noalloc_max_elements(void) { return kL1NoAllocMaxN; }
@@ -820,7 +930,7 @@ int gsx_l1_fwd_noalloc(int64_t n, const float* pred, const float* target, float*
     if (!partials) return GSX_ERR_HIP;
     // every workgroup writes both of its partial words, and the reduction
     // reads only this call's nblk of them: nothing needs clearing first
-    return l1_fwd_into(n, pred, target, partials, out, st);
+    return l1_fwd_into(n, pred, target, partials, nullptr, out, st);
 }
 
 int gsx_l1_bwd(int64_t n, const float* pred, const float* target, const float* grad_out,
@@ -836,6 +946,23 @@ int gsx_l1_bwd(int64_t n, const float* pred, const float* target, const float* g
     else
         hipLaunchKernelGGL(k_l1_bwd<false>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st, n,
                            pred, target, grad_out, (float)n, grad_pred);
+    GSX_LAUNCH_CHECK();
+    return GSX_OK;
+}
+
+int gsx_l1_bwd_signs(int64_t n, const uint8_t* signs, const float* pred, const float* target,
+                     const float* grad_out, float* grad_pred, void* stream) {
+    if (n <= 0 || !signs || !pred || !target || !grad_out || !grad_pred) return GSX_ERR_INVALID;
+    const int64_t nblk = (n + kL1Block - 1) / kL1Block;
+    if (nblk > 0x7FFFFFFF) return GSX_ERR_TOO_LARGE;
+    hipStream_t st = (hipStream_t)stream;
+    const bool vec = ((uintptr_t)grad_pred & 15u) == 0 && ((uintptr_t)signs & 3u) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_l1_bwd_signs<true>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st,
+                           n, signs, pred, target, grad_out, (float)n, grad_pred);
+    else
+        hipLaunchKernelGGL(k_l1_bwd_signs<false>, dim3((unsigned)nblk), dim3(kL1Threads), 0, st,
+                           n, signs, pred, target, grad_out, (float)n, grad_pred);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }

@@ -7,8 +7,8 @@ combination of the two from a second (``gsx_photometric_bwd``).
 (trainer.py:303-305) as one op: the same kernels form the scalar and take
 its cotangent (``gsx_photometric_loss_fwd`` / ``_bwd``), the values that
 expression's autograd graph gives.  ``ssim`` is the reference's function on
-top of ``photometric``, and ``l1_loss`` the L1 term alone (``gsx_l1_fwd`` /
-``gsx_l1_bwd``).
+top of ``photometric``, and ``l1_loss`` the L1 term alone
+(``gsx_l1_fwd_signs`` / ``gsx_l1_bwd_signs``).
 """
 
 from __future__ import annotations
@@ -150,28 +150,32 @@ class _L1Fn(torch.autograd.Function):
         nbytes = int(L.gsx_l1_workspace_bytes(n))
         ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=pred.device)
         out = torch.empty((1,), dtype=torch.float32, device=pred.device)
+        # the signs of pred - target, kept for the backward (1 byte each)
+        signs = torch.empty((n,), dtype=torch.uint8, device=pred.device)
         with stage("l1_fwd"):
-            _lib.check(L.gsx_l1_fwd(n, _lib.ptr(pred), _lib.ptr(target), _lib.ptr(ws), nbytes,
-                                    _lib.ptr(out), _lib.stream_handle(pred.device)), "gsx_l1_fwd")
-        ctx.save_for_backward(pred, target)
+            _lib.check(L.gsx_l1_fwd_signs(n, _lib.ptr(pred), _lib.ptr(target), _lib.ptr(ws),
+                                          nbytes, _lib.ptr(signs), _lib.ptr(out),
+                                          _lib.stream_handle(pred.device)), "gsx_l1_fwd_signs")
+        ctx.save_for_backward(pred, target, signs)
         return out[0]
 
     @staticmethod
     def backward(ctx, g_out):
-        pred, target = ctx.saved_tensors
+        pred, target, signs = ctx.saved_tensors
         g = _lib.f32c(g_out.reshape(1))
         grad = torch.empty_like(pred)
         with stage("l1_bwd"):
-            _lib.check(_lib.load().gsx_l1_bwd(pred.numel(), _lib.ptr(pred), _lib.ptr(target),
-                                              _lib.ptr(g), _lib.ptr(grad),
-                                              _lib.stream_handle(pred.device)), "gsx_l1_bwd")
+            _lib.check(_lib.load().gsx_l1_bwd_signs(
+                pred.numel(), _lib.ptr(signs), _lib.ptr(pred), _lib.ptr(target), _lib.ptr(g),
+                _lib.ptr(grad), _lib.stream_handle(pred.device)), "gsx_l1_bwd_signs")
         return grad, None
 
 
 def l1_loss(pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
     """Mean absolute error (image_metrics.py:13-14), differentiable with
-    respect to ``pred``: one reduction kernel forward, one elementwise
-    gradient kernel backward (gsx_l1_fwd / gsx_l1_bwd)."""
+    respect to ``pred``: one reduction kernel forward that also keeps the
+    sign of each difference, one elementwise gradient kernel backward from
+    those signs (gsx_l1_fwd_signs / gsx_l1_bwd_signs)."""
     if pred.shape != target.shape:
         raise ValueError("pred and target must have the same shape.")
     if pred.numel() == 0:

@@ -33,7 +33,7 @@ def test_python_binding_covers_header():
 
 def test_status_strings_and_version():
     L = _lib.load()
-    assert L.gsx_abi_version() == 5
+    assert L.gsx_abi_version() == 6
     assert _lib.strerror(0) == "ok"
     assert "invalid" in _lib.strerror(-1)
     assert "capacity" in _lib.strerror(1)
@@ -84,6 +84,12 @@ def test_invalid_arguments_rejected_before_launch():
     assert L.gsx_l1_fwd_noalloc(limit + 1, p, p, p, None) == -4
     assert L.gsx_l1_fwd_noalloc(0, p, p, p, None) == -1
     assert L.gsx_l1_fwd_noalloc(10, None, p, p, None) == -1
+    # the sign-keeping L1 pair checks its arguments before any launch
+    assert L.gsx_l1_fwd_signs(0, p, p, p, 64, p, p, None) == -1
+    assert L.gsx_l1_fwd_signs(10, p, p, p, 64, None, p, None) == -1
+    assert L.gsx_l1_fwd_signs(10, p, p, p, 0, p, p, None) == -3  # workspace too small
+    assert L.gsx_l1_bwd_signs(10, None, p, p, p, p, None) == -1
+    assert L.gsx_l1_bwd_signs(-1, p, p, p, p, p, None) == -1
 
 
 def test_bin_status_check_is_host_only():

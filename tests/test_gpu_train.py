@@ -151,6 +151,51 @@ def test_l1_loss_matches_closed_form(n, offset):
     assert_bits(host(g), want, "l1 grad")
 
 
+@pytest.mark.parametrize("n,soff", [(4101, 0), (65537, 1), (1080 * 1920 * 3, 0)])
+def test_l1_sign_pair_matches_plain_pair(n, soff):
+    """gsx_l1_fwd_signs / gsx_l1_bwd_signs against gsx_l1_fwd / gsx_l1_bwd
+    through the C ABI: loss and gradient bit for bit, with NaN, +-inf and
+    equal entries; the codes against numpy's comparisons.  soff = 1 puts the
+    sign bytes at an odd address (the byte-wise path)."""
+    say(f"l1 signs n={n} soff={soff}")
+    rng = np.random.default_rng(n)
+    p = rng.standard_normal(n).astype(np.float32)
+    t = rng.standard_normal(n).astype(np.float32)
+    t[::7] = p[::7]
+    p[3::101] = np.nan
+    t[5::211] = np.inf
+    pc, tc = cu(p), cu(t)
+    L, st = _lib.load(), _lib.stream_handle(pc.device)
+    ws = torch.empty((int(L.gsx_l1_workspace_bytes(n)),), dtype=torch.uint8, device=pc.device)
+    sbuf = torch.full((n + 8,), 0xAB, dtype=torch.uint8, device=pc.device)
+    signs = sbuf[soff:soff + n]
+    g = cu(np.array([1.75], np.float32))
+    outs, grads = [], []
+    for pair in ("plain", "signs"):
+        out = torch.empty((1,), dtype=torch.float32, device=pc.device)
+        grad = torch.empty_like(pc)
+        if pair == "plain":
+            _lib.check(L.gsx_l1_fwd(n, _lib.ptr(pc), _lib.ptr(tc), _lib.ptr(ws), ws.numel(),
+                                    _lib.ptr(out), st), "gsx_l1_fwd")
+            _lib.check(L.gsx_l1_bwd(n, _lib.ptr(pc), _lib.ptr(tc), _lib.ptr(g), _lib.ptr(grad),
+                                    st), "gsx_l1_bwd")
+        else:
+            _lib.check(L.gsx_l1_fwd_signs(n, _lib.ptr(pc), _lib.ptr(tc), _lib.ptr(ws),
+                                          ws.numel(), _lib.ptr(signs), _lib.ptr(out), st),
+                       "gsx_l1_fwd_signs")
+            _lib.check(L.gsx_l1_bwd_signs(n, _lib.ptr(signs), _lib.ptr(pc), _lib.ptr(tc),
+                                          _lib.ptr(g), _lib.ptr(grad), st), "gsx_l1_bwd_signs")
+        outs.append(host(out))
+        grads.append(host(grad))
+    assert_bits(outs[1], outs[0], "l1 loss")
+    assert_bits(grads[1], grads[0], "l1 grad")
+    d = p - t
+    want = np.where(d > 0, 0, np.where(d < 0, 1, np.where(d == 0, 2, 3))).astype(np.uint8)
+    got = host(sbuf)
+    assert (got[soff:soff + n] == want).all()
+    assert (np.delete(got, np.arange(soff, soff + n)) == 0xAB).all()  # nothing outside
+
+
 def test_l1_loss_errors():
     with pytest.raises(ValueError):
         l1_loss(torch.zeros(3), torch.zeros(3))  # host tensors
