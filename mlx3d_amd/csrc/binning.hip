@@ -129,14 +129,17 @@ struct Publish {
     uint32_t seq;
 };
 
+// The words were written by earlier kernels of the stream (a kernel
+// boundary makes them visible), so plain loads fetch all eight in one
+// round trip.
 __device__ __forceinline__ void publish(const Publish& p) {
+    uint32_t v[kStatusWords];
 #pragma unroll
-    for (int k = 0; k < kStatusWords; ++k) {
-        const uint32_t v =
-            __hip_atomic_load(p.words + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.host + k, ((unsigned long long)p.seq << 32) | v, __ATOMIC_RELAXED,
+    for (int k = 0; k < kStatusWords; ++k) v[k] = p.words[k];
+#pragma unroll
+    for (int k = 0; k < kStatusWords; ++k)
+        __hip_atomic_store(p.host + k, ((unsigned long long)p.seq << 32) | v[k], __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_SYSTEM);
-    }
     __threadfence_system();
 }
 
@@ -394,14 +397,25 @@ __global__ __launch_bounds__(kHistThreads) void k_depth_hist(
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * (kHistThreads * kHistItems) + wave * (64 * kHistItems);
     uint64_t sum = 0, hsum = 0;
+    // every load issued before the histogram work (clamped indices, n >= 1)
+    uint32_t kk[kHistItems], cc[kHistItems];
+    uint2 rr[kHistItems];
+#pragma unroll
+    for (int r = 0; r < kHistItems; ++r) {
+        const int64_t i = min(base + r * 64 + lane, n - 1);
+        kk[r] = keys[i];
+        cc[r] = counts[i];
+        rr[r] = rects[i];
+    }
+#pragma unroll
     for (int r = 0; r < kHistItems; ++r) {
         const int64_t i = base + r * 64 + lane;
         const bool valid = i < n;
-        const uint32_t key = valid ? keys[i] : 0u;
-        const uint32_t cnt = valid ? counts[i] : 0u;
+        const uint32_t key = valid ? kk[r] : 0u;
+        const uint32_t cnt = valid ? cc[r] : 0u;
         sum += cnt;
         if (cnt) {
-            const uint2 rc = rects[i];
+            const uint2 rc = rr[r];
             const uint32_t h = rc.y >> 16;
             hsum += h;
             if (rows > 0 && (rc.x >> 16) + h <= (uint32_t)rows) {
@@ -691,9 +705,15 @@ __global__ __launch_bounds__(kScanThreads) void k_row_scan(
     const int64_t chunk = s_chunk;
     if (chunk < nchunks) {  // always: the other workgroups are exactly nchunks
         const int64_t i0 = chunk * kScanChunk + (int64_t)tid * kScanItems;
-        uint32_t c[kScanItems];
+        // clamped indices, so the id loads and then the rectangle loads
+        // issue together (n >= 1 here); items past n count zero
+        uint32_t g[kScanItems], c[kScanItems];
 #pragma unroll
-        for (int j = 0; j < kScanItems; ++j) c[j] = i0 + j < n ? rects[gids[i0 + j]].y >> 16 : 0u;
+        for (int j = 0; j < kScanItems; ++j) g[j] = gids[min(i0 + j, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) c[j] = rects[g[j]].y >> 16;
+#pragma unroll
+        for (int j = 0; j < kScanItems; ++j) c[j] = i0 + j < n ? c[j] : 0u;
         uint32_t total;
         uint32_t csum = 0;
 #pragma unroll
