@@ -48,9 +48,14 @@
 // with wave-level multi-split, publishes its digit counts and finds its
 // global offsets by decoupled look-back (Merrill & Garland, 2016), then
 // writes the chunk through LDS in digit order so the global stores are runs
-// of consecutive addresses.  Chunks are claimed through an atomic counter,
-// so a chunk only waits for chunks that are already running; each wait is
-// bounded and raises an error flag instead of spinning forever.
+// of consecutive addresses.  A chunk is its workgroup's index: workgroups
+// are dispatched in index order (round robin over the XCDs, in order on
+// each), so the lowest unfinished chunk is always running or next to start
+// and only waits for finished chunks -- no claim counter (a same-address
+// atomic per workgroup, microseconds under contention) is needed.  Each
+// wait is bounded and raises an error flag instead of spinning forever,
+// which also covers a dispatcher that did otherwise.  (The general path's
+// count scan still claims its chunks through a counter.)
 //
 // Host status without stream copies: when the caller passes pinned host
 // memory, the first depth pass (its workgroup 0, which starts after the
@@ -471,7 +476,7 @@ __global__ __launch_bounds__(kHistThreads) void k_depth_hist(
 
 // ------------------------------------------------------------ radix pass --
 // One stable LSD pass over the BITS-bit digit at `shift` (`nbits`
-// significant).  Chunk c (claimed in launch order) holds keys
+// significant).  Chunk c (workgroup c) holds keys
 // [c * chunk, (c + 1) * chunk); wave w of it owns a contiguous slice, ranked
 // round by round, so the order is stable.  The chunk is regrouped by digit
 // in LDS, then written out: element j of the regrouped chunk goes to
@@ -488,7 +493,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n_host,
     const uint32_t* __restrict__ n_dev, int shift, int nbits, const uint32_t* __restrict__ hist,
     int hist_stride, bool skip_constant, uint32_t* __restrict__ status,
-    uint32_t* __restrict__ counter, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ err, Publish pub,
     const uint32_t* __restrict__ route_hist, uint32_t* __restrict__ keys_alt,
     uint32_t* __restrict__ vals_alt) {
@@ -502,12 +507,11 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     __shared__ uint32_t s_shift[kR];
     __shared__ uint32_t s_w[2 * kWaves];
     __shared__ uint32_t s_key[kChunk], s_val[kChunk];
-    __shared__ uint32_t s_chunk;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (pub.host && blockIdx.x == 0 && tid == 0) publish(pub);
     const int64_t n = live_count(n_host, n_dev);
-    // The first ceil(n / chunk) workgroups claim exactly the live chunks;
-    // the rest leave without claiming, so no live chunk waits on them.
+    // The first ceil(n / chunk) workgroups are the live chunks; the rest
+    // leave at once.
     if ((int64_t)blockIdx.x * kChunk >= n) return;
     uint32_t dsum[kBPT];
 #pragma unroll
@@ -526,10 +530,9 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         for (int k = 0; k < kBPT; ++k) whole |= (int64_t)dsum[k] == n;
         if (__syncthreads_or(whole)) return;  // identity permutation
     }
-    if (tid == 0) s_chunk = atomicAdd(counter, 1u);
     for (int k = tid; k < kWaves * kR; k += THREADS) (&s_cnt[0][0])[k] = 0u;
     __syncthreads();
-    const int64_t chunk = s_chunk;
+    const int64_t chunk = blockIdx.x;
     const int64_t base = chunk * kChunk + wave * (64 * ITEMS);
     const uint64_t lt = (1ull << lane) - 1ull;
     uint32_t key[ITEMS], val[ITEMS], rank[ITEMS];
@@ -679,12 +682,12 @@ __device__ __forceinline__ void row_plan(const uint32_t* __restrict__ row_diff, 
 // launched after this kernel, is its first reader.
 __global__ __launch_bounds__(kScanThreads) void k_row_scan(
     int64_t n, const uint2* __restrict__ rects, const uint32_t* __restrict__ gids,
-    uint32_t* __restrict__ sstatus, uint32_t* __restrict__ counter, uint32_t* __restrict__ roffs,
+    uint32_t* __restrict__ sstatus, uint32_t* __restrict__ roffs, uint32_t* __restrict__ prect,
     uint32_t* __restrict__ owner, int64_t n_owner, uint32_t* __restrict__ status,
     uint32_t* __restrict__ clear, int64_t n_clear, const uint32_t* __restrict__ row_diff,
     int tiles_y, RowPlan* __restrict__ plan, uint32_t* __restrict__ segrow, int64_t max_segs) {
     __shared__ uint32_t s_w[kScanThreads / 64];
-    __shared__ uint32_t s_chunk, s_prefix;
+    __shared__ uint32_t s_prefix;
     const int tid = threadIdx.x;
     uint32_t* err = status + 1;
     // the row emission's look-back status words start at zero (those of
@@ -700,20 +703,28 @@ __global__ __launch_bounds__(kScanThreads) void k_row_scan(
         row_plan(row_diff, tiles_y, plan, segrow, max_segs, status, s_w);
         return;
     }
-    if (tid == 0) s_chunk = atomicAdd(counter, 1u);
-    __syncthreads();
-    const int64_t chunk = s_chunk;
-    if (chunk < nchunks) {  // always: the other workgroups are exactly nchunks
+    const int64_t chunk = blockIdx.x;  // the other workgroups are exactly nchunks
+    if (chunk < nchunks) {
         const int64_t i0 = chunk * kScanChunk + (int64_t)tid * kScanItems;
         // clamped indices, so the id loads and then the rectangle loads
         // issue together (n >= 1 here); items past n count zero
         uint32_t g[kScanItems], c[kScanItems];
+        uint2 rc[kScanItems];
 #pragma unroll
         for (int j = 0; j < kScanItems; ++j) g[j] = gids[min(i0 + j, n - 1)];
 #pragma unroll
-        for (int j = 0; j < kScanItems; ++j) c[j] = rects[g[j]].y >> 16;
+        for (int j = 0; j < kScanItems; ++j) rc[j] = rects[g[j]];
 #pragma unroll
-        for (int j = 0; j < kScanItems; ++j) c[j] = i0 + j < n ? c[j] : 0u;
+        for (int j = 0; j < kScanItems; ++j) {
+            c[j] = i0 + j < n ? rc[j].y >> 16 : 0u;
+            // the rectangle packed into one word for the row emission:
+            // x0 | y0 << 8 | (w - 1) << 16 (every field below 256), bit 24
+            // set for a nonzero height
+            if (i0 + j < n)
+                prect[i0 + j] = (rc[j].x & 0xFFu) | (((rc[j].x >> 16) & 0xFFu) << 8) |
+                                ((((rc[j].y & 0xFFFFu) - 1u) & 0xFFu) << 16) |
+                                ((rc[j].y >> 16) != 0u ? 1u << 24 : 0u);
+        }
         uint32_t total;
         uint32_t csum = 0;
 #pragma unroll
@@ -758,11 +769,13 @@ __global__ __launch_bounds__(kScanThreads) void k_row_scan(
 // and the entry's first duplicate within its row's duplicate sequence (the
 // widths of the row's earlier entries, a second look-back column).  The
 // entry holding a segment's first duplicate records itself in segk0.
-__global__ __launch_bounds__(kEmitThreads) void k_row_emit(
+// Two workgroups per CU (eight waves per SIMD: at most 64 VGPRs), so all
+// 512 chunk slots are resident at once.
+__global__ __launch_bounds__(kEmitThreads, 8) void k_row_emit(
     int64_t n, int64_t cap, const uint32_t* __restrict__ roffs, const uint32_t* __restrict__ owner,
-    const uint32_t* __restrict__ gids, const uint2* __restrict__ rects,
+    const uint32_t* __restrict__ gids, const uint32_t* __restrict__ prect,
     const RowPlan* __restrict__ plan, int tiles_y, uint32_t* __restrict__ rstatus,
-    uint32_t* __restrict__ counter, uint32_t* __restrict__ e_gid, uint32_t* __restrict__ e_pack,
+    uint32_t* __restrict__ e_gid, uint32_t* __restrict__ e_pack,
     uint32_t* __restrict__ e_doff, uint32_t* __restrict__ segk0, int64_t max_segs,
     uint32_t* __restrict__ err) {
     constexpr int kWaves = kEmitThreads / 64;
@@ -779,13 +792,19 @@ __global__ __launch_bounds__(kEmitThreads) void k_row_emit(
     __shared__ uint32_t s_row[kMaxFastTiles];  // rowbase
     __shared__ uint32_t s_seg[kMaxFastTiles];  // segbase
     __shared__ uint32_t s_w[2 * kWaves];
-    __shared__ uint32_t s_chunk;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // the duplicates (and so the row entries) do not fit: nothing is written
     if ((int64_t)plan->dups > cap || (int64_t)plan->entries > cap) return;
     const int64_t nr = (int64_t)plan->entries;
-    if ((int64_t)blockIdx.x * kRowChunk >= nr) return;
-    if (tid == 0) s_chunk = atomicAdd(counter, 1u);
+    const int64_t chunk = blockIdx.x;
+    const int64_t r0 = chunk * kRowChunk;
+    if (r0 >= nr) return;
+    const int64_t r1 = min<int64_t>(r0 + kRowChunk, nr);
+    // owner of the first entry, and a bound on the owner of the last (the
+    // loads issue beside the plan's)
+    const int64_t lo = owner[chunk];
+    const int64_t hi = r1 < nr ? (int64_t)owner[chunk + 1]
+                               : block_find_owner<kEmitThreads>(roffs, n, (uint32_t)(r1 - 1));
     for (int k = tid; k < kWaves * kMaxFastTiles; k += kEmitThreads) (&s_cnt[0][0])[k] = 0u;
     for (int k = tid; k < kRowChunk; k += kEmitThreads) s_own[k] = 0u;
     if (tid < kMaxFastTiles) {
@@ -793,13 +812,6 @@ __global__ __launch_bounds__(kEmitThreads) void k_row_emit(
         s_seg[tid] = tid < tiles_y ? plan->segbase[tid] : 0u;
     }
     __syncthreads();
-    const int64_t chunk = s_chunk;
-    const int64_t r0 = chunk * kRowChunk;
-    const int64_t r1 = min<int64_t>(r0 + kRowChunk, nr);
-    // owner of the first entry, and a bound on the owner of the last
-    const int64_t lo = owner[chunk];
-    const int64_t hi = r1 < nr ? (int64_t)owner[chunk + 1]
-                               : block_find_owner<kEmitThreads>(roffs, n, (uint32_t)(r1 - 1));
     const int64_t wo = hi - lo + 1;
     const bool staged = wo <= kRowChunk;  // uniform
     // a rectangle of the fast path packs into one word: x0 | y0 << 8 |
@@ -807,10 +819,6 @@ __global__ __launch_bounds__(kEmitThreads) void k_row_emit(
     uint32_t* s_off = s_buf;
     uint32_t* s_gid = s_buf + kRowChunk;
     uint32_t* s_rect = s_buf + 2 * kRowChunk;
-    auto pack_rect = [](uint2 rc) {
-        return (rc.x & 0xFFu) | (((rc.x >> 16) & 0xFFu) << 8) |
-               ((((rc.y & 0xFFFFu) - 1u) & 0xFFu) << 16);
-    };
     if (staged) {
         // slot owners: staged owner k >= 1 of nonzero height starts at slot
         // roffs - r0 (distinct slots); a max-scan then gives every slot its
@@ -818,11 +826,11 @@ __global__ __launch_bounds__(kEmitThreads) void k_row_emit(
         for (int k = tid; k < wo; k += kEmitThreads) {
             const uint32_t g = gids[lo + k];
             const uint32_t off = roffs[lo + k];
-            const uint2 rc = rects[g];
+            const uint32_t rc = prect[lo + k];
             s_off[k] = off;
             s_gid[k] = g;
-            s_rect[k] = pack_rect(rc);
-            if (k > 0 && (rc.y >> 16) != 0u && (int64_t)off < r1)
+            s_rect[k] = rc;
+            if (k > 0 && (rc >> 24) != 0u && (int64_t)off < r1)
                 s_own[off - (uint32_t)r0] = (uint16_t)k;
         }
     }
@@ -877,7 +885,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_row_emit(
                 }
                 off = roffs[a];
                 g = gids[a];
-                rc = pack_rect(rects[g]);
+                rc = prect[a];
             }
             yy[r] = (((rc >> 8) & 0xFFu) + ((uint32_t)e - off)) & 0xFFu;
             gg[r] = g;
@@ -1538,8 +1546,7 @@ inline bool fast_tiles(int tiles_x, int tiles_y) {
     return tiles_x <= kMaxFastTiles && tiles_y <= kMaxFastTiles;
 }
 
-// misc words: [0..3] depth-pass chunk counters, [4..7] tile-pass counters,
-// [8] count-scan counter, [9] row-scan counter, [10] row-emission counter,
+// misc words: [8] the count scan's chunk counter ([0..7], [9..15] unused),
 // [16..23] the status words of gsx_bin_sort, then the histogram copies of
 // the depth sort, of the tile sort and the row histograms.
 constexpr int kSyncStatusWord = 16;
@@ -1734,7 +1741,7 @@ int depth_phase(int64_t n, const uint32_t* depth_keys, void* depth_ws, int64_t d
         hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems, kDepthBits>), dim3(grid),
                            dim3(kDepthThreads), 0, st, kin, vin, n, nil, p * kDepthBits,
                            kDepthBits, hist + p * kDepthRadix, kDepthHistStride, false,
-                           status + p * per_pass, misc + p, ko, vo, bin_status + 1, pb, route,
+                           status + p * per_pass, ko, vo, bin_status + 1, pb, route,
                            ka, va);
     };
     pass10(0, depth_keys, nil, dk[0], dv[0], pub, nil, no, no);
@@ -1744,7 +1751,7 @@ int depth_phase(int64_t n, const uint32_t* depth_keys, void* depth_ws, int64_t d
     hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems, kDepthTopBits>), dim3(grid),
                        dim3(kDepthThreads), 0, st, dk[0], dv[0], n, nil, kDepthTopShift,
                        kDepthTopBits, hist + 3 * kDepthRadix, kDepthHistStride, true,
-                       status + 3 * per_pass, misc + 3, dk[2], dv[2], bin_status + 1, none, nil,
+                       status + 3 * per_pass, dk[2], dv[2], bin_status + 1, none, nil,
                        no, no);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
@@ -1787,6 +1794,9 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
         // row scan (+ row plan, D into bin_status[0]); row emission;
         // segment counts; per-row tile scan (ranges); placement
         RowPlan* plan = at<RowPlan>(depth_ws, D.plan);
+        // the rectangles in depth order, packed (the depth sort's first key
+        // buffer is free once the sort has ended)
+        uint32_t* prect = at<uint32_t>(depth_ws, D.dk[0]);
         uint32_t* rstatus = at<uint32_t>(tile_ws, L.rstatus);
         uint32_t* e_gid = at<uint32_t>(tile_ws, L.e_gid);
         uint32_t* e_pack = at<uint32_t>(tile_ws, L.e_pack);
@@ -1795,7 +1805,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
         uint32_t* segrow = at<uint32_t>(tile_ws, L.segrow);
         uint32_t* segk0 = at<uint32_t>(tile_ws, L.segk0);
         hipLaunchKernelGGL(k_row_scan, dim3((unsigned)D.scan_chunks + 1u), dim3(kScanThreads), 0, st,
-                           n, (const uint2*)tile_rects, gids, sstatus, misc + 9, offs, owner,
+                           n, (const uint2*)tile_rects, gids, sstatus, offs, prect, owner,
                            L.row_chunks, bin_status, rstatus, L.rstatus_words,
                            (const uint32_t*)(misc + kMiscRowDiff), tiles_y, plan, segrow,
                            L.segments);
@@ -1807,8 +1817,8 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
         }
         hipLaunchKernelGGL(k_row_emit, dim3((unsigned)L.row_chunks), dim3(kEmitThreads), 0, st,
                            n, capacity, (const uint32_t*)offs, (const uint32_t*)owner, gids,
-                           (const uint2*)tile_rects, (const RowPlan*)plan, tiles_y, rstatus,
-                           misc + 10, e_gid, e_pack, e_doff, segk0, L.segments, err);
+                           (const uint32_t*)prect, (const RowPlan*)plan, tiles_y, rstatus,
+                           e_gid, e_pack, e_doff, segk0, L.segments, err);
         hipLaunchKernelGGL(k_seg_count, dim3((unsigned)L.segments), dim3(kMaxFastTiles), 0, st,
                            capacity, (const RowPlan*)plan, (const uint32_t*)segrow,
                            (const uint32_t*)segk0, tiles_x, (const uint32_t*)e_pack,
@@ -1861,7 +1871,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
                            tv[cur], capacity, (const uint32_t*)d_total, p * kRadixBits,
                            std::min(kRadixBits, tile_bits - p * kRadixBits),
                            tile_hist + p * kRadix, kTileHistStride, false,
-                           tstatus + (size_t)p * L.tile_chunks * kRadix, misc + 4 + p,
+                           tstatus + (size_t)p * L.tile_chunks * kRadix,
                            tk[cur ^ 1], tv[cur ^ 1], err, nopub, (const uint32_t*)nullptr,
                            (uint32_t*)nullptr, (uint32_t*)nullptr);
         cur ^= 1;
