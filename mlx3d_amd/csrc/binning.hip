@@ -718,12 +718,10 @@ __global__ __launch_bounds__(kScanThreads) void k_row_scan(
         for (int j = 0; j < kScanItems; ++j) {
             c[j] = i0 + j < n ? rc[j].y >> 16 : 0u;
             // the rectangle packed into one word for the row emission:
-            // x0 | y0 << 8 | (w - 1) << 16 (every field below 256), bit 24
-            // set for a nonzero height
+            // x0 | y0 << 8 | (w - 1) << 16 (every field below 256)
             if (i0 + j < n)
                 prect[i0 + j] = (rc[j].x & 0xFFu) | (((rc[j].x >> 16) & 0xFFu) << 8) |
-                                ((((rc[j].y & 0xFFFFu) - 1u) & 0xFFu) << 16) |
-                                ((rc[j].y >> 16) != 0u ? 1u << 24 : 0u);
+                                ((((rc[j].y & 0xFFFFu) - 1u) & 0xFFu) << 16);
         }
         uint32_t total;
         uint32_t csum = 0;
@@ -806,7 +804,6 @@ __global__ __launch_bounds__(kEmitThreads, 8) void k_row_emit(
     const int64_t hi = r1 < nr ? (int64_t)owner[chunk + 1]
                                : block_find_owner<kEmitThreads>(roffs, n, (uint32_t)(r1 - 1));
     for (int k = tid; k < kWaves * kMaxFastTiles; k += kEmitThreads) (&s_cnt[0][0])[k] = 0u;
-    for (int k = tid; k < kRowChunk; k += kEmitThreads) s_own[k] = 0u;
     if (tid < kMaxFastTiles) {
         s_row[tid] = tid < tiles_y ? plan->rowbase[tid] : 0u;
         s_seg[tid] = tid < tiles_y ? plan->segbase[tid] : 0u;
@@ -820,41 +817,20 @@ __global__ __launch_bounds__(kEmitThreads, 8) void k_row_emit(
     uint32_t* s_gid = s_buf + kRowChunk;
     uint32_t* s_rect = s_buf + 2 * kRowChunk;
     if (staged) {
-        // slot owners: staged owner k >= 1 of nonzero height starts at slot
-        // roffs - r0 (distinct slots); a max-scan then gives every slot its
-        // owner (a zero-height owner owns no entry and marks nothing)
+        // slot owners: staged owner k holds the chunk's entries
+        // [max(roffs[k], r0), min(roffs[k + 1], r1)) (its height from the
+        // next offset; roffs has n + 1 words); the spans are disjoint and
+        // cover the chunk, so each slot is written once
         for (int k = tid; k < wo; k += kEmitThreads) {
             const uint32_t g = gids[lo + k];
             const uint32_t off = roffs[lo + k];
-            const uint32_t rc = prect[lo + k];
+            const uint32_t end = roffs[lo + k + 1];
             s_off[k] = off;
             s_gid[k] = g;
-            s_rect[k] = rc;
-            if (k > 0 && (rc >> 24) != 0u && (int64_t)off < r1)
-                s_own[off - (uint32_t)r0] = (uint16_t)k;
+            s_rect[k] = prect[lo + k];
+            for (uint32_t x = max(off, (uint32_t)r0); x < min(end, (uint32_t)r1); ++x)
+                s_own[x - (uint32_t)r0] = (uint16_t)k;
         }
-    }
-    __syncthreads();
-    if (staged) {  // inclusive max-scan of the slot owners (4 consecutive slots per thread)
-        uint32_t m[4], mx = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            mx = max(mx, (uint32_t)s_own[tid * 4 + k]);
-            m[k] = mx;
-        }
-        uint32_t wm = mx;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t t = __shfl_up(wm, (unsigned)o, 64);
-            if (lane >= o) wm = max(wm, t);
-        }
-        if (lane == 63) s_w[wave] = wm;
-        __syncthreads();
-        uint32_t prev = __shfl_up(wm, 1u, 64);
-        if (lane == 0) prev = 0u;
-        for (int w = 0; w < wave; ++w) prev = max(prev, s_w[w]);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) s_own[tid * 4 + k] = (uint16_t)max(prev, m[k]);
     }
     __syncthreads();
     // item r of a thread is entry r0 + wave * 256 + r * 64 + lane (the
@@ -1137,9 +1113,9 @@ __global__ __launch_bounds__(kScanParts * kMaxFastTiles) void k_tile_scan(
 // right, in entry order) are ranked by column, stably in duplicate order,
 // and written at sc[segment][column] + (earlier duplicates of that column
 // in the segment).  Duplicate i of the segment is item i of the ranking
-// order (wave-contiguous slices, rounds of 64 lanes); its entry is the last
-// staged entry whose first duplicate is <= i, found by a max-scan over the
-// segment's slots.  With pub.host, workgroup 0 copies the status words to
+// order (wave-contiguous slices, rounds of 64 lanes); its entry, the staged
+// entry whose span holds i, is written into the segment's slots by the
+// entry itself.  With pub.host, workgroup 0 copies the status words to
 // the host first (every earlier kernel of the binning has finished).
 __global__ __launch_bounds__(kEmitThreads) void k_place(
     int64_t cap, const RowPlan* __restrict__ plan, const uint32_t* __restrict__ segrow,
@@ -1162,44 +1138,23 @@ __global__ __launch_bounds__(kEmitThreads) void k_place(
     uint32_t* s_doff = s_ent;
     uint32_t* s_gid = s_ent + kSegDups;
     uint32_t* s_pack = s_ent + 2 * kSegDups;
-    for (int k = tid; k < kSegDups; k += kEmitThreads) s_own[k] = 0u;
     for (int k = tid; k < kWaves * kMaxFastTiles; k += kEmitThreads) (&s_cnt[0][0])[k] = 0u;
     if (tid < tiles_x) s_base[tid] = sc[(int64_t)blockIdx.x * kMaxFastTiles + tid];
-    __syncthreads();
     for (int k = tid; k < ne; k += kEmitThreads) {
         const uint32_t e = sg.rb + sg.k0 + (uint32_t)k;
         const uint32_t doff = e_doff[e];
+        const uint32_t pack = e_pack[e];
         s_doff[k] = doff;
         s_gid[k] = e_gid[e];
-        s_pack[k] = e_pack[e];
-        // k = 0 starts at or before a; entries starting at or after e
-        // (the candidate past the segment) own no slot
-        if (k > 0 && doff < sg.e) s_own[doff - sg.a] = (uint16_t)k;
+        s_pack[k] = pack;
+        // slot owners: entry k holds the segment's duplicates
+        // [max(doff, a), min(doff + w, e)) (k = 0 starts at or before a; an
+        // entry starting at or after e, the candidate past the segment,
+        // holds none); the spans are disjoint and cover the segment
+        const uint32_t end = min(doff + ((pack >> 8) & 0xFFu) + 1u, sg.e);
+        for (uint32_t x = max(doff, sg.a); x < end; ++x) s_own[x - sg.a] = (uint16_t)k;
     }
     __syncthreads();
-    // inclusive max-scan of the slot owners (4 consecutive slots per thread)
-    {
-        uint32_t m[4], mx = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            mx = max(mx, (uint32_t)s_own[tid * 4 + k]);
-            m[k] = mx;
-        }
-        uint32_t wm = mx;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t t = __shfl_up(wm, (unsigned)o, 64);
-            if (lane >= o) wm = max(wm, t);
-        }
-        if (lane == 63) s_w[wave] = wm;
-        __syncthreads();
-        uint32_t prev = __shfl_up(wm, 1u, 64);
-        if (lane == 0) prev = 0u;
-        for (int w = 0; w < wave; ++w) prev = max(prev, s_w[w]);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) s_own[tid * 4 + k] = (uint16_t)max(prev, m[k]);
-        __syncthreads();
-    }
     const uint32_t nd = sg.e - sg.a;
     const int xbits = 32 - __builtin_clz((uint32_t)max(tiles_x - 1, 1));
     const int base = wave * (64 * kEmitItems);
