@@ -1321,6 +1321,8 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tile = __builtin_amdgcn_readfirstlane(tile_at(order, blockIdx.x, gridDim.x, true));
     if (tile < 0) return;  // past the end of this XCD's band
+    // rows of CH channels at 16-byte aligned addresses: float4 loads
+    const bool vec4 = nc >= CH && ((C | c0) & 3) == 0 && ((uintptr_t)feat & 15u) == 0;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px0 = tx * kTile, py0 = ty * kTile;
     const int qx0 = px0 + (wave & 1) * 8, qy0 = py0 + (wave >> 1) * 8;
@@ -1415,6 +1417,34 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
         // pieces (the ids come from the records above), so no thread holds a
         // Gaussian's 32 channels beside the walk's cotangent registers
         __syncthreads();
+        if (vec4) {
+            // whole aligned rows: the 16-byte loads issue together (entries
+            // without a Gaussian read row 0 and are dropped)
+            constexpr int NIT = BB * F4 / kThreads;
+            static_assert(BB * F4 % kThreads == 0, "whole rounds");
+            int g[NIT];
+            float4 v[NIT];
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int k = tid + it * kThreads, j = k / F4, q = k - j * F4;
+                g[it] = __float_as_int(s_r1[j].w);
+                const int64_t gi = g[it] >= 0 ? g[it] : 0;
+                v[it] = *reinterpret_cast<const float4*>(feat + gi * C + c0 + 4 * q);
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int k = tid + it * kThreads, j = k / F4, q = k - j * F4;
+                if (g[it] >= 0) {
+                    float* d = s_fT + (4 * q) * kMxFPad + j;
+                    d[0] = v[it].x;
+                    d[kMxFPad] = v[it].y;
+                    d[2 * kMxFPad] = v[it].z;
+                    d[3 * kMxFPad] = v[it].w;
+                    plain = plain && fabsf(v[it].x) < 1e30f && fabsf(v[it].y) < 1e30f &&
+                            fabsf(v[it].z) < 1e30f && fabsf(v[it].w) < 1e30f;
+                }
+            }
+        } else
         for (int k = tid; k < BB * F4; k += kThreads) {
             const int j = k / F4, q = k - j * F4;
             const int g = __float_as_int(s_r1[j].w);
@@ -1662,6 +1692,8 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
         s_r1[BB] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     if (tid < kMfFeat) s_feat[BB * kMfFeat + tid] = 0.0f;
+    // rows of 32 channels at 16-byte aligned addresses: float4 loads
+    const bool vec4 = nc >= 4 * F4 && ((C | c0) & 3) == 0 && ((uintptr_t)feat & 15u) == 0;
 
     for (int base = 0; base < num; base += BB) {
         if (lane == 0) s_alive[wave] = alive != 0ull;
@@ -1687,8 +1719,36 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
             }
         }
         // the features: thread t stages piece t % 8 of entries t / 8 + 32 i
+        constexpr int NIT = BB * F4 / kThreads;
+        if (vec4) {
+            // whole aligned rows: the id loads, then the 16-byte feature
+            // loads, each issued together (invalid entries read row 0 and
+            // are dropped)
+            int g[NIT];
+            float4 v[NIT];
 #pragma unroll
-        for (int it = 0; it < BB * F4 / kThreads; ++it) {
+            for (int it = 0; it < NIT; ++it) {
+                const int k = base + (tid >> 3) + (kThreads / F4) * it;
+                g[it] = ids[start + min(k, num - 1)];
+                if (k >= num) g[it] = -1;
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int64_t gi = (uint32_t)g[it] < (uint64_t)n ? g[it] : 0;
+                v[it] = *reinterpret_cast<const float4*>(feat + gi * C + c0 + 4 * (tid & 7));
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                if ((uint32_t)g[it] < (uint64_t)n) {
+                    const int j = (tid >> 3) + (kThreads / F4) * it;
+                    *reinterpret_cast<float4*>(s_feat + j * kMfFeat + 4 * (tid & 7)) = v[it];
+                    finite = finite && fabsf(v[it].x) < 1e30f && fabsf(v[it].y) < 1e30f &&
+                             fabsf(v[it].z) < 1e30f && fabsf(v[it].w) < 1e30f;
+                }
+            }
+        } else {
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
             const int j = (tid >> 3) + (kThreads / F4) * it, q = tid & 7;
             const int k = base + j;
             if (k < num) {
@@ -1705,6 +1765,7 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
                              fabsf(v.z) < 1e30f && fabsf(v.w) < 1e30f;
                 }
             }
+        }
         }
         if (wave < NLW) {
 #pragma unroll
