@@ -407,16 +407,16 @@ __device__ __forceinline__ const float4& rec_at(const float4* base, int off) {
 template <int CH>
 __device__ __forceinline__ void stage_features(float4* dst, const float* f, int nc) {
     constexpr int F4 = (CH + 3) / 4;
+    float v[4 * F4];
+    if (nc >= CH) {  // uniform: every channel, loads without branches
 #pragma unroll
-    for (int k = 0; k < F4; ++k) {
-        float v[4];
+        for (int ch = 0; ch < 4 * F4; ++ch) v[ch] = ch < CH ? f[ch] : 0.0f;
+    } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int ch = 4 * k + e;
-            v[e] = (ch < CH && ch < nc) ? f[ch] : 0.0f;
-        }
-        dst[k] = make_float4(v[0], v[1], v[2], v[3]);
+        for (int ch = 0; ch < 4 * F4; ++ch) v[ch] = (ch < CH && ch < nc) ? f[ch] : 0.0f;
     }
+#pragma unroll
+    for (int k = 0; k < F4; ++k) dst[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
 }
 
 __device__ __forceinline__ float comp4(const float4& v, int e) {
@@ -569,13 +569,14 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
         if (k < num) {
             const int g = ids[start + k];
             if ((uint32_t)g < (uint64_t)n) {
+                // the record, depth and feature loads issue together
                 const float2 m = xy[g];
                 const float4 c = co[g];
+                const float dz = DEPTH ? depths[g] : 0.0f;
+                stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                 const float thr = alpha_floor_power(c.w);
                 s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
-                const float dz = DEPTH ? depths[g] : 0.0f;
                 s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, dz);
-                stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                 qm = quadrant_mask(m.x, m.y, c, px0, py0);
                 plain = plain_gaussian<CH>(m.x, m.y, c, thr, s_f[tid]) && fabsf(dz) < 1e30f;
             }
@@ -926,17 +927,28 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
     tile_span(ranges[tile], n_ids, start, num);
 
     BwdPixel<CH> st;
-    const float T_final = inside ? final_T[pid] : 1.0f;
+    // the pixel's loads issue together (clamped indices, masked after)
+    const int64_t pidc = inside ? pid : 0;
+    const float tf = final_T[pidc];
+    const int nct = n_contrib[pidc];
+    float gp[CH], bgv[CH];
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+        gp[ch] = grad_out[pidc * C + c0 + min(ch, nc - 1)];
+        bgv[ch] = bg ? bg[c0 + min(ch, nc - 1)] : 0.0f;
+    }
+    const float gt = grad_T ? grad_T[pidc] : 0.0f;
+    const float T_final = inside ? tf : 1.0f;
     st.T = T_final;
-    st.last = inside ? n_contrib[pid] : 0;
+    st.last = inside ? nct : 0;
     float bg_dot = 0.0f;
 #pragma unroll
     for (int ch = 0; ch < CH; ++ch) {
-        st.gpix[ch] = (inside && ch < nc) ? grad_out[pid * C + c0 + ch] : 0.0f;
-        if (ch < nc) bg_dot = bg_dot + (bg ? bg[c0 + ch] : 0.0f) * st.gpix[ch];
+        st.gpix[ch] = (inside && ch < nc) ? gp[ch] : 0.0f;
+        if (ch < nc) bg_dot = bg_dot + bgv[ch] * st.gpix[ch];
     }
     // The alpha output's cotangent enters once, with the first channel block.
-    if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + grad_T[pid];
+    if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + gt;
     st.Q = T_final * bg_dot;
 
     // the padding record (written before the barrier below)
@@ -971,12 +983,13 @@ __global__ __launch_bounds__(kThreads, bwd_min_waves(CH)) void k_raster_bwd(
             if (k < num) {
                 const int g = ids[start + k];
                 if ((uint32_t)g < (uint64_t)n) {
+                    // the record and feature loads issue together
                     const float2 m = xy[g];
                     const float4 c = co[g];
+                    stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                     const float thr = alpha_floor_power(c.w);
                     s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
                     r1 = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, __int_as_float(g));
-                    stage_features<CH>(s_f[tid], feat + (int64_t)g * C + c0, nc);
                     qm = quadrant_mask(m.x, m.y, c, px0, py0);
 #pragma unroll
                     for (int q = 0; q < kWaves; ++q)
@@ -1336,13 +1349,27 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_bwd_mx(
     tile_span(ranges[tile], n_ids, start, num);
 
     MxPixel st;
-    const float T_final = inside ? final_T[pid] : 1.0f;
+    // the pixel's loads issue together (clamped indices, masked after)
+    const int64_t pidc = inside ? pid : 0;
+    const float tf = final_T[pidc];
+    const int nct = n_contrib[pidc];
+    const float gt = grad_T ? grad_T[pidc] : 0.0f;
+    const float T_final = inside ? tf : 1.0f;
     st.T = T_final;
-    st.last = inside ? n_contrib[pid] : 0;
+    st.last = inside ? nct : 0;
     float bg_dot = 0.0f;
-    for (int ch = 0; ch < nc; ++ch)
-        bg_dot = bg_dot + (bg ? bg[c0 + ch] : 0.0f) * (inside ? grad_out[pid * C + c0 + ch] : 0.0f);
-    if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + grad_T[pid];
+    {
+        float gp[CH], bgv[CH];
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+            gp[ch] = grad_out[pidc * C + c0 + min(ch, nc - 1)];
+            bgv[ch] = bg ? bg[c0 + min(ch, nc - 1)] : 0.0f;
+        }
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch)
+            if (ch < nc) bg_dot = bg_dot + bgv[ch] * (inside ? gp[ch] : 0.0f);
+    }
+    if (inside && c0 == 0 && grad_T) bg_dot = bg_dot + gt;
     st.Q = T_final * bg_dot;
     // the quadrant's cotangents in the two B-operand layouts (pixel q of
     // the quadrant is (q % 8, q / 8))
