@@ -519,8 +519,12 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         const int b = tid * kBPT + k;
         uint32_t s = 0;
         if (b < kR) {
-#pragma unroll 4
-            for (int c = 0; c < kHistCopies; ++c) s += hist[c * hist_stride + b];
+            // the copies' loads issue together (one round trip)
+            uint32_t v[kHistCopies];
+#pragma unroll
+            for (int c = 0; c < kHistCopies; ++c) v[c] = hist[c * hist_stride + b];
+#pragma unroll
+            for (int c = 0; c < kHistCopies; ++c) s += v[c];
         }
         dsum[k] = s;
     }
@@ -1020,15 +1024,28 @@ __global__ __launch_bounds__(kMaxFastTiles) void k_seg_count(
     s_diff[tid] = 0u;
     if (tid == 0) s_diff[kMaxFastTiles] = 0u;
     __syncthreads();
-    for (uint32_t k = sg.k0 + tid; k < sg.k1; k += kMaxFastTiles) {
-        const uint32_t doff = e_doff[sg.rb + k];
-        if (doff >= sg.e) continue;
-        const uint32_t p = e_pack[sg.rb + k];
-        const uint32_t x0 = p & 0xFFu, w = ((p >> 8) & 0xFFu) + 1u;
-        const uint32_t from = max(sg.a, doff) - doff;
-        const uint32_t to = min(sg.e, doff + w) - doff;
-        atomicAdd(&s_diff[min(x0 + from, (uint32_t)kMaxFastTiles)], 1u);
-        atomicAdd(&s_diff[min(x0 + to, (uint32_t)kMaxFastTiles)], 0xFFFFFFFFu);
+    // four entries per thread per round, their loads issued together
+    // (clamped to the segment's last entry, masked after)
+    constexpr int kBatch = 4;
+    for (uint32_t k0 = sg.k0 + tid; k0 < sg.k1; k0 += kBatch * kMaxFastTiles) {
+        uint32_t dv[kBatch], pv[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const uint32_t k = min(k0 + i * kMaxFastTiles, sg.k1 - 1u);
+            dv[i] = e_doff[sg.rb + k];
+            pv[i] = e_pack[sg.rb + k];
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const uint32_t doff = dv[i];
+            if (k0 + i * kMaxFastTiles >= sg.k1 || doff >= sg.e) continue;
+            const uint32_t p = pv[i];
+            const uint32_t x0 = p & 0xFFu, w = ((p >> 8) & 0xFFu) + 1u;
+            const uint32_t from = max(sg.a, doff) - doff;
+            const uint32_t to = min(sg.e, doff + w) - doff;
+            atomicAdd(&s_diff[min(x0 + from, (uint32_t)kMaxFastTiles)], 1u);
+            atomicAdd(&s_diff[min(x0 + to, (uint32_t)kMaxFastTiles)], 0xFFFFFFFFu);
+        }
     }
     __syncthreads();
     uint32_t tot;
@@ -1063,10 +1080,10 @@ __global__ __launch_bounds__(kScanParts * kMaxFastTiles) void k_tile_scan(
         for (uint32_t s = s0; s < s1; s += kBatch) {
             uint32_t v[kBatch];
 #pragma unroll
-            for (int k = 0; k < kBatch; ++k)
-                v[k] = s + k < s1 ? sc[(int64_t)(s + k) * kMaxFastTiles + x] : 0u;
+            for (int k = 0; k < kBatch; ++k)  // clamped: the loads issue together
+                v[k] = sc[(int64_t)min(s + k, s1 - 1u) * kMaxFastTiles + x];
 #pragma unroll
-            for (int k = 0; k < kBatch; ++k) sum += v[k];
+            for (int k = 0; k < kBatch; ++k) sum += s + k < s1 ? v[k] : 0u;
         }
     }
     s_part[q][x] = sum;
@@ -1095,7 +1112,7 @@ __global__ __launch_bounds__(kScanParts * kMaxFastTiles) void k_tile_scan(
             uint32_t v[kBatch];
 #pragma unroll
             for (int k = 0; k < kBatch; ++k)
-                v[k] = s + k < s1 ? sc[(int64_t)(s + k) * kMaxFastTiles + x] : 0u;
+                v[k] = s + k < s1 ? sc[(int64_t)min(s + k, s1 - 1u) * kMaxFastTiles + x] : 0u;
 #pragma unroll
             for (int k = 0; k < kBatch; ++k) {
                 const uint32_t t = v[k];

@@ -2007,12 +2007,15 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __rest
     // Bands of more than kBandItems * 1024 tiles are placed in rounds, each
     // round sorted on its own (the rounds in raster order).
     for (int r0 = lo; r0 < hi; r0 += kBandItems * kOrderThreads) {
-        int bk[kBandItems];
+        int bk[kBandItems], est[kBandItems];
         uint32_t rk[kBandItems];
+#pragma unroll
+        for (int k = 0; k < kBandItems; ++k)  // clamped: the loads issue together
+            est[k] = estimate(min(r0 + k * kOrderThreads + tid, hi - 1));
 #pragma unroll
         for (int k = 0; k < kBandItems; ++k) {
             const int t = r0 + k * kOrderThreads + tid;
-            bk[k] = t < hi ? order_bucket(estimate(t)) : -1;
+            bk[k] = t < hi ? order_bucket(est[k]) : -1;
         }
 #pragma unroll
         for (int k = 0; k < kBandItems; ++k) {
