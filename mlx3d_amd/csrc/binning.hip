@@ -569,7 +569,10 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
                 s_cnt[w][b] = acc;
                 acc += c;
             }
-            status_store(status + chunk * kR + b, (chunk == 0 ? kFlagInc : kFlagAgg) | acc);
+            // a digit no key of the pass holds (zero in the histogram) is
+            // never looked up: no status, no look-back
+            if (dsum[k] != 0u)
+                status_store(status + chunk * kR + b, (chunk == 0 ? kFlagInc : kFlagAgg) | acc);
         }
         local[k] = acc;
         lsum += acc;
@@ -603,7 +606,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         const int b = tid * kBPT + k;
         if (b < kR) {
             uint32_t prefix = 0;
-            if (chunk > 0) {
+            if (chunk > 0 && dsum[k] != 0u) {
                 prefix = look_back(status, chunk, kR, b, err);
                 status_store(status + chunk * kR + b, kFlagInc | ((prefix + local[k]) & kCountMask));
             }
