@@ -1909,15 +1909,13 @@ __host__ __device__ inline int64_t tile_order_words(int64_t tiles) {
 }
 
 template <bool BWD>
-__global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __restrict__ ranges,
-                                                              const int* __restrict__ work,
-                                                              int64_t n_ids, int tiles,
-                                                              int* __restrict__ order) {
+__device__ __forceinline__ void tile_order_band(int band, const int2* __restrict__ ranges,
+                                                const int* __restrict__ work, int64_t n_ids,
+                                                int tiles, int* __restrict__ order) {
     constexpr int kBandItems = 4;
     __shared__ uint32_t s_cnt[kOrderBuckets * kBandItems * (kOrderThreads / kWave)];
     __shared__ uint32_t s_w[kOrderThreads / kWave];
     __shared__ int s_start[kOrderBands + 1];  // first tile of each band
-    const int band = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cap = 2 * ((tiles + kOrderBands - 1) / kOrderBands);
     auto estimate = [&](int t) {
@@ -2071,17 +2069,47 @@ __global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __rest
     }
 }
 
-// Clears the four gradient outputs in one launch (a fill kernel rather than
-// hipMemsetAsync, so the call can sit inside a captured graph).
-__global__ __launch_bounds__(256) void k_zero_grads(float* __restrict__ a, int64_t na,
-                                                    float* __restrict__ b, int64_t nb,
-                                                    float* __restrict__ c, int64_t nc,
-                                                    float* __restrict__ d, int64_t nd) {
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < na; i += stride) a[i] = 0.0f;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nb; i += stride) b[i] = 0.0f;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nc; i += stride) c[i] = 0.0f;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nd; i += stride) d[i] = 0.0f;
+// One workgroup per band (the forward's order, or the backward's).
+template <bool BWD>
+__global__ __launch_bounds__(kOrderThreads) void k_tile_order(const int2* __restrict__ ranges,
+                                                              const int* __restrict__ work,
+                                                              int64_t n_ids, int tiles,
+                                                              int* __restrict__ order) {
+    tile_order_band<BWD>(blockIdx.x, ranges, work, n_ids, tiles, order);
+}
+
+// The gradient outputs to clear: one record (a, na floats, 16-byte aligned,
+// na a multiple of 4) or four arrays.
+struct ZeroGrads {
+    float* p[4];
+    int64_t n[4];
+    bool record;
+};
+
+// The backward's prologue in one launch: workgroups [0, bands) build the
+// backward's tile order from the forward's per-tile work (bands = 0 without
+// one), the others clear the gradient outputs (a fill kernel rather than
+// hipMemsetAsync, so the call can sit inside a captured graph).  The order's
+// few long-lived workgroups run beside the clearing instead of after it.
+__global__ __launch_bounds__(kOrderThreads) void k_bwd_prologue(ZeroGrads z, int bands,
+                                                                const int* __restrict__ work,
+                                                                int64_t n_ids, int tiles,
+                                                                int* __restrict__ order) {
+    if ((int)blockIdx.x < bands) {
+        tile_order_band<true>(blockIdx.x, nullptr, work, n_ids, tiles, order);
+        return;
+    }
+    const int64_t b = (int64_t)blockIdx.x - bands;
+    const int64_t stride = ((int64_t)gridDim.x - bands) * kOrderThreads;
+    if (z.record) {
+        float4* a = reinterpret_cast<float4*>(z.p[0]);
+        for (int64_t i = b * kOrderThreads + threadIdx.x; i < z.n[0] / 4; i += stride)
+            a[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        for (int64_t i = b * kOrderThreads + threadIdx.x; i < z.n[r]; i += stride) z.p[r][i] = 0.0f;
 }
 
 int pick_ch(int nc) {
@@ -2227,18 +2255,6 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
         return GSX_ERR_INVALID;
     hipStream_t st = (hipStream_t)stream;
     if (n == 0) return GSX_OK;
-    {
-        const int64_t most = rec ? (int64_t)grad_stride * n : std::max<int64_t>((int64_t)C, 3) * n;
-        const unsigned blocks = (unsigned)std::min<int64_t>((most + 255) / 256, 8192);
-        if (rec)
-            hipLaunchKernelGGL(k_zero_grads, dim3(blocks), dim3(256), 0, st, g_means2d,
-                               (int64_t)grad_stride * n, (float*)nullptr, (int64_t)0,
-                               (float*)nullptr, (int64_t)0, (float*)nullptr, (int64_t)0);
-        else
-            hipLaunchKernelGGL(k_zero_grads, dim3(blocks), dim3(256), 0, st, g_means2d, 2 * n,
-                               g_conics, 3 * n, g_features, (int64_t)C * n, g_opacities, n);
-        GSX_LAUNCH_CHECK();
-    }
     const int tiles_x = (width + kTile - 1) / kTile;
     const int tiles_y = (height + kTile - 1) / kTile;
     const int tiles = tiles_x * tiles_y;
@@ -2246,9 +2262,29 @@ int gsx_raster_bwd(int64_t n, int32_t C, const float* means2d, const float* coni
     // call's order, one entry per workgroup
     int* const order = tile_order ? tile_order + tiles : nullptr;
     const dim3 grid((unsigned)(order ? tile_order_words(tiles) - tiles : tiles));
-    if (order) {
-        hipLaunchKernelGGL(k_tile_order<true>, dim3(kOrderBands), dim3(kOrderThreads), 0, st,
-                           (const int2*)nullptr, (const int*)tile_order, num_ids, tiles, order);
+    {
+        // gradient clearing and the tile order in one launch
+        ZeroGrads z{};
+        z.record = rec;
+        if (rec) {
+            z.p[0] = g_means2d;
+            z.n[0] = (int64_t)grad_stride * n;
+        } else {
+            z.p[0] = g_means2d;
+            z.n[0] = 2 * n;
+            z.p[1] = g_conics;
+            z.n[1] = 3 * n;
+            z.p[2] = g_features;
+            z.n[2] = (int64_t)C * n;
+            z.p[3] = g_opacities;
+            z.n[3] = n;
+        }
+        const int64_t most = rec ? z.n[0] / 4 : std::max<int64_t>((int64_t)C, 3) * n;
+        const int bands = order ? kOrderBands : 0;
+        const unsigned blocks =
+            (unsigned)std::min<int64_t>((most + kOrderThreads - 1) / kOrderThreads, 2048);
+        hipLaunchKernelGGL(k_bwd_prologue, dim3(blocks + (unsigned)bands), dim3(kOrderThreads), 0,
+                           st, z, bands, (const int*)tile_order, num_ids, tiles, order);
         GSX_LAUNCH_CHECK();
     }
     for (int c0 = 0; c0 < C; c0 += kMaxChunk) {
