@@ -204,6 +204,105 @@ __device__ __forceinline__ uint32_t look_back(const uint32_t* status, int64_t ch
     return prefix;
 }
 
+// Two-level look-back for many chunks per column.  Chunks are grouped in
+// blocks of kLookBlock; besides its status word (aggregate, then inclusive
+// prefix) every chunk writes its aggregate once more into `aggs`, and the
+// last chunk of each block publishes the block's status in `bstat`: the sum
+// of the block's aggregates as soon as they are all published, then the
+// inclusive prefix through the block.  A chunk walks its own block's
+// predecessors, then the block statuses, so the prefix of chunk c needs
+// about c / (8 kLookBlock) rounds instead of c / 8 when all chunks publish
+// together (an inclusive prefix otherwise spreads 8 chunks per round).  The
+// in-block reads take the whole block at once (one round trip).
+constexpr int kLookBlock = 16;
+
+// Prefix of the column over chunks [base, chunk) of the chunk's block
+// (base = its first chunk), stopping at the nearest inclusive one; *done
+// when one was found (or the block is the first).
+__device__ __forceinline__ uint32_t look_back_in_block(const uint32_t* status, int64_t chunk,
+                                                       int stride, int col, uint32_t* err,
+                                                       bool* done) {
+    const int64_t base = chunk - chunk % kLookBlock;
+    uint32_t prefix = 0;
+    uint32_t spins = 0;
+    int64_t c = chunk - 1;
+    *done = base == 0 && chunk == 0;
+    while (c >= base) {
+        uint32_t s[kLookBlock];
+#pragma unroll
+        for (int k = 0; k < kLookBlock; ++k)
+            s[k] = c - k >= base ? status_load(status + (c - k) * stride + col) : 0u;
+        int used = 0;
+        bool stalled = false, found = false;
+#pragma unroll
+        for (int k = 0; k < kLookBlock; ++k) {
+            if (found || stalled || c - k < base) continue;
+            const uint32_t flag = s[k] & ~kCountMask;
+            if (flag == 0u) {
+                stalled = true;
+                continue;
+            }
+            prefix += s[k] & kCountMask;
+            ++used;
+            found = flag == kFlagInc;
+        }
+        if (found) {
+            *done = true;
+            break;
+        }
+        c -= used;
+        if (stalled) {
+            if (++spins > kSpinLimit) {
+                atomicOr(err, GSX_BIN_ERR_LOOKBACK);
+                *done = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    // chunk 0 is inclusive: a walk in the first block always ends there
+    if (base == 0) *done = true;
+    return prefix;
+}
+
+// The aggregate of the last chunk's block: its own count plus the
+// aggregates the block's other chunks wrote into `aggs` (polled until all
+// are there, bounded as above).
+__device__ __forceinline__ uint32_t block_aggregate(const uint32_t* aggs, int64_t chunk,
+                                                    int stride, int col, uint32_t own,
+                                                    uint32_t* err) {
+    const int64_t base = chunk - chunk % kLookBlock;
+    uint32_t sum = own;
+    uint32_t spins = 0;
+    for (int64_t c = base; c < chunk;) {
+        uint32_t s[kLookBlock];
+#pragma unroll
+        for (int k = 0; k < kLookBlock; ++k)
+            s[k] = c + k < chunk ? status_load(aggs + (c + k) * stride + col) : kFlagAgg;
+        int got = 0;
+        bool stalled = false;
+#pragma unroll
+        for (int k = 0; k < kLookBlock; ++k) {
+            if (stalled || c + k >= chunk) continue;
+            if ((s[k] & ~kCountMask) == 0u) {
+                stalled = true;
+                continue;
+            }
+            sum += s[k] & kCountMask;
+            ++got;
+        }
+        c += got;
+        if (stalled) {
+            if (++spins > kSpinLimit) {
+                atomicOr(err, GSX_BIN_ERR_LOOKBACK);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    return sum;
+}
+
 // The same for a single counter column (stride 1, column 0), walked by one
 // whole wave: each round reads the 64 statuses before the current position
 // at once (lane l: chunk c - l) and adds them up to the nearest inclusive
@@ -493,7 +592,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n_host,
     const uint32_t* __restrict__ n_dev, int shift, int nbits, const uint32_t* __restrict__ hist,
     int hist_stride, bool skip_constant, uint32_t* __restrict__ status,
-    uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ aggs, uint32_t* __restrict__ bstat, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ err, Publish pub,
     const uint32_t* __restrict__ route_hist, uint32_t* __restrict__ keys_alt,
     uint32_t* __restrict__ vals_alt) {
@@ -571,8 +670,10 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             }
             // a digit no key of the pass holds (zero in the histogram) is
             // never looked up: no status, no look-back
-            if (dsum[k] != 0u)
+            if (dsum[k] != 0u) {
                 status_store(status + chunk * kR + b, (chunk == 0 ? kFlagInc : kFlagAgg) | acc);
+                if (bstat) status_store(aggs + chunk * kR + b, kFlagAgg | acc);
+            }
         }
         local[k] = acc;
         lsum += acc;
@@ -606,7 +707,26 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         const int b = tid * kBPT + k;
         if (b < kR) {
             uint32_t prefix = 0;
-            if (chunk > 0 && dsum[k] != 0u) {
+            if (dsum[k] != 0u && bstat) {
+                // two levels: the block's last chunk publishes the block's
+                // aggregate first, its inclusive prefix after the walk
+                const int64_t blk = chunk / kLookBlock;
+                const bool last = chunk % kLookBlock == kLookBlock - 1;
+                if (last)
+                    status_store(bstat + blk * kR + b,
+                                 (blk == 0 ? kFlagInc : kFlagAgg) |
+                                     (block_aggregate(aggs, chunk, kR, b, local[k], err) &
+                                      kCountMask));
+                bool done;
+                prefix = look_back_in_block(status, chunk, kR, b, err, &done);
+                if (!done) prefix += look_back(bstat, blk, kR, b, err);
+                if (chunk > 0)
+                    status_store(status + chunk * kR + b,
+                                 kFlagInc | ((prefix + local[k]) & kCountMask));
+                if (last && blk > 0)
+                    status_store(bstat + blk * kR + b,
+                                 kFlagInc | ((prefix + local[k]) & kCountMask));
+            } else if (chunk > 0 && dsum[k] != 0u) {
                 prefix = look_back(status, chunk, kR, b, err);
                 status_store(status + chunk * kR + b, kFlagInc | ((prefix + local[k]) & kCountMask));
             }
@@ -1560,6 +1680,15 @@ struct Taker {
     }
 };
 
+// Look-back words of one depth pass over `chunks` chunks and `radix`
+// digits: the statuses, the aggregates and the block statuses.
+inline int64_t depth_pass_words(int64_t chunks, int radix) {
+    return (2 * chunks + ceil_div(chunks, kLookBlock)) * radix;
+}
+inline int64_t depth_status_words(int64_t chunks) {
+    return 3 * depth_pass_words(chunks, kDepthRadix) + depth_pass_words(chunks, 1 << kDepthTopBits);
+}
+
 DepthLayout make_depth_layout(int64_t n) {
     DepthLayout L{};
     Taker take;
@@ -1567,8 +1696,7 @@ DepthLayout make_depth_layout(int64_t n) {
     L.depth_chunks = ceil_div((int64_t)nn, kDepthChunk);
     L.scan_chunks = ceil_div((int64_t)nn, kScanChunk);
     L.hist_blocks = ceil_div((int64_t)nn, kHistThreads * kHistItems);
-    L.status_words =
-        L.depth_chunks * (3 * kDepthRadix + (1 << kDepthTopBits)) + L.scan_chunks;
+    L.status_words = depth_status_words(L.depth_chunks) + L.scan_chunks;
     for (int k = 0; k < 3; ++k) {
         L.dk[k] = take(4 * nn);
         L.dv[k] = take(4 * nn);
@@ -1707,7 +1835,9 @@ int depth_phase(int64_t n, const uint32_t* depth_keys, void* depth_ws, int64_t d
     const Publish none{nullptr, nullptr, 0};
     const Publish pub = host_status ? make_publish(bin_status, host_status, seq) : none;
     const unsigned grid = (unsigned)L.depth_chunks;
-    const size_t per_pass = (size_t)L.depth_chunks * kDepthRadix;
+    // per pass: statuses, aggregates, block statuses (depth_pass_words)
+    const size_t per_pass = (size_t)depth_pass_words(L.depth_chunks, kDepthRadix);
+    const size_t chunk_words = (size_t)L.depth_chunks * kDepthRadix;
     const uint32_t* nil = nullptr;
     uint32_t* no = nullptr;
     auto pass10 = [&](int p, const uint32_t* kin, const uint32_t* vin, uint32_t* ko,
@@ -1716,7 +1846,9 @@ int depth_phase(int64_t n, const uint32_t* depth_keys, void* depth_ws, int64_t d
         hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems, kDepthBits>), dim3(grid),
                            dim3(kDepthThreads), 0, st, kin, vin, n, nil, p * kDepthBits,
                            kDepthBits, hist + p * kDepthRadix, kDepthHistStride, false,
-                           status + p * per_pass, ko, vo, bin_status + 1, pb, route,
+                           status + p * per_pass, status + p * per_pass + chunk_words,
+                           status + p * per_pass + 2 * chunk_words, ko, vo, bin_status + 1, pb,
+                           route,
                            ka, va);
     };
     pass10(0, depth_keys, nil, dk[0], dv[0], pub, nil, no, no);
@@ -1726,7 +1858,10 @@ int depth_phase(int64_t n, const uint32_t* depth_keys, void* depth_ws, int64_t d
     hipLaunchKernelGGL((k_onesweep<kDepthThreads, kDepthItems, kDepthTopBits>), dim3(grid),
                        dim3(kDepthThreads), 0, st, dk[0], dv[0], n, nil, kDepthTopShift,
                        kDepthTopBits, hist + 3 * kDepthRadix, kDepthHistStride, true,
-                       status + 3 * per_pass, dk[2], dv[2], bin_status + 1, none, nil,
+                       status + 3 * per_pass,
+                       status + 3 * per_pass + (size_t)L.depth_chunks * (1 << kDepthTopBits),
+                       status + 3 * per_pass + 2 * (size_t)L.depth_chunks * (1 << kDepthTopBits),
+                       dk[2], dv[2], bin_status + 1, none, nil,
                        no, no);
     GSX_LAUNCH_CHECK();
     return GSX_OK;
@@ -1759,8 +1894,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
     uint32_t* err = bin_status + 1;
     const uint32_t* gids = at<uint32_t>(depth_ws, D.dv[2]);  // the depth sort's order
     uint32_t* offs = at<uint32_t>(depth_ws, D.offs);
-    uint32_t* sstatus = at<uint32_t>(depth_ws, D.status) +
-                        (size_t)D.depth_chunks * (3 * kDepthRadix + (1 << kDepthTopBits));
+    uint32_t* sstatus = at<uint32_t>(depth_ws, D.status) + depth_status_words(D.depth_chunks);
     uint32_t* owner = at<uint32_t>(tile_ws, 0);
     const Publish none{nullptr, nullptr, 0};
     const Publish pub = host_status ? make_publish(bin_status, host_status, seq) : none;
@@ -1846,8 +1980,9 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
                            tv[cur], capacity, (const uint32_t*)d_total, p * kRadixBits,
                            std::min(kRadixBits, tile_bits - p * kRadixBits),
                            tile_hist + p * kRadix, kTileHistStride, false,
-                           tstatus + (size_t)p * L.tile_chunks * kRadix,
-                           tk[cur ^ 1], tv[cur ^ 1], err, nopub, (const uint32_t*)nullptr,
+                           tstatus + (size_t)p * L.tile_chunks * kRadix, (uint32_t*)nullptr,
+                           (uint32_t*)nullptr, tk[cur ^ 1], tv[cur ^ 1], err, nopub,
+                           (const uint32_t*)nullptr,
                            (uint32_t*)nullptr, (uint32_t*)nullptr);
         cur ^= 1;
     }
