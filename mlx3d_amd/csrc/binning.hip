@@ -27,7 +27,7 @@
 //                  with each entry's offset in its row's duplicate sequence
 //                  (a second look-back column of width sums).
 //     seg count    a row's duplicates (its entries expanded left to right,
-//                  in depth order) are cut into 4096-duplicate segments;
+//                  in depth order) are cut into 2048-duplicate segments;
 //                  per segment and tile column, the number of duplicates.
 //     tile scan    per row: exclusive prefix over the row's segments of each
 //                  column's counts, the tile totals, the tile ranges
@@ -97,7 +97,10 @@ constexpr int kHistThreads = 1024, kHistItems = 8;
 constexpr int kScanThreads = 1024, kScanItems = 4, kScanChunk = kScanThreads * kScanItems;
 constexpr int kEmitThreads = 1024, kEmitItems = 4, kEmitDups = kEmitThreads * kEmitItems;
 constexpr int kRowChunk = kEmitDups;  // row entries per row-emission workgroup
-constexpr int kSegDups = kEmitDups;   // duplicates per placement segment
+// placement: 512 threads x 4 duplicates per segment (four workgroups per
+// CU: 38 KB of LDS each)
+constexpr int kPlaceThreads = 512;
+constexpr int kSegDups = kPlaceThreads * kEmitItems;  // duplicates per placement segment
 // fast tile path limits: tile rows and columns fit an 8-bit digit
 constexpr int kMaxFastTiles = 256;
 constexpr int kRowWords = kMaxFastTiles + 1;  // one row histogram (diff form)
@@ -779,11 +782,25 @@ __device__ __forceinline__ void row_plan(const uint32_t* __restrict__ row_diff, 
     const uint32_t db = block_excl_scan<kScanThreads>(tid < tiles_y ? dup : 0u, s_w, &dup_tot);
     __syncthreads();
     const uint32_t sb = block_excl_scan<kScanThreads>(segs, s_w, &seg_tot);
+    __shared__ uint32_t s_sb[kMaxFastTiles + 1];  // segment base of each row
     if (tid < tiles_y) {
         plan->rowcnt[tid] = cnt;
         plan->rowdup[tid] = dup;
-        for (uint32_t k = 0; k < segs; ++k)
-            if ((int64_t)(sb + k) < max_segs) segrow[sb + k] = (uint32_t)tid;
+        s_sb[tid] = sb;
+    }
+    if (tid == 0) s_sb[tiles_y] = seg_tot;
+    __syncthreads();
+    // the row of every segment, spread over the workgroup: the last row
+    // whose segment base is <= k (rows without segments share a base with
+    // the next row, so the search takes the last of equal bases)
+    for (uint32_t k = tid; k < seg_tot && (int64_t)k < max_segs; k += kScanThreads) {
+        int lo = 0, hi = tiles_y - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_sb[mid] <= k) lo = mid;
+            else hi = mid - 1;
+        }
+        segrow[k] = (uint32_t)lo;
     }
     if (tid <= tiles_y) {
         plan->rowbase[tid] = eb;
@@ -1257,18 +1274,18 @@ __global__ __launch_bounds__(kScanParts * kMaxFastTiles) void k_tile_scan(
 // entry whose span holds i, is written into the segment's slots by the
 // entry itself.  With pub.host, workgroup 0 copies the status words to
 // the host first (every earlier kernel of the binning has finished).
-__global__ __launch_bounds__(kEmitThreads) void k_place(
+__global__ __launch_bounds__(kPlaceThreads) void k_place(
     int64_t cap, const RowPlan* __restrict__ plan, const uint32_t* __restrict__ segrow,
     const uint32_t* __restrict__ segk0, int tiles_x, const uint32_t* __restrict__ e_gid,
     const uint32_t* __restrict__ e_pack, const uint32_t* __restrict__ e_doff,
     const uint32_t* __restrict__ sc, int32_t* __restrict__ ids, Publish pub) {
-    constexpr int kWaves = kEmitThreads / 64;
+    constexpr int kWaves = kPlaceThreads / 64;
     __shared__ uint32_t s_ent[3 * kSegDups];   // staged (doff, gid, pack); then (pos, gid)
     __shared__ uint16_t s_own[kSegDups];
     __shared__ uint32_t s_cnt[kWaves][kMaxFastTiles];
     __shared__ uint32_t s_base[kMaxFastTiles];
     __shared__ uint32_t s_dexcl[kMaxFastTiles];
-    __shared__ uint32_t s_w[kEmitThreads / 64];
+    __shared__ uint32_t s_w[kPlaceThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (pub.host && blockIdx.x == 0 && tid == 0) publish(pub);
     if ((int64_t)plan->dups > cap) return;
@@ -1278,9 +1295,9 @@ __global__ __launch_bounds__(kEmitThreads) void k_place(
     uint32_t* s_doff = s_ent;
     uint32_t* s_gid = s_ent + kSegDups;
     uint32_t* s_pack = s_ent + 2 * kSegDups;
-    for (int k = tid; k < kWaves * kMaxFastTiles; k += kEmitThreads) (&s_cnt[0][0])[k] = 0u;
+    for (int k = tid; k < kWaves * kMaxFastTiles; k += kPlaceThreads) (&s_cnt[0][0])[k] = 0u;
     if (tid < tiles_x) s_base[tid] = sc[(int64_t)blockIdx.x * kMaxFastTiles + tid];
-    for (int k = tid; k < ne; k += kEmitThreads) {
+    for (int k = tid; k < ne; k += kPlaceThreads) {
         const uint32_t e = sg.rb + sg.k0 + (uint32_t)k;
         const uint32_t doff = e_doff[e];
         const uint32_t pack = e_pack[e];
@@ -1330,7 +1347,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_place(
         }
     }
     uint32_t tot;
-    const uint32_t dexcl = block_excl_scan<kEmitThreads>(tid < kMaxFastTiles ? local : 0u, s_w, &tot);
+    const uint32_t dexcl = block_excl_scan<kPlaceThreads>(tid < kMaxFastTiles ? local : 0u, s_w, &tot);
     if (tid < kMaxFastTiles) s_dexcl[tid] = dexcl;
     __syncthreads();
     uint32_t* q_pos = s_ent;
@@ -1346,7 +1363,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_place(
         }
     }
     __syncthreads();
-    for (uint32_t j = tid; j < nd; j += kEmitThreads) {
+    for (uint32_t j = tid; j < nd; j += kPlaceThreads) {
         const uint32_t pos = q_pos[j];
         if (pos < (uint64_t)cap) ids[pos] = (int32_t)q_gid[j];  // always true for a consistent plan
     }
@@ -1729,7 +1746,7 @@ TileLayout make_tile_layout(int64_t cap, int64_t num_tiles) {
     {
         // the row entries are at most the duplicates (each binned Gaussian
         // has at least one column per row), the segments at most one per
-        // 4096 duplicates plus one partial per row
+        // kSegDups duplicates plus one partial per row
         Taker take;
         L.row_chunks = ceil_div((int64_t)cc, kRowChunk);
         L.segments = ceil_div((int64_t)cc, kSegDups) + kMaxFastTiles;
@@ -1935,7 +1952,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
         hipLaunchKernelGGL(k_tile_scan, dim3((unsigned)tiles_y), dim3(kScanParts * kMaxFastTiles),
                            0, st,
                            capacity, (const RowPlan*)plan, tiles_x, sc, (int2*)tile_ranges);
-        hipLaunchKernelGGL(k_place, dim3((unsigned)L.segments), dim3(kEmitThreads), 0, st,
+        hipLaunchKernelGGL(k_place, dim3((unsigned)L.segments), dim3(kPlaceThreads), 0, st,
                            capacity, (const RowPlan*)plan, (const uint32_t*)segrow,
                            (const uint32_t*)segk0, tiles_x, (const uint32_t*)e_gid,
                            (const uint32_t*)e_pack, (const uint32_t*)e_doff, (const uint32_t*)sc,
