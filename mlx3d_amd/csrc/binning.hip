@@ -615,29 +615,32 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     // The first ceil(n / chunk) workgroups are the live chunks; the rest
     // leave at once.
     if ((int64_t)blockIdx.x * kChunk >= n) return;
+    // digit totals over the histogram copies (the copies' loads issue
+    // together, one round trip)
     uint32_t dsum[kBPT];
+    auto digit_totals = [&]() {
 #pragma unroll
-    for (int k = 0; k < kBPT; ++k) {
-        const int b = tid * kBPT + k;
-        uint32_t s = 0;
-        if (b < kR) {
-            // the copies' loads issue together (one round trip)
-            uint32_t v[kHistCopies];
+        for (int k = 0; k < kBPT; ++k) {
+            const int b = tid * kBPT + k;
+            uint32_t s = 0;
+            if (b < kR) {
+                uint32_t v[kHistCopies];
 #pragma unroll
-            for (int c = 0; c < kHistCopies; ++c) v[c] = hist[c * hist_stride + b];
+                for (int c = 0; c < kHistCopies; ++c) v[c] = hist[c * hist_stride + b];
 #pragma unroll
-            for (int c = 0; c < kHistCopies; ++c) s += v[c];
+                for (int c = 0; c < kHistCopies; ++c) s += v[c];
+            }
+            dsum[k] = s;
         }
-        dsum[k] = s;
-    }
+    };
     if (skip_constant) {
+        digit_totals();
         bool whole = false;
 #pragma unroll
         for (int k = 0; k < kBPT; ++k) whole |= (int64_t)dsum[k] == n;
         if (__syncthreads_or(whole)) return;  // identity permutation
     }
     for (int k = tid; k < kWaves * kR; k += THREADS) (&s_cnt[0][0])[k] = 0u;
-    __syncthreads();
     const int64_t chunk = blockIdx.x;
     const int64_t base = chunk * kChunk + wave * (64 * ITEMS);
     const uint64_t lt = (1ull << lane) - 1ull;
@@ -648,6 +651,10 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         key[r] = i < n ? keys_in[i] : 0u;
         val[r] = i < n ? (vals_in ? vals_in[i] : (uint32_t)i) : 0u;
     }
+    // without the skip test the totals are first needed after the ranking:
+    // their loads go out behind the keys'
+    if (!skip_constant) digit_totals();
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < ITEMS; ++r) {
         const bool valid = base + r * 64 + lane < n;
