@@ -167,11 +167,29 @@ __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, in
 // is finite and small enough that the float32 power is finite and, for a
 // pixel that passes the alpha bound, within [-86, 0]: then exp needs no
 // range handling and a zero weight leaves the accumulators unchanged.
-template <int CH>
+//
+// SIGN (the forwards): the conic must also be well conditioned,
+// det > 1e-6 (a + c)^2 with a + c in [1e-12, 1e19), and then the float32
+// power (splat_power) is never positive, so the loop needs no power > 0
+// test.  Its rounding error is at
+// most eps (a dx^2 + c dy^2 + 2 |b dx dy|) <= 1.25 eps (a + c) |d|^2
+// (eps = 2^-24, |b| < (a + c) / 2), while the exact value is at most
+// -lambda_min |d|^2 / 2 with lambda_min >= det / (a + c) > 1e-6 (a + c) (the
+// float32 det and trace lose far less than the factor 6.7 of margin).  A
+// nonzero offset has |d| >= 2^-25 (pixel centres are >= 0.5 and the
+// difference of two floats within a factor two of each other is exact), so
+// the exact value stays above 4e-34 in magnitude, far from where the
+// denormal rounding of the products (<= 2^-150 each) could matter; at d = 0
+// the power is a signed zero.
+template <int CH, bool SIGN = false>
 __device__ __forceinline__ bool plain_gaussian(float x, float y, float4 c, float thr,
                                                const float4* f) {
     bool ok = fabsf(x) < 1e6f && fabsf(y) < 1e6f && fabsf(c.x) < 1e20f && fabsf(c.y) < 1e20f &&
               fabsf(c.z) < 1e20f && c.w >= 0.0f && c.w < 1e30f && thr >= -86.0f;
+    if (SIGN) {
+        const float tr = c.x + c.z, det = fmaf(c.x, c.z, -c.y * c.y);
+        ok = ok && tr >= 1e-12f && tr < 1e19f && det > 1e-6f * (tr * tr);
+    }
     constexpr int F4 = (CH + 3) / 4;
 #pragma unroll
     for (int k = 0; k < F4; ++k)
@@ -378,10 +396,10 @@ __device__ __forceinline__ void store_tile_work(int* work, int tile, int last, i
 // 64 lw + l), compacted in LDS as 32-bit record byte offsets (16 x index)
 // so the walk is a counted loop over uniform offsets.  Built by the wave
 // itself after the workgroup barrier that publishes the masks; ascending
-// index order (REV: descending).  list[cnt] and list[cnt + 1] are set to
+// index order (REV: descending).  list[cnt .. cnt + PADS - 1] are set to
 // pad, a valid record offset, for the walks' look-ahead.  Returns cnt
 // (uniform).
-template <int NW, bool REV>
+template <int NW, bool REV, int PADS = 2>
 __device__ __forceinline__ int build_list(const uint64_t* words, uint32_t* list, int lane,
                                           int pad) {
     int total = 0;
@@ -395,7 +413,7 @@ __device__ __forceinline__ int build_list(const uint64_t* words, uint32_t* list,
             list[total + __popcll(m & (REV ? above : below))] = (uint32_t)((lw * kWave + lane) * 16);
         total += __popcll(m);
     }
-    if (lane < 2) list[total + lane] = (uint32_t)pad;
+    if (lane < PADS) list[total + lane] = (uint32_t)pad;
     return total;
 }
 
@@ -423,26 +441,26 @@ __device__ __forceinline__ float comp4(const float4& v, int e) {
     return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
 }
 
-// One (pixel, Gaussian) step of the front-to-back loop (rasterize.py:74-87),
-// straight-line: lanes that do not composite keep their state through
-// selects.  PLAIN: the Gaussian passed plain_gaussian(), so exp needs no
-// range handling and a non-compositing lane can add a zero weight.  The
-// per-lane decisions are kept as wave masks (alive: the pixel has not
-// stopped): a ballot of one comparison is that comparison's lane mask, the
-// masks combine in scalar registers, and inverse_ballot hands one back to
-// the lanes as a select condition, so none of it costs vector ALU work.
+// One (pixel, Gaussian) step of the front-to-back loop (rasterize.py:74-87):
+// lanes that do not composite keep their state.  PLAIN: the Gaussian passed
+// plain_gaussian(), so its power is never positive and exp needs no range
+// handling; the channel sums then run under the compositing lanes' exec
+// mask (a branch that no lane takes is skipped).  Otherwise every update is
+// a select.  The per-lane decisions are kept as wave masks (alive: the
+// pixel has not stopped): a ballot of one comparison is that comparison's
+// lane mask, the masks combine in scalar registers, and inverse_ballot
+// hands one back to the lanes as a select condition, so none of it costs
+// vector ALU work.
 template <int CH, bool DEPTH, bool PLAIN>
 __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
-                                         const float4* __restrict__ fsrc, int off, float pxf,
-                                         float pyf, float& T, float* acc, float& dacc,
-                                         int& last_off, uint64_t& alive) {
-    constexpr int F4 = (CH + 3) / 4;
-    float4 fv[F4];
-#pragma unroll
-    for (int q = 0; q < F4; ++q) fv[q] = fsrc[q];
+                                         const float4 (&fv)[(CH + 3) / 4], int off,
+                                         float pxf, float pyf, float& T, float* acc,
+                                         float& dacc, int& last_off, uint64_t& alive) {
     const float dx = r0.x - pxf, dy = r0.y - pyf;
     const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
-    const uint64_t live = alive & __ballot(!(power > 0.0f)) & __ballot(!(power < r0.z));
+    const uint64_t live =
+        PLAIN ? alive & __ballot(!(power < r0.z))
+              : alive & __ballot(!(power > 0.0f)) & __ballot(!(power < r0.z));
     const float e = PLAIN ? splat_exp_core(power) : splat_exp_sel(power);
     const float alpha = fminf(0.99f, r0.w * e);
     const uint64_t pass = live & __ballot(!(alpha < 1.0f / 255.0f));
@@ -454,10 +472,17 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
     // the contraction Metal's default fast-math applies to the reference
     const float w = alpha * T;
     if (PLAIN) {
-        const float wa = add ? w : 0.0f;
+        T = add ? next_T : T;
+        last_off = add ? off : last_off;
+        if (add) {
+            // keeps the sums a branch (the compiler would turn them into
+            // selects) and w computed before it
+            asm volatile("" ::"v"(w) : "memory");
 #pragma unroll
-        for (int ch = 0; ch < CH; ++ch) acc[ch] = fmaf(comp4(fv[ch >> 2], ch & 3), wa, acc[ch]);
-        if (DEPTH) dacc = fmaf(r1.w, wa, dacc);
+            for (int ch = 0; ch < CH; ++ch) acc[ch] = fmaf(comp4(fv[ch >> 2], ch & 3), w, acc[ch]);
+            if (DEPTH) dacc = fmaf(r1.w, w, dacc);
+        }
+        return;
     } else {
 #pragma unroll
         for (int ch = 0; ch < CH; ++ch) {
@@ -473,33 +498,55 @@ __device__ __forceinline__ void fwd_pair(const float4& r0, const float4& r1,
     last_off = add ? off : last_off;
 }
 
-// Front-to-back walk of one quadrant wave over its list, two Gaussians per
-// round: each Gaussian's records are read while the one before it is
-// evaluated, and list entries two places ahead (list[cnt] and
-// list[cnt + 1] are the padding record, which no pixel takes, so an odd
-// count needs no exit in the middle of a round; later entries may be stale
-// and are never used).  The wave stops once its 64 pixels have terminated.
-// last_off gets the offset of each pixel's last composited Gaussian of this
-// batch.
+// Front-to-back walk of one quadrant wave over its list, four Gaussians per
+// round: each Gaussian's records (and, up to four channels, its channels)
+// are read while the one before it is evaluated, and list entries two
+// places ahead.  list[cnt .. cnt + 3] are the padding record, which no pixel
+// takes, so a round may run past the list's end (a stale entry is read only
+// as the next round's offsets and never used, since the round count ends
+// first).  The wave stops once its 64 pixels have terminated.  last_off gets
+// the offset of each pixel's last composited Gaussian of this batch.
 template <int CH, bool DEPTH, bool PLAIN>
 __device__ __forceinline__ void fwd_walk(const uint32_t* list, int cnt, const float4* s_r0,
                                          const float4* s_r1, const float4 (*s_f)[(CH + 3) / 4],
                                          float pxf, float pyf, float& T, float* acc, float& dacc,
                                          int& last_off, uint64_t& alive) {
     constexpr int F4 = (CH + 3) / 4;
+    // more channels are read just before their pair (registers)
+    constexpr bool kAhead = F4 == 1;
+    if (cnt == 0) return;
     const float4* sf = &s_f[0][0];
+    float4 fa[F4], fb[F4];
+    auto feat = [&](float4 (&f)[F4], int off) {
+#pragma unroll
+        for (int q = 0; q < F4; ++q) f[q] = (&rec_at(sf, off * F4))[q];
+    };
+    auto pair = [&](const float4& r0, const float4& r1, float4 (&f)[F4], int off) {
+        if (!kAhead) feat(f, off);
+        fwd_pair<CH, DEPTH, PLAIN>(r0, r1, f, off, pxf, pyf, T, acc, dacc, last_off, alive);
+    };
     int oa = list[0], ob = list[1];
     float4 a0 = rec_at(s_r0, oa), a1 = rec_at(s_r1, oa);
-    for (int i = 0; i < cnt; i += 2) {
-        const int na = list[i + 2], nb = list[i + 3];
-        const float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
-        fwd_pair<CH, DEPTH, PLAIN>(a0, a1, &rec_at(sf, oa * F4), oa, pxf, pyf, T, acc, dacc,
-                                   last_off, alive);
+    if (kAhead) feat(fa, oa);
+    for (int i = 0;; i += 4) {
+        const int nc = list[i + 2], nd = list[i + 3];
+        float4 b0 = rec_at(s_r0, ob), b1 = rec_at(s_r1, ob);
+        if (kAhead) feat(fb, ob);
+        pair(a0, a1, fa, oa);
+        a0 = rec_at(s_r0, nc);
+        a1 = rec_at(s_r1, nc);
+        if (kAhead) feat(fa, nc);
+        pair(b0, b1, fb, ob);
+        const int na = list[i + 4], nb = list[i + 5];
+        b0 = rec_at(s_r0, nd);
+        b1 = rec_at(s_r1, nd);
+        if (kAhead) feat(fb, nd);
+        pair(a0, a1, fa, nc);
         a0 = rec_at(s_r0, na);
         a1 = rec_at(s_r1, na);
-        fwd_pair<CH, DEPTH, PLAIN>(b0, b1, &rec_at(sf, ob * F4), ob, pxf, pyf, T, acc, dacc,
-                                   last_off, alive);
-        if (alive == 0ull) return;
+        if (kAhead) feat(fa, na);
+        pair(b0, b1, fb, nd);
+        if (alive == 0ull || i + 4 >= cnt) return;
         oa = na;
         ob = nb;
     }
@@ -524,7 +571,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
     __shared__ float4 s_r1[kThreads + 1];     // -a/2, -b, -c/2 (conic), depth
     __shared__ float4 s_f[kThreads + 1][F4];  // channels, zero padded
     __shared__ uint64_t s_mask[kWaves][kWaves];  // [quadrant][loader wave]
-    __shared__ uint32_t s_list[kWaves][kThreads + 4];  // walk lists (+ look-ahead room)
+    __shared__ uint32_t s_list[kWaves][kThreads + 8];  // walk lists (+ look-ahead room)
     // one word per wave, written before a barrier and read by every thread
     // after it (a 16-byte read): some pixel of the wave still composites /
     // every Gaussian the wave staged is plain.  Each batch's reads come
@@ -578,7 +625,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
                 s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
                 s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, dz);
                 qm = quadrant_mask(m.x, m.y, c, px0, py0);
-                plain = plain_gaussian<CH>(m.x, m.y, c, thr, s_f[tid]) && fabsf(dz) < 1e30f;
+                plain = plain_gaussian<CH, true>(m.x, m.y, c, thr, s_f[tid]) && fabsf(dz) < 1e30f;
             }
         }
 #pragma unroll
@@ -593,7 +640,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
         const bool batch_plain = (pl.x & pl.y & pl.z & pl.w) != 0u;
         if (alive == 0ull) continue;
         const int cnt =
-            build_list<kWaves, false>(s_mask[wave], s_list[wave], lane, kThreads * 16);
+            build_list<kWaves, false, 4>(s_mask[wave], s_list[wave], lane, kThreads * 16);
         int last_off = -1;
         if (batch_plain)
             fwd_walk<CH, DEPTH, true>(s_list[wave], cnt, s_r0, s_r1, s_f, pxf, pyf, T, acc, dacc,
@@ -1565,7 +1612,9 @@ __device__ __forceinline__ float fwd_weight(const float4& r0, const float4& r1, 
                                             int& last_off, uint64_t& alive) {
     const float dx = r0.x - pxf, dy = r0.y - pyf;
     const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
-    const uint64_t live = alive & __ballot(!(power > 0.0f)) & __ballot(!(power < r0.z));
+    const uint64_t live =
+        PLAIN ? alive & __ballot(!(power < r0.z))
+              : alive & __ballot(!(power > 0.0f)) & __ballot(!(power < r0.z));
     const float e = PLAIN ? splat_exp_core(power) : splat_exp_sel(power);
     const float alpha = fminf(0.99f, r0.w * e);
     const uint64_t pass = live & __ballot(!(alpha < 1.0f / 255.0f));
@@ -1741,7 +1790,7 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
                     const float dz = DEPTH ? depths[g] : 0.0f;
                     s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, dz);
                     qm = quadrant_mask(m.x, m.y, c, px0, py0);
-                    plain = plain_gaussian<0>(m.x, m.y, c, thr, nullptr) && fabsf(dz) < 1e30f;
+                    plain = plain_gaussian<0, true>(m.x, m.y, c, thr, nullptr) && fabsf(dz) < 1e30f;
                 }
             }
         }

@@ -118,6 +118,47 @@ def test_splat_power_relative_bound_for_culling():
     assert worst <= 4.8e-4
 
 
+def test_splat_power_never_positive_for_plain_conics():
+    # The forward's plain batches skip the power > 0 test: a conic with
+    # a + c in [1e-12, 1e19) and det > 1e-6 (a + c)^2 (float32, as
+    # plain_gaussian computes them) never yields a positive float32 power.
+    # Worst cases: condition numbers up to the bound, offsets along the
+    # minor axis (where the exact power is smallest), offsets of a few
+    # 2^-25 steps (the least nonzero pixel offset) up to 1e3 pixels.
+    rng = np.random.default_rng(13)
+    f32 = np.float32
+    checked = 0
+    for _ in range(4000):
+        lam = 10.0 ** rng.uniform(-10, 6)
+        kappa = 10.0 ** rng.uniform(0, 6.05)
+        th = rng.uniform(0, np.pi)
+        ct, st = np.cos(th), np.sin(th)
+        l1, l2 = lam, lam * kappa
+        a = f32(l1 * ct * ct + l2 * st * st)
+        c = f32(l1 * st * st + l2 * ct * ct)
+        b = f32((l1 - l2) * ct * st)
+        tr = f32(a + c)
+        det = f32(np.float64(a) * np.float64(c) - np.float64(f32(b * b)))
+        if not (1e-12 <= tr < 1e19 and det > f32(1e-6) * f32(tr * tr)):
+            continue
+        for _ in range(8):
+            r = 2.0 ** rng.uniform(-25, 10)
+            u = rng.normal(0, 1e-3)  # near the minor axis (eigenvalue l1)
+            dx = f32(r * (ct + u * st))
+            dy = f32(r * (st - u * ct))
+            if rng.random() < 0.3:  # exact multiples of the least offset
+                dx = f32(np.round(dx * 2.0**25) * 2.0**-25)
+                dy = f32(np.round(dy * 2.0**25) * 2.0**-25)
+            p = O.splat_power(float(a), float(b), float(c), float(dx), float(dy))
+            assert not p > 0.0, (a, b, c, dx, dy, p)
+            checked += 1
+    assert checked > 10000
+    # the bound is needed: a conic with det / (a + c)^2 = 2e-9 (condition
+    # number ~5e8) gives a positive power near its minor axis
+    assert O.splat_power(311017312.0, -62711700.0, 12644819.0, 0.0762607529759407,
+                         0.3782143294811249) > 0.0
+
+
 def test_splat_power_closed_forms():
     # isotropic unit conic: -(dx^2 + dy^2)/2, exact for small integers
     for dx, dy in ((0, 0), (1, 0), (0, -2), (3, 4), (-5, 12)):
