@@ -90,8 +90,9 @@ constexpr int kDepthHistStride = kDepthPasses * kDepthRadix;
 // workgroups fit a CU: 124 VGPRs, 65 KB of LDS)
 constexpr int kTileThreads = 512, kTileItems = 14;
 constexpr int kTileHistStride = kMaxTilePasses * kRadix;
-// count phase: 1024 threads x 8 keys
-constexpr int kHistThreads = 1024, kHistItems = 8;
+// count phase: 1024 threads x 4 keys (245 workgroups per million keys, so
+// every CU takes one)
+constexpr int kHistThreads = 1024, kHistItems = 4;
 // count / row scans: 1024 threads x 4 Gaussians; emission, row emission,
 // segments: 1024 threads x 4
 constexpr int kScanThreads = 1024, kScanItems = 4, kScanChunk = kScanThreads * kScanItems;
