@@ -490,18 +490,22 @@ __global__ __launch_bounds__(256) void k_zero_ranges(ZeroRanges z) {
 // and the sum of the rectangle heights (the row entries) to status[4]; with
 // rows > 0 the row histograms in difference form: row_diff[copy][0][y] gets
 // +1 at each binned Gaussian's first row and -1 one past its last,
-// row_diff[copy][1][y] the same weighted by the rectangle's width.
+// row_diff[copy][1][y] the same weighted by the rectangle's width.  The
+// workgroup counts rows in eight LDS copies (lane % 8): the lanes of a
+// spatially sorted table share rows, and same-address LDS atomics of a wave
+// serialize.
 __global__ __launch_bounds__(kHistThreads) void k_depth_hist(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ counts,
     const uint2* __restrict__ rects, int64_t n, int rows, uint32_t* __restrict__ hist,
     uint32_t* __restrict__ row_diff, uint32_t* __restrict__ status) {
     constexpr int kHistBins = 3 * kDepthRadix + (1 << kDepthTopBits);
     __shared__ uint32_t s_h[kHistBins];
-    __shared__ uint32_t s_rows[2][kRowWords];
+    constexpr int kRowCopies = 8;
+    __shared__ uint32_t s_rows[kRowCopies][2][kRowWords];
     __shared__ uint64_t s_sum[2][kHistThreads / 64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     for (int k = tid; k < kHistBins; k += kHistThreads) s_h[k] = 0u;
-    for (int k = tid; k < 2 * kRowWords; k += kHistThreads) (&s_rows[0][0])[k] = 0u;
+    for (int k = tid; k < kRowCopies * 2 * kRowWords; k += kHistThreads) (&s_rows[0][0][0])[k] = 0u;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * (kHistThreads * kHistItems) + wave * (64 * kHistItems);
     uint64_t sum = 0, hsum = 0;
@@ -528,10 +532,11 @@ __global__ __launch_bounds__(kHistThreads) void k_depth_hist(
             hsum += h;
             if (rows > 0 && (rc.x >> 16) + h <= (uint32_t)rows) {
                 const uint32_t y0 = rc.x >> 16, w = rc.y & 0xFFFFu;
-                atomicAdd(&s_rows[0][y0], 1u);
-                atomicAdd(&s_rows[0][y0 + h], 0xFFFFFFFFu);
-                atomicAdd(&s_rows[1][y0], w);
-                atomicAdd(&s_rows[1][y0 + h], 0u - w);
+                uint32_t (*sr)[kRowWords] = s_rows[lane & (kRowCopies - 1)];
+                atomicAdd(&sr[0][y0], 1u);
+                atomicAdd(&sr[0][y0 + h], 0xFFFFFFFFu);
+                atomicAdd(&sr[1][y0], w);
+                atomicAdd(&sr[1][y0 + h], 0u - w);
             }
         }
 #pragma unroll
@@ -571,7 +576,9 @@ __global__ __launch_bounds__(kHistThreads) void k_depth_hist(
     if (rows > 0) {
         uint32_t* rd = row_diff + copy * 2 * kRowWords;
         for (int k = tid; k < 2 * kRowWords; k += kHistThreads) {
-            const uint32_t v = (&s_rows[0][0])[k];
+            uint32_t v = 0u;
+#pragma unroll
+            for (int c = 0; c < kRowCopies; ++c) v += (&s_rows[c][0][0])[k];
             if (v) atomicAdd(&rd[k], v);
         }
     }
