@@ -53,6 +53,9 @@ def _parse():
     ap.add_argument("--train-steps", type=int, default=12,
                     help="also time GaussianTrainer.step (SH configs with a backward); 0 = off")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB")
+    ap.add_argument("--layout", default="morton", choices=["morton", "creation"],
+                    help="row order of the Gaussian table: 3D Morton order of the means "
+                         "(spatial_order, the default) or the scene's creation order")
     ap.add_argument("--reference-suite", action="store_true",
                     help="time the reference's own published benchmark cases "
                          "(examples/benchmark.py) and print them as one JSON line")
@@ -405,6 +408,8 @@ def train_step(model, cams, targets, steps: int, warmup: int, antialias: bool,
     from mlx3d_amd.splatting.trainer import GaussianTrainer, TrainerConfig
 
     big = 1 << 30
+    # the table keeps the bench's row order (spatial_order would leave an
+    # already sorted table as it is)
     cfg = TrainerConfig(densify_from=big, densify_until=big, opacity_reset_every=big,
                         sh_increase_every=big, antialias=antialias)
     tr = GaussianTrainer(model, cfg)
@@ -559,7 +564,7 @@ def main():
     from mlx3d_amd import _lib, scenes
     from mlx3d_amd.profiling import StageTimer
     from mlx3d_amd.losses import l1_loss
-    from mlx3d_amd.splatting import GaussianModel, render_gaussian_features
+    from mlx3d_amd.splatting import GaussianModel, render_gaussian_features, spatial_order
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
@@ -574,9 +579,13 @@ def main():
     feat_mode = scene.features is not None
     cu = lambda a: torch.as_tensor(a).to(dev)  # noqa: E731
     if feat_mode:
-        leaf = {k: cu(v).requires_grad_(scene.backward) for k, v in dict(
+        leaf = {k: cu(v) for k, v in dict(
             means=scene.means, quats=scene.quats, scales=scene.scales,
             opacities=scene.opacities, features=scene.features).items()}
+        if args.layout == "morton":
+            perm = spatial_order(leaf["means"])
+            leaf = {k: v[perm].contiguous() for k, v in leaf.items()}
+        leaf = {k: v.requires_grad_(scene.backward) for k, v in leaf.items()}
     else:
         model = GaussianModel({"means": cu(scene.means), "quats": cu(scene.quats),
                                "scales": cu(scene.log_scales),
@@ -584,6 +593,8 @@ def main():
                                "sh_dc": cu(scene.sh_dc), "sh_rest": cu(scene.sh_rest)},
                               sh_degree=3)
         model.active_sh_degree = scene.sh_degree
+        if args.layout == "morton":
+            model.reorder_spatial()
         model.requires_grad_(scene.backward)
         leaf = model.params
     targets = [cu(scene.target(c)) for c in cams]
@@ -702,6 +713,7 @@ def main():
         "config": {"workload": workload, "gaussians": N, "width": cams[0].width,
                    "height": cams[0].height, "views": nviews, "sh_degree": scene.sh_degree,
                    "channels": C, "antialias": scene.antialias, "depth": scene.depth,
+                   "layout": args.layout,
                    "duplicates_mean": int(D), "needed_entries_mean": int(Dn)},
         "fwd_fps": round(1e3 / ms_fwd, 2),
         "fwd_ms": round(ms_fwd, 4),

@@ -1,6 +1,7 @@
 """3D Gaussian splatting on MI355X: the drop-in surface of ``mlx3d.splatting``
 (``src/mlx3d/splatting/__init__.py:1-30``), the same public names."""
 
+from .layout import spatial_order
 from .model import GaussianModel
 from .projection import project_gaussians, project_gaussians_ut, quat_scale_to_cov3d
 from .rasterize import rasterize, rasterize_depth, rasterize_features
@@ -30,4 +31,5 @@ __all__ = [
     "render_gaussians_reference",
     "rgb_to_sh",
     "sh_to_rgb",
+    "spatial_order",
 ]

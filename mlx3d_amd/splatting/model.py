@@ -269,6 +269,19 @@ class GaussianModel:
         with torch.no_grad():
             self._replace({k: v[idx] for k, v in self.params.items()})
 
+    def reorder_spatial(self) -> torch.Tensor:
+        """Store the rows in 3D Morton order of their means (``spatial_order``;
+        no counterpart in the reference): Gaussians close in space share cache
+        lines in the rasterizers' gathers.  Renders are unchanged except for
+        Gaussians at exactly equal depths.  Returns the permutation (new row i
+        was row ``perm[i]``)."""
+        from .layout import spatial_order
+
+        perm = spatial_order(self.params["means"])
+        with torch.no_grad():
+            self._replace({k: v[perm] for k, v in self.params.items()})
+        return perm
+
     def append(self, new_params: dict[str, torch.Tensor]) -> None:
         """Concatenate rows (model.py:400-404)."""
         with torch.no_grad():

@@ -93,6 +93,10 @@ class TrainerConfig:
     max_gaussians: int | None = None
     low_memory: bool = False
     cache_limit_gb: float = 2.0
+    # no counterpart in the reference: keep the table in 3D Morton order of
+    # the means (GaussianModel.reorder_spatial) from the start and after
+    # every density event, the Adam moments permuted alongside
+    spatial_order: bool = False
 
 
 class _StepResult:
@@ -137,6 +141,7 @@ class GaussianTrainer:
         self._constrain()
         self.optimizers = {name: Adam(learning_rate=rate, eps=1e-15)
                            for name, rate in self._group_rates().items()}
+        self._reorder()
         self._new_screen_stats()
 
     # ------------------------------------------------------------ set-up
@@ -173,6 +178,18 @@ class GaussianTrainer:
             if st is not None:
                 out[name] = {"m": st["m"], "v": st["v"]}
         return out
+
+    def _reorder(self) -> None:
+        """With ``spatial_order``: the table (and the Adam moments) in Morton
+        order."""
+        if not self.config.spatial_order:
+            return
+        perm = self.model.reorder_spatial()
+        for name, opt in self.optimizers.items():
+            st = opt.state.get(name)
+            if st is not None:
+                st["m"] = st["m"][perm].contiguous()
+                st["v"] = st["v"][perm].contiguous()
 
     def _constrain(self) -> None:
         """2DGS keeps the third scale a thin surfel (trainer.py:181-185)."""
@@ -320,6 +337,7 @@ class GaussianTrainer:
             for name, slots in result.pop("_moments", {}).items():
                 self.optimizers[name].state[name] = slots
         self._constrain()
+        self._reorder()
         self._new_screen_stats()
         return {k: v for k, v in result.items() if not str(k).startswith("_")}
 
