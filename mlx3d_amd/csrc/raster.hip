@@ -168,10 +168,9 @@ __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, in
 // pixel that passes the alpha bound, within [-86, 0]: then exp needs no
 // range handling and a zero weight leaves the accumulators unchanged.
 //
-// SIGN (the forwards): the conic must also be well conditioned,
-// det > 1e-6 (a + c)^2 with a + c in [1e-12, 1e19), and then the float32
-// power (splat_power) is never positive, so the loop needs no power > 0
-// test.  Its rounding error is at
+// The conic must also be well conditioned, det > 1e-6 (a + c)^2 with
+// a + c in [1e-12, 1e19), and then the float32 power (splat_power) is never
+// positive, so the loops need no power > 0 test.  Its rounding error is at
 // most eps (a dx^2 + c dy^2 + 2 |b dx dy|) <= 1.25 eps (a + c) |d|^2
 // (eps = 2^-24, |b| < (a + c) / 2), while the exact value is at most
 // -lambda_min |d|^2 / 2 with lambda_min >= det / (a + c) > 1e-6 (a + c) (the
@@ -181,15 +180,12 @@ __device__ __forceinline__ uint32_t quadrant_mask(float x, float y, float4 c, in
 // the exact value stays above 4e-34 in magnitude, far from where the
 // denormal rounding of the products (<= 2^-150 each) could matter; at d = 0
 // the power is a signed zero.
-template <int CH, bool SIGN = false>
+template <int CH>
 __device__ __forceinline__ bool plain_gaussian(float x, float y, float4 c, float thr,
                                                const float4* f) {
-    bool ok = fabsf(x) < 1e6f && fabsf(y) < 1e6f && fabsf(c.x) < 1e20f && fabsf(c.y) < 1e20f &&
-              fabsf(c.z) < 1e20f && c.w >= 0.0f && c.w < 1e30f && thr >= -86.0f;
-    if (SIGN) {
-        const float tr = c.x + c.z, det = fmaf(c.x, c.z, -c.y * c.y);
-        ok = ok && tr >= 1e-12f && tr < 1e19f && det > 1e-6f * (tr * tr);
-    }
+    const float tr = c.x + c.z, det = fmaf(c.x, c.z, -c.y * c.y);
+    bool ok = fabsf(x) < 1e6f && fabsf(y) < 1e6f && tr >= 1e-12f && tr < 1e19f &&
+              det > 1e-6f * (tr * tr) && c.w >= 0.0f && c.w < 1e30f && thr >= -86.0f;
     constexpr int F4 = (CH + 3) / 4;
 #pragma unroll
     for (int k = 0; k < F4; ++k)
@@ -625,7 +621,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
                 s_r0[tid] = make_float4(m.x, m.y, thr, c.w);
                 s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, dz);
                 qm = quadrant_mask(m.x, m.y, c, px0, py0);
-                plain = plain_gaussian<CH, true>(m.x, m.y, c, thr, s_f[tid]) && fabsf(dz) < 1e30f;
+                plain = plain_gaussian<CH>(m.x, m.y, c, thr, s_f[tid]) && fabsf(dz) < 1e30f;
             }
         }
 #pragma unroll
@@ -716,9 +712,11 @@ __device__ __forceinline__ bool bwd_values(const float4& r0, const float4& r1,
     // the wave-wide tests ballot each comparison on its own: a ballot of a
     // single comparison is its lane mask, one of a combined condition is
     // first materialised in a vector register
-    const bool c1 = off < lim, c2 = !(power > 0.0f), c3 = !(power < r0.z);
+    // PLAIN: the power is never positive (plain_gaussian's conic bound)
+    const bool c1 = off < lim, c2 = PLAIN || !(power > 0.0f), c3 = !(power < r0.z);
     bool ok = c1 && c2 && c3;
-    const uint64_t m123 = __ballot(c1) & __ballot(c2) & __ballot(c3);
+    const uint64_t m123 = PLAIN ? __ballot(c1) & __ballot(c3)
+                                : __ballot(c1) & __ballot(c2) & __ballot(c3);
     if (m123 == 0ull) {
 #pragma unroll
         for (int q = 0; q < NV; ++q) out[S * q + O] = 0.0f;
@@ -1199,9 +1197,11 @@ __device__ __forceinline__ bool bwd_geo(const float4& r0, const float4& r1, floa
                                         float (&v)[8], float& aT_out) {
     const float dx = r0.x - pxf, dy = r0.y - pyf;
     const float power = splat_power(r1.x, r1.y, r1.z, dx, dy);
-    const bool c1 = off < lim, c2 = !(power > 0.0f), c3 = !(power < r0.z);
+    // PLAIN: the power is never positive (plain_gaussian's conic bound)
+    const bool c1 = off < lim, c2 = PLAIN || !(power > 0.0f), c3 = !(power < r0.z);
     bool ok = c1 && c2 && c3;
-    const uint64_t m123 = __ballot(c1) & __ballot(c2) & __ballot(c3);
+    const uint64_t m123 = PLAIN ? __ballot(c1) & __ballot(c3)
+                                : __ballot(c1) & __ballot(c2) & __ballot(c3);
 #pragma unroll
     for (int q = 0; q < 8; ++q) v[q] = 0.0f;
     aT_out = 0.0f;
@@ -1790,7 +1790,7 @@ __global__ __launch_bounds__(kThreads, 3) void k_raster_fwd_mx(
                     const float dz = DEPTH ? depths[g] : 0.0f;
                     s_r1[tid] = make_float4(-0.5f * c.x, -c.y, -0.5f * c.z, dz);
                     qm = quadrant_mask(m.x, m.y, c, px0, py0);
-                    plain = plain_gaussian<0, true>(m.x, m.y, c, thr, nullptr) && fabsf(dz) < 1e30f;
+                    plain = plain_gaussian<0>(m.x, m.y, c, thr, nullptr) && fabsf(dz) < 1e30f;
                 }
             }
         }
