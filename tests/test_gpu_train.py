@@ -697,3 +697,37 @@ def test_2dgs_geometry_terms_leave_screen_stats_alone():
     e = float(np.abs(a1 - a0).max() / np.abs(a0).max())
     say(f"  grad_accum rel diff {e:.2e}")
     assert e < 1e-5
+
+
+def test_2dgs_unprojection_maps_follow_the_camera():
+    """The 2DGS trainer caches the unprojection maps by camera content: two
+    differently posed cameras created one after another (a new object may
+    reuse a freed one's id) and a camera moved in place each get their own
+    maps, equal to a fresh unprojection_maps call."""
+    from mlx3d_amd.cameras import Camera
+    from mlx3d_amd.splatting.geometry import unprojection_maps
+
+    say("2dgs unprojection-map cache keyed by camera content")
+    _, model, _, _ = _model(61, 1500, degree=0)
+    cfg = TrainerConfig(method="2dgs", densify_from=1 << 30, densify_until=1 << 30,
+                        opacity_reset_every=1 << 30, lambda_2d_depth_variance=0.2,
+                        lambda_2d_normal_consistency=0.2)
+    tr = GaussianTrainer(model, cfg, scene_extent=2.0)
+    dev = model.params["means"].device
+    target = torch.zeros((112, 160, 3), dtype=torch.float32, device=dev)
+    for i in range(4):
+        eye = (0.0, 0.3 * (i % 2), -4.0 + 0.5 * (i % 2))
+        cam = Camera.look_at(eye=eye, at=(0, 0, 0), width=160, height=112, fov=50.0)
+        info = tr.step(cam, target)
+        assert np.isfinite(info["loss"])
+        base, dirs = tr._maps(cam, dev)
+        rb, rd = unprojection_maps(cam, dev)
+        assert torch.equal(base, rb) and torch.equal(dirs, rd), i
+        del cam
+    # the same object moved in place
+    cam = Camera.look_at(eye=(0.0, 0.0, -4.0), at=(0, 0, 0), width=160, height=112, fov=50.0)
+    tr.step(cam, target)
+    cam.t = torch.as_tensor(cam.t, dtype=torch.float32) + 0.25
+    base, dirs = tr._maps(cam, dev)
+    rb, rd = unprojection_maps(cam, dev)
+    assert torch.equal(base, rb) and torch.equal(dirs, rd)
