@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define GSX_ABI_VERSION 6
+#define GSX_ABI_VERSION 7
 #define GSX_TILE_SIZE 16 /* tiles.py:14 */
 
 enum gsx_status {
@@ -300,7 +300,11 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts,
  * num_tiles)).  bin_status then holds what gsx_bin_sort_async documents;
  * with capacity = bin_status[3] the duplicates always fit.  With
  * host_status != NULL (8 words) its last kernel writes the final status
- * there the same way.
+ * there the same way.  tile_order: NULL, or the gsx_tile_order_words(W, H)
+ * buffer of the frame's gsx_raster_fwd: the call writes the forward's tile
+ * order for the ranges it produces into words [T, 2T) (the placement's
+ * first workgroups compute it beside the placement; it is what
+ * gsx_raster_fwd would compute), to be passed with order_ready = 1.
  *
  * gsx_bin_sort_async is the three in sequence on one workspace (depth part
  * first, all bin_status words cleared); gsx_bin_workspace_bytes is the sum
@@ -323,7 +327,7 @@ int gsx_bin_tiles_async(int64_t n, const uint32_t* tile_counts,
                         int64_t tile_ws_bytes, int64_t capacity,
                         int32_t* sorted_ids, int32_t* tile_ranges,
                         uint32_t* bin_status, uint64_t* host_status,
-                        uint32_t seq, void* stream);
+                        uint32_t seq, int32_t* tile_order, void* stream);
 
 /* Host-side: interprets a host copy of the bin_status words.  Returns
  * GSX_OK with *num_dups = D (duplicates kept), 1 with *num_dups = the
@@ -357,8 +361,10 @@ int gsx_pack_conic_opacity(int64_t n, const float* conics,
  * int32 words that the call fills: words [0, T) (T = ceil(W/16)
  * ceil(H/16)) each tile's largest n_contrib, which gsx_raster_bwd orders
  * its tiles by; words [T, 2T) the order the workgroups take the tiles in
- * (each XCD's contiguous band of tiles, longest lists first).  The outputs
- * do not depend on the order.  The buffer has no counterpart in the
+ * (each XCD's contiguous band of tiles, longest lists first).  With
+ * order_ready != 0 words [T, 2T) already hold that order, written by
+ * gsx_bin_tiles_async for these ranges, and the call only reads them.  The
+ * outputs do not depend on the order.  The buffer has no counterpart in the
  * reference (whose Metal dispatch has no such control). */
 int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
                    const float* conic_opacity, const float* features,
@@ -367,7 +373,7 @@ int gsx_raster_fwd(int64_t n, int32_t C, const float* means2d,
                    const float* background,
                    int32_t width, int32_t height, float* out, float* final_T,
                    int32_t* n_contrib, float* depth_out, float* alpha_out,
-                   int32_t* tile_order, void* stream);
+                   int32_t* tile_order, int32_t order_ready, void* stream);
 
 /* Replaces gs_rasterize_backward (rasterize.py:100-221) and the vjp wiring
  * of _rasterize_core (rasterize.py:364-403).  grad_out (H,W,C);

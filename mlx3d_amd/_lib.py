@@ -138,13 +138,13 @@ SIGNATURES = {
     "gsx_bin_count_async": (ctypes.c_int, [_I64, _P, _P, _P, _I32, _I32, _P, _I64, _P, _P, _P]),
     "gsx_bin_depth_async": (ctypes.c_int, [_I64, _P, _P, _I64, _P, _P, _U32, _P]),
     "gsx_bin_tiles_async": (ctypes.c_int, [_I64, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I64, _P,
-                                           _I64, _I64, _P, _P, _P, _P, _U32, _P]),
+                                           _I64, _I64, _P, _P, _P, _P, _U32, _P, _P]),
     "gsx_bin_status_check": (ctypes.c_int, [_P, _I64, ctypes.POINTER(_I64)]),
     "gsx_host_status_alloc": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p)]),
     "gsx_host_status_free": (ctypes.c_int, [_P]),
     "gsx_pack_conic_opacity": (ctypes.c_int, [_I64, _P, _P, _P, _P]),
     "gsx_raster_fwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32,
-                                      _P, _P, _P, _P, _P, _P, _P]),
+                                      _P, _P, _P, _P, _P, _P, _I32, _P]),
     "gsx_tile_order_words": (_I64, [_I32, _I32]),
     "gsx_raster_bwd": (ctypes.c_int, [_I64, _I32, _P, _P, _P, _P, _I64, _P, _P, _I32, _I32, _P,
                                       _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P]),

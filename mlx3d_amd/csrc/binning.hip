@@ -67,6 +67,7 @@
 #include <cstring>
 
 #include "gsx_device.h"
+#include "tile_order.h"
 
 using namespace gsx;
 
@@ -1289,13 +1290,24 @@ __global__ __launch_bounds__(kScanParts * kMaxFastTiles) void k_tile_scan(
 // entry whose span holds i, is written into the segment's slots by the
 // entry itself.  With pub.host, workgroup 0 copies the status words to
 // the host first (every earlier kernel of the binning has finished).
+// The forward rasterizer's tile order where no placement launch computes it
+// (the general path, no duplicates): one workgroup per band.
+__global__ __launch_bounds__(kOrderThreads) void k_fwd_order(const int2* __restrict__ ranges,
+                                                             int64_t n_ids, int tiles,
+                                                             int* __restrict__ order) {
+    __shared__ uint32_t s_order[tile_order_lds_words<kOrderThreads>()];
+    tile_order_band<false>(blockIdx.x, ranges, nullptr, n_ids, tiles, order, s_order);
+}
+
 __global__ __launch_bounds__(kPlaceThreads) void k_place(
     int64_t cap, const RowPlan* __restrict__ plan, const uint32_t* __restrict__ segrow,
     const uint32_t* __restrict__ segk0, int tiles_x, const uint32_t* __restrict__ e_gid,
     const uint32_t* __restrict__ e_pack, const uint32_t* __restrict__ e_doff,
-    const uint32_t* __restrict__ sc, int32_t* __restrict__ ids, Publish pub) {
+    const uint32_t* __restrict__ sc, int32_t* __restrict__ ids, Publish pub, int bands,
+    const int2* __restrict__ ranges, int tiles, int* __restrict__ order) {
     constexpr int kWaves = kPlaceThreads / 64;
     __shared__ uint32_t s_ent[3 * kSegDups];   // staged (doff, gid, pack); then (pos, gid)
+    static_assert(3 * kSegDups >= tile_order_lds_words<kPlaceThreads>(), "order scratch fits");
     __shared__ uint16_t s_own[kSegDups];
     __shared__ uint32_t s_cnt[kWaves][kMaxFastTiles];
     __shared__ uint32_t s_base[kMaxFastTiles];
@@ -1303,15 +1315,24 @@ __global__ __launch_bounds__(kPlaceThreads) void k_place(
     __shared__ uint32_t s_w[kPlaceThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (pub.host && blockIdx.x == 0 && tid == 0) publish(pub);
+    if ((int)blockIdx.x < bands) {
+        // the forward rasterizer's tile order (k_tile_order's), band
+        // blockIdx.x, beside the placement: the ranges are final (zero when
+        // the duplicates overflowed, which still gives a valid order)
+        tile_order_band<false, kPlaceThreads>(blockIdx.x, ranges, nullptr, cap, tiles, order,
+                                              s_ent);
+        return;
+    }
+    const uint32_t seg = blockIdx.x - (uint32_t)bands;
     if ((int64_t)plan->dups > cap) return;
     Segment sg;
-    if (!find_segment(plan, segrow, segk0, blockIdx.x, sg)) return;
+    if (!find_segment(plan, segrow, segk0, seg, sg)) return;
     const int ne = (int)min(sg.k1 - sg.k0, (uint32_t)kSegDups);
     uint32_t* s_doff = s_ent;
     uint32_t* s_gid = s_ent + kSegDups;
     uint32_t* s_pack = s_ent + 2 * kSegDups;
     for (int k = tid; k < kWaves * kMaxFastTiles; k += kPlaceThreads) (&s_cnt[0][0])[k] = 0u;
-    if (tid < tiles_x) s_base[tid] = sc[(int64_t)blockIdx.x * kMaxFastTiles + tid];
+    if (tid < tiles_x) s_base[tid] = sc[(int64_t)seg * kMaxFastTiles + tid];
     for (int k = tid; k < ne; k += kPlaceThreads) {
         const uint32_t e = sg.rb + sg.k0 + (uint32_t)k;
         const uint32_t doff = e_doff[e];
@@ -1904,11 +1925,23 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
                 int32_t height, void* depth_ws, int64_t depth_ws_bytes, void* tile_ws,
                 int64_t tile_ws_bytes, int64_t capacity, int32_t* sorted_ids,
                 int32_t* tile_ranges, uint32_t* bin_status, uint64_t* host_status, uint32_t seq,
-                hipStream_t st) {
+                int32_t* tile_order, hipStream_t st) {
     int rc = check_args(n, width, height, capacity);
     if (rc != GSX_OK) return rc;
     if (!tile_ranges || !bin_status) return GSX_ERR_INVALID;
-    if (n == 0) return GSX_OK;  // the count phase cleared the ranges and status
+    // the forward rasterizer's order, when asked: [T, T + T) of tile_order
+    const int64_t tiles = (int64_t)tiles_x_of(width) * tiles_y_of(height);
+    int* const order = tile_order ? tile_order + tiles : nullptr;
+    auto order_alone = [&]() {
+        if (order)
+            hipLaunchKernelGGL(k_fwd_order, dim3(kOrderBands), dim3(kOrderThreads), 0, st,
+                               (const int2*)tile_ranges, capacity, (int)tiles, order);
+    };
+    if (n == 0) {  // the count phase cleared the ranges and status
+        order_alone();
+        GSX_LAUNCH_CHECK();
+        return GSX_OK;
+    }
     if (!tile_counts || !tile_rects || !depth_ws || !tile_ws) return GSX_ERR_INVALID;
     const bool refine = conics != nullptr;
     if (refine && (!means2d || ((uintptr_t)means2d & 7u) != 0u || conic_stride < 3))
@@ -1953,6 +1986,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
         GSX_LAUNCH_CHECK();
         if (capacity == 0) {
             if (pub.host) hipLaunchKernelGGL(k_publish, dim3(1), dim3(64), 0, st, pub);
+            order_alone();
             GSX_LAUNCH_CHECK();
             return GSX_OK;
         }
@@ -1967,11 +2001,14 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
         hipLaunchKernelGGL(k_tile_scan, dim3((unsigned)tiles_y), dim3(kScanParts * kMaxFastTiles),
                            0, st,
                            capacity, (const RowPlan*)plan, tiles_x, sc, (int2*)tile_ranges);
-        hipLaunchKernelGGL(k_place, dim3((unsigned)L.segments), dim3(kPlaceThreads), 0, st,
-                           capacity, (const RowPlan*)plan, (const uint32_t*)segrow,
-                           (const uint32_t*)segk0, tiles_x, (const uint32_t*)e_gid,
-                           (const uint32_t*)e_pack, (const uint32_t*)e_doff, (const uint32_t*)sc,
-                           sorted_ids, pub);
+        // the first kOrderBands workgroups build the forward's tile order
+        const int bands = order ? kOrderBands : 0;
+        hipLaunchKernelGGL(k_place, dim3((unsigned)L.segments + (unsigned)bands),
+                           dim3(kPlaceThreads), 0, st, capacity, (const RowPlan*)plan,
+                           (const uint32_t*)segrow, (const uint32_t*)segk0, tiles_x,
+                           (const uint32_t*)e_gid, (const uint32_t*)e_pack,
+                           (const uint32_t*)e_doff, (const uint32_t*)sc, sorted_ids, pub, bands,
+                           (const int2*)tile_ranges, (int)T, order);
         GSX_LAUNCH_CHECK();
         return GSX_OK;
     }
@@ -1996,6 +2033,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
     GSX_LAUNCH_CHECK();
     if (capacity == 0) {
         if (pub.host) hipLaunchKernelGGL(k_publish, dim3(1), dim3(64), 0, st, pub);
+        order_alone();
         GSX_LAUNCH_CHECK();
         return GSX_OK;
     }
@@ -2021,6 +2059,7 @@ int tiles_phase(int64_t n, const uint32_t* tile_counts, const uint32_t* tile_rec
     GSX_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_tile_ranges, dim3(grid_for(capacity, 1024)), dim3(256), 0, st, capacity,
                        (const uint32_t*)d_total, tk[cur], T, (int2*)tile_ranges, pub);
+    order_alone();
     GSX_LAUNCH_CHECK();
     return GSX_OK;
 }
@@ -2064,10 +2103,11 @@ int gsx_bin_tiles_async(int64_t n, const uint32_t* tile_counts, const uint32_t* 
                         int32_t width, int32_t height, void* depth_ws, int64_t depth_ws_bytes,
                         void* tile_ws, int64_t tile_ws_bytes, int64_t capacity,
                         int32_t* sorted_ids, int32_t* tile_ranges, uint32_t* bin_status,
-                        uint64_t* host_status, uint32_t seq, void* stream) {
+                        uint64_t* host_status, uint32_t seq, int32_t* tile_order, void* stream) {
     return tiles_phase(n, tile_counts, tile_rects, means2d, conics, conic_stride, width, height,
                        depth_ws, depth_ws_bytes, tile_ws, tile_ws_bytes, capacity, sorted_ids,
-                       tile_ranges, bin_status, host_status, seq, (hipStream_t)stream);
+                       tile_ranges, bin_status, host_status, seq, tile_order,
+                       (hipStream_t)stream);
 }
 
 int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* depth_keys,
@@ -2091,7 +2131,7 @@ int gsx_bin_sort_async(int64_t n, const uint32_t* tile_counts, const uint32_t* d
     if (rc != GSX_OK) return rc;
     return tiles_phase(n, tile_counts, tile_rects, means2d, conics, conic_stride, width, height,
                        workspace, dbytes, static_cast<char*>(workspace) + dbytes, tbytes,
-                       capacity, sorted_ids, tile_ranges, bin_status, nullptr, 0,
+                       capacity, sorted_ids, tile_ranges, bin_status, nullptr, 0, nullptr,
                        (hipStream_t)stream);
 }
 

@@ -34,12 +34,13 @@ def tile_order_buffer(width, height, dev):
 
 
 def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, background, width,
-                   height, depths=None, tile_order=None):
+                   height, depths=None, tile_order=None, order_ready=False):
     """gsx_raster_fwd on prepared float32 contiguous tensors (no autograd):
     (out, final_T, n_contrib, depth_map or None, alpha = 1 - final_T).
     With ``tile_order`` (tile_order_buffer) the workgroups take the tiles
     with the longest lists first, and the kernel records each tile's
-    contributor bound there, which raster_backward orders its tiles by."""
+    contributor bound there, which raster_backward orders its tiles by;
+    ``order_ready``: the binning already wrote this frame's order there."""
     dev = means2d.device
     n, C = feats.shape
     out = _empty((height, width, C), dev)
@@ -53,7 +54,9 @@ def raster_forward(means2d, conic_opac, feats, sorted_ids, tile_ranges, backgrou
                                 _lib.ptr(tile_ranges),
                                 _lib.ptr(background), width, height, _lib.ptr(out),
                                 _lib.ptr(final_T), _lib.ptr(n_contrib), _lib.ptr(depth_map),
-                                _lib.ptr(alpha), _lib.ptr(tile_order), _lib.stream_handle(dev)),
+                                _lib.ptr(alpha), _lib.ptr(tile_order),
+                                1 if (order_ready and tile_order is not None) else 0,
+                                _lib.stream_handle(dev)),
                "gsx_raster_fwd")
     return out, final_T, n_contrib, depth_map, alpha
 

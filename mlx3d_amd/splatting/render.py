@@ -83,17 +83,17 @@ def _forward(cfg: _Cfg, means, quats, scales, opacities, sh_a, sh_b, colors, bac
             _lib.ptr(colors_out), _lib.ptr(counts), _lib.ptr(dkeys), _lib.ptr(rects), st),
             "gsx_preprocess_fwd")
     feats = colors_out if cfg.sh_mode else colors
+    # the binning's placement launch writes the forward's tile order too
+    order = tile_order_buffer(cfg.width, cfg.height, dev)
     with stage("binning"):
         job = BinJob(counts, dkeys, rects, cfg.width, cfg.height,
-                     refine=(means2d, co) if cfg.refine else None)
-
-    order = tile_order_buffer(cfg.width, cfg.height, dev)
+                     refine=(means2d, co) if cfg.refine else None, tile_order=order)
 
     def raster(ids):
         with stage("raster_fwd"):
             return raster_forward(means2d, co, feats, ids, job.ranges, background, cfg.width,
                                   cfg.height, depths=depths if cfg.return_depth else None,
-                                  tile_order=order)
+                                  tile_order=order, order_ready=True)
 
     # The rasterizer runs on the id buffer (its ranges never reach past D)
     # and is enqueued before the host reads D.  If D exceeded the guessed

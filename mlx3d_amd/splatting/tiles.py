@@ -172,8 +172,10 @@ class BinJob:
     """
 
     def __init__(self, counts, dkeys, rects, width: int, height: int, refine=None,
-                 final: bool = False):
-        """``refine`` = (means2d (N,2), conics (N,k>=3)) enables refine_tiles."""
+                 final: bool = False, tile_order=None):
+        """``refine`` = (means2d (N,2), conics (N,k>=3)) enables refine_tiles;
+        ``tile_order`` (tile_order_buffer) receives the forward rasterizer's
+        tile order for the ranges (gsx_raster_fwd then runs with order_ready)."""
         self.dev = counts.device
         self.n = counts.shape[0]
         self.width, self.height = int(width), int(height)
@@ -184,6 +186,7 @@ class BinJob:
         self.ranges = torch.empty((self.tiles_x * self.tiles_y, 2), dtype=torch.int32,
                                   device=self.dev)
         self.inputs = (counts, dkeys, rects, refine)
+        self.tile_order = tile_order
         self.exact = refine is not None or final  # D read before the tile phase, kept as is
         self._enqueue(None if self.exact else self.ws.capacity_hint())
 
@@ -217,7 +220,8 @@ class BinJob:
             n, _lib.ptr(counts), _lib.ptr(rects), _lib.ptr(m2), _lib.ptr(co),
             0 if co is None else co.shape[1], self.width, self.height, _lib.ptr(dws),
             dws.numel(), _lib.ptr(tws), tws.numel(), self.cap, _lib.ptr(self.ids),
-            _lib.ptr(self.ranges), _lib.ptr(status), ws.host.slot(1), seq, stream),
+            _lib.ptr(self.ranges), _lib.ptr(status), ws.host.slot(1), seq,
+            _lib.ptr(self.tile_order), stream),
             "gsx_bin_tiles_async")
         self.ready = n > 0  # n == 0 launches nothing after the count phase
         self.num_dups = None if (self.exact or self.guessed) else self.cap

@@ -33,7 +33,7 @@ def test_python_binding_covers_header():
 
 def test_status_strings_and_version():
     L = _lib.load()
-    assert L.gsx_abi_version() == 6
+    assert L.gsx_abi_version() == 7
     assert _lib.strerror(0) == "ok"
     assert "invalid" in _lib.strerror(-1)
     assert "capacity" in _lib.strerror(1)
@@ -128,11 +128,11 @@ def test_bin_status_check_is_host_only():
     rg = np.zeros(32, np.int32)
     p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731  (never dereferenced)
     assert L.gsx_bin_tiles_async(10, p(st), p(st), None, None, 0, 64, 64, p(st), 16, p(st), 16,
-                                 100, p(rg), p(rg), p(st), None, 0, None) == -3
+                                 100, p(rg), p(rg), p(st), None, 0, None, None) == -3
     assert L.gsx_bin_tiles_async(10, None, None, None, None, 0, 64, 64, None, 0, None, 0, 100,
-                                 None, p(rg), p(st), None, 0, None) == -1
+                                 None, p(rg), p(st), None, 0, None, None) == -1
     assert L.gsx_bin_tiles_async(10, None, None, None, None, 0, 64, 64, None, 0, None, 0,
-                                 1 << 30, None, p(rg), p(st), None, 0, None) == -4
+                                 1 << 30, None, p(rg), p(st), None, 0, None, None) == -4
     assert L.gsx_host_status_alloc(None) == -1
     assert L.gsx_host_status_free(None) == 0
 

@@ -56,7 +56,7 @@ class _FakeLib:
         return 0
 
     def gsx_bin_tiles_async(self, n, counts, rects, m2, co, cs, w, h, dws, dnb, tws, tnb, cap,
-                            ids, ranges, status, slot, seq, st):
+                            ids, ranges, status, slot, seq, order, st):
         self.calls.append(("tiles", cap, seq))
         fits = cap >= self.dups
         self._publish(slot, seq, [self.dups if fits else 0, 0, 0, self.dups, 0, 0, 0, 0])

@@ -250,7 +250,7 @@ def test_bin_two_phase_abi_exact_capacity():
             n, _lib.ptr(counts), _lib.ptr(rects), _lib.ptr(m2) if refine else None,
             _lib.ptr(con) if refine else None, 3 if refine else 0, 640, 360, _lib.ptr(dws),
             dws.numel(), _lib.ptr(tws), tws.numel(), cap, _lib.ptr(ids), _lib.ptr(ranges),
-            _lib.ptr(status), hs.slot(1), seq, st), "tile phase")
+            _lib.ptr(status), hs.slot(1), seq, None, st), "tile phase")
         final, tag = hs.wait(1, seq)
         assert tag == seq
         words = host(status).view(np.uint32)
@@ -549,7 +549,7 @@ def test_features_non_finite_forward(channels):
     P = _lib.ptr
     _lib.check(L.gsx_raster_fwd(n, channels, P(dm2), P(dcon), P(dfe), P(ddp), P(dids), n,
                                 P(drg), None, W, H, P(out), P(fT), P(nct), P(dout), P(aout),
-                                None, _lib.stream_handle(out.device)), "raster_fwd")
+                                None, 0, _lib.stream_handle(out.device)), "raster_fwd")
     torch.cuda.synchronize()
     ref = O.raster_fwd(m2, con, op, feats, ids, ranges, W, H, depths=depths)
     np.testing.assert_array_equal(host(nct), ref["n_contrib"])
@@ -853,3 +853,53 @@ def test_tile_order(C):
         for name, a, b in zip(("means2d", "conics", "features", "opacities"), ref, got):
             e = float((a - b).abs().max() / a.abs().max().clamp_min(1e-30))
             assert e < 1e-6, name
+
+
+@pytest.mark.parametrize("case", ["fast", "refine", "culled", "empty"])
+def test_binning_writes_the_forward_order(case):
+    """gsx_bin_tiles_async with a tile-order buffer writes the forward
+    rasterizer's order for the ranges it produces (the placement launch's
+    first workgroups, or a launch of its own on the refine_tiles path and
+    without duplicates): the same words gsx_raster_fwd computes itself, and
+    a forward run with order_ready gives bit-identical outputs."""
+    from mlx3d_amd.splatting.rasterize import raster_forward, tile_order_buffer
+    from mlx3d_amd.splatting.tiles import BinJob
+
+    say(f"binning-written tile order: {case}")
+    W, H = 328, 200
+    T = 21 * 13
+    n = 0 if case == "empty" else 6000
+    cam, means, quats, scales, opac, _ = random_scene(91, n=max(n, 1), width=W, height=H)
+    means, quats, scales, opac = means[:n], quats[:n], scales[:n], opac[:n]
+    if case == "culled":
+        means = means + np.float32(50.0)  # every Gaussian off screen: no duplicates
+    proj = project_gaussians(cam, cu(means), cu(quats), cu(scales))
+    m2 = proj["means2d"].contiguous()
+    co = torch.cat([proj["conics"], (cu(opac) * proj["compensation"])[:, None]], 1).contiguous()
+    L = _lib.load()
+    dev = m2.device
+    counts = torch.empty((n,), dtype=torch.int32, device=dev)
+    dkeys = torch.empty((n,), dtype=torch.int32, device=dev)
+    rects = torch.empty((n, 2), dtype=torch.int32, device=dev)
+    _lib.check(L.gsx_bin_prepare(n, _lib.ptr(m2), _lib.ptr(proj["radii"].contiguous()),
+                                 _lib.ptr(proj["depths"].contiguous()), W, H, _lib.ptr(counts),
+                                 _lib.ptr(dkeys), _lib.ptr(rects), _lib.stream_handle(dev)),
+               "gsx_bin_prepare")
+    order = tile_order_buffer(W, H, dev)
+    order.fill_(-7)
+    job = BinJob(counts, dkeys, rects, W, H, final=True, tile_order=order,
+                 refine=(m2, co[:, :3].contiguous()) if case == "refine" else None)
+    ids, ranges = job.result()
+    ids_full = job.ids
+    feats = cu(np.random.default_rng(5).random((n, 3), dtype=np.float32))
+    own = tile_order_buffer(W, H, dev)
+    base = raster_forward(m2, co, feats, ids_full, ranges, None, W, H, tile_order=own)
+    ready = raster_forward(m2, co, feats, ids_full, ranges, None, W, H, tile_order=order,
+                           order_ready=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(order)[T:2 * T], host(own)[T:2 * T])
+    assert np.array_equal(np.sort(host(order)[T:2 * T]), np.arange(T))
+    for name, k in (("out", 0), ("final_T", 1), ("n_contrib", 2), ("alpha", 4)):
+        assert torch.equal(base[k], ready[k]), name
+    if case != "empty":
+        assert (int(ids.numel()) == 0) == (case == "culled")
