@@ -296,6 +296,25 @@ __device__ __forceinline__ void reduce_step1(const float (&v)[NVP], float (&h)[N
     }
 }
 
+// Step 2 alone for row groups M0..M1-1: q[m] = swap16-sum of h[2m],
+// h[2m + 1] (the row's partial of value 4m + row_value(row)).
+template <int M0, int M1, int NVP>
+__device__ __forceinline__ void reduce_step2(const float (&h)[NVP / 2], float (&q)[NVP / 4]) {
+    if constexpr (M0 < M1) {
+        constexpr int N = (M1 - M0) < 4 ? (M1 - M0) : 4;
+        float a[N], b[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            a[k] = h[2 * (M0 + k)];
+            b[k] = h[2 * (M0 + k) + 1];
+        }
+        swap_rows16<N>(a, b);
+#pragma unroll
+        for (int k = 0; k < N; ++k) q[M0 + k] = a[k] + b[k];
+        reduce_step2<M0 + N, M1, NVP>(h, q);
+    }
+}
+
 // Steps 2 and 3 for row groups M0..M1-1: swap16-sum of h[2m], h[2m + 1],
 // then the four DPP steps within each row.
 template <int M0, int M1, int NVP>
@@ -814,13 +833,80 @@ __device__ __forceinline__ void bwd_reduce2(float (&w)[4 * ((CH + 7) / 2)], int 
     constexpr int NV = CH + 6;
     constexpr int NH = (NV + 1) / 2;  // value pairs per Gaussian
     static_assert(2 * NH <= 4 * ((NV + 3) / 4), "a Gaussian's slot holds its padded pairs");
-    float tot[NH];
-    wave_reduce_rows<4 * NH, 2 * NV>(w, tot);
-    if ((lane & 15) == 15) {
-        const int rv = row_value(lane >> 4);
-        float* dst = slot_at<CH>(part, (rv & 1) ? ob : oa) + (rv >> 1);
+    constexpr int K1 = NV;            // value pairs with a non-zero member (of 2 NH)
+    constexpr int K2 = (K1 + 1) / 2;  // row groups with a non-zero member
+    float h[2 * NH];
 #pragma unroll
-        for (int m = 0; m < NH; ++m) dst[2 * m] = tot[m];
+    for (int k = K1; k < 2 * NH; ++k) h[k] = 0.0f;
+    reduce_step1<0, K1, 4 * NH, 2 * NV>(w, h);
+    // step 2 (swap16-sum between rows) as in wave_reduce_rows: a[m] holds in
+    // row r the row's partial of value 4m + row_value(r)
+    float a[NH];
+#pragma unroll
+    for (int m = K2; m < NH; ++m) a[m] = 0.0f;
+    reduce_step2<0, K2, 4 * NH>(h, a);
+    // Step 3 within the row with halving exchanges.  A: row_mirror pairs
+    // a[2j], a[2j + 1] (lanes 8..15 keep the second); B: row_half_mirror
+    // pairs those results (lanes with bit 2 set keep the second); then two
+    // quad steps.  Afterwards d[k] holds the total of a[4k + 2 bit2 + bit3],
+    // bl (nb odd) that of a[2 (nb - 1) + bit3] and c (NH odd) that of
+    // a[NH - 1]: 3 instructions per exchanged pair instead of 2 per value
+    // and step.
+    const int l = lane & 15;
+    const bool hi8 = (l & 8) != 0, hi4 = (l & 4) != 0;
+    constexpr int NB = NH / 2, ND = NB / 2;
+    float b[NB + 1];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const float x = hi8 ? a[2 * j + 1] : a[2 * j];
+        const float y = hi8 ? a[2 * j] : a[2 * j + 1];
+        b[j] = x + dpp_f<0x140, 0xF, 0xF>(y);  // row_mirror
+    }
+    float c = 0.0f;
+    if constexpr (NH % 2 == 1) {
+        c = a[NH - 1];
+        c += dpp_f<0x140, 0xF, 0xF>(c);
+        c += dpp_f<0x141, 0xF, 0xF>(c);  // row_half_mirror
+    }
+    float d[ND + 1];
+#pragma unroll
+    for (int k = 0; k < ND; ++k) {
+        const float x = hi4 ? b[2 * k + 1] : b[2 * k];
+        const float y = hi4 ? b[2 * k] : b[2 * k + 1];
+        d[k] = x + dpp_f<0x141, 0xF, 0xF>(y);  // row_half_mirror
+    }
+    float bl = 0.0f;
+    if constexpr (NB % 2 == 1) {
+        bl = b[NB - 1];
+        bl += dpp_f<0x141, 0xF, 0xF>(bl);
+    }
+    auto quad_sum = [](float t) {
+        t += dpp_f<0xB1, 0xF, 0xF>(t);  // quad_perm [1,0,3,2]
+        t += dpp_f<0x4E, 0xF, 0xF>(t);  // quad_perm [2,3,0,1]
+        return t;
+    };
+#pragma unroll
+    for (int k = 0; k < ND; ++k) d[k] = quad_sum(d[k]);
+    if constexpr (NB % 2 == 1) bl = quad_sum(bl);
+    if constexpr (NH % 2 == 1) c = quad_sum(c);
+    // the sums complete before the stores' lane branches (the compiler would
+    // move the last add into them and lose its DPP form)
+#pragma unroll
+    for (int k = 0; k < ND; ++k) asm volatile("" ::"v"(d[k]));
+    if constexpr (NB % 2 == 1) asm volatile("" ::"v"(bl));
+    if constexpr (NH % 2 == 1) asm volatile("" ::"v"(c));
+    const int rv = row_value(lane >> 4);
+    float* dst = slot_at<CH>(part, (rv & 1) ? ob : oa) + (rv >> 1);
+    const int sel = (hi4 ? 2 : 0) + (hi8 ? 1 : 0);
+    if ((l & 3) == 3) {
+#pragma unroll
+        for (int k = 0; k < ND; ++k) dst[2 * (4 * k + sel)] = d[k];
+    }
+    if constexpr (NB % 2 == 1) {
+        if ((l & 7) == 7) dst[2 * (2 * (NB - 1) + (hi8 ? 1 : 0))] = bl;
+    }
+    if constexpr (NH % 2 == 1) {
+        if (l == 15) dst[2 * (NH - 1)] = c;
     }
 }
 
