@@ -1382,21 +1382,33 @@ __device__ __forceinline__ void bwd_walk_mx(const uint32_t* list, int cnt, int l
             b0 = rec_at(s_r0, nb);
             b1 = rec_at(s_r1, nb);
             if (ha || hb) {
-                float w[12], tot[3];
+                float w[12], h[6], q[3];
 #pragma unroll
-                for (int q = 0; q < kMxGeo; ++q) {
-                    w[2 * q] = va[q];
-                    w[2 * q + 1] = vb[q];
+                for (int k = 0; k < kMxGeo; ++k) {
+                    w[2 * k] = va[k];
+                    w[2 * k + 1] = vb[k];
                 }
-                wave_reduce_rows<12, 12>(w, tot);
-                if ((lane & 15) == 15) {
-                    // rows with row_value 0 and 2 hold a's values 2m and
-                    // 2m + 1, rows with 1 and 3 b's
-                    const int rv = row_value(lane >> 4);
-                    float* dst = sum[((rv & 1) ? ob : oa) >> 4] + (rv >> 1);
-#pragma unroll
-                    for (int m = 0; m < 3; ++m) atomicAdd(dst + 2 * m, tot[m]);
-                }
+                reduce_step1<0, 6, 12, 12>(w, h);
+                reduce_step2<0, 3, 12>(h, q);
+                // within the row: q[0], q[1] exchanged by halving over
+                // row_mirror (lanes 8..15 keep q[1]), q[2] summed whole;
+                // rows with row_value 0 and 2 hold a's values 2m and 2m + 1,
+                // rows with 1 and 3 b's
+                const bool hi8 = (lane & 8) != 0;
+                const float x = hi8 ? q[1] : q[0], y = hi8 ? q[0] : q[1];
+                float b = x + dpp_f<0x140, 0xF, 0xF>(y);  // row_mirror
+                float c = q[2] + dpp_f<0x140, 0xF, 0xF>(q[2]);
+                b += dpp_f<0x141, 0xF, 0xF>(b);  // row_half_mirror
+                c += dpp_f<0x141, 0xF, 0xF>(c);
+                b += dpp_f<0xB1, 0xF, 0xF>(b);  // quad_perm [1,0,3,2]
+                c += dpp_f<0xB1, 0xF, 0xF>(c);
+                b += dpp_f<0x4E, 0xF, 0xF>(b);  // quad_perm [2,3,0,1]
+                c += dpp_f<0x4E, 0xF, 0xF>(c);
+                asm volatile("" ::"v"(b), "v"(c));
+                const int rv = row_value(lane >> 4);
+                float* dst = sum[((rv & 1) ? ob : oa) >> 4] + (rv >> 1);
+                if ((lane & 7) == 7) atomicAdd(dst + (hi8 ? 2 : 0), b);
+                if ((lane & 15) == 15) atomicAdd(dst + 4, c);
             }
             oa = na;
             ob = nb;
