@@ -560,9 +560,10 @@ __device__ __forceinline__ void fwd_walk(const uint32_t* list, int cnt, const fl
     }
 }
 
-// Occupancy targets that the compiler meets without spilling: six waves per
-// SIMD (<= 80 VGPRs) up to four channels, five up to eight.
-constexpr int fwd_min_waves(int ch) { return ch <= 4 ? 6 : (ch <= 8 ? 5 : 1); }
+// Occupancy targets that the compiler meets without spilling: seven waves
+// per SIMD (<= 72 VGPRs) up to three channels (C3's forward 193.8 -> 190.4
+// us against six), six up to four, five up to eight.
+constexpr int fwd_min_waves(int ch) { return ch <= 3 ? 7 : (ch <= 4 ? 6 : (ch <= 8 ? 5 : 1)); }
 
 template <int CH, bool DEPTH>
 __global__ __launch_bounds__(kThreads, fwd_min_waves(CH)) void k_raster_fwd(
